@@ -1,0 +1,129 @@
+"""Loader for the in-tree HIP library ``libsnhip.so``.
+
+The library is the product's only compute path: nothing here falls back to a
+CPU implementation. If the library is missing, every entry point raises.
+
+``torch`` is imported first on purpose: torch ships its own
+``libamdhip64.so.7``, and loading it before ``libsnhip.so`` makes the two
+share one HIP runtime (same SONAME), so device pointers and streams from
+torch are valid in the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libsnhip.so"
+INCLUDE = PKG.parent / "include"
+
+STATUS = {
+    0: "OK",
+    -1: "E_INVAL (NULL pointer or non-positive dimension)",
+    -2: "E_NOMEM (allocation failed)",
+    -3: "E_IO (open or read failed)",
+    -4: "E_FORMAT (magic / version / size mismatch)",
+    -5: "E_UNSUPPORTED (not supported by this build)",
+    -6: "E_DEVICE (HIP runtime error)",
+}
+
+
+class SnHipError(RuntimeError):
+    def __init__(self, what: str, code: int):
+        detail = last_error() if code == -6 else ""
+        super().__init__(f"{what}: {STATUS.get(code, code)}" + (f": {detail}" if detail else ""))
+        self.code = code
+
+
+_lib = None
+
+V = ctypes.c_void_p
+I32 = ctypes.c_int32
+U32 = ctypes.c_uint32
+CP = ctypes.c_char_p
+INT = ctypes.c_int
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "snhip_abi_version": (I32, []),
+    "snhip_abi_caps": (U32, []),
+    "snhip_abi_check": (I32, [I32]),
+    "snhip_abi_version_string": (I32, [V, I32]),
+    "snhip_abi_backend_string": (I32, [V, I32]),
+    "snhip_abi_last_error": (I32, [V, I32]),
+    "snhip_abi_set_threads": (I32, [I32]),
+    "snhip_abi_get_threads": (I32, []),
+    "snhip_abi_recur_step": (I32, [V, V, V, I32, I32, I32]),
+    "snhip_abi_recur_scan": (I32, [V, V, V, V, V, I32, I32, I32, I32]),
+    "snhip_abi_recur_step_dev": (I32, [V, V, V, I32, I32, I32, V]),
+    "snhip_abi_recur_scan_dev": (I32, [V, V, V, V, V, I32, I32, I32, I32, V]),
+    "snhip_abi_quant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
+    "snhip_abi_dequant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
+}
+
+
+def available() -> bool:
+    return LIB_PATH.exists()
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built; run `python -m sunnynet_amd.build` "
+                           "(the HIP backend has no CPU fallback)")
+    L = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGS.items():
+        if hasattr(L, name):
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+    _lib = L
+    return L
+
+
+def register(sigs: dict) -> None:
+    """Declare more signatures (used by the model bindings)."""
+    _SIGS.update(sigs)
+    if _lib is not None:
+        for name, (res, args) in sigs.items():
+            if hasattr(_lib, name):
+                f = getattr(_lib, name)
+                f.restype = res
+                f.argtypes = args
+
+
+def last_error() -> str:
+    L = lib()
+    n = L.snhip_abi_last_error(None, 0)
+    buf = ctypes.create_string_buffer(max(1, n))
+    L.snhip_abi_last_error(buf, n)
+    return buf.value.decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise SnHipError(what, int(rc))
+
+
+def stream_handle(device=None) -> int:
+    """The raw hipStream_t of torch's current stream."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int:
+    return t.data_ptr()
+
+
+def declared_symbols() -> list:
+    """Every snhip_* function declared in include/*.h."""
+    names = set()
+    for h in sorted(INCLUDE.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(snhip_\w+)\s*\(", text))
+    return sorted(names)

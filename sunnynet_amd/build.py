@@ -1,0 +1,58 @@
+"""Build recipe for the HIP backend library (libsnhip.so, gfx950).
+
+Compiles every ``csrc/*.hip`` in one hipcc invocation into an in-tree shared
+library. Runs on a machine without a GPU (hipcc cross-compiles).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+LIB = PKG / "libsnhip.so"
+ARCH = os.environ.get("SNHIP_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}",
+    # Packed-FP32 VALU forms are kept out of generated code on this target.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-rdc",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if c and Path(c).exists():
+            return c
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def sources() -> list:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False, extra: list | None = None) -> Path:
+    """Compile libsnhip.so (always rebuilds)."""
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc()] + HIPCC_FLAGS + (extra or []) + [f"-I{INCLUDE}", f"-I{CSRC}"]
+    cmd += [str(s) for s in sources()] + ["-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-6000:]}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    p = build(verbose="-v" in sys.argv)
+    print(p)

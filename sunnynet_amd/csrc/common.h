@@ -1,0 +1,74 @@
+// Shared host/device helpers for the SunnyNet HIP backend (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "snhip_abi.h"
+
+namespace snhip {
+
+// Per-thread text of the last HIP failure, exposed by snhip_abi_last_error.
+void set_last_error(const std::string& msg);
+const std::string& last_error();
+
+// Records the failing call and returns SNHIP_E_DEVICE from the enclosing
+// function (which must return snhip_status).
+#define SNHIP_CHECK(expr)                                                     \
+    do {                                                                      \
+        hipError_t e_ = (expr);                                               \
+        if (e_ != hipSuccess) {                                               \
+            ::snhip::set_last_error(std::string(#expr) + ": " +               \
+                                    hipGetErrorString(e_));                   \
+            return SNHIP_E_DEVICE;                                            \
+        }                                                                     \
+    } while (0)
+
+// Same, for functions returning a pointer (returns nullptr).
+#define SNHIP_CHECK_NULL(expr)                                                \
+    do {                                                                      \
+        hipError_t e_ = (expr);                                               \
+        if (e_ != hipSuccess) {                                               \
+            ::snhip::set_last_error(std::string(#expr) + ": " +               \
+                                    hipGetErrorString(e_));                   \
+            return nullptr;                                                   \
+        }                                                                     \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Waits for this wave's outstanding LDS operations only (gfx9 s_waitcnt
+// encoding: vmcnt = 63, expcnt = 7, lgkmcnt = 0); global loads stay in flight.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// Workgroup barrier that orders LDS traffic but does not drain outstanding
+// global loads (a full __syncthreads() would wait for every prefetch).
+__device__ __forceinline__ void barrier_lds() {
+    wait_lds();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Reference-order arithmetic helpers: no contraction into FMA.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+
+}  // namespace snhip
+
+// Internal launchers shared across translation units.
+namespace snhip {
+snhip_status launch_recur_scan(const float* a, const float* b, const float* s0,
+                               float* out, float* send, int B, int T, int N,
+                               int gated, hipStream_t st);
+snhip_status launch_recur_step(const float* a, const float* b, float* s, int B,
+                               int N, int gated, hipStream_t st);
+snhip_status launch_quant_i4(const float* x, uint8_t* q, float* scale, int rows,
+                             int N, int block, hipStream_t st);
+snhip_status launch_dequant_i4(const uint8_t* q, const float* scale, float* x,
+                               int rows, int N, int block, hipStream_t st);
+}  // namespace snhip

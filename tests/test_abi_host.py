@@ -1,0 +1,70 @@
+"""C-ABI contract checks that need no GPU (mirrors the reference's
+tests/test_abi.py:28-95): the library loads, exports every declared symbol,
+reports version / caps / backend, and rejects bad arguments before touching
+the device."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from sunnynet_amd import _native
+from sunnynet_amd.runtime import abi
+
+
+def test_library_exports_every_declared_symbol():
+    L = _native.lib()
+    declared = _native.declared_symbols()
+    assert len(declared) >= 14
+    missing = [n for n in declared if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_version_matches_header():
+    assert abi.version() == abi.ABI_VERSION == 0x10100
+    assert abi.version_string() == "1.1.0"
+    assert abi.backend_string() == "hip"
+
+
+def test_caps_include_core():
+    names = abi.cap_names()
+    for want in ("recur_scan", "recur_step", "threads", "device_ptr", "int4"):
+        assert want in names
+    assert "quant_i8" not in names
+
+
+def test_check_compat_and_incompat():
+    assert abi.check(abi.ABI_MAJOR) == abi.STATUS_OK
+    assert abi.check(abi.ABI_MAJOR + 1) == -5
+
+
+def test_status_messages_are_defined():
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert abi.status_str(code)
+
+
+def test_invalid_args_return_einval():
+    """tests/test_abi.py:86-95: NULL pointers, non-positive dims, zero threads."""
+    L = _native.lib()
+    a = np.zeros((2, 8), np.float32)
+    pa = a.ctypes.data
+    assert L.snhip_abi_recur_step(None, pa, pa, 2, 8, 0) == -1
+    assert L.snhip_abi_recur_step(pa, pa, pa, 2, -8, 0) == -1
+    assert L.snhip_abi_recur_scan(pa, pa, pa, pa, pa, 2, 0, 8, 1) == -1
+    assert L.snhip_abi_recur_scan(pa, None, pa, pa, pa, 2, 1, 8, 1) == -1
+    assert L.snhip_abi_recur_scan_dev(pa, pa, pa, pa, pa, 0, 1, 8, 1, None) == -1
+    assert L.snhip_abi_recur_step_dev(pa, pa, None, 2, 8, 1, None) == -1
+    assert L.snhip_abi_quant_i4_dev(pa, pa, pa, 2, 8, 3, None) == -1      # odd block
+    assert L.snhip_abi_quant_i4_dev(pa, pa, pa, 2, 48, 32, None) == -1    # N % block
+    assert L.snhip_abi_dequant_i4_dev(None, pa, pa, 2, 64, 32, None) == -1
+    assert L.snhip_abi_set_threads(0) == -1
+    assert L.snhip_abi_set_threads(4) == 0 and L.snhip_abi_get_threads() == 4
+
+
+def test_string_buffer_protocol():
+    L = _native.lib()
+    n = L.snhip_abi_backend_string(None, 0)
+    assert n == 4
+    small = ctypes.create_string_buffer(2)
+    assert L.snhip_abi_backend_string(small, 2) == 4 and small.value == b""
