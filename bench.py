@@ -31,6 +31,10 @@ from sunnynet_amd import runtime  # noqa: E402
 from sunnynet_amd.workloads import SCAN_B, SCAN_D, SCAN_T, scan_bytes, scan_inputs  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per scan launch on this workload from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE, each scaled by the counter's reading for a plain copy of known
+# size (FETCH x2.0, WRITE x1.0): profiles/scan_gated_B16_D2048_T4096.md.
+SCAN_TRAFFIC_BYTES = 1_611_150_336
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
 
 
@@ -96,7 +100,8 @@ def bench_scan(steps: int, warmup: int, cpu: bool):
                    "B": B, "D": D, "T": T, "bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "k_recur_scan", "kernel_avg_us": round(avg_ms * 1e3, 2)},
+                     "traffic": SCAN_TRAFFIC_BYTES, "kernel": "k_recur_scan_buf",
+                     "kernel_avg_us": round(avg_ms * 1e3, 2)},
     }
     if cpu:
         res["cpu_baseline"] = cpu_scan_baseline(a, b, s0)
@@ -135,6 +140,24 @@ def cpu_scan_baseline(a, b, s0):
                       f"({med*1e3:.1f} ms each)"}
 
 
+def pmc_probe():
+    """A short fixed sequence for `rocprofv3 --pmc` runs: 3 scans of the
+    workload, then 3 plain device copies of one 537 MB input array (the copy
+    calibrates FETCH_SIZE / WRITE_SIZE against a known byte count)."""
+    dev = torch.device("cuda:0")
+    a, b, s0 = scan_inputs(SCAN_B, SCAN_T, SCAN_D, gated=True)
+    da, db, d0 = (torch.from_numpy(x).to(dev) for x in (a, b, s0))
+    for _ in range(3):
+        runtime.scan(da, db, d0, gated=True)
+    y = torch.empty_like(da)
+    for _ in range(3):
+        y.copy_(da)
+    torch.cuda.synchronize()
+    log(f"[pmc] scan bytes/launch {scan_bytes(SCAN_B, SCAN_T, SCAN_D)}; copy bytes/launch "
+        f"read {da.numel() * 4} write {da.numel() * 4}")
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,7 +165,11 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="scan", choices=["scan"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run the fixed launch sequence used for rocprofv3 --pmc and exit")
     args = ap.parse_args(argv)
+    if args.pmc_probe:
+        return pmc_probe()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one GPU only: this build has no multi-GPU path "
             "(each channel / sequence shards with no communication; see DESIGN.md).")

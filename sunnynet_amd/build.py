@@ -24,6 +24,9 @@ HIPCC_FLAGS = [
     # Packed-FP32 VALU forms are kept out of generated code on this target.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fno-gpu-rdc",
+    # No implicit contraction: kernels write fmaf() exactly where the
+    # reference fuses, and keep a*b + c as two roundings elsewhere.
+    "-ffp-contract=off",
     "-Wall", "-Wno-unused-function",
 ]
 

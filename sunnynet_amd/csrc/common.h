@@ -53,7 +53,8 @@ __device__ __forceinline__ void barrier_lds() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Reference-order arithmetic helpers: no contraction into FMA.
+// Reference-order arithmetic helpers. The library is compiled with
+// -ffp-contract=off, so these stay separate roundings.
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }

@@ -49,72 +49,116 @@ __device__ __forceinline__ void st(float* p, const float (&v)[CPL]) {
     *reinterpret_cast<V*>(p) = x;
 }
 
-template <int CPL, int W, int TC, bool GATED>
+template <int CPL, int W, int TC, bool GATED, bool ALLFUSED>
 __global__ __launch_bounds__(64 * W)
 void k_recur_scan(const float* __restrict__ a, const float* __restrict__ b,
                   const float* __restrict__ s0, float* __restrict__ out,
                   float* __restrict__ send, int B, int T, int N, int N8) {
+    static_assert(W >= 2, "the hand-off pipeline needs at least two waves");
     __shared__ float carry[CPL * 64];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
-    const long flat = ((long)blockIdx.x * 64 + lane) * CPL;
-    const bool valid = flat < (long)B * N;
-    const long bb = valid ? flat / N : 0;
-    const int n = valid ? (int)(flat - bb * N) : 0;
+    const long total = (long)B * N;
+    const long flat_raw = ((long)blockIdx.x * 64 + lane) * CPL;
+    const bool valid = flat_raw < total;
+    // Lanes past the last channel load (but never store) the last valid
+    // vector, so loads need no predicate.
+    const long flat = valid ? flat_raw : total - CPL;
+    const long bb = flat / N;
+    const int n = (int)(flat - bb * N);
     const size_t base = (size_t)bb * T * N + n;
     bool fused[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) fused[c] = (n + c) < N8;
+    for (int c = 0; c < CPL; ++c) fused[c] = ALLFUSED || (n + c) < N8;
 
     constexpr int TILE = W * TC;
     const int ntiles = (T + TILE - 1) / TILE;
+    const int nfull = T / TILE;
     float av[TC][CPL], bv[TC][CPL];
 
+    // Time indices are clamped to T-1, so every prefetch is in bounds and
+    // branch-free; only the final partial tile checks t < T when stepping.
     auto load_slot = [&](int tile) {
         const int t0 = tile * TILE + w * TC;
-        const float* pa = a + base + (size_t)t0 * N;
-        const float* pb = b + base + (size_t)t0 * N;
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
-            if (valid && t0 + k < T) {
-                ld<CPL>(av[k], pa + (size_t)k * N);
-                ld<CPL>(bv[k], pb + (size_t)k * N);
-            }
+            const size_t off = base + (size_t)min(t0 + k, T - 1) * N;
+            ld<CPL>(av[k], a + off);
+            ld<CPL>(bv[k], b + off);
+        }
+    };
+    // b' = (1 - a) * u, computed off the critical path (in the slot before
+    // this wave's own), exactly once per loaded slot.
+    auto prep = [&]() {
+        if constexpr (GATED) {
+#pragma unroll
+            for (int k = 0; k < TC; ++k)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) bv[k][c] = mul_rn(sub_rn(1.0f, av[k][c]), bv[k][c]);
+        }
+    };
+    auto step = [&](float (&s)[CPL], int k) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            if constexpr (ALLFUSED) s[c] = fmaf(av[k][c], s[c], bv[k][c]);
+            else s[c] = fused[c] ? fmaf(av[k][c], s[c], bv[k][c])
+                                 : add_rn(mul_rn(av[k][c], s[c]), bv[k][c]);
         }
     };
 
+    // The initial state enters through the same LDS slot as every later
+    // carry, so no slot ever waits on a global load into the state registers
+    // (such a wait would also drain the slot's own output stores).
+    if (w == 0) {
+        float s[CPL];
+        ld<CPL>(s, s0 + (size_t)bb * N + n);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = s[c];
+    }
     load_slot(0);
-    for (int tile = 0; tile < ntiles; ++tile) {
+    if (w == 0) prep();
+    __syncthreads();
+    // Slot j of tile t: wave j steps its TC time steps; wave j+1 prepares
+    // its own slot of tile t; at j = W-1 wave 0 prepares its slot of t+1.
+    for (int tile = 0; tile < nfull; ++tile) {
         for (int j = 0; j < W; ++j) {
             if (w == j) {
                 float s[CPL];
-                if (tile == 0 && j == 0) {
-                    if (valid) ld<CPL>(s, s0 + (size_t)bb * N + n);
-                    else {
 #pragma unroll
-                        for (int c = 0; c < CPL; ++c) s[c] = 0.0f;
-                    }
-                } else {
-#pragma unroll
-                    for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
-                }
-                const int t0 = tile * TILE + j * TC;
-                float* po = out + base + (size_t)t0 * N;
+                for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
+                float* po = out + base + (size_t)(tile * TILE + j * TC) * N;
 #pragma unroll
                 for (int k = 0; k < TC; ++k) {
-                    if (t0 + k < T) {
-#pragma unroll
-                        for (int c = 0; c < CPL; ++c) {
-                            const float x = av[k][c];
-                            const float bp = GATED ? mul_rn(sub_rn(1.0f, x), bv[k][c]) : bv[k][c];
-                            s[c] = fused[c] ? fmaf(x, s[c], bp) : add_rn(mul_rn(x, s[c]), bp);
-                        }
-                        if (valid) st<CPL>(po + (size_t)k * N, s);
-                    }
+                    step(s, k);
+                    if (valid) st<CPL>(po + (size_t)k * N, s);
                 }
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = s[c];
                 if (tile + 1 < ntiles) load_slot(tile + 1);
+            } else if (w == j + 1 || (j == W - 1 && w == 0 && tile + 1 < ntiles)) {
+                prep();
+            }
+            barrier_lds();
+        }
+    }
+    if (nfull < ntiles) {
+        for (int j = 0; j < W; ++j) {
+            if (w == j) {
+                float s[CPL];
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
+                const int t0 = nfull * TILE + j * TC;
+#pragma unroll
+                for (int k = 0; k < TC; ++k) {
+                    if (t0 + k < T) {
+                        step(s, k);
+                        if (valid) st<CPL>(out + base + (size_t)(t0 + k) * N, s);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = s[c];
+            } else if (w == j + 1) {
+                prep();
             }
             barrier_lds();
         }
@@ -124,6 +168,164 @@ void k_recur_scan(const float* __restrict__ a, const float* __restrict__ b,
 #pragma unroll
         for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
         st<CPL>(send + (size_t)bb * N + n, s);
+    }
+}
+
+// Fast path for the common layout: every workgroup's 64*CPL channels lie in
+// one batch row (N % (64*CPL) == 0) and a row fits a 2 GiB buffer window.
+// Same slot pipeline as above, but all global traffic goes through buffer
+// resources: the per-step row offset t*N*4 is a scalar (SGPR) operand, so the
+// active slot issues only its FMAs and stores (no per-access 64-bit address
+// arithmetic), and the prefetch registers hold data only, which leaves room
+// for deeper time chunks. Prefetches past T read as zero (hardware range
+// check) and are never used.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int CPL> struct BufIO;
+template <> struct BufIO<1> {
+    static __device__ __forceinline__ void load(float (&v)[1], __amdgpu_buffer_rsrc_t r, int vo, int so) {
+        v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+    }
+    static __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r, int vo, int so, const float (&v)[1]) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, vo, so, 0);
+    }
+};
+template <> struct BufIO<2> {
+    using U = u32x2;
+    static __device__ __forceinline__ void load(float (&v)[2], __amdgpu_buffer_rsrc_t r, int vo, int so) {
+        U x = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+        v[0] = __uint_as_float(x[0]); v[1] = __uint_as_float(x[1]);
+    }
+    static __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r, int vo, int so, const float (&v)[2]) {
+        U x; x[0] = __float_as_uint(v[0]); x[1] = __float_as_uint(v[1]);
+        __builtin_amdgcn_raw_buffer_store_b64(x, r, vo, so, 0);
+    }
+};
+template <> struct BufIO<4> {
+    using U = u32x4;
+    static __device__ __forceinline__ void load(float (&v)[4], __amdgpu_buffer_rsrc_t r, int vo, int so) {
+        U x = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+        for (int c = 0; c < 4; ++c) v[c] = __uint_as_float(x[c]);
+    }
+    static __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r, int vo, int so, const float (&v)[4]) {
+        U x;
+        for (int c = 0; c < 4; ++c) x[c] = __float_as_uint(v[c]);
+        __builtin_amdgcn_raw_buffer_store_b128(x, r, vo, so, 0);
+    }
+};
+
+// Raw (stride 0) buffer descriptor word 3 for gfx9-family targets.
+constexpr int kBufDword3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufDword3);
+}
+
+template <int CPL, int W, int TC, bool GATED>
+__global__ __launch_bounds__(64 * W)
+void k_recur_scan_buf(const float* __restrict__ a, const float* __restrict__ b,
+                      const float* __restrict__ s0, float* __restrict__ out,
+                      float* __restrict__ send, int T, int N) {
+    static_assert(W >= 2, "the hand-off pipeline needs at least two waves");
+    using IO = BufIO<CPL>;
+    __shared__ float carry[CPL * 64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wg_per_row = N / (64 * CPL);
+    const int bb = blockIdx.x / wg_per_row;
+    const int n0 = (blockIdx.x - bb * wg_per_row) * 64 * CPL;
+    const size_t row = (size_t)bb * T * N;
+    const uint32_t nbytes = (uint32_t)((size_t)T * N * 4);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a + row, nbytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(b + row, nbytes);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + row, nbytes);
+    const int voff = (n0 + lane * CPL) * 4;
+    const int rowb = N * 4;
+
+    constexpr int TILE = W * TC;
+    const int ntiles = (T + TILE - 1) / TILE;
+    const int nfull = T / TILE;
+    // bv holds the loaded b; bp the step addend b' (prepared off the critical
+    // path). Separate arrays keep the two lifetimes disjoint for the allocator.
+    float av[TC][CPL], bv[TC][CPL], bp[TC][CPL];
+
+    auto load_slot = [&](int tile) {
+        const int t0 = tile * TILE + w * TC;
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            IO::load(av[k], ra, voff, (t0 + k) * rowb);
+            IO::load(bv[k], rb, voff, (t0 + k) * rowb);
+        }
+    };
+    auto prep = [&]() {
+        if constexpr (GATED) {
+#pragma unroll
+            for (int k = 0; k < TC; ++k)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) bp[k][c] = mul_rn(sub_rn(1.0f, av[k][c]), bv[k][c]);
+        }
+    };
+
+    if (w == 0) {
+        float s[CPL];
+        ld<CPL>(s, s0 + (size_t)bb * N + n0 + lane * CPL);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = s[c];
+    }
+    load_slot(0);
+    if (w == 0) prep();
+    __syncthreads();
+    for (int tile = 0; tile < nfull; ++tile) {
+        for (int j = 0; j < W; ++j) {
+            if (w == j) {
+                float s[CPL];
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
+                const int t0 = tile * TILE + j * TC;
+#pragma unroll
+                for (int k = 0; k < TC; ++k) {
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) s[c] = fmaf(av[k][c], s[c], GATED ? bp[k][c] : bv[k][c]);
+                    IO::store(ro, voff, (t0 + k) * rowb, s);
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = s[c];
+                if (tile + 1 < ntiles) load_slot(tile + 1);
+            } else if (w == j + 1 || (j == W - 1 && w == 0 && tile + 1 < ntiles)) {
+                prep();
+            }
+            barrier_lds();
+        }
+    }
+    if (nfull < ntiles) {
+        for (int j = 0; j < W; ++j) {
+            if (w == j) {
+                float s[CPL];
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
+                const int t0 = nfull * TILE + j * TC;
+#pragma unroll
+                for (int k = 0; k < TC; ++k) {
+                    if (t0 + k < T) {
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) s[c] = fmaf(av[k][c], s[c], GATED ? bp[k][c] : bv[k][c]);
+                        IO::store(ro, voff, (t0 + k) * rowb, s);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = s[c];
+            } else if (w == j + 1) {
+                prep();
+            }
+            barrier_lds();
+        }
+    }
+    if (w == 0) {
+        float s[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) s[c] = carry[c * 64 + lane];
+        st<CPL>(send + (size_t)bb * N + n0 + lane * CPL, s);
     }
 }
 
@@ -145,52 +347,95 @@ hipError_t launch_cfg(const float* a, const float* b, const float* s0, float* ou
     const long lanes = ((long)B * N + CPL - 1) / CPL;
     const unsigned grid = (unsigned)((lanes + 63) / 64);
     const int N8 = N & ~7;
-    if (gated)
-        hipLaunchKernelGGL((k_recur_scan<CPL, W, TC, true>), dim3(grid), dim3(64 * W), 0, st,
-                           a, b, s0, out, send, B, T, N, N8);
-    else
-        hipLaunchKernelGGL((k_recur_scan<CPL, W, TC, false>), dim3(grid), dim3(64 * W), 0, st,
-                           a, b, s0, out, send, B, T, N, N8);
+    const dim3 g(grid), blk(64 * W);
+    if (N == N8) {
+        if (gated)
+            hipLaunchKernelGGL((k_recur_scan<CPL, W, TC, true, true>), g, blk, 0, st,
+                               a, b, s0, out, send, B, T, N, N8);
+        else
+            hipLaunchKernelGGL((k_recur_scan<CPL, W, TC, false, true>), g, blk, 0, st,
+                               a, b, s0, out, send, B, T, N, N8);
+    } else {
+        if (gated)
+            hipLaunchKernelGGL((k_recur_scan<CPL, W, TC, true, false>), g, blk, 0, st,
+                               a, b, s0, out, send, B, T, N, N8);
+        else
+            hipLaunchKernelGGL((k_recur_scan<CPL, W, TC, false, false>), g, blk, 0, st,
+                               a, b, s0, out, send, B, T, N, N8);
+    }
     return hipGetLastError();
 }
 
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 }  // namespace
 
-// Launch-shape selection. SNHIP_SCAN_SHAPE="cpl,w,tc" pins one of the compiled
-// shapes (used by the tuning sweep); otherwise the widest vector width the
-// layout allows, with enough workgroups to cover the chip.
+template <int CPL, int W, int TC>
+hipError_t launch_buf(const float* a, const float* b, const float* s0, float* out, float* send,
+                      int B, int T, int N, int gated, hipStream_t st) {
+    const unsigned grid = (unsigned)((long)B * N / (64 * CPL));
+    if (gated)
+        hipLaunchKernelGGL((k_recur_scan_buf<CPL, W, TC, true>), dim3(grid), dim3(64 * W), 0, st,
+                           a, b, s0, out, send, T, N);
+    else
+        hipLaunchKernelGGL((k_recur_scan_buf<CPL, W, TC, false>), dim3(grid), dim3(64 * W), 0, st,
+                           a, b, s0, out, send, T, N);
+    return hipGetLastError();
+}
+
+// Launch-shape selection. SNHIP_SCAN_SHAPE="kind,cpl,w,tc" (kind "buf" or
+// "gen") pins one compiled shape for the tuning sweep and tests; otherwise the
+// buffer kernel when the layout allows it, else the generic kernel.
 snhip_status launch_recur_scan(const float* a, const float* b, const float* s0,
                                float* out, float* send, int B, int T, int N,
                                int gated, hipStream_t st) {
-    int cpl = 1, w = 8, tc = 16;
     const bool al8 = aligned(a, 8) && aligned(b, 8) && aligned(s0, 8) && aligned(out, 8) &&
                      aligned(send, 8);
     const bool al16 = aligned(a, 16) && aligned(b, 16) && aligned(s0, 16) &&
                       aligned(out, 16) && aligned(send, 16);
     const long chans = (long)B * N;
+    auto buf_ok = [&](int cpl, int tile) {
+        return N % (64 * cpl) == 0 && (cpl < 2 || al8) && (cpl < 4 || al16) &&
+               (long)(T + tile) * N * 4 < (1L << 31);
+    };
+    char kind = 'g';
+    int cpl = 1, w = 8, tc = 16;
     if (N % 2 == 0 && al8 && chans / 128 >= 192) cpl = 2;
-    if (N % 4 == 0 && al16 && chans / 256 >= 256) cpl = 4;
+    if (buf_ok(2, 2 * 32) && chans / 128 >= 128) { kind = 'b'; cpl = 2; w = 2; tc = 32; }
+    else if (buf_ok(1, 4 * 32)) { kind = 'b'; cpl = 1; w = 4; tc = 32; }
     if (const char* env = getenv("SNHIP_SCAN_SHAPE")) {
+        char k[8] = {0};
         int c = 0, ww = 0, t = 0;
-        if (sscanf(env, "%d,%d,%d", &c, &ww, &t) == 3) { cpl = c; w = ww; tc = t; }
-        if ((cpl == 2 && (N % 2 || !al8)) || (cpl == 4 && (N % 4 || !al16))) return SNHIP_E_INVAL;
+        if (sscanf(env, "%3[a-z],%d,%d,%d", k, &c, &ww, &t) == 4) {
+            kind = k[0]; cpl = c; w = ww; tc = t;
+        }
+        if (kind == 'b' && !buf_ok(cpl, w * tc)) return SNHIP_E_INVAL;
+        if (kind == 'g' && ((cpl == 2 && (N % 2 || !al8)) || (cpl == 4 && (N % 4 || !al16))))
+            return SNHIP_E_INVAL;
     }
     hipError_t e = hipErrorInvalidValue;
-#define SNHIP_SCAN_CASE(C, WW, TT)                                                  \
-    if (cpl == C && w == WW && tc == TT)                                            \
+#define SNHIP_GEN_CASE(C, WW, TT)                                                   \
+    if (kind == 'g' && cpl == C && w == WW && tc == TT)                             \
         e = launch_cfg<C, WW, TT>(a, b, s0, out, send, B, T, N, gated, st);         \
     else
-    SNHIP_SCAN_CASE(1, 8, 16)
-    SNHIP_SCAN_CASE(1, 16, 16)
-    SNHIP_SCAN_CASE(2, 8, 16)
-    SNHIP_SCAN_CASE(2, 16, 8)
-    SNHIP_SCAN_CASE(2, 8, 32)
-    SNHIP_SCAN_CASE(2, 4, 32)
-    SNHIP_SCAN_CASE(4, 8, 16)
-    SNHIP_SCAN_CASE(4, 8, 8)
+#define SNHIP_BUF_CASE(C, WW, TT)                                                   \
+    if (kind == 'b' && cpl == C && w == WW && tc == TT)                             \
+        e = launch_buf<C, WW, TT>(a, b, s0, out, send, B, T, N, gated, st);         \
+    else
+    SNHIP_GEN_CASE(1, 8, 16)
+    SNHIP_GEN_CASE(2, 8, 16)
+    SNHIP_GEN_CASE(2, 2, 32)
+    SNHIP_GEN_CASE(4, 4, 16)
+    SNHIP_BUF_CASE(1, 4, 32)
+    SNHIP_BUF_CASE(1, 4, 64)
+    SNHIP_BUF_CASE(2, 2, 32)
+    SNHIP_BUF_CASE(2, 2, 64)
+    SNHIP_BUF_CASE(2, 4, 32)
+    SNHIP_BUF_CASE(2, 4, 64)
+    SNHIP_BUF_CASE(2, 8, 32)
+    SNHIP_BUF_CASE(4, 2, 32)
     { set_last_error("SNHIP_SCAN_SHAPE names a shape that is not compiled"); return SNHIP_E_UNSUPPORTED; }
-#undef SNHIP_SCAN_CASE
+#undef SNHIP_GEN_CASE
+#undef SNHIP_BUF_CASE
     if (e != hipSuccess) {
         set_last_error(std::string("recur_scan launch: ") + hipGetErrorString(e));
         return SNHIP_E_DEVICE;

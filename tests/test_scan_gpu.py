@@ -55,10 +55,12 @@ def test_scan_bitexact_host_pointers(gpu, gated):
 
 def test_scan_pinned_shapes(gpu, monkeypatch):
     """Every compiled launch shape gives the same bits."""
-    a, b, s0 = _rand(4, 333, 1024, 5)
+    a, b, s0 = _rand(4, 333, 1024, 5)   # T not a multiple of any tile
     ro, rs = oracle.recur_scan(a, b, s0, True)
     da, db, d0 = (torch.from_numpy(x).to(gpu) for x in (a, b, s0))
-    for shape in ("1,8,16", "1,16,16", "2,8,16", "2,16,8", "2,8,32", "2,4,32", "4,8,16", "4,8,8"):
+    for shape in ("gen,1,8,16", "gen,2,8,16", "gen,2,2,32", "gen,4,4,16", "buf,1,4,32",
+                  "buf,1,4,64", "buf,2,2,32", "buf,2,2,64", "buf,2,4,32", "buf,2,4,64",
+                  "buf,2,8,32", "buf,4,2,32"):
         print("shape", shape, flush=True)
         monkeypatch.setenv("SNHIP_SCAN_SHAPE", shape)
         out, send = runtime.scan(da, db, d0, gated=True)
