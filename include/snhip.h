@@ -1,0 +1,90 @@
+/* SunnyNet HIP backend: whole-model decode handle.
+ *
+ * Mirrors the reference's internal C ABI, sunnynet/runtime/sunnynet.h:18-47
+ * (sn_load / sn_step / sn_prefill / sn_reset / sn_free / sn_vocab / sn_ready),
+ * with the prefix snhip_ and the same argument order, meaning and error
+ * behaviour: loaders return NULL on an IO, magic, dimension or allocation
+ * failure; void functions tolerate a NULL handle; logits buffers of the
+ * mirrored calls are caller-owned HOST memory of length vocab. The weight file
+ * is the reference's packed fp32 runtime blob.
+ *
+ * Extensions (no reference counterpart; the reference is B=1, host-only):
+ * batched decode over independent sequences, device-pointer entry points on a
+ * caller stream, INT4 group-quantized weights, on-device greedy decoding, and
+ * state import/export in the torch SunnyState layout:
+ *   s    (B, layers, dim)             fp32
+ *   hist (B, layers, taps-1, dim)     fp32, hist[..., 0, :] the newest input.
+ *
+ * A handle owns its device memory and is not reentrant (one caller at a time),
+ * like the reference's (per-handle scratch, sunnynet.c:214).
+ */
+#ifndef SNHIP_H
+#define SNHIP_H
+
+#include <stdint.h>
+
+#include "snhip_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct SnHipModel SnHipModel;
+
+/* Weight formats for snhip_load_ex. */
+#define SNHIP_WEIGHTS_F32   0   /* fp32, as in the blob                        */
+#define SNHIP_WEIGHTS_INT4  1   /* V, U, W_z, W_c, W_s_eff and the LM head
+                                   quantized at load with quant.c's symmetric
+                                   group format; embedding lookup stays fp32  */
+
+/* sunnynet.h:22-23: B = 1, fp32 weights. */
+SnHipModel* snhip_load(const char* path, int vocab, int dim, int inner, int rank,
+                       int taps, int layers, int group, int tied);
+
+/* Same checks as snhip_load; max_batch sequences, weight_format SNHIP_WEIGHTS_*,
+ * block = INT4 group size along the input dim (even, divides dim, inner, rank). */
+SnHipModel* snhip_load_ex(const char* path, int vocab, int dim, int inner, int rank,
+                          int taps, int layers, int group, int tied,
+                          int32_t max_batch, int32_t weight_format, int32_t block);
+
+/* sunnynet.h:30 */
+void snhip_free(SnHipModel* m);
+/* sunnynet.h:31: zero every sequence's state and conv history. */
+void snhip_reset(SnHipModel* m);
+/* sunnynet.h:34: one decode step of sequence 0; logits: host, length vocab. */
+void snhip_step(SnHipModel* m, int token, float* logits);
+/* sunnynet.h:37: feed n tokens of sequence 0 in order; last logits to host. */
+void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits);
+/* sunnynet.h:39-40 */
+int snhip_vocab(const SnHipModel* m);
+int snhip_ready(const SnHipModel* m);
+
+/* ---- extensions ---------------------------------------------------------- */
+/* Stream for all later work of this handle (NULL = the null stream). */
+snhip_status snhip_set_stream(SnHipModel* m, void* stream);
+int32_t snhip_max_batch(const SnHipModel* m);
+
+/* One decode step of sequences [0, B): tokens_dev (B) int32 on the device,
+ * logits_dev (B, vocab) fp32 on the device. Enqueued on the handle's stream. */
+snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                  float* logits_dev);
+/* Same with host tokens and host logits (synchronous). Tokens are range-checked. */
+snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits);
+
+/* Greedy decoding on the device: feeds tokens_dev (B), then repeatedly takes
+ * the first maximal logit as the next token, for n_steps steps. out_tokens_dev
+ * (n_steps, B) receives the tokens chosen after each step; logits_dev (B,
+ * vocab), if not NULL, the last step's logits. No host synchronization. */
+snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                     int32_t n_steps, int32_t* out_tokens_dev,
+                                     float* logits_dev);
+
+/* State of sequences [0, B) in the SunnyState layout above, device pointers. */
+snhip_status snhip_get_state_dev(SnHipModel* m, float* s_dev, float* hist_dev, int32_t B);
+snhip_status snhip_set_state_dev(SnHipModel* m, const float* s_dev, const float* hist_dev,
+                                 int32_t B);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SNHIP_H */

@@ -62,6 +62,22 @@ _SIGS = {
     "snhip_abi_recur_scan_dev": (I32, [V, V, V, V, V, I32, I32, I32, I32, V]),
     "snhip_abi_quant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
     "snhip_abi_dequant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
+    # include/snhip.h
+    "snhip_load": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT]),
+    "snhip_load_ex": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT, I32, I32, I32]),
+    "snhip_free": (None, [V]),
+    "snhip_reset": (None, [V]),
+    "snhip_step": (None, [V, INT, V]),
+    "snhip_prefill": (None, [V, V, INT, V]),
+    "snhip_vocab": (INT, [V]),
+    "snhip_ready": (INT, [V]),
+    "snhip_set_stream": (I32, [V, V]),
+    "snhip_max_batch": (I32, [V]),
+    "snhip_step_batch_dev": (I32, [V, V, I32, V]),
+    "snhip_step_batch": (I32, [V, V, I32, V]),
+    "snhip_decode_greedy_dev": (I32, [V, V, I32, I32, V, V]),
+    "snhip_get_state_dev": (I32, [V, V, V, I32]),
+    "snhip_set_state_dev": (I32, [V, V, V, I32]),
 }
 
 

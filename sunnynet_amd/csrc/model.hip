@@ -1,0 +1,767 @@
+// SunnyNet whole-model decode on gfx950 (include/snhip.h).
+//
+// The math is the reference's decode step, sunnynet/runtime/sunnynet.c:212-334
+// (= SunnyNet.forward_step, sunnynet/model.py:113-124, sunnynet/layers.py:287-326):
+//   raw = LN(x); at = raw + conv(raw, hist); v = V at; q = U v
+//   u = u_raw * sig(g_i - g_{i+1}) * sig(g_i - g_{i+2})   (groups of 8)
+//   p = 1 - delta (1 - sig(g)); sfb = W_eff s; s' = p s + (1 - p) u
+//   z = W_z u; y = LN_I(z (1 + a/2 / (1 + |z|))); out = W_c y + b s' + sfb + x
+//   logits = E LN(x_L)
+//
+// One step is a short sequence of kernels on the handle's stream; every
+// kernel processes all B sequences. Weights live row-major (out, in) in HBM,
+// fp32 or INT4 (quant.c's packing, dequantized in registers and bit-identical
+// to sn_dequant_i4). Elementwise work keeps the reference's operation order;
+// the GEMV reductions use a parallel (wavefront) order, so logits agree with
+// the reference to float rounding, not bit for bit.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "snhip.h"
+
+namespace snhip {
+namespace {
+
+constexpr int kMagic = 0x4E4E5355;   // "USNN", sunnynet.c:33
+constexpr int kMaxTaps = 8;
+
+// ------------------------------------------------------------------ device
+__device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Sum within aligned segments of `seg` lanes (seg a power of two <= 64).
+__device__ __forceinline__ float seg_sum(float v, int seg) {
+    for (int o = seg >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// 256-thread block sum (4 waves); `red` holds 4 floats of LDS.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Two-pass LayerNorm statistics over n values (sunnynet.c:198-210 form).
+__device__ __forceinline__ void ln_stats(const float* x, int n, float eps, float* red,
+                                         float& mean, float& rstd) {
+    float sum = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) sum += x[i];
+    mean = block_sum256(sum, red) / (float)n;
+    float vs = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float d = x[i] - mean;
+        vs += d * d;
+    }
+    rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
+}
+
+__global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
+                        float* __restrict__ x, int D, int vocab) {
+    const int b = blockIdx.x;
+    const int t = tok[b];
+    const bool ok = t >= 0 && t < vocab;
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        x[(size_t)b * D + i] = ok ? embed[(size_t)t * D + i] : __builtin_nanf("");
+}
+
+// raw = LN(x); at = raw + conv(raw, hist); hist <- [raw, hist[0..K-3]] in place.
+// One block per sequence; conv order as sunnynet.c:227-237.
+__global__ __launch_bounds__(256) void k_ln_conv(
+        const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ c,
+        const float* __restrict__ dw, float* __restrict__ hist, size_t hist_bstride,
+        float* __restrict__ at, int D, int K, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    const float* xb = x + (size_t)b * D;
+    float* hb = hist + (size_t)b * hist_bstride;
+    float mean, rstd;
+    ln_stats(xb, D, eps, red, mean, rstd);
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float raw = (xb[i] - mean) * rstd * g[i] + c[i];
+        if (K > 1) {
+            float h[kMaxTaps];
+            for (int k = 0; k < K - 1; ++k) h[k] = hb[(size_t)k * D + i];
+            float acc = raw * dw[(size_t)(K - 1) * D + i];
+            for (int k = 0; k < K - 1; ++k) acc = acc + h[k] * dw[(size_t)(K - 2 - k) * D + i];
+            at[(size_t)b * D + i] = raw + acc;
+            for (int k = K - 2; k >= 1; --k) hb[(size_t)k * D + i] = h[k - 1];
+            hb[i] = raw;
+        } else {
+            at[(size_t)b * D + i] = raw;
+        }
+    }
+}
+
+// y = LN(x) per sequence (norm_mix and norm_out).
+__global__ __launch_bounds__(256) void k_ln(const float* __restrict__ x, int ldx,
+                                            const float* __restrict__ g,
+                                            const float* __restrict__ c, float* __restrict__ y,
+                                            int ldy, int n, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    const float* xb = x + (size_t)b * ldx;
+    float mean, rstd;
+    ln_stats(xb, n, eps, red, mean, rstd);
+    for (int i = threadIdx.x; i < n; i += 256) y[(size_t)b * ldy + i] = (xb[i] - mean) * rstd * g[i] + c[i];
+}
+
+// Competitive gate, decay gate and state update for every (b, channel):
+// sunnynet.c:252-266 (groups of 8, state update after the feedback GEMV).
+__global__ void k_compete_state(const float* __restrict__ q, const float* __restrict__ delta,
+                                float* __restrict__ s, size_t s_bstride, float* __restrict__ u,
+                                int B, int D, int clamp, float p_floor) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)B * D) return;
+    const int b = (int)(idx / D), i = (int)(idx - (long)b * D);
+    const float* qb = q + (size_t)b * 2 * D;
+    const float* gate = qb + D;
+    const int base = i & ~7, off = i - base;
+    const float gi = gate[i];
+    const float uu = qb[i] * (sgm(gi - gate[base + ((off + 1) & 7)]) *
+                              sgm(gi - gate[base + ((off + 2) & 7)]));
+    float p = 1.0f - delta[i] * (1.0f - sgm(gi));
+    if (clamp && p < p_floor) p = p_floor;
+    float* sp = s + (size_t)b * s_bstride + i;
+    *sp = p * *sp + (1.0f - p) * uu;
+    u[(size_t)b * D + i] = uu;
+}
+
+// ------------------------------------------------------------------- GEMV
+enum { EPI_STORE = 0, EPI_WEDGE = 1, EPI_RESID = 2 };
+
+struct GemvJob {
+    const float* w;       // fp32 (M, Kd) or nullptr
+    const uint8_t* q;     // int4 (M, Kd/2)
+    const float* sc;      // int4 scales (M, Kd/BLK)
+    int M, Kd, B;
+    const float* X; int ldx;
+    float* Y; int ldy;
+    int epi;
+    float a_tanh, b_gain;
+    const float* s; int lds;
+    const float* sfb; int ldf;
+    int nblk;
+};
+
+__device__ __forceinline__ void epilogue(const GemvJob& J, int b, int m, float acc) {
+    float* y = J.Y + (size_t)b * J.ldy + m;
+    if (J.epi == EPI_STORE) {
+        *y = acc;
+    } else if (J.epi == EPI_WEDGE) {
+        // sunnynet.c:270-271
+        *y = acc * (1.0f + 0.5f * J.a_tanh / (1.0f + fabsf(acc)));
+    } else {
+        // sunnynet.c:276: out += b_gain * s + sfb + x (x is Y itself)
+        *y = acc + (J.b_gain * J.s[(size_t)b * J.lds + m] + J.sfb[(size_t)b * J.ldf + m] + *y);
+    }
+}
+
+// Y[b, m] = sum_k W[m, k] X[b, k] for up to two independent jobs in one
+// launch (blocks [0, j0.nblk) run job 0, the rest job 1).
+// BLK = 0: fp32 weights; BLK = 32 / 64: INT4 groups of BLK inputs.
+// X is staged in LDS in chunks of BT sequences. fp32: plain rows, read as
+// float4 at the lane's columns. INT4: transposed inside each group
+// (xs[j * ngroups + g] = x[g * BLK + j]) so lanes reading the same in-group
+// position of different groups hit different banks. Each wave streams whole
+// weight rows (fp32: two rows in flight; INT4: 64/ngroups rows per pass when
+// the group count divides 64).
+template <int BLK, int BT>
+__global__ __launch_bounds__(256) void k_gemv(GemvJob j0, GemvJob j1) {
+    extern __shared__ float xs[];
+    const bool second = (int)blockIdx.x >= j0.nblk;
+    const GemvJob& J = second ? j1 : j0;
+    const int blk = second ? (int)blockIdx.x - j0.nblk : (int)blockIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int M = J.M, Kd = J.Kd, B = J.B;
+    const int nw = J.nblk * 4;
+    const int gw = blk * 4 + wv;
+
+    for (int b0 = 0; b0 < B; b0 += BT) {
+        const int nb = min(BT, B - b0);
+        __syncthreads();
+        if constexpr (BLK == 0) {
+            for (int i = threadIdx.x; i < nb * Kd; i += 256) {
+                const int bb = i / Kd, k = i - bb * Kd;
+                xs[i] = J.X[(size_t)(b0 + bb) * J.ldx + k];
+            }
+        } else {
+            const int ng = Kd / BLK;
+            for (int i = threadIdx.x; i < nb * Kd; i += 256) {
+                const int bb = i / Kd, k = i - bb * Kd;
+                const int g = k / BLK, j = k - g * BLK;
+                xs[bb * Kd + j * ng + g] = J.X[(size_t)(b0 + bb) * J.ldx + k];
+            }
+        }
+        __syncthreads();
+
+        if constexpr (BLK == 0) {
+            for (int r = gw * 2; r < M; r += nw * 2) {
+                const bool two = r + 1 < M;
+                const float* w0 = J.w + (size_t)r * Kd;
+                const float* w1 = two ? w0 + Kd : w0;
+                float a0[BT], a1[BT];
+#pragma unroll
+                for (int bb = 0; bb < BT; ++bb) { a0[bb] = 0.0f; a1[bb] = 0.0f; }
+                for (int k = lane * 4; k < Kd; k += 256) {
+                    const float4 x0 = *reinterpret_cast<const float4*>(w0 + k);
+                    const float4 x1 = *reinterpret_cast<const float4*>(w1 + k);
+#pragma unroll
+                    for (int bb = 0; bb < BT; ++bb) {
+                        if (bb < nb) {
+                            const float4 xv = *reinterpret_cast<const float4*>(xs + bb * Kd + k);
+                            a0[bb] = fmaf(x0.x, xv.x, a0[bb]); a0[bb] = fmaf(x0.y, xv.y, a0[bb]);
+                            a0[bb] = fmaf(x0.z, xv.z, a0[bb]); a0[bb] = fmaf(x0.w, xv.w, a0[bb]);
+                            a1[bb] = fmaf(x1.x, xv.x, a1[bb]); a1[bb] = fmaf(x1.y, xv.y, a1[bb]);
+                            a1[bb] = fmaf(x1.z, xv.z, a1[bb]); a1[bb] = fmaf(x1.w, xv.w, a1[bb]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int bb = 0; bb < BT; ++bb) {
+                    if (bb < nb) {
+                        const float s0 = wave_sum(a0[bb]);
+                        const float s1 = wave_sum(a1[bb]);
+                        if (lane == 0) {
+                            epilogue(J, b0 + bb, r, s0);
+                            if (two) epilogue(J, b0 + bb, r + 1, s1);
+                        }
+                    }
+                }
+            }
+        } else {
+            constexpr int HB = BLK / 2;              // bytes per group
+            const int ng = Kd / BLK;
+            const int seg = (ng < 64 && (64 % ng) == 0) ? ng : 64;
+            const int rpi = 64 / seg;                // rows per wave pass
+            const int lrow = lane / seg, lg = lane - lrow * seg;
+            for (int r0 = gw * rpi; r0 < M; r0 += nw * rpi) {
+                const int r = r0 + lrow;
+                const bool live = r < M;
+                float acc[BT];
+#pragma unroll
+                for (int bb = 0; bb < BT; ++bb) acc[bb] = 0.0f;
+                if (live) {
+                    const uint8_t* qr = J.q + (size_t)r * (Kd / 2);
+                    const float* sr = J.sc + (size_t)r * ng;
+                    for (int g = lg; g < ng; g += seg) {
+                        uint4 qv[HB / 16];
+#pragma unroll
+                        for (int h = 0; h < HB / 16; ++h)
+                            qv[h] = *reinterpret_cast<const uint4*>(qr + (size_t)g * HB + h * 16);
+                        const float sc = sr[g];
+#pragma unroll
+                        for (int j = 0; j < HB; ++j) {
+                            const uint32_t word = reinterpret_cast<const uint32_t*>(qv)[j >> 2];
+                            const uint32_t byte = (word >> ((j & 3) * 8)) & 0xFFu;
+                            // quant.c:82-83, bit-identical dequantization
+                            const float wl = (float)((int)(byte & 0x0Fu) - 8) * sc;
+                            const float wh = (float)((int)(byte >> 4) - 8) * sc;
+#pragma unroll
+                            for (int bb = 0; bb < BT; ++bb) {
+                                if (bb < nb) {
+                                    const float* xb = xs + bb * Kd;
+                                    acc[bb] = fmaf(wl, xb[j * ng + g], acc[bb]);
+                                    acc[bb] = fmaf(wh, xb[(j + HB) * ng + g], acc[bb]);
+                                }
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int bb = 0; bb < BT; ++bb) {
+                    if (bb < nb) {
+                        const float t = seg_sum(acc[bb], seg);
+                        if (live && lg == 0) epilogue(J, b0 + bb, r, t);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// First maximal index per row (torch.argmax convention, sunnynet/cli.py:41);
+// writes the token to next[b] and, if `hist_out` is set, to hist_out[b].
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, int V,
+                                                int32_t* __restrict__ next,
+                                                int32_t* __restrict__ hist_out) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int b = blockIdx.x;
+    const float* l = logits + (size_t)b * V;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += 256) {
+        const float v = l[i];
+        if (v > best || (v == best && i < idx) || (v != v && best == best)) { best = v; idx = i; }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) {
+            const float v = bv[threadIdx.x + o];
+            const int i = bi[threadIdx.x + o];
+            const float cb = bv[threadIdx.x];
+            const int ci = bi[threadIdx.x];
+            if (v > cb || (v == cb && i < ci)) { bv[threadIdx.x] = v; bi[threadIdx.x] = i; }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        next[b] = bi[0];
+        if (hist_out) hist_out[b] = bi[0];
+    }
+}
+
+// (in, out) row-major -> (out, in) row-major, 32x32 tiles through LDS.
+__global__ void k_transpose(const float* __restrict__ src, float* __restrict__ dst, int in,
+                            int out) {
+    __shared__ float tile[32][33];
+    const int bo = blockIdx.x * 32, bi = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const int i = bi + r, o = bo + tx;
+        if (i < in && o < out) tile[r][tx] = src[(size_t)i * out + o];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int o = bo + r, i = bi + tx;
+        if (o < out && i < in) dst[(size_t)o * in + i] = tile[tx][r];
+    }
+}
+
+// ------------------------------------------------------------------- host
+struct Mat {
+    int M = 0, Kd = 0;
+    float* w = nullptr;
+    uint8_t* q = nullptr;
+    float* sc = nullptr;
+};
+
+struct Layer {
+    const float *ni_g, *ni_c, *nm_g, *nm_c, *dw, *delta;
+    float a_tanh, b_gain;
+    Mat V, U, Wz, Wc, Ws;
+};
+
+}  // namespace
+}  // namespace snhip
+
+struct SnHipModel {
+    int vocab = 0, D = 0, I = 0, R = 0, K = 0, L = 0, G = 0, tied = 0, clamp = 0, kh = 0;
+    float eps = 0.f, p_floor = 0.f;
+    int max_batch = 1, wfmt = 0, block = 32;
+    std::vector<snhip::Layer> layers;
+    const float *no_g = nullptr, *no_c = nullptr, *embed = nullptr;
+    snhip::Mat head;
+    float* s = nullptr;       // (maxB, L, D)
+    float* hist = nullptr;    // (maxB, L, kh, D)
+    float *x = nullptr, *at = nullptr, *v = nullptr, *q = nullptr, *u = nullptr, *z = nullptr,
+          *yn = nullptr, *sfb = nullptr, *nrm = nullptr, *logits = nullptr;
+    int32_t* tok = nullptr;
+    std::vector<void*> allocs;
+    hipStream_t stream = nullptr;
+    int ready = 0;
+};
+
+namespace snhip {
+namespace {
+
+template <typename T>
+T* dalloc(SnHipModel* m, size_t n) {
+    void* p = nullptr;
+    if (hipMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 4) != hipSuccess) return nullptr;
+    m->allocs.push_back(p);
+    return static_cast<T*>(p);
+}
+
+void free_model(SnHipModel* m) {
+    if (!m) return;
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+// Reads the blob like sn_load (sunnynet.c:358-454): same header check,
+// same float count, NULL on any mismatch.
+bool read_blob(const char* path, const int32_t want[9], std::vector<float>& payload,
+               int32_t& clamp) {
+    FILE* f = fopen(path, "rb");
+    if (!f) { set_last_error(std::string("cannot open ") + path); return false; }
+    int32_t h[10];
+    if (fread(h, sizeof(int32_t), 10, f) != 10 || h[0] != kMagic) {
+        fclose(f); set_last_error("bad blob header (magic)"); return false;
+    }
+    for (int i = 0; i < 8; ++i)
+        if (h[i + 1] != want[i]) { fclose(f); set_last_error("blob header does not match the given dimensions"); return false; }
+    clamp = h[9];
+    const size_t D = want[1], I = want[2], R = want[3], K = want[4], L = want[5], V = want[0];
+    const size_t per_layer = 2 * D + 2 * I + K * D + D * R + R * 2 * D + D * I + I * D + D * D + D + 2;
+    const size_t total = L * per_layer + 2 + 2 * D + V * D + D * V;
+    payload.resize(total);
+    const size_t got = fread(payload.data(), sizeof(float), total, f);
+    fclose(f);
+    if (got != total) { set_last_error("blob is truncated"); return false; }
+    return true;
+}
+
+bool upload(SnHipModel* m, float*& dst, const float* src, size_t n) {
+    dst = dalloc<float>(m, n);
+    return dst && hipMemcpy(dst, src, n * sizeof(float), hipMemcpyHostToDevice) == hipSuccess;
+}
+
+// Upload an (in,out) blob matrix as (out,in), optionally quantizing to INT4.
+bool upload_mat(SnHipModel* m, Mat& M, const float* src, int in, int out, float* tmp_in,
+                float* tmp_out) {
+    M.M = out;
+    M.Kd = in;
+    const size_t n = (size_t)in * out;
+    if (hipMemcpy(tmp_in, src, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) return false;
+    float* dst = m->wfmt == SNHIP_WEIGHTS_F32 ? (M.w = dalloc<float>(m, n)) : tmp_out;
+    if (!dst) return false;
+    dim3 grid((out + 31) / 32, (in + 31) / 32);
+    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, nullptr, tmp_in, dst, in, out);
+    if (hipGetLastError() != hipSuccess) return false;
+    if (m->wfmt == SNHIP_WEIGHTS_INT4) {
+        M.q = dalloc<uint8_t>(m, n / 2);
+        M.sc = dalloc<float>(m, n / m->block);
+        if (!M.q || !M.sc) return false;
+        if (launch_quant_i4(tmp_out, M.q, M.sc, out, in, m->block, nullptr) != SNHIP_OK) return false;
+    }
+    return hipDeviceSynchronize() == hipSuccess;
+}
+
+SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank, int taps,
+                       int layers, int group, int tied, int max_batch, int wfmt, int block) {
+    if (!path || vocab <= 0 || dim <= 0 || inner <= 0 || rank <= 0 || taps <= 0 || layers <= 0 ||
+        max_batch <= 0) {
+        set_last_error("invalid arguments");
+        return nullptr;
+    }
+    if (group != 8 || dim % 8 || taps > kMaxTaps) {
+        set_last_error("unsupported shape: group must be 8, dim a multiple of 8, taps <= 8");
+        return nullptr;
+    }
+    if (dim % 4 || inner % 4 || rank % 4) { set_last_error("dim, inner, rank must be multiples of 4"); return nullptr; }
+    if (wfmt == SNHIP_WEIGHTS_INT4) {
+        if (block != 32 && block != 64) { set_last_error("INT4 block must be 32 or 64"); return nullptr; }
+        if (dim % block || inner % block || rank % block) {
+            set_last_error("INT4 block must divide dim, inner and rank");
+            return nullptr;
+        }
+    } else if (wfmt != SNHIP_WEIGHTS_F32) {
+        set_last_error("unknown weight format");
+        return nullptr;
+    }
+    const int32_t want[9] = {vocab, dim, inner, rank, taps, layers, group, tied, 0};
+    std::vector<float> P;
+    int32_t clamp = 0;
+    if (!read_blob(path, want, P, clamp)) return nullptr;
+
+    SnHipModel* m = new SnHipModel();
+    m->vocab = vocab; m->D = dim; m->I = inner; m->R = rank; m->K = taps; m->L = layers;
+    m->G = group; m->tied = tied; m->clamp = clamp; m->kh = taps > 1 ? taps - 1 : 0;
+    m->max_batch = max_batch; m->wfmt = wfmt; m->block = block;
+    const size_t D = dim, I = inner, R = rank, K = taps, V = vocab;
+    const size_t big = std::max(std::max(D * R, R * 2 * D), std::max(D * I, std::max(D * D, D * V)));
+    float* tmp_in = dalloc<float>(m, big);
+    float* tmp_out = wfmt == SNHIP_WEIGHTS_INT4 ? dalloc<float>(m, big) : nullptr;
+    if (!tmp_in || (wfmt == SNHIP_WEIGHTS_INT4 && !tmp_out)) { free_model(m); set_last_error("out of device memory"); return nullptr; }
+
+    const float* p = P.data();
+    bool ok = true;
+    m->layers.resize(layers);
+    for (int l = 0; l < layers && ok; ++l) {
+        Layer& A = m->layers[l];
+        float* t;
+        ok &= upload(m, t, p, D); A.ni_g = t; p += D;
+        ok &= upload(m, t, p, D); A.ni_c = t; p += D;
+        ok &= upload(m, t, p, I); A.nm_g = t; p += I;
+        ok &= upload(m, t, p, I); A.nm_c = t; p += I;
+        ok &= upload(m, t, p, K * D); A.dw = t; p += K * D;
+        ok = ok && upload_mat(m, A.V, p, dim, rank, tmp_in, tmp_out); p += D * R;
+        ok = ok && upload_mat(m, A.U, p, rank, 2 * dim, tmp_in, tmp_out); p += R * 2 * D;
+        ok = ok && upload_mat(m, A.Wz, p, dim, inner, tmp_in, tmp_out); p += D * I;
+        ok = ok && upload_mat(m, A.Wc, p, inner, dim, tmp_in, tmp_out); p += I * D;
+        ok = ok && upload_mat(m, A.Ws, p, dim, dim, tmp_in, tmp_out); p += D * D;
+        ok &= upload(m, t, p, D); A.delta = t; p += D;
+        A.a_tanh = p[0]; A.b_gain = p[1]; p += 2;
+    }
+    if (ok) {
+        m->eps = p[0]; m->p_floor = p[1]; p += 2;
+        float* t;
+        ok &= upload(m, t, p, D); m->no_g = t; p += D;
+        ok &= upload(m, t, p, D); m->no_c = t; p += D;
+        ok &= upload(m, t, p, V * D); m->embed = t; p += V * D;
+        ok = ok && upload_mat(m, m->head, p, dim, vocab, tmp_in, tmp_out);
+    }
+    const size_t B = max_batch;
+    if (ok) {
+        m->s = dalloc<float>(m, B * layers * D);
+        m->hist = dalloc<float>(m, B * layers * (m->kh ? m->kh : 1) * D);
+        m->x = dalloc<float>(m, B * D);
+        m->at = dalloc<float>(m, B * D);
+        m->v = dalloc<float>(m, B * R);
+        m->q = dalloc<float>(m, B * 2 * D);
+        m->u = dalloc<float>(m, B * D);
+        m->z = dalloc<float>(m, B * I);
+        m->yn = dalloc<float>(m, B * I);
+        m->sfb = dalloc<float>(m, B * D);
+        m->nrm = dalloc<float>(m, B * D);
+        m->logits = dalloc<float>(m, B * V);
+        m->tok = dalloc<int32_t>(m, B);
+        ok = m->s && m->hist && m->x && m->at && m->v && m->q && m->u && m->z && m->yn && m->sfb &&
+             m->nrm && m->logits && m->tok;
+    }
+    if (!ok) {
+        if (last_error().empty()) set_last_error("device allocation or upload failed");
+        free_model(m);
+        return nullptr;
+    }
+    // The transpose staging buffers are no longer needed.
+    for (auto it = m->allocs.begin(); it != m->allocs.end();) {
+        if (*it == tmp_in || (tmp_out && *it == tmp_out)) { (void)hipFree(*it); it = m->allocs.erase(it); }
+        else ++it;
+    }
+    if (hipMemset(m->s, 0, B * layers * D * sizeof(float)) != hipSuccess ||
+        hipMemset(m->hist, 0, B * layers * (m->kh ? m->kh : 1) * D * sizeof(float)) != hipSuccess) {
+        free_model(m);
+        return nullptr;
+    }
+    m->ready = 1;
+    return m;
+}
+
+GemvJob make_job(const Mat& W, int B, const float* X, int ldx, float* Y, int ldy) {
+    GemvJob j{};
+    j.w = W.w; j.q = W.q; j.sc = W.sc;
+    j.M = W.M; j.Kd = W.Kd; j.B = B;
+    j.X = X; j.ldx = ldx; j.Y = Y; j.ldy = ldy;
+    j.epi = EPI_STORE;
+    return j;
+}
+
+int gemv_blocks(const GemvJob& j, int wfmt, int block) {
+    int rows_per_wave = 2;
+    if (wfmt == SNHIP_WEIGHTS_INT4) {
+        const int ng = j.Kd / block;
+        rows_per_wave = (ng < 64 && 64 % ng == 0) ? 64 / ng : 1;
+    }
+    const int rows_per_block = 4 * rows_per_wave;
+    int nb = (j.M + rows_per_block - 1) / rows_per_block;
+    return nb > 4096 ? 4096 : nb;
+}
+
+template <int BLK>
+hipError_t launch_gemv_fmt(GemvJob j0, GemvJob j1, int bt, hipStream_t st) {
+    const int kd = std::max(j0.Kd, j1.nblk ? j1.Kd : 0);
+    const dim3 grid(j0.nblk + j1.nblk), blk(256);
+    if (bt == 1)
+        hipLaunchKernelGGL((k_gemv<BLK, 1>), grid, blk, (size_t)kd * 4, st, j0, j1);
+    else
+        hipLaunchKernelGGL((k_gemv<BLK, 8>), grid, blk, (size_t)kd * 4 * 8, st, j0, j1);
+    return hipGetLastError();
+}
+
+// Launch one or two GEMV jobs (pass j1.nblk = 0 for a single job).
+hipError_t launch_gemv(const SnHipModel* m, GemvJob j0, GemvJob j1, hipStream_t st) {
+    j0.nblk = gemv_blocks(j0, m->wfmt, m->block);
+    if (j1.M > 0) j1.nblk = gemv_blocks(j1, m->wfmt, m->block);
+    else j1.nblk = 0;
+    const int kd = std::max(j0.Kd, j1.nblk ? j1.Kd : 0);
+    const int bt = (j0.B > 1 && (size_t)kd * 4 * 8 <= 65536) ? 8 : 1;
+    if (m->wfmt == SNHIP_WEIGHTS_F32) return launch_gemv_fmt<0>(j0, j1, bt, st);
+    if (m->block == 32) return launch_gemv_fmt<32>(j0, j1, bt, st);
+    return launch_gemv_fmt<64>(j0, j1, bt, st);
+}
+
+// One decode step for sequences [0, B); tokens already in m->tok.
+snhip_status run_step(SnHipModel* m, int B, float* logits_out, int32_t* next_tok,
+                      int32_t* tok_record) {
+    hipStream_t st = m->stream;
+    const int D = m->D, I = m->I, R = m->R, L = m->L;
+    const size_t sbs = (size_t)L * D;                               // s batch stride
+    const size_t hbs = (size_t)L * (m->kh ? m->kh : 1) * D;         // hist batch stride
+    hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->x, D, m->vocab);
+    for (int l = 0; l < L; ++l) {
+        const Layer& A = m->layers[l];
+        float* s_l = m->s + (size_t)l * D;
+        float* h_l = m->hist + (size_t)l * (m->kh ? m->kh : 1) * D;
+        hipLaunchKernelGGL(k_ln_conv, dim3(B), dim3(256), 0, st, m->x, A.ni_g, A.ni_c, A.dw, h_l,
+                           hbs, m->at, D, m->K, m->eps);
+        // v = V at and sfb = W_eff s (old state), one launch.
+        GemvJob jv = make_job(A.V, B, m->at, D, m->v, R);
+        GemvJob js = make_job(A.Ws, B, s_l, (int)sbs, m->sfb, D);
+        SNHIP_CHECK(launch_gemv(m, jv, js, st));
+        GemvJob ju = make_job(A.U, B, m->v, R, m->q, 2 * D);
+        GemvJob none{};
+        SNHIP_CHECK(launch_gemv(m, ju, none, st));
+        const long n = (long)B * D;
+        hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
+        GemvJob jz = make_job(A.Wz, B, m->u, D, m->z, I);
+        jz.epi = EPI_WEDGE;
+        jz.a_tanh = A.a_tanh;
+        SNHIP_CHECK(launch_gemv(m, jz, none, st));
+        hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->z, I, A.nm_g, A.nm_c, m->yn, I, I,
+                           m->eps);
+        GemvJob jc = make_job(A.Wc, B, m->yn, I, m->x, D);
+        jc.epi = EPI_RESID;
+        jc.b_gain = A.b_gain;
+        jc.s = s_l; jc.lds = (int)sbs;
+        jc.sfb = m->sfb; jc.ldf = D;
+        SNHIP_CHECK(launch_gemv(m, jc, none, st));
+    }
+    hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->x, D, m->no_g, m->no_c, m->nrm, D, D,
+                       m->eps);
+    GemvJob jh = make_job(m->head, B, m->nrm, D, logits_out, m->vocab);
+    GemvJob none{};
+    SNHIP_CHECK(launch_gemv(m, jh, none, st));
+    if (next_tok)
+        hipLaunchKernelGGL(k_argmax, dim3(B), dim3(256), 0, st, logits_out, m->vocab, next_tok,
+                           tok_record);
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
+bool tokens_ok(const SnHipModel* m, const int32_t* t, int n) {
+    for (int i = 0; i < n; ++i)
+        if (t[i] < 0 || t[i] >= m->vocab) return false;
+    return true;
+}
+
+}  // namespace
+}  // namespace snhip
+
+using namespace snhip;
+
+extern "C" {
+
+SnHipModel* snhip_load(const char* path, int vocab, int dim, int inner, int rank, int taps,
+                       int layers, int group, int tied) {
+    return load_model(path, vocab, dim, inner, rank, taps, layers, group, tied, 1,
+                      SNHIP_WEIGHTS_F32, 32);
+}
+
+SnHipModel* snhip_load_ex(const char* path, int vocab, int dim, int inner, int rank, int taps,
+                          int layers, int group, int tied, int32_t max_batch,
+                          int32_t weight_format, int32_t block) {
+    return load_model(path, vocab, dim, inner, rank, taps, layers, group, tied, max_batch,
+                      weight_format, block);
+}
+
+void snhip_free(SnHipModel* m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    else (void)hipDeviceSynchronize();
+    free_model(m);
+}
+
+void snhip_reset(SnHipModel* m) {
+    if (!m) return;
+    const size_t B = m->max_batch;
+    (void)hipMemsetAsync(m->s, 0, B * m->L * m->D * sizeof(float), m->stream);
+    (void)hipMemsetAsync(m->hist, 0, B * m->L * (m->kh ? m->kh : 1) * m->D * sizeof(float),
+                         m->stream);
+    (void)hipStreamSynchronize(m->stream);
+}
+
+int snhip_vocab(const SnHipModel* m) { return m ? m->vocab : 0; }
+int snhip_ready(const SnHipModel* m) { return m && m->ready; }
+int32_t snhip_max_batch(const SnHipModel* m) { return m ? m->max_batch : 0; }
+
+snhip_status snhip_set_stream(SnHipModel* m, void* stream) {
+    if (!m) return SNHIP_E_INVAL;
+    m->stream = as_stream(stream);
+    return SNHIP_OK;
+}
+
+snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                  float* logits_dev) {
+    if (!m || !tokens_dev || !logits_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens_dev, B * sizeof(int32_t), hipMemcpyDeviceToDevice,
+                               m->stream));
+    return run_step(m, B, logits_dev, nullptr, nullptr);
+}
+
+snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits) {
+    if (!m || !tokens || !logits || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    if (!tokens_ok(m, tokens, B)) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens, B * sizeof(int32_t), hipMemcpyHostToDevice,
+                               m->stream));
+    const snhip_status rc = run_step(m, B, m->logits, nullptr, nullptr);
+    if (rc != SNHIP_OK) return rc;
+    SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)B * m->vocab * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream));
+    SNHIP_CHECK(hipStreamSynchronize(m->stream));
+    return SNHIP_OK;
+}
+
+void snhip_step(SnHipModel* m, int token, float* logits) {
+    if (!m || !logits) return;
+    const int32_t t = token;
+    (void)snhip_step_batch(m, &t, 1, logits);
+}
+
+void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits) {
+    if (!m || !tokens || n <= 0 || !logits) return;
+    for (int i = 0; i < n; ++i) {
+        if (tokens[i] < 0 || tokens[i] >= m->vocab) return;
+        (void)hipMemcpyAsync(m->tok, &tokens[i], sizeof(int32_t), hipMemcpyHostToDevice, m->stream);
+        if (run_step(m, 1, m->logits, nullptr, nullptr) != SNHIP_OK) return;
+    }
+    (void)hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float),
+                         hipMemcpyDeviceToHost, m->stream);
+    (void)hipStreamSynchronize(m->stream);
+}
+
+snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                     int32_t n_steps, int32_t* out_tokens_dev,
+                                     float* logits_dev) {
+    if (!m || !tokens_dev || !out_tokens_dev || B <= 0 || B > m->max_batch || n_steps <= 0)
+        return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens_dev, B * sizeof(int32_t), hipMemcpyDeviceToDevice,
+                               m->stream));
+    float* lg = logits_dev ? logits_dev : m->logits;
+    for (int i = 0; i < n_steps; ++i) {
+        const snhip_status rc = run_step(m, B, lg, m->tok, out_tokens_dev + (size_t)i * B);
+        if (rc != SNHIP_OK) return rc;
+    }
+    return SNHIP_OK;
+}
+
+snhip_status snhip_get_state_dev(SnHipModel* m, float* s_dev, float* hist_dev, int32_t B) {
+    if (!m || !s_dev || B <= 0 || B > m->max_batch || (m->kh && !hist_dev)) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(s_dev, m->s, (size_t)B * m->L * m->D * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->stream));
+    if (m->kh)
+        SNHIP_CHECK(hipMemcpyAsync(hist_dev, m->hist, (size_t)B * m->L * m->kh * m->D * sizeof(float),
+                                   hipMemcpyDeviceToDevice, m->stream));
+    return SNHIP_OK;
+}
+
+snhip_status snhip_set_state_dev(SnHipModel* m, const float* s_dev, const float* hist_dev,
+                                 int32_t B) {
+    if (!m || !s_dev || B <= 0 || B > m->max_batch || (m->kh && !hist_dev)) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->s, s_dev, (size_t)B * m->L * m->D * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->stream));
+    if (m->kh)
+        SNHIP_CHECK(hipMemcpyAsync(m->hist, hist_dev, (size_t)B * m->L * m->kh * m->D * sizeof(float),
+                                   hipMemcpyDeviceToDevice, m->stream));
+    return SNHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,142 @@
+"""Whole-model decode handle on the GPU, with the reference's ``SnModel``
+interface (sunnynet/runtime/model.py:92-128).
+
+``HipModel(path, vocab, dim, inner, rank, taps, layers, group=8, tied=1)``
+loads the reference's packed fp32 runtime blob; ``reset()``, ``step(token)``
+and ``prefill(tokens)`` behave like the reference's (one B=1 sequence, host
+``list[float]`` logits, ``RuntimeError`` when loading fails).
+
+Extensions: ``max_batch`` independent sequences, ``weights="int4"`` with a
+group ``block`` (INT4 quantized at load in the reference's quant.c format),
+``step_batch`` / ``decode_greedy`` on torch device tensors without host
+round trips, and ``get_state`` / ``set_state`` in the torch ``SunnyState``
+layout (s (B,L,D), hist (B,L,K-1,D), newest entry first).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from .. import _native
+
+__all__ = ["HipModel", "SnModel", "model_available"]
+
+WEIGHT_FORMATS = {"fp32": 0, "int4": 1}
+
+
+def model_available() -> bool:
+    return _native.available()
+
+
+class HipModel:
+    """Decode handle (B sequences) backed by libsnhip.so."""
+
+    def __init__(self, path, vocab, dim, inner, rank, taps, layers, group=8, tied=1,
+                 half=False, *, max_batch: int = 1, weights: str = "fp32", block: int = 32,
+                 device=None):
+        if half:
+            raise RuntimeError("fp16 weights are not provided by the HIP backend; "
+                               "use weights='int4' for reduced-precision weights")
+        self._lib = _native.lib()
+        self.device = torch.device(device or "cuda:0")
+        self.vocab, self.dim, self.layers, self.taps = vocab, dim, layers, taps
+        self.kh = max(0, taps - 1)
+        self.max_batch = int(max_batch)
+        with torch.cuda.device(self.device):
+            self._h = self._lib.snhip_load_ex(str(path).encode(), vocab, dim, inner, rank, taps,
+                                              layers, group, int(tied), self.max_batch,
+                                              WEIGHT_FORMATS[weights], int(block))
+        if not self._h:
+            raise RuntimeError(f"snhip_load failed: {path}: {_native.last_error()}")
+        if not self._lib.snhip_ready(self._h):
+            raise RuntimeError("snhip_load returned a handle that is not ready")
+        self._logits = (ctypes.c_float * vocab)()
+        self._bind_stream()
+
+    def _bind_stream(self):
+        _native.check(self._lib.snhip_set_stream(self._h, _native.stream_handle(self.device)),
+                      "snhip_set_stream")
+
+    # ---------------------------------------------- reference-shaped surface
+    def reset(self):
+        self._bind_stream()
+        self._lib.snhip_reset(self._h)
+
+    def step(self, token: int) -> list:
+        self._bind_stream()
+        self._lib.snhip_step(self._h, int(token), ctypes.byref(self._logits))
+        return list(self._logits)
+
+    def prefill(self, tokens) -> list:
+        toks = list(tokens)
+        self._bind_stream()
+        buf = (ctypes.c_int * len(toks))(*toks)
+        self._lib.snhip_prefill(self._h, buf, len(toks), ctypes.byref(self._logits))
+        return list(self._logits)
+
+    # -------------------------------------------------------- device surface
+    def step_batch(self, tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """tokens (B,) int32 on the device -> logits (B, vocab) on the device."""
+        B = int(tokens.shape[0])
+        tokens = tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        if out is None:
+            out = torch.empty(B, self.vocab, device=self.device, dtype=torch.float32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_step_batch_dev(self._h, tokens.data_ptr(), B, out.data_ptr()),
+                      "snhip_step_batch_dev")
+        return out
+
+    def step_batch_host(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        out = np.empty((t.size, self.vocab), np.float32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_step_batch(self._h, t.ctypes.data, t.size, out.ctypes.data),
+                      "snhip_step_batch")
+        return out
+
+    def decode_greedy(self, tokens: torch.Tensor, n_steps: int, logits: torch.Tensor | None = None):
+        """Greedy decoding on the device; returns (n_steps, B) int32 tokens."""
+        B = int(tokens.shape[0])
+        tokens = tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        out = torch.empty(n_steps, B, device=self.device, dtype=torch.int32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_decode_greedy_dev(
+            self._h, tokens.data_ptr(), B, int(n_steps), out.data_ptr(),
+            logits.data_ptr() if logits is not None else None), "snhip_decode_greedy_dev")
+        return out
+
+    def get_state(self, B: int | None = None):
+        B = self.max_batch if B is None else B
+        s = torch.empty(B, self.layers, self.dim, device=self.device)
+        h = torch.empty(B, self.layers, self.kh, self.dim, device=self.device)
+        self._bind_stream()
+        _native.check(self._lib.snhip_get_state_dev(self._h, s.data_ptr(), h.data_ptr(), B),
+                      "snhip_get_state_dev")
+        return s, h
+
+    def set_state(self, s: torch.Tensor, hist: torch.Tensor):
+        B = int(s.shape[0])
+        s = s.to(device=self.device, dtype=torch.float32).contiguous()
+        hist = hist.to(device=self.device, dtype=torch.float32).contiguous()
+        if s.shape != (B, self.layers, self.dim) or hist.shape != (B, self.layers, self.kh, self.dim):
+            raise ValueError("state must be s (B,L,D) and hist (B,L,K-1,D)")
+        self._bind_stream()
+        _native.check(self._lib.snhip_set_state_dev(self._h, s.data_ptr(), hist.data_ptr(), B),
+                      "snhip_set_state_dev")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.snhip_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# The reference's name, for drop-in use with the same constructor arguments.
+SnModel = HipModel

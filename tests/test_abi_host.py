@@ -68,3 +68,34 @@ def test_string_buffer_protocol():
     assert n == 4
     small = ctypes.create_string_buffer(2)
     assert L.snhip_abi_backend_string(small, 2) == 4 and small.value == b""
+
+
+def test_model_load_rejects_bad_blobs(tmp_path):
+    """sn_load semantics (sunnynet.c:358-413): NULL on missing file, wrong
+    magic, dimension mismatch or truncation — all detected before any device
+    work, so this runs without a GPU."""
+    from sunnynet_amd.blob import pack_sunny_blob
+    from sunnynet_amd.config import TINY
+    from sunnynet_amd.weights import init_sunnynet
+    L = _native.lib()
+    c = TINY
+    buf = pack_sunny_blob(init_sunnynet(c, 0))
+    good = tmp_path / "good.bin"
+    good.write_bytes(buf)
+    args = (c.vocab_size, c.dim, c.inner, c.rank, c.taps, c.layers, 8, 1)
+    assert not L.snhip_load(str(tmp_path / "missing.bin").encode(), *args)
+    bad = tmp_path / "magic.bin"
+    bad.write_bytes(b"\0\0\0\0" + buf[4:])
+    assert not L.snhip_load(str(bad).encode(), *args)
+    assert not L.snhip_load(str(good).encode(), c.vocab_size, c.dim + 8, *args[2:])
+    trunc = tmp_path / "trunc.bin"
+    trunc.write_bytes(buf[:-4])
+    assert not L.snhip_load(str(trunc).encode(), *args)
+    assert "truncated" in _native.last_error()
+    # group other than 8 is refused up front
+    assert not L.snhip_load(str(good).encode(), *args[:6], 4, 1)
+    # NULL handles are tolerated by the void entry points
+    L.snhip_free(None)
+    L.snhip_reset(None)
+    assert L.snhip_vocab(None) == 0 and L.snhip_ready(None) == 0
+    assert L.snhip_step_batch(None, None, 1, None) == -1
