@@ -19,6 +19,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "common.h"
@@ -55,18 +56,34 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// Two-pass LayerNorm statistics over n values (sunnynet.c:198-210 form).
-__device__ __forceinline__ void ln_stats(const float* x, int n, float eps, float* red,
-                                         float& mean, float& rstd) {
+// Values per thread held in registers by the LayerNorm kernels (n <= 4096).
+constexpr int kLnPer = 16;
+
+// Two-pass LayerNorm statistics (sunnynet.c:198-210 form) over n values held
+// in registers, kLnPer per thread of a 256-thread block (element i*256+tid).
+__device__ __forceinline__ void ln_stats_reg(const float (&xv)[kLnPer], int n, float eps,
+                                             float* red, float& mean, float& rstd) {
     float sum = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) sum += x[i];
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k)
+        if (k * 256 + (int)threadIdx.x < n) sum += xv[k];
     mean = block_sum256(sum, red) / (float)n;
     float vs = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float d = x[i] - mean;
-        vs += d * d;
-    }
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k)
+        if (k * 256 + (int)threadIdx.x < n) {
+            const float d = xv[k] - mean;
+            vs += d * d;
+        }
     rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
+}
+
+__device__ __forceinline__ void load_row(float (&xv)[kLnPer], const float* x, int n) {
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        xv[k] = i < n ? x[i] : 0.0f;
+    }
 }
 
 __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
@@ -88,17 +105,27 @@ __global__ __launch_bounds__(256) void k_ln_conv(
     const int b = blockIdx.x;
     const float* xb = x + (size_t)b * D;
     float* hb = hist + (size_t)b * hist_bstride;
+    float xv[kLnPer];
+    load_row(xv, xb, D);
     float mean, rstd;
-    ln_stats(xb, D, eps, red, mean, rstd);
-    for (int i = threadIdx.x; i < D; i += 256) {
-        const float raw = (xb[i] - mean) * rstd * g[i] + c[i];
+    ln_stats_reg(xv, D, eps, red, mean, rstd);
+#pragma unroll
+    for (int kk = 0; kk < kLnPer; ++kk) {
+        const int i = kk * 256 + threadIdx.x;
+        if (i >= D) continue;
+        const float raw = (xv[kk] - mean) * rstd * g[i] + c[i];
         if (K > 1) {
-            float h[kMaxTaps];
-            for (int k = 0; k < K - 1; ++k) h[k] = hb[(size_t)k * D + i];
+            float h[kMaxTaps - 1];
+#pragma unroll
+            for (int k = 0; k < kMaxTaps - 1; ++k) h[k] = k < K - 1 ? hb[(size_t)k * D + i] : 0.0f;
             float acc = raw * dw[(size_t)(K - 1) * D + i];
-            for (int k = 0; k < K - 1; ++k) acc = acc + h[k] * dw[(size_t)(K - 2 - k) * D + i];
+#pragma unroll
+            for (int k = 0; k < kMaxTaps - 1; ++k)
+                if (k < K - 1) acc = acc + h[k] * dw[(size_t)(K - 2 - k) * D + i];
             at[(size_t)b * D + i] = raw + acc;
-            for (int k = K - 2; k >= 1; --k) hb[(size_t)k * D + i] = h[k - 1];
+#pragma unroll
+            for (int k = kMaxTaps - 2; k >= 1; --k)
+                if (k <= K - 2) hb[(size_t)k * D + i] = h[k - 1];
             hb[i] = raw;
         } else {
             at[(size_t)b * D + i] = raw;
@@ -113,10 +140,15 @@ __global__ __launch_bounds__(256) void k_ln(const float* __restrict__ x, int ldx
                                             int ldy, int n, float eps) {
     __shared__ float red[4];
     const int b = blockIdx.x;
-    const float* xb = x + (size_t)b * ldx;
+    float xv[kLnPer];
+    load_row(xv, x + (size_t)b * ldx, n);
     float mean, rstd;
-    ln_stats(xb, n, eps, red, mean, rstd);
-    for (int i = threadIdx.x; i < n; i += 256) y[(size_t)b * ldy + i] = (xb[i] - mean) * rstd * g[i] + c[i];
+    ln_stats_reg(xv, n, eps, red, mean, rstd);
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        if (i < n) y[(size_t)b * ldy + i] = (xv[k] - mean) * rstd * g[i] + c[i];
+    }
 }
 
 // Competitive gate, decay gate and state update for every (b, channel):
@@ -141,7 +173,7 @@ __global__ void k_compete_state(const float* __restrict__ q, const float* __rest
 }
 
 // ------------------------------------------------------------------- GEMV
-enum { EPI_STORE = 0, EPI_WEDGE = 1, EPI_RESID = 2 };
+enum { EPI_STORE = 0, EPI_WEDGE = 1, EPI_RESID = 2, EPI_ARGMAX = 3 };
 
 struct GemvJob {
     const float* w;       // fp32 (M, Kd) or nullptr
@@ -154,13 +186,24 @@ struct GemvJob {
     float a_tanh, b_gain;
     const float* s; int lds;
     const float* sfb; int ldf;
+    unsigned long long* best;   // EPI_ARGMAX: per-block packed maxima, [b * nblk + blk]
     int nblk;
 };
+
+// Orderable key of (value, index): larger value wins, then smaller index,
+// so the maximum key is torch.argmax's first maximal index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
 
 __device__ __forceinline__ void epilogue(const GemvJob& J, int b, int m, float acc) {
     float* y = J.Y + (size_t)b * J.ldy + m;
     if (J.epi == EPI_STORE) {
         *y = acc;
+    } else if (J.epi == EPI_ARGMAX) {
+        *y = acc;   // the maximum is reduced by the caller (k_gemv)
     } else if (J.epi == EPI_WEDGE) {
         // sunnynet.c:270-271
         *y = acc * (1.0f + 0.5f * J.a_tanh / (1.0f + fabsf(acc)));
@@ -190,8 +233,13 @@ __global__ __launch_bounds__(256) void k_gemv(GemvJob j0, GemvJob j1) {
     const int nw = J.nblk * 4;
     const int gw = blk * 4 + wv;
 
+    const bool amax = J.epi == EPI_ARGMAX;
+    __shared__ unsigned long long kbest[4][BT];
     for (int b0 = 0; b0 < B; b0 += BT) {
         const int nb = min(BT, B - b0);
+        unsigned long long best[BT];
+#pragma unroll
+        for (int bb = 0; bb < BT; ++bb) best[bb] = 0ull;
         __syncthreads();
         if constexpr (BLK == 0) {
             for (int i = threadIdx.x; i < nb * Kd; i += 256) {
@@ -238,6 +286,11 @@ __global__ __launch_bounds__(256) void k_gemv(GemvJob j0, GemvJob j1) {
                         if (lane == 0) {
                             epilogue(J, b0 + bb, r, s0);
                             if (two) epilogue(J, b0 + bb, r + 1, s1);
+                        }
+                        if (amax) {
+                            unsigned long long k = argmax_key(s0, r);
+                            if (two) k = max(k, argmax_key(s1, r + 1));
+                            best[bb] = max(best[bb], k);
                         }
                     }
                 }
@@ -286,44 +339,66 @@ __global__ __launch_bounds__(256) void k_gemv(GemvJob j0, GemvJob j1) {
                     if (bb < nb) {
                         const float t = seg_sum(acc[bb], seg);
                         if (live && lg == 0) epilogue(J, b0 + bb, r, t);
+                        if (amax && live && lg == 0) best[bb] = max(best[bb], argmax_key(t, r));
                     }
                 }
+            }
+        }
+        if (amax) {
+            // Per-wave maximum (int4 keeps one candidate per row segment),
+            // then per block; one plain store per (sequence, block).
+#pragma unroll
+            for (int bb = 0; bb < BT; ++bb) {
+                unsigned long long k = best[bb];
+                for (int o = 32; o > 0; o >>= 1) {
+                    const unsigned long long other =
+                        ((unsigned long long)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
+                        (uint32_t)__shfl_xor((int)(k & 0xFFFFFFFFull), o, 64);
+                    k = max(k, other);
+                }
+                if (lane == 0) kbest[wv][bb] = k;
+            }
+            __syncthreads();
+            if (threadIdx.x < (unsigned)nb) {
+                const int bb = threadIdx.x;
+                const unsigned long long k = max(max(kbest[0][bb], kbest[1][bb]),
+                                                 max(kbest[2][bb], kbest[3][bb]));
+                J.best[(size_t)(b0 + bb) * J.nblk + blk] = k;
             }
         }
     }
 }
 
-// First maximal index per row (torch.argmax convention, sunnynet/cli.py:41);
-// writes the token to next[b] and, if `hist_out` is set, to hist_out[b].
-__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, int V,
-                                                int32_t* __restrict__ next,
-                                                int32_t* __restrict__ hist_out) {
-    __shared__ float bv[256];
-    __shared__ int bi[256];
+// Greedy token from the per-block maxima (first maximal index, the
+// torch.argmax convention of sunnynet/cli.py:41). One block per sequence
+// reduces the nblk partial keys; next[b] = token, and the token is appended to
+// hist_tok at the device step counter. The last block to finish advances the
+// counter (a done-count keeps the counter read and its update in order).
+__global__ __launch_bounds__(256) void k_finalize_tok(const unsigned long long* __restrict__ part,
+                                                      int nblk, int B, int32_t* __restrict__ next,
+                                                      int32_t* __restrict__ hist_tok,
+                                                      int32_t* __restrict__ counter,
+                                                      int32_t* __restrict__ done, int cap) {
+    __shared__ unsigned long long red[256];
     const int b = blockIdx.x;
-    const float* l = logits + (size_t)b * V;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += 256) {
-        const float v = l[i];
-        if (v > best || (v == best && i < idx) || (v != v && best == best)) { best = v; idx = i; }
-    }
-    bv[threadIdx.x] = best;
-    bi[threadIdx.x] = idx;
+    unsigned long long k = 0ull;
+    for (int i = threadIdx.x; i < nblk; i += 256) k = max(k, part[(size_t)b * nblk + i]);
+    red[threadIdx.x] = k;
     __syncthreads();
     for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) {
-            const float v = bv[threadIdx.x + o];
-            const int i = bi[threadIdx.x + o];
-            const float cb = bv[threadIdx.x];
-            const int ci = bi[threadIdx.x];
-            if (v > cb || (v == cb && i < ci)) { bv[threadIdx.x] = v; bi[threadIdx.x] = i; }
-        }
+        if ((int)threadIdx.x < o) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + o]);
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        next[b] = bi[0];
-        if (hist_out) hist_out[b] = bi[0];
+        const int32_t t = (int32_t)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFull));
+        const int step = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        next[b] = t;
+        if ((long)step * B + b < (long)cap) hist_tok[(size_t)step * B + b] = t;
+        __threadfence();
+        if (atomicAdd(done, 1) == B - 1) {
+            *done = 0;
+            __hip_atomic_store(counter, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -373,8 +448,18 @@ struct SnHipModel {
     float *x = nullptr, *at = nullptr, *v = nullptr, *q = nullptr, *u = nullptr, *z = nullptr,
           *yn = nullptr, *sfb = nullptr, *nrm = nullptr, *logits = nullptr;
     int32_t* tok = nullptr;
+    unsigned long long* best = nullptr;   // (maxB, 4096) per-block packed argmax keys
+    int32_t* counter = nullptr;           // device step counter of greedy decoding
+    int32_t* done = nullptr;              // blocks finished in the current finalize
+    int32_t* tok_hist = nullptr;          // greedy tokens, step-major rows of B
+    int hist_cap = 0;                     // capacity of tok_hist in tokens
     std::vector<void*> allocs;
-    hipStream_t stream = nullptr;
+    hipStream_t stream = nullptr;         // caller's stream
+    hipStream_t work = nullptr;           // internal stream that runs the step graphs
+    hipEvent_t ev_in = nullptr, ev_out = nullptr;
+    // Captured step graphs keyed by (B, logits pointer, greedy).
+    std::map<std::tuple<int, const void*, int>, hipGraphExec_t> graphs;
+    bool use_graphs = true;
     int ready = 0;
 };
 
@@ -391,6 +476,10 @@ T* dalloc(SnHipModel* m, size_t n) {
 
 void free_model(SnHipModel* m) {
     if (!m) return;
+    for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+    if (m->ev_in) (void)hipEventDestroy(m->ev_in);
+    if (m->ev_out) (void)hipEventDestroy(m->ev_out);
+    if (m->work) (void)hipStreamDestroy(m->work);
     for (void* p : m->allocs) (void)hipFree(p);
     delete m;
 }
@@ -456,6 +545,8 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         return nullptr;
     }
     if (dim % 4 || inner % 4 || rank % 4) { set_last_error("dim, inner, rank must be multiples of 4"); return nullptr; }
+    if (dim > kLnPer * 256 || inner > kLnPer * 256) { set_last_error("dim and inner must be <= 4096"); return nullptr; }
+    if (max_batch > 1024) { set_last_error("max_batch must be <= 1024"); return nullptr; }
     if (wfmt == SNHIP_WEIGHTS_INT4) {
         if (block != 32 && block != 64) { set_last_error("INT4 block must be 32 or 64"); return nullptr; }
         if (dim % block || inner % block || rank % block) {
@@ -523,8 +614,11 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         m->nrm = dalloc<float>(m, B * D);
         m->logits = dalloc<float>(m, B * V);
         m->tok = dalloc<int32_t>(m, B);
+        m->best = dalloc<unsigned long long>(m, B * 4096);
+        m->counter = dalloc<int32_t>(m, 1);
+        m->done = dalloc<int32_t>(m, 1);
         ok = m->s && m->hist && m->x && m->at && m->v && m->q && m->u && m->z && m->yn && m->sfb &&
-             m->nrm && m->logits && m->tok;
+             m->nrm && m->logits && m->tok && m->best && m->counter && m->done;
     }
     if (!ok) {
         if (last_error().empty()) set_last_error("device allocation or upload failed");
@@ -537,10 +631,17 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         else ++it;
     }
     if (hipMemset(m->s, 0, B * layers * D * sizeof(float)) != hipSuccess ||
-        hipMemset(m->hist, 0, B * layers * (m->kh ? m->kh : 1) * D * sizeof(float)) != hipSuccess) {
+        hipMemset(m->hist, 0, B * layers * (m->kh ? m->kh : 1) * D * sizeof(float)) != hipSuccess ||
+        hipMemset(m->counter, 0, sizeof(int32_t)) != hipSuccess ||
+        hipMemset(m->done, 0, sizeof(int32_t)) != hipSuccess ||
+        hipStreamCreateWithFlags(&m->work, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming) != hipSuccess) {
+        set_last_error("device setup failed");
         free_model(m);
         return nullptr;
     }
+    if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
     m->ready = 1;
     return m;
 }
@@ -588,10 +689,10 @@ hipError_t launch_gemv(const SnHipModel* m, GemvJob j0, GemvJob j1, hipStream_t 
     return launch_gemv_fmt<64>(j0, j1, bt, st);
 }
 
-// One decode step for sequences [0, B); tokens already in m->tok.
-snhip_status run_step(SnHipModel* m, int B, float* logits_out, int32_t* next_tok,
-                      int32_t* tok_record) {
-    hipStream_t st = m->stream;
+// Enqueue one decode step for sequences [0, B) on `st`; tokens in m->tok.
+// greedy: the head also reduces the first maximal logit per sequence and a
+// final kernel writes it to m->tok (the next step's input) and m->tok_hist.
+snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, hipStream_t st) {
     const int D = m->D, I = m->I, R = m->R, L = m->L;
     const size_t sbs = (size_t)L * D;                               // s batch stride
     const size_t hbs = (size_t)L * (m->kh ? m->kh : 1) * D;         // hist batch stride
@@ -628,12 +729,62 @@ snhip_status run_step(SnHipModel* m, int B, float* logits_out, int32_t* next_tok
     hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->x, D, m->no_g, m->no_c, m->nrm, D, D,
                        m->eps);
     GemvJob jh = make_job(m->head, B, m->nrm, D, logits_out, m->vocab);
+    if (greedy) {
+        jh.epi = EPI_ARGMAX;
+        jh.best = m->best;
+    }
     GemvJob none{};
     SNHIP_CHECK(launch_gemv(m, jh, none, st));
-    if (next_tok)
-        hipLaunchKernelGGL(k_argmax, dim3(B), dim3(256), 0, st, logits_out, m->vocab, next_tok,
-                           tok_record);
+    if (greedy)
+        hipLaunchKernelGGL(k_finalize_tok, dim3(B), dim3(256), 0, st, m->best,
+                           gemv_blocks(jh, m->wfmt, m->block), B, m->tok, m->tok_hist, m->counter,
+                           m->done, m->hist_cap);
     SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
+// Runs `reps` decode steps on the internal stream, ordered after the work
+// already queued on the caller's stream and before anything queued on it
+// later. The step's kernels are captured once per (B, logits, greedy) into a
+// HIP graph and replayed.
+snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int reps) {
+    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
+    SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
+    if (!m->use_graphs) {
+        for (int i = 0; i < reps; ++i) {
+            const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
+            if (rc != SNHIP_OK) return rc;
+        }
+    } else {
+        const auto key = std::make_tuple(B, (const void*)logits_out, greedy ? 1 : 0);
+        auto it = m->graphs.find(key);
+        if (it == m->graphs.end()) {
+            if (m->graphs.size() >= 16) {
+                for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+                m->graphs.clear();
+            }
+            hipGraph_t g = nullptr;
+            SNHIP_CHECK(hipStreamBeginCapture(m->work, hipStreamCaptureModeThreadLocal));
+            const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
+            const hipError_t ec = hipStreamEndCapture(m->work, &g);
+            if (rc != SNHIP_OK) { if (g) (void)hipGraphDestroy(g); return rc; }
+            SNHIP_CHECK(ec);
+            hipGraphExec_t ex = nullptr;
+            const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            SNHIP_CHECK(ei);
+            it = m->graphs.emplace(key, ex).first;
+        }
+        for (int i = 0; i < reps; ++i) SNHIP_CHECK(hipGraphLaunch(it->second, m->work));
+    }
+    SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
+    SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
+    return SNHIP_OK;
+}
+
+// Copies B tokens into m->tok on the caller's stream.
+snhip_status put_tokens(SnHipModel* m, const int32_t* t, int B, hipMemcpyKind kind) {
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, t, B * sizeof(int32_t), kind, m->stream));
     return SNHIP_OK;
 }
 
@@ -692,17 +843,15 @@ snhip_status snhip_set_stream(SnHipModel* m, void* stream) {
 snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                   float* logits_dev) {
     if (!m || !tokens_dev || !logits_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
-    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens_dev, B * sizeof(int32_t), hipMemcpyDeviceToDevice,
-                               m->stream));
-    return run_step(m, B, logits_dev, nullptr, nullptr);
+    const snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
+    return rc != SNHIP_OK ? rc : run_steps(m, B, logits_dev, false, 1);
 }
 
 snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits) {
     if (!m || !tokens || !logits || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
     if (!tokens_ok(m, tokens, B)) return SNHIP_E_INVAL;
-    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens, B * sizeof(int32_t), hipMemcpyHostToDevice,
-                               m->stream));
-    const snhip_status rc = run_step(m, B, m->logits, nullptr, nullptr);
+    snhip_status rc = put_tokens(m, tokens, B, hipMemcpyHostToDevice);
+    if (rc == SNHIP_OK) rc = run_steps(m, B, m->logits, false, 1);
     if (rc != SNHIP_OK) return rc;
     SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)B * m->vocab * sizeof(float),
                                hipMemcpyDeviceToHost, m->stream));
@@ -718,14 +867,18 @@ void snhip_step(SnHipModel* m, int token, float* logits) {
 
 void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits) {
     if (!m || !tokens || n <= 0 || !logits) return;
-    for (int i = 0; i < n; ++i) {
-        if (tokens[i] < 0 || tokens[i] >= m->vocab) return;
-        (void)hipMemcpyAsync(m->tok, &tokens[i], sizeof(int32_t), hipMemcpyHostToDevice, m->stream);
-        if (run_step(m, 1, m->logits, nullptr, nullptr) != SNHIP_OK) return;
-    }
-    (void)hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float),
-                         hipMemcpyDeviceToHost, m->stream);
+    if (!tokens_ok(m, tokens, n)) return;
+    int32_t* dt = nullptr;
+    if (hipMalloc(&dt, (size_t)n * sizeof(int32_t)) != hipSuccess) return;
+    bool ok = hipMemcpy(dt, tokens, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess;
+    for (int i = 0; i < n && ok; ++i)
+        ok = put_tokens(m, dt + i, 1, hipMemcpyDeviceToDevice) == SNHIP_OK &&
+             run_steps(m, 1, m->logits, false, 1) == SNHIP_OK;
+    if (ok)
+        (void)hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float),
+                             hipMemcpyDeviceToHost, m->stream);
     (void)hipStreamSynchronize(m->stream);
+    (void)hipFree(dt);
 }
 
 snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
@@ -733,13 +886,34 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
                                      float* logits_dev) {
     if (!m || !tokens_dev || !out_tokens_dev || B <= 0 || B > m->max_batch || n_steps <= 0)
         return SNHIP_E_INVAL;
-    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens_dev, B * sizeof(int32_t), hipMemcpyDeviceToDevice,
-                               m->stream));
-    float* lg = logits_dev ? logits_dev : m->logits;
-    for (int i = 0; i < n_steps; ++i) {
-        const snhip_status rc = run_step(m, B, lg, m->tok, out_tokens_dev + (size_t)i * B);
-        if (rc != SNHIP_OK) return rc;
+    if ((long)n_steps * B > (long)m->hist_cap || !m->tok_hist) {
+        // Grow the token history; graphs bake its address, so drop them.
+        SNHIP_CHECK(hipStreamSynchronize(m->stream));
+        SNHIP_CHECK(hipStreamSynchronize(m->work));
+        for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+        m->graphs.clear();
+        long cap = 256L * m->max_batch;
+        while (cap < (long)n_steps * B) cap *= 2;
+        if (cap > (1L << 30)) return SNHIP_E_INVAL;
+        int32_t* h = nullptr;
+        SNHIP_CHECK(hipMalloc(&h, (size_t)cap * sizeof(int32_t)));
+        if (m->tok_hist) {
+            (void)hipFree(m->tok_hist);
+            for (auto it = m->allocs.begin(); it != m->allocs.end(); ++it)
+                if (*it == m->tok_hist) { m->allocs.erase(it); break; }
+        }
+        m->tok_hist = h;
+        m->allocs.push_back(h);
+        m->hist_cap = (int)cap;
     }
+        snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
+    if (rc != SNHIP_OK) return rc;
+    SNHIP_CHECK(hipMemsetAsync(m->counter, 0, sizeof(int32_t), m->stream));
+    float* lg = logits_dev ? logits_dev : m->logits;
+    rc = run_steps(m, B, lg, true, n_steps);
+    if (rc != SNHIP_OK) return rc;
+    SNHIP_CHECK(hipMemcpyAsync(out_tokens_dev, m->tok_hist, (size_t)n_steps * B * sizeof(int32_t),
+                               hipMemcpyDeviceToDevice, m->stream));
     return SNHIP_OK;
 }
 

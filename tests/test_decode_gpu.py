@@ -260,3 +260,25 @@ def test_100m_b64_matches_oracle_on_sampled_sequences(gpu, m100):
         b = orc.step(toks[pick])
         assert np.abs(a[pick] - b).max() < TOL
         assert np.array_equal(a[pick].argmax(1), b.argmax(1))
+
+
+def test_graph_replays_match_eager(gpu, small, monkeypatch):
+    """The step runs as a captured HIP graph; replay it many times with host
+    work and synchronization in between and compare every replay with the
+    eager (uncaptured) launch sequence."""
+    w, buf, path = small
+    B = 4
+    rng = np.random.default_rng(11)
+    seqs = [rng.integers(0, SMALL.vocab_size, B).astype(np.int32) for _ in range(10)]
+    hg = _model(path, SMALL, max_batch=B)
+    monkeypatch.setenv("SNHIP_NO_GRAPH", "1")
+    he = _model(path, SMALL, max_batch=B)
+    for toks in seqs:
+        t = torch.from_numpy(toks).to(gpu)
+        a = hg.step_batch(t).cpu().numpy()
+        torch.cuda.synchronize()
+        b = he.step_batch(t).cpu().numpy()
+        assert np.array_equal(a, b)
+    ga = hg.decode_greedy(torch.from_numpy(seqs[0]).to(gpu), 16).cpu().numpy()
+    gb = he.decode_greedy(torch.from_numpy(seqs[0]).to(gpu), 16).cpu().numpy()
+    assert np.array_equal(ga, gb)
