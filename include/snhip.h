@@ -53,7 +53,8 @@ void snhip_free(SnHipModel* m);
 void snhip_reset(SnHipModel* m);
 /* sunnynet.h:34: one decode step of sequence 0; logits: host, length vocab. */
 void snhip_step(SnHipModel* m, int token, float* logits);
-/* sunnynet.h:37: feed n tokens of sequence 0 in order; last logits to host. */
+/* sunnynet.h:37: feed n tokens of sequence 0 in order; last logits to host.
+ * Runs the chunked prefill (snhip_prefill_batch_dev with B = 1). */
 void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits);
 /* sunnynet.h:39-40 */
 int snhip_vocab(const SnHipModel* m);
@@ -70,6 +71,15 @@ snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int3
                                   float* logits_dev);
 /* Same with host tokens and host logits (synchronous). Tokens are range-checked. */
 snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits);
+
+/* Chunked prefill of sequences [0, B) from their current state: tokens_dev
+ * (B, T) int32 row-major on the device. Runs the model over the whole prompt
+ * with matrix-core GEMMs and the fused gate + exact sequential scan, T cut in
+ * chunks with the state carried between them; leaves s and hist as stepping
+ * token by token would (to float rounding). logits_dev (B, vocab), if not
+ * NULL, receives the last token's logits (the sn_prefill contract). */
+snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                     int32_t T, float* logits_dev);
 
 /* Greedy decoding on the device: feeds tokens_dev (B), then repeatedly takes
  * the first maximal logit as the next token, for n_steps steps. out_tokens_dev

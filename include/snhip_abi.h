@@ -108,6 +108,14 @@ snhip_status snhip_abi_dequant_i4_dev(const uint8_t* q, const float* scale,
                                       float* x, int32_t rows, int32_t N,
                                       int32_t block, void* stream);
 
+/* ------------------------------------------------------- dense linear */
+/* y (M, N) = x (M, K) w^T with w row-major (N, K), fp32, on the FP32 matrix
+ * cores (torch.nn.functional.linear without bias). Device pointers, 16-byte
+ * aligned, K % 32 == 0. No reference counterpart: the batched decode and the
+ * chunked prefill are built on it. */
+snhip_status snhip_abi_linear_dev(const float* x, const float* w, float* y, int32_t M,
+                                  int32_t N, int32_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

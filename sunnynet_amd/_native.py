@@ -62,6 +62,7 @@ _SIGS = {
     "snhip_abi_recur_scan_dev": (I32, [V, V, V, V, V, I32, I32, I32, I32, V]),
     "snhip_abi_quant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
     "snhip_abi_dequant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
+    "snhip_abi_linear_dev": (I32, [V, V, V, I32, I32, I32, V]),
     # include/snhip.h
     "snhip_load": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT]),
     "snhip_load_ex": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT, I32, I32, I32]),
@@ -76,6 +77,7 @@ _SIGS = {
     "snhip_step_batch_dev": (I32, [V, V, I32, V]),
     "snhip_step_batch": (I32, [V, V, I32, V]),
     "snhip_decode_greedy_dev": (I32, [V, V, I32, I32, V, V]),
+    "snhip_prefill_batch_dev": (I32, [V, V, I32, I32, V]),
     "snhip_get_state_dev": (I32, [V, V, V, I32]),
     "snhip_set_state_dev": (I32, [V, V, V, I32]),
 }

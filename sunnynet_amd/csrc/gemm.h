@@ -1,0 +1,37 @@
+// FP32 MFMA GEMM shared by the batched decode and the chunked prefill:
+//   Y[m, n] = sum_k X[m, k] * W[n, k]   (+ fused epilogue)
+// X: activations, row-major (M, K); W: weights, row-major (N, K) in fp32 or
+// INT4 groups (quant.c's packing, dequantized bit-exactly while staging).
+#pragma once
+
+#include "common.h"
+
+namespace snhip {
+
+enum GemmEpi { GEPI_STORE = 0, GEPI_WEDGE = 1, GEPI_RESID = 2 };
+
+struct GemmArgs {
+    // X rows. If shift_T > 0, row m reads X[m - 1] except when m % shift_T == 0,
+    // where it reads X0[m / shift_T] (the previous time step within each
+    // sequence, the carried state at t = 0).
+    const float* X; long ldx;
+    const float* X0; long ldx0; int shift_T;
+    // weights
+    const float* w;           // fp32 (N, K) row-major, or nullptr
+    const uint8_t* q;         // int4 (N, K/2)
+    const float* sc;          // int4 scales (N, K/block)
+    int block;                // int4 group size (32 or 64), 0 for fp32
+    int M, N, K;
+    float* Y; long ldy;
+    // epilogue
+    int epi;
+    float a_tanh, b_gain;
+    const float* s; long lds;     // GEPI_RESID: Y = acc + (b_gain * s + sfb + Y)
+    const float* sfb; long ldf;
+};
+
+// Enqueue Y = X W^T with the epilogue. `work` is scratch for split-K partials
+// (may be nullptr; then no split is used) of `work_floats` floats.
+snhip_status launch_gemm(const GemmArgs& g, float* work, size_t work_floats, hipStream_t st);
+
+}  // namespace snhip

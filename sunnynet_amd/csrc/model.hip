@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gemm.h"
 #include "snhip.h"
 
 namespace snhip {
@@ -433,6 +434,162 @@ struct Layer {
     Mat V, U, Wz, Wc, Ws;
 };
 
+// ---------------------------------------------------------------- prefill
+// x[b*T + t] = embed[tokens[b*T + t]]  (NaN rows for out-of-range ids).
+__global__ void k_gather_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
+                               float* __restrict__ x, int D, int vocab) {
+    const long row = blockIdx.x;
+    const int t = tok[row];
+    const bool ok = t >= 0 && t < vocab;
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        x[row * D + i] = ok ? embed[(size_t)t * D + i] : __builtin_nanf("");
+}
+
+// at[b,t] = raw[b,t] + conv: the depthwise causal conv of the step form
+// (sunnynet.c:227-233) applied to every row, with raw[b, t-1-k] taken from the
+// carried history (newest first) when t-1-k < 0.
+__global__ void k_conv_rows(const float* __restrict__ raw, const float* __restrict__ hist,
+                            size_t hist_bstride, const float* __restrict__ dw,
+                            float* __restrict__ at, int B, int T, int D, int K) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)B * T * D) return;
+    const int i = (int)(idx % D);
+    const long row = idx / D;
+    const int b = (int)(row / T), t = (int)(row % T);
+    const float r = raw[idx];
+    float acc = r * dw[(size_t)(K - 1) * D + i];
+    for (int k = 0; k < K - 1; ++k) {
+        const int j = t - 1 - k;
+        const float prev = j >= 0 ? raw[((long)b * T + j) * D + i]
+                                  : hist[(size_t)b * hist_bstride + (size_t)(k - t) * D + i];
+        acc = acc + prev * dw[(size_t)(K - 2 - k) * D + i];
+    }
+    at[idx] = r + acc;
+}
+
+// hist' = the K-1 newest raw rows (newest first), shifting in older history
+// when the chunk is shorter than K-1. Runs after k_conv_rows.
+__global__ void k_hist_update(const float* __restrict__ raw, float* __restrict__ hist,
+                              size_t hist_bstride, int B, int T, int D, int kh) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)B * D) return;
+    const int b = (int)(idx / D), i = (int)(idx % D);
+    float* hb = hist + (size_t)b * hist_bstride;
+    for (int k = kh - 1; k >= 0; --k) {
+        const int j = T - 1 - k;
+        hb[(size_t)k * D + i] = j >= 0 ? raw[((long)b * T + j) * D + i] : hb[(size_t)(k - T) * D + i];
+    }
+}
+
+// Fused competitive gate + decay gate + exact sequential scan over T for the
+// prefill (the core of sunnynet/layers.py:194-206 with the recurrence of
+// layers.py:314, in the operation order of the decode step). Same slot
+// pipeline as the standalone scan: wave w owns TC steps of every W*TC tile;
+// the wave whose slot is next prepares p and (1-p)*u (and writes u) while
+// the active wave runs the chain s = p*s + (1-p)*u from registers and hands
+// the state on through LDS. One lane per channel; D % 64 == 0.
+template <int W, int TC>
+__global__ __launch_bounds__(64 * W) void k_core_scan(
+        const float* __restrict__ q, const float* __restrict__ delta,
+        const float* __restrict__ s_in, size_t s_bstride, float* __restrict__ s_out,
+        size_t out_bstride, float* __restrict__ u_out, float* __restrict__ states, int T, int D,
+        int clamp, float p_floor) {
+    __shared__ float carry[64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gpr = D / 64;
+    const int b = blockIdx.x / gpr;
+    const int i = (blockIdx.x - b * gpr) * 64 + lane;
+    const long row0 = (long)b * T;
+    const float dl = delta[i];
+    const int base = lane & ~7, off = lane & 7;
+    const int n1 = base + ((off + 1) & 7), n2 = base + ((off + 2) & 7);
+    constexpr int TILE = W * TC;
+    const int ntiles = (T + TILE - 1) / TILE;
+    const int nfull = T / TILE;
+    float ur[TC], gt[TC], pa[TC], pb[TC];
+
+    auto load_slot = [&](int tile) {
+        const int t0 = tile * TILE + w * TC;
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const long r = row0 + min(t0 + k, T - 1);
+            ur[k] = q[r * 2 * D + i];
+            gt[k] = q[r * 2 * D + D + i];
+        }
+    };
+    auto prep = [&](int tile) {
+        const int t0 = tile * TILE + w * TC;
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const float gi = gt[k];
+            const float g1 = __shfl(gi, n1, 64), g2 = __shfl(gi, n2, 64);
+            const float uu = ur[k] * (sgm(gi - g1) * sgm(gi - g2));
+            float p = 1.0f - dl * (1.0f - sgm(gi));
+            if (clamp && p < p_floor) p = p_floor;
+            pa[k] = p;
+            pb[k] = (1.0f - p) * uu;
+            if (t0 + k < T) u_out[(row0 + t0 + k) * D + i] = uu;
+        }
+    };
+
+    if (w == 0) carry[lane] = s_in[(size_t)b * s_bstride + i];
+    load_slot(0);
+    if (w == 0) prep(0);
+    __syncthreads();
+    for (int tile = 0; tile < ntiles; ++tile) {
+        const bool full = tile < nfull;
+        for (int j = 0; j < W; ++j) {
+            if (w == j) {
+                float s = carry[lane];
+                const int t0 = tile * TILE + j * TC;
+#pragma unroll
+                for (int k = 0; k < TC; ++k) {
+                    if (full || t0 + k < T) {
+                        s = pa[k] * s + pb[k];
+                        states[(row0 + t0 + k) * D + i] = s;
+                    }
+                }
+                carry[lane] = s;
+                if (tile + 1 < ntiles) load_slot(tile + 1);
+            } else if (w == j + 1) {
+                prep(tile);
+            } else if (j == W - 1 && w == 0 && tile + 1 < ntiles) {
+                prep(tile + 1);
+            }
+            barrier_lds();
+        }
+    }
+    if (w == 0) s_out[(size_t)b * out_bstride + i] = carry[lane];
+}
+
+// Rows t = T-1 of each sequence: dst[b] = src[b*T + T-1].
+__global__ void k_last_rows(const float* __restrict__ src, float* __restrict__ dst, int T, int D) {
+    const int b = blockIdx.x;
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        dst[(size_t)b * D + i] = src[((size_t)b * T + T - 1) * D + i];
+}
+
+// Per-block partial maxima of logits rows (packed keys as argmax_key), for
+// the greedy token after a GEMM-computed head: grid (nblk, B).
+__global__ __launch_bounds__(256) void k_argmax_partial(const float* __restrict__ logits, int V,
+                                                        unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[256];
+    const int b = blockIdx.y, nblk = gridDim.x;
+    const int chunk = (V + nblk - 1) / nblk;
+    const int lo = blockIdx.x * chunk, hi = min(V, lo + chunk);
+    unsigned long long k = 0ull;
+    for (int i = lo + (int)threadIdx.x; i < hi; i += 256)
+        k = max(k, argmax_key(logits[(size_t)b * V + i], i));
+    red[threadIdx.x] = k;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + o]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[(size_t)b * nblk + blockIdx.x] = red[0];
+}
+
 }  // namespace
 }  // namespace snhip
 
@@ -460,6 +617,18 @@ struct SnHipModel {
     // Captured step graphs keyed by (B, logits pointer, greedy).
     std::map<std::tuple<int, const void*, int>, hipGraphExec_t> graphs;
     bool use_graphs = true;
+    // Decode batches of at least this many sequences run their matmuls on the
+    // MFMA GEMM; smaller batches use the GEMV kernels.
+    int gemm_min_batch = 16;
+    bool gemm_ok = true;
+    float* gemm_work = nullptr;           // split-K partials
+    size_t gemm_work_floats = 0;
+    // Chunked prefill workspace for (max_batch x pf_chunk) rows, on first use.
+    int pf_chunk = 0;
+    float *pf_x = nullptr, *pf_raw = nullptr, *pf_at = nullptr, *pf_v = nullptr, *pf_q = nullptr,
+          *pf_u = nullptr, *pf_st = nullptr, *pf_z = nullptr, *pf_yn = nullptr, *pf_sfb = nullptr,
+          *pf_send = nullptr;
+    int32_t* pf_tok = nullptr;
     int ready = 0;
 };
 
@@ -642,6 +811,13 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         return nullptr;
     }
     if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
+    if (const char* e = getenv("SNHIP_GEMM_MIN_BATCH")) m->gemm_min_batch = std::max(1, atoi(e));
+    // The MFMA GEMM needs every contraction length to be a multiple of 32.
+    m->gemm_ok = dim % 32 == 0 && inner % 32 == 0 && rank % 32 == 0;
+    if (!m->gemm_ok) m->gemm_min_batch = 1 << 30;
+    m->gemm_work_floats = (size_t)16 << 20;
+    m->gemm_work = dalloc<float>(m, m->gemm_work_floats);
+    if (!m->gemm_work) { set_last_error("out of device memory"); free_model(m); return nullptr; }
     m->ready = 1;
     return m;
 }
@@ -689,6 +865,61 @@ hipError_t launch_gemv(const SnHipModel* m, GemvJob j0, GemvJob j1, hipStream_t 
     return launch_gemv_fmt<64>(j0, j1, bt, st);
 }
 
+GemmArgs gemm_for(const SnHipModel* m, const Mat& W, const float* X, long ldx, int M, float* Y,
+                  long ldy) {
+    GemmArgs g{};
+    g.X = X; g.ldx = ldx;
+    g.w = W.w; g.q = W.q; g.sc = W.sc;
+    g.block = W.q ? m->block : 0;
+    g.M = M; g.N = W.M; g.K = W.Kd;
+    g.Y = Y; g.ldy = ldy;
+    g.epi = GEPI_STORE;
+    return g;
+}
+
+snhip_status run_gemm(SnHipModel* m, const GemmArgs& g, hipStream_t st) {
+    return launch_gemm(g, m->gemm_work, m->gemm_work_floats, st);
+}
+
+__global__ void k_copy_rows(const float* __restrict__ src, long lds, float* __restrict__ dst,
+                            long ldd, int D) {
+    const int b = blockIdx.x;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) dst[b * ldd + i] = src[b * lds + i];
+}
+
+// Final norm, LM head and (greedy) token selection for B rows of x.
+snhip_status enqueue_head(SnHipModel* m, int B, const float* x, float* logits_out, bool greedy,
+                          hipStream_t st) {
+    const int D = m->D;
+    hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, x, D, m->no_g, m->no_c, m->nrm, D, D,
+                       m->eps);
+    if (B >= m->gemm_min_batch) {
+        const snhip_status rc = run_gemm(m, gemm_for(m, m->head, m->nrm, D, B, logits_out, m->vocab), st);
+        if (rc != SNHIP_OK) return rc;
+        if (greedy) {
+            const int nblk = 64;
+            hipLaunchKernelGGL(k_argmax_partial, dim3(nblk, B), dim3(256), 0, st, logits_out,
+                               m->vocab, m->best);
+            hipLaunchKernelGGL(k_finalize_tok, dim3(B), dim3(256), 0, st, m->best, nblk, B, m->tok,
+                               m->tok_hist, m->counter, m->done, m->hist_cap);
+        }
+    } else {
+        GemvJob jh = make_job(m->head, B, m->nrm, D, logits_out, m->vocab);
+        if (greedy) {
+            jh.epi = EPI_ARGMAX;
+            jh.best = m->best;
+        }
+        GemvJob none{};
+        SNHIP_CHECK(launch_gemv(m, jh, none, st));
+        if (greedy)
+            hipLaunchKernelGGL(k_finalize_tok, dim3(B), dim3(256), 0, st, m->best,
+                               gemv_blocks(jh, m->wfmt, m->block), B, m->tok, m->tok_hist,
+                               m->counter, m->done, m->hist_cap);
+    }
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
 // Enqueue one decode step for sequences [0, B) on `st`; tokens in m->tok.
 // greedy: the head also reduces the first maximal logit per sequence and a
 // final kernel writes it to m->tok (the next step's input) and m->tok_hist.
@@ -697,12 +928,35 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
     const size_t sbs = (size_t)L * D;                               // s batch stride
     const size_t hbs = (size_t)L * (m->kh ? m->kh : 1) * D;         // hist batch stride
     hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->x, D, m->vocab);
+    const bool mm = B >= m->gemm_min_batch;
     for (int l = 0; l < L; ++l) {
         const Layer& A = m->layers[l];
         float* s_l = m->s + (size_t)l * D;
         float* h_l = m->hist + (size_t)l * (m->kh ? m->kh : 1) * D;
         hipLaunchKernelGGL(k_ln_conv, dim3(B), dim3(256), 0, st, m->x, A.ni_g, A.ni_c, A.dw, h_l,
                            hbs, m->at, D, m->K, m->eps);
+        const long n = (long)B * D;
+        if (mm) {
+            snhip_status rc;
+            if ((rc = run_gemm(m, gemm_for(m, A.V, m->at, D, B, m->v, R), st)) != SNHIP_OK) return rc;
+            if ((rc = run_gemm(m, gemm_for(m, A.Ws, s_l, (long)sbs, B, m->sfb, D), st)) != SNHIP_OK) return rc;
+            if ((rc = run_gemm(m, gemm_for(m, A.U, m->v, R, B, m->q, 2 * D), st)) != SNHIP_OK) return rc;
+            hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                               m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
+            GemmArgs gz = gemm_for(m, A.Wz, m->u, D, B, m->z, I);
+            gz.epi = GEPI_WEDGE;
+            gz.a_tanh = A.a_tanh;
+            if ((rc = run_gemm(m, gz, st)) != SNHIP_OK) return rc;
+            hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->z, I, A.nm_g, A.nm_c, m->yn, I, I,
+                               m->eps);
+            GemmArgs gc = gemm_for(m, A.Wc, m->yn, I, B, m->x, D);
+            gc.epi = GEPI_RESID;
+            gc.b_gain = A.b_gain;
+            gc.s = s_l; gc.lds = (long)sbs;
+            gc.sfb = m->sfb; gc.ldf = D;
+            if ((rc = run_gemm(m, gc, st)) != SNHIP_OK) return rc;
+            continue;
+        }
         // v = V at and sfb = W_eff s (old state), one launch.
         GemvJob jv = make_job(A.V, B, m->at, D, m->v, R);
         GemvJob js = make_job(A.Ws, B, s_l, (int)sbs, m->sfb, D);
@@ -710,7 +964,6 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
         GemvJob ju = make_job(A.U, B, m->v, R, m->q, 2 * D);
         GemvJob none{};
         SNHIP_CHECK(launch_gemv(m, ju, none, st));
-        const long n = (long)B * D;
         hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                            m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
         GemvJob jz = make_job(A.Wz, B, m->u, D, m->z, I);
@@ -726,21 +979,7 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
         jc.sfb = m->sfb; jc.ldf = D;
         SNHIP_CHECK(launch_gemv(m, jc, none, st));
     }
-    hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->x, D, m->no_g, m->no_c, m->nrm, D, D,
-                       m->eps);
-    GemvJob jh = make_job(m->head, B, m->nrm, D, logits_out, m->vocab);
-    if (greedy) {
-        jh.epi = EPI_ARGMAX;
-        jh.best = m->best;
-    }
-    GemvJob none{};
-    SNHIP_CHECK(launch_gemv(m, jh, none, st));
-    if (greedy)
-        hipLaunchKernelGGL(k_finalize_tok, dim3(B), dim3(256), 0, st, m->best,
-                           gemv_blocks(jh, m->wfmt, m->block), B, m->tok, m->tok_hist, m->counter,
-                           m->done, m->hist_cap);
-    SNHIP_CHECK(hipGetLastError());
-    return SNHIP_OK;
+    return enqueue_head(m, B, m->x, logits_out, greedy, st);
 }
 
 // Runs `reps` decode steps on the internal stream, ordered after the work
@@ -785,6 +1024,132 @@ snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int
 // Copies B tokens into m->tok on the caller's stream.
 snhip_status put_tokens(SnHipModel* m, const int32_t* t, int B, hipMemcpyKind kind) {
     SNHIP_CHECK(hipMemcpyAsync(m->tok, t, B * sizeof(int32_t), kind, m->stream));
+    return SNHIP_OK;
+}
+
+// Workspace of the chunked prefill for max_batch x chunk rows.
+snhip_status ensure_prefill_ws(SnHipModel* m, int chunk) {
+    if (m->pf_chunk >= chunk) return SNHIP_OK;
+    SNHIP_CHECK(hipStreamSynchronize(m->stream));
+    SNHIP_CHECK(hipStreamSynchronize(m->work));
+    float** bufs[] = {&m->pf_x, &m->pf_raw, &m->pf_at, &m->pf_v, &m->pf_q, &m->pf_u,
+                      &m->pf_st, &m->pf_z, &m->pf_yn, &m->pf_sfb, &m->pf_send};
+    for (float** b : bufs)
+        if (*b) {
+            (void)hipFree(*b);
+            for (auto it = m->allocs.begin(); it != m->allocs.end(); ++it)
+                if (*it == *b) { m->allocs.erase(it); break; }
+            *b = nullptr;
+        }
+    if (m->pf_tok) {
+        (void)hipFree(m->pf_tok);
+        for (auto it = m->allocs.begin(); it != m->allocs.end(); ++it)
+            if (*it == m->pf_tok) { m->allocs.erase(it); break; }
+        m->pf_tok = nullptr;
+    }
+    const size_t rows = (size_t)m->max_batch * chunk, D = m->D, I = m->I, R = m->R;
+    m->pf_x = dalloc<float>(m, rows * D);
+    m->pf_raw = dalloc<float>(m, rows * D);
+    m->pf_at = dalloc<float>(m, rows * D);
+    m->pf_v = dalloc<float>(m, rows * R);
+    m->pf_q = dalloc<float>(m, rows * 2 * D);
+    m->pf_u = dalloc<float>(m, rows * D);
+    m->pf_st = dalloc<float>(m, rows * D);
+    m->pf_z = dalloc<float>(m, rows * I);
+    m->pf_yn = dalloc<float>(m, rows * I);
+    m->pf_sfb = dalloc<float>(m, rows * D);
+    m->pf_send = dalloc<float>(m, (size_t)m->max_batch * D);
+    m->pf_tok = dalloc<int32_t>(m, rows);
+    for (float** b : bufs)
+        if (!*b) { m->pf_chunk = 0; set_last_error("out of device memory (prefill)"); return SNHIP_E_NOMEM; }
+    if (!m->pf_tok) { m->pf_chunk = 0; return SNHIP_E_NOMEM; }
+    m->pf_chunk = chunk;
+    return SNHIP_OK;
+}
+
+// One chunk of Tc tokens for sequences [0, B), all layers, carrying s and
+// hist. Tokens already in m->pf_tok (B x Tc). If logits_out, also the last
+// token's logits.
+snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_out,
+                                   hipStream_t st) {
+    const int D = m->D, I = m->I, R = m->R, L = m->L;
+    const long rows = (long)B * Tc;
+    const size_t sbs = (size_t)L * D;
+    const size_t hbs = (size_t)L * (m->kh ? m->kh : 1) * D;
+    snhip_status rc;
+    hipLaunchKernelGGL(k_gather_embed, dim3((unsigned)rows), dim3(256), 0, st, m->pf_tok, m->embed,
+                       m->pf_x, D, m->vocab);
+    for (int l = 0; l < L; ++l) {
+        const Layer& A = m->layers[l];
+        float* s_l = m->s + (size_t)l * D;
+        float* h_l = m->hist + (size_t)l * (m->kh ? m->kh : 1) * D;
+        hipLaunchKernelGGL(k_ln, dim3((unsigned)rows), dim3(256), 0, st, m->pf_x, D, A.ni_g, A.ni_c,
+                           m->pf_raw, D, D, m->eps);
+        const float* at = m->pf_raw;
+        if (m->K > 1) {
+            const long n = rows * D;
+            hipLaunchKernelGGL(k_conv_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                               m->pf_raw, h_l, hbs, A.dw, m->pf_at, B, Tc, D, m->K);
+            hipLaunchKernelGGL(k_hist_update, dim3((unsigned)(((long)B * D + 255) / 256)), dim3(256),
+                               0, st, m->pf_raw, h_l, hbs, B, Tc, D, m->kh);
+            at = m->pf_at;
+        }
+        if ((rc = run_gemm(m, gemm_for(m, A.V, at, D, (int)rows, m->pf_v, R), st)) != SNHIP_OK) return rc;
+        if ((rc = run_gemm(m, gemm_for(m, A.U, m->pf_v, R, (int)rows, m->pf_q, 2 * D), st)) != SNHIP_OK) return rc;
+        hipLaunchKernelGGL((k_core_scan<4, 16>), dim3((unsigned)(B * (D / 64))), dim3(256), 0, st,
+                           m->pf_q, A.delta, s_l, sbs, m->pf_send, (size_t)D, m->pf_u, m->pf_st,
+                           Tc, D, m->clamp, m->p_floor);
+        GemmArgs gz = gemm_for(m, A.Wz, m->pf_u, D, (int)rows, m->pf_z, I);
+        gz.epi = GEPI_WEDGE;
+        gz.a_tanh = A.a_tanh;
+        if ((rc = run_gemm(m, gz, st)) != SNHIP_OK) return rc;
+        hipLaunchKernelGGL(k_ln, dim3((unsigned)rows), dim3(256), 0, st, m->pf_z, I, A.nm_g, A.nm_c,
+                           m->pf_yn, I, I, m->eps);
+        // sfb_t = W_eff s_{t-1}, with s_{-1} the carried state (layers.py:208-217,243-250)
+        GemmArgs gs = gemm_for(m, A.Ws, m->pf_st, D, (int)rows, m->pf_sfb, D);
+        gs.X0 = s_l; gs.ldx0 = (long)sbs; gs.shift_T = Tc;
+        if ((rc = run_gemm(m, gs, st)) != SNHIP_OK) return rc;
+        GemmArgs gc = gemm_for(m, A.Wc, m->pf_yn, I, (int)rows, m->pf_x, D);
+        gc.epi = GEPI_RESID;
+        gc.b_gain = A.b_gain;
+        gc.s = m->pf_st; gc.lds = D;
+        gc.sfb = m->pf_sfb; gc.ldf = D;
+        if ((rc = run_gemm(m, gc, st)) != SNHIP_OK) return rc;
+        hipLaunchKernelGGL(k_copy_rows, dim3(B), dim3(256), 0, st, m->pf_send, (long)D, s_l,
+                           (long)sbs, D);
+    }
+    if (logits_out) {
+        hipLaunchKernelGGL(k_last_rows, dim3(B), dim3(256), 0, st, m->pf_x, m->x, Tc, D);
+        if ((rc = enqueue_head(m, B, m->x, logits_out, false, st)) != SNHIP_OK) return rc;
+    }
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
+// Chunked prefill of tokens (B, T) (row-major, device) from the current state.
+snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
+                         float* logits_out) {
+    if (!m->gemm_ok || m->D % 64) {
+        set_last_error("chunked prefill needs dim % 64 == 0 and dim, inner, rank % 32 == 0");
+        return SNHIP_E_UNSUPPORTED;
+    }
+    int chunk = 512;
+    if (const char* e = getenv("SNHIP_PREFILL_CHUNK")) chunk = std::max(1, atoi(e));
+    chunk = std::min(chunk, T);
+    snhip_status rc = ensure_prefill_ws(m, chunk);
+    if (rc != SNHIP_OK) return rc;
+    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
+    SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
+    for (int c0 = 0; c0 < T; c0 += chunk) {
+        const int Tc = std::min(chunk, T - c0);
+        SNHIP_CHECK(hipMemcpy2DAsync(m->pf_tok, (size_t)Tc * sizeof(int32_t), tokens_dev + c0,
+                                     (size_t)T * sizeof(int32_t), (size_t)Tc * sizeof(int32_t), B,
+                                     hipMemcpyDeviceToDevice, m->work));
+        rc = enqueue_prefill_chunk(m, B, Tc, c0 + Tc >= T ? logits_out : nullptr, m->work);
+        if (rc != SNHIP_OK) return rc;
+    }
+    SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
+    SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
     return SNHIP_OK;
 }
 
@@ -871,14 +1236,24 @@ void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits) {
     int32_t* dt = nullptr;
     if (hipMalloc(&dt, (size_t)n * sizeof(int32_t)) != hipSuccess) return;
     bool ok = hipMemcpy(dt, tokens, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess;
-    for (int i = 0; i < n && ok; ++i)
-        ok = put_tokens(m, dt + i, 1, hipMemcpyDeviceToDevice) == SNHIP_OK &&
-             run_steps(m, 1, m->logits, false, 1) == SNHIP_OK;
+    if (ok && m->gemm_ok && m->D % 64 == 0) {
+        ok = run_prefill(m, dt, 1, n, m->logits) == SNHIP_OK;
+    } else {
+        for (int i = 0; i < n && ok; ++i)    // the reference's step loop (sunnynet.c:347-349)
+            ok = put_tokens(m, dt + i, 1, hipMemcpyDeviceToDevice) == SNHIP_OK &&
+                 run_steps(m, 1, m->logits, false, 1) == SNHIP_OK;
+    }
     if (ok)
         (void)hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float),
                              hipMemcpyDeviceToHost, m->stream);
     (void)hipStreamSynchronize(m->stream);
     (void)hipFree(dt);
+}
+
+snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                     int32_t T, float* logits_dev) {
+    if (!m || !tokens_dev || B <= 0 || B > m->max_batch || T <= 0) return SNHIP_E_INVAL;
+    return run_prefill(m, tokens_dev, B, T, logits_dev);
 }
 
 snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,

@@ -96,6 +96,18 @@ class HipModel:
                       "snhip_step_batch")
         return out
 
+    def prefill_batch(self, tokens: torch.Tensor, logits: bool = True):
+        """Chunked prefill of tokens (B, T) (sequences [0, B)) from the current
+        state; returns the last token's logits (B, vocab) on the device."""
+        B, T = (int(x) for x in tokens.shape)
+        tokens = tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        out = torch.empty(B, self.vocab, device=self.device) if logits else None
+        self._bind_stream()
+        _native.check(self._lib.snhip_prefill_batch_dev(self._h, tokens.data_ptr(), B, T,
+                                                        out.data_ptr() if logits else None),
+                      "snhip_prefill_batch_dev")
+        return out
+
     def decode_greedy(self, tokens: torch.Tensor, n_steps: int, logits: torch.Tensor | None = None):
         """Greedy decoding on the device; returns (n_steps, B) int32 tokens."""
         B = int(tokens.shape[0])

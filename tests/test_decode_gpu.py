@@ -109,7 +109,8 @@ def test_small_prefill_then_greedy_matches_oracle(gpu, small):
 
 
 def test_reference_surface(gpu, small):
-    """prefill == stepping; reset clears the state (runtime/model.py:110-121)."""
+    """prefill == stepping (the chunked prefill, to float rounding); reset
+    clears the state (runtime/model.py:110-121)."""
     w, buf, path = small
     hm = _model(path, SMALL)
     toks = list(np.random.default_rng(3).integers(0, SMALL.vocab_size, 12))
@@ -117,18 +118,18 @@ def test_reference_surface(gpu, small):
     hm.reset()
     for t in toks:
         b = np.asarray(hm.step(int(t)))
-    assert np.array_equal(a, b)
+    assert np.abs(a - b).max() < TOL and a.argmax() == b.argmax()
     hm.reset()
     s, h = hm.get_state(1)
     assert float(s.abs().max()) == 0.0 and float(h.abs().max()) == 0.0
     assert hm.vocab == SMALL.vocab_size
 
 
-@pytest.mark.parametrize("B", [3, 8, 11])
+@pytest.mark.parametrize("B", [3, 8, 11, 16, 33])
 def test_batched_matches_oracle(gpu, small, B):
     w, buf, path = small
     print(f"small fp32 batched B={B}", flush=True)
-    hm = _model(path, SMALL, max_batch=16)
+    hm = _model(path, SMALL, max_batch=64)
     orc = oracle.SnOracle(buf, batch=B)
     rng = np.random.default_rng(B)
     for _ in range(12):
