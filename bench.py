@@ -1,15 +1,21 @@
 """Benchmark of the SunnyNet token loop on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload scan]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|scan|decode]
 
-Workload (the headline): the standalone gated prefill scan, B=16, D=2048
+Headline (``value``): the standalone gated prefill scan, B=16, D=2048
 channels, T=4096, fp32, inputs resident in HBM (``sunnynet_amd.workloads``).
-A step is one full scan. ``value`` is algorithmic HBM GB/s (read a and b,
-write s: 3*B*T*D*4 bytes per step) over the K timed steps. The ``roofline``
-object times each launch with HIP events on the stream the kernel runs on;
+A step is one full scan; ``value`` is algorithmic HBM GB/s (read a and b,
+write s: 3*B*T*D*4 bytes per step) over the K timed steps. ``roofline``
+times each launch with HIP events on the stream the kernel runs on;
 ``cpu_baseline`` times the reference C runtime's ``sn_recur_scan`` (built
-from the reference sources into oracle/_ref) on the host cores on the same
-inputs.
+from the reference sources into oracle/_ref) on host cores, same inputs.
+
+``decode`` (same JSON line): SunnyNet-100M (L=12, D=1024, V=32000, seed-1
+random init), chunked prefill of a T=1024 random prompt, then 256 greedy
+steps on the device at B=1 and B=64, fp32; and the same shape with INT4 g32
+weights (matmuls ~ N(0, 0.02)) after a T=2048 prefill at B=1, 8, 32. Each
+entry gives tokens/s, us/step and the HBM roofline of the step's weight
+bytes; ``cpu_baseline`` there is the reference ``sn_step`` on host cores.
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -29,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 from sunnynet_amd import runtime  # noqa: E402
 from sunnynet_amd.workloads import SCAN_B, SCAN_D, SCAN_T, scan_bytes, scan_inputs  # noqa: E402
+from sunnynet_amd.config import SUNNY_100M, matmul_params  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per scan launch on this workload from rocprofv3 --pmc FETCH_SIZE and
@@ -140,6 +147,113 @@ def cpu_scan_baseline(a, b, s0):
                       f"({med*1e3:.1f} ms each)"}
 
 
+def decode_bytes(cfg, int4: bool, block: int = 32) -> int:
+    """Weight bytes one decode step must read: every matmul and the head
+    (fp32: 4 B per weight; INT4: 0.5 B + one fp32 scale per group)."""
+    n = matmul_params(cfg)
+    return int(n * 4) if not int4 else int(n // 2 + (n // block) * 4)
+
+
+def _time_ms(fn):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
+def bench_decode(cpu: bool):
+    import tempfile
+
+    from sunnynet_amd.blob import pack_sunny_blob
+    from sunnynet_amd.runtime.model import HipModel
+    from sunnynet_amd.weights import gaussian_matmuls, init_sunnynet
+    cfg = SUNNY_100M
+    dev = torch.device("cuda:0")
+    tmp = tempfile.mkdtemp(prefix="snhip_bench_")
+    log("[bench] SunnyNet-100M weights (seed 1)")
+    w = init_sunnynet(cfg, 1)
+    p32 = os.path.join(tmp, "m100_fp32.bin")
+    with open(p32, "wb") as f:
+        f.write(pack_sunny_blob(w))
+    w4 = gaussian_matmuls(init_sunnynet(cfg, 1), seed=3)
+    p4 = os.path.join(tmp, "m100_gauss.bin")
+    with open(p4, "wb") as f:
+        f.write(pack_sunny_blob(w4))
+    out = {"model": "SunnyNet-100M L=12 D=1024 I=1536 R=512 V=32000",
+           "steps": 256, "cases": []}
+    g = torch.Generator(device="cpu").manual_seed(123)
+    for fmt, path, T, batches in (("fp32", p32, 1024, (1, 64)), ("int4", p4, 2048, (1, 8, 32))):
+        nbytes = decode_bytes(cfg, fmt == "int4")
+        for B in batches:
+            hm = HipModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
+                          max_batch=B, weights=fmt, block=32)
+            prompts = torch.randint(0, cfg.vocab_size, (B, T), generator=g, dtype=torch.int32).to(dev)
+            hm.prefill_batch(prompts[:, :32])          # warm the prefill graph-free path
+            hm.reset()
+            torch.cuda.synchronize()
+            lg = None
+
+            def pre():
+                nonlocal lg
+                lg = hm.prefill_batch(prompts)
+            pms = _time_ms(pre)
+            tok = lg.argmax(1).int()
+            hm.decode_greedy(tok, 8)                    # capture + warm the step graph
+            torch.cuda.synchronize()
+            n = out["steps"]
+            ms = _time_ms(lambda: hm.decode_greedy(tok, n)) / n
+            hm.close()
+            case = {"weights": fmt, "B": B, "prefill_T": T, "prefill_ms": round(pms, 2),
+                    "prefill_tok_s": round(B * T / pms * 1e3, 1), "us_per_step": round(ms * 1e3, 2),
+                    "tok_s": round(B / ms * 1e3, 1), "weight_bytes_per_step": nbytes,
+                    "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] decode {fmt} B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s, "
+                f"prefill T={T} {pms:.1f} ms")
+            out["cases"].append(case)
+    if cpu:
+        out["cpu_baseline"] = cpu_decode_baseline(p32, cfg)
+    return out
+
+
+def cpu_decode_baseline(path, cfg):
+    """The reference sn_step on the fp32 blob (B = 1, host cores), after a
+    16-token prefill by stepping; bounded to a few seconds."""
+    import oracle
+    threads = min(16, physical_cores())
+    if oracle.ref_available():
+        lib = oracle.ref_lib("model")
+        lib.sn_set_threads(threads)
+        m = oracle.RefSnModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers)
+        kind = "reference"
+    else:
+        m = None
+        kind = "port"
+    if m is None:
+        blob = np.fromfile(path, np.uint8)
+        orc = oracle.SnOracle(blob)
+        os.environ["OMP_NUM_THREADS"] = str(threads)
+        step = lambda t: orc.step([t])
+    else:
+        step = m.step
+    for t in range(16):
+        step(t)
+    times = []
+    deadline = time.perf_counter() + 10.0
+    while len(times) < 16 and time.perf_counter() < deadline:
+        t0 = time.perf_counter()
+        step(len(times) + 100)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    log(f"[bench] cpu {kind} sn_step 100M fp32: {med*1e3:.2f} ms/token, {threads} threads")
+    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": threads, "kind": kind,
+            "ms_per_token": round(med * 1e3, 3),
+            "sample": f"SunnyNet-100M fp32, 16-token prefill then median of {len(times)} single steps; "
+                      "B=64 on this runtime is 64 sequential handles (64x the B=1 time)"}
+
+
 def pmc_probe():
     """A short fixed sequence for `rocprofv3 --pmc` runs: 3 scans of the
     workload, then 3 plain device copies of one 537 MB input array (the copy
@@ -163,7 +277,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="scan", choices=["scan"])
+    ap.add_argument("--workload", default="all", choices=["all", "scan", "decode"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the fixed launch sequence used for rocprofv3 --pmc and exit")
@@ -174,6 +288,19 @@ def main(argv=None):
         log("bench.py measures one GPU only: this build has no multi-GPU path "
             "(each channel / sequence shards with no communication; see DESIGN.md).")
         return 2
+    dec = None
+    if args.workload in ("all", "decode"):
+        dec = bench_decode(cpu=not args.no_cpu)
+    if args.workload == "decode":
+        # Decode-only run: the headline is the B=1 fp32 decode rate.
+        c = dec["cases"][0]
+        line = {"metric": METRIC, "value": c["tok_s"], "unit": "tok/s", "n_gpus": 1,
+                "steps": dec["steps"], "warmup": 8, "ms_per_step": c["us_per_step"] / 1e3,
+                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                "data": "synthetic (seeded random ids, random-init weights)",
+                "config": {"workload": "SunnyNet-100M greedy decode B=1 fp32"}, "decode": dec}
+        print(json.dumps(line), flush=True)
+        return 0
     res = bench_scan(args.steps, args.warmup, cpu=not args.no_cpu)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
@@ -182,6 +309,8 @@ def main(argv=None):
             "config": res["config"], "roofline": res["roofline"]}
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
+    if dec is not None:
+        line["decode"] = dec
     print(json.dumps(line), flush=True)
     return 0
 

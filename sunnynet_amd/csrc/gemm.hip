@@ -145,8 +145,15 @@ __global__ void k_gemm_reduce(GemmArgs g, int splits, const float* __restrict__ 
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const long MN = (long)g.M * g.N;
     if (idx >= MN) return;
+    // Loads issued ahead of the (in-order) sum, four splits at a time.
     float acc = part[idx];
-    for (int z = 1; z < splits; ++z) acc += part[(long)z * MN + idx];
+    int z = 1;
+    for (; z + 4 <= splits; z += 4) {
+        const float p0 = part[(long)z * MN + idx], p1 = part[(long)(z + 1) * MN + idx];
+        const float p2 = part[(long)(z + 2) * MN + idx], p3 = part[(long)(z + 3) * MN + idx];
+        acc += p0; acc += p1; acc += p2; acc += p3;
+    }
+    for (; z < splits; ++z) acc += part[(long)z * MN + idx];
     gemm_epilogue(g, (int)(idx / g.N), (int)(idx % g.N), acc);
 }
 

@@ -619,7 +619,7 @@ struct SnHipModel {
     bool use_graphs = true;
     // Decode batches of at least this many sequences run their matmuls on the
     // MFMA GEMM; smaller batches use the GEMV kernels.
-    int gemm_min_batch = 16;
+    int gemm_min_batch = 8;
     bool gemm_ok = true;
     float* gemm_work = nullptr;           // split-K partials
     size_t gemm_work_floats = 0;
