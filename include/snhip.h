@@ -89,6 +89,12 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
                                      int32_t n_steps, int32_t* out_tokens_dev,
                                      float* logits_dev);
 
+/* Grid size of the persistent single-sequence decode (B = 1 steps and greedy
+ * decoding run every layer of every step in one cooperative launch), or 0 when
+ * this handle uses the per-kernel step (shape above 2048 wide, taps > 8, no
+ * cooperative launch, or SNHIP_PERSIST=0 in the environment at load). */
+int32_t snhip_persistent_grid(const SnHipModel* m);
+
 /* State of sequences [0, B) in the SunnyState layout above, device pointers. */
 snhip_status snhip_get_state_dev(SnHipModel* m, float* s_dev, float* hist_dev, int32_t B);
 snhip_status snhip_set_state_dev(SnHipModel* m, const float* s_dev, const float* hist_dev,

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "common.h"
+#include "decode.h"
 #include "gemm.h"
 #include "snhip.h"
 
@@ -629,6 +630,14 @@ struct SnHipModel {
           *pf_u = nullptr, *pf_st = nullptr, *pf_z = nullptr, *pf_yn = nullptr, *pf_sfb = nullptr,
           *pf_send = nullptr;
     int32_t* pf_tok = nullptr;
+    // Persistent single-sequence decode (persist.hip): grid size, 0 when the
+    // model's shape or the device does not allow it.
+    int persist_wg = 0;
+    snhip::PLayer* dlayers = nullptr;     // device copy of the layer table
+    unsigned* pbar = nullptr;             // grid barrier words
+    unsigned* h_err = nullptr;            // pinned copy of the barrier time-out flag
+    unsigned persist_spin = 1u << 22;     // barrier poll limit (SNHIP_PERSIST_SPIN)
+    unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests)
     int ready = 0;
 };
 
@@ -645,6 +654,7 @@ T* dalloc(SnHipModel* m, size_t n) {
 
 void free_model(SnHipModel* m) {
     if (!m) return;
+    if (m->h_err) (void)hipHostFree(m->h_err);
     for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
     if (m->ev_in) (void)hipEventDestroy(m->ev_in);
     if (m->ev_out) (void)hipEventDestroy(m->ev_out);
@@ -700,6 +710,48 @@ bool upload_mat(SnHipModel* m, Mat& M, const float* src, int in, int out, float*
         if (launch_quant_i4(tmp_out, M.q, M.sc, out, in, m->block, nullptr) != SNHIP_OK) return false;
     }
     return hipDeviceSynchronize() == hipSuccess;
+}
+
+PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M}; }
+
+// Enables the persistent single-sequence decode when the shape fits it and the
+// device supports cooperative launches (SNHIP_PERSIST=0 turns it off;
+// SNHIP_PERSIST_WG sets the grid size, default one workgroup per CU).
+void setup_persist(SnHipModel* m) {
+    if (const char* e = getenv("SNHIP_PERSIST"))
+        if (e[0] == '0') return;
+    if (m->D > kPersistMaxDim || m->I > kPersistMaxDim || m->R > kPersistMaxDim ||
+        m->K > kPersistMaxTaps || m->D % 8)
+        return;
+    int dev = 0, coop = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return;
+    const int occ = persist_occupancy(m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0);
+    if (occ < 1) return;
+    int nwg = ncu;
+    if (const char* e = getenv("SNHIP_PERSIST_WG")) nwg = atoi(e);
+    nwg = std::min(std::min(nwg, ncu * occ), 1024);
+    if (nwg < 1) return;
+    if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->persist_spin = (unsigned)std::max(1, atoi(e));
+    if (const char* e = getenv("SNHIP_PERSIST_STALL")) m->persist_stall = (unsigned)std::max(0, atoi(e));
+    std::vector<PLayer> hl(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const Layer& A = m->layers[l];
+        PLayer& P = hl[l];
+        P.ni_g = A.ni_g; P.ni_c = A.ni_c; P.nm_g = A.nm_g; P.nm_c = A.nm_c;
+        P.dw = A.dw; P.delta = A.delta; P.a_tanh = A.a_tanh; P.b_gain = A.b_gain;
+        P.V = pmat(A.V); P.U = pmat(A.U); P.Wz = pmat(A.Wz); P.Wc = pmat(A.Wc); P.Ws = pmat(A.Ws);
+    }
+    m->dlayers = dalloc<PLayer>(m, m->L);
+    m->pbar = dalloc<unsigned>(m, kPersistBarWords);
+    if (!m->dlayers || !m->pbar || hipHostMalloc((void**)&m->h_err, sizeof(unsigned), 0) != hipSuccess)
+        return;
+    *m->h_err = 0;
+    if (hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PLayer), hipMemcpyHostToDevice) != hipSuccess)
+        return;
+    m->persist_wg = nwg;
 }
 
 SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank, int taps,
@@ -818,6 +870,7 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     m->gemm_work_floats = (size_t)16 << 20;
     m->gemm_work = dalloc<float>(m, m->gemm_work_floats);
     if (!m->gemm_work) { set_last_error("out of device memory"); free_model(m); return nullptr; }
+    setup_persist(m);
     m->ready = 1;
     return m;
 }
@@ -1153,6 +1206,73 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
     return SNHIP_OK;
 }
 
+// n_steps decode steps of sequence 0 in persistent launches on the internal
+// stream (ordered like run_steps). The first input token is in m->tok. greedy:
+// out_tok (n_steps) receives each step's argmax token, fed to the next step;
+// otherwise n_steps must be 1. logits (device), if not NULL, gets the last
+// step's logits.
+snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_tok,
+                         float* logits) {
+    constexpr int kMaxStepsPerLaunch = 1 << 20;   // keeps barrier counters far from wrapping
+    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
+    SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
+    SNHIP_CHECK(hipMemsetAsync(m->pbar, 0, kPersistBarWords * sizeof(unsigned), m->work));
+    PersistArgs a{};
+    a.layers = m->dlayers;
+    a.L = m->L; a.D = m->D; a.I = m->I; a.R = m->R; a.K = m->K; a.kh = m->kh;
+    a.vocab = m->vocab; a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
+    a.embed = m->embed; a.no_g = m->no_g; a.no_c = m->no_c;
+    a.head = pmat(m->head);
+    a.s = m->s; a.hist = m->hist;
+    a.x = m->x; a.v = m->v; a.sfb = m->sfb; a.u = m->u; a.z = m->z;
+    a.part = m->best;
+    a.bar = m->pbar;
+    a.greedy = greedy ? 1 : 0;
+    a.spin_limit = m->persist_spin;
+    a.stall = m->persist_stall;
+    const int blk = m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0;
+    for (int done = 0; done < n_steps;) {
+        const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
+        if (done > 0)   // counters only; the time-out flag accumulates
+            SNHIP_CHECK(hipMemsetAsync(m->pbar, 0, kPersistBarErr * sizeof(unsigned), m->work));
+        a.tok_in = done == 0 ? m->tok : out_tok + done - 1;
+        a.out_tok = greedy ? out_tok + done : nullptr;
+        a.logits = done + n == n_steps ? logits : nullptr;
+        a.n_steps = n;
+        const snhip_status rc = launch_decode_persist(a, m->persist_wg, blk, m->work);
+        if (rc != SNHIP_OK) return rc;
+        done += n;
+    }
+    SNHIP_CHECK(hipMemcpyAsync(m->h_err, m->pbar + kPersistBarErr, sizeof(unsigned),
+                               hipMemcpyDeviceToHost, m->work));
+    SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
+    SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
+    return SNHIP_OK;
+}
+
+// After a synchronization: did a persistent launch time out at a barrier?
+snhip_status persist_status(SnHipModel* m) {
+    if (m->h_err && *m->h_err) {
+        *m->h_err = 0;
+        set_last_error("persistent decode: grid barrier timed out");
+        return SNHIP_E_DEVICE;
+    }
+    return SNHIP_OK;
+}
+
+// One step of sequence 0 (tokens already in m->tok): the persistent kernel
+// when enabled, else the captured per-kernel step. A failed cooperative launch
+// turns the persistent path off for this handle and falls back.
+snhip_status step_one(SnHipModel* m, float* logits_out) {
+    if (m->persist_wg) {
+        const snhip_status rc = run_persist(m, 1, false, nullptr, logits_out);
+        if (rc == SNHIP_OK) return rc;
+        m->persist_wg = 0;
+        (void)hipGetLastError();
+    }
+    return run_steps(m, 1, logits_out, false, 1);
+}
+
 bool tokens_ok(const SnHipModel* m, const int32_t* t, int n) {
     for (int i = 0; i < n; ++i)
         if (t[i] < 0 || t[i] >= m->vocab) return false;
@@ -1198,6 +1318,7 @@ void snhip_reset(SnHipModel* m) {
 int snhip_vocab(const SnHipModel* m) { return m ? m->vocab : 0; }
 int snhip_ready(const SnHipModel* m) { return m && m->ready; }
 int32_t snhip_max_batch(const SnHipModel* m) { return m ? m->max_batch : 0; }
+int32_t snhip_persistent_grid(const SnHipModel* m) { return m ? m->persist_wg : 0; }
 
 snhip_status snhip_set_stream(SnHipModel* m, void* stream) {
     if (!m) return SNHIP_E_INVAL;
@@ -1209,19 +1330,20 @@ snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int3
                                   float* logits_dev) {
     if (!m || !tokens_dev || !logits_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
     const snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
-    return rc != SNHIP_OK ? rc : run_steps(m, B, logits_dev, false, 1);
+    if (rc != SNHIP_OK) return rc;
+    return B == 1 ? step_one(m, logits_dev) : run_steps(m, B, logits_dev, false, 1);
 }
 
 snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits) {
     if (!m || !tokens || !logits || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
     if (!tokens_ok(m, tokens, B)) return SNHIP_E_INVAL;
     snhip_status rc = put_tokens(m, tokens, B, hipMemcpyHostToDevice);
-    if (rc == SNHIP_OK) rc = run_steps(m, B, m->logits, false, 1);
+    if (rc == SNHIP_OK) rc = B == 1 ? step_one(m, m->logits) : run_steps(m, B, m->logits, false, 1);
     if (rc != SNHIP_OK) return rc;
     SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)B * m->vocab * sizeof(float),
                                hipMemcpyDeviceToHost, m->stream));
     SNHIP_CHECK(hipStreamSynchronize(m->stream));
-    return SNHIP_OK;
+    return persist_status(m);
 }
 
 void snhip_step(SnHipModel* m, int token, float* logits) {
@@ -1261,6 +1383,13 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
                                      float* logits_dev) {
     if (!m || !tokens_dev || !out_tokens_dev || B <= 0 || B > m->max_batch || n_steps <= 0)
         return SNHIP_E_INVAL;
+    if (B == 1 && m->persist_wg) {
+        snhip_status rc = put_tokens(m, tokens_dev, 1, hipMemcpyDeviceToDevice);
+        if (rc == SNHIP_OK) rc = run_persist(m, n_steps, true, out_tokens_dev, logits_dev);
+        if (rc == SNHIP_OK) return rc;
+        m->persist_wg = 0;
+        (void)hipGetLastError();
+    }
     if ((long)n_steps * B > (long)m->hist_cap || !m->tok_hist) {
         // Grow the token history; graphs bake its address, so drop them.
         SNHIP_CHECK(hipStreamSynchronize(m->stream));
@@ -1281,7 +1410,7 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
         m->allocs.push_back(h);
         m->hist_cap = (int)cap;
     }
-        snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
+    snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
     if (rc != SNHIP_OK) return rc;
     SNHIP_CHECK(hipMemsetAsync(m->counter, 0, sizeof(int32_t), m->stream));
     float* lg = logits_dev ? logits_dev : m->logits;

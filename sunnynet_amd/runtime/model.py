@@ -119,6 +119,11 @@ class HipModel:
             logits.data_ptr() if logits is not None else None), "snhip_decode_greedy_dev")
         return out
 
+    @property
+    def persistent_grid(self) -> int:
+        """Workgroups of the persistent B=1 decode kernel (0: per-kernel steps)."""
+        return int(self._lib.snhip_persistent_grid(self._h))
+
     def get_state(self, B: int | None = None):
         B = self.max_batch if B is None else B
         s = torch.empty(B, self.layers, self.dim, device=self.device)

@@ -1,0 +1,179 @@
+"""The persistent single-sequence decode (one cooperative launch per call,
+grid barriers between the phases of every layer) against the oracle and the
+per-kernel step path.
+
+Bar as for every decode path: logits within 2e-5 absolute of the C oracle
+(bit-identical to the reference's sn_step), the greedy token equal to the
+oracle's argmax on every step. INT4 compares with the oracle on the
+bit-identically dequantized weights.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from sunnynet_amd.blob import pack_sunny_blob
+from sunnynet_amd.config import SMALL, SUNNY_100M, TINY
+from sunnynet_amd.runtime.model import HipModel
+from sunnynet_amd.weights import gaussian_matmuls, init_sunnynet
+from tests.test_decode_gpu import dequant_blob
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-5
+
+
+def _model(path, cfg, **kw):
+    return HipModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers, **kw)
+
+
+def _blob(tmp_path_factory, name, buf):
+    p = tmp_path_factory.mktemp("pblobs") / name
+    p.write_bytes(buf)
+    return p
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    w = init_sunnynet(TINY, 0)
+    buf = pack_sunny_blob(w)
+    return w, buf, _blob(tmp_path_factory, "tiny.bin", buf)
+
+
+@pytest.fixture(scope="module")
+def small(tmp_path_factory):
+    w = init_sunnynet(SMALL, 0)
+    buf = pack_sunny_blob(w)
+    return w, buf, _blob(tmp_path_factory, "small.bin", buf)
+
+
+def _greedy_vs_oracle(gpu, hm, orc, start, n):
+    """decode_greedy on the device vs the oracle's greedy chain; also the
+    last step's logits."""
+    lg = torch.empty(hm.vocab, device=gpu)
+    out = hm.decode_greedy(torch.tensor([start], dtype=torch.int32, device=gpu), n,
+                           logits=lg).cpu().numpy()[:, 0]
+    cur = start
+    for i in range(n):
+        ref = orc.step([cur])[0]
+        nxt = int(ref.argmax())
+        assert out[i] == nxt, f"step {i}: {out[i]} != {nxt}"
+        cur = nxt
+    d = float(np.abs(lg.cpu().numpy() - ref).max())
+    assert d < TOL, d
+    return out
+
+
+def test_enabled_and_switch(gpu, tiny, monkeypatch):
+    w, buf, path = tiny
+    hm = _model(path, TINY)
+    assert hm.persistent_grid > 0
+    monkeypatch.setenv("SNHIP_PERSIST", "0")
+    assert _model(path, TINY).persistent_grid == 0
+
+
+def test_step_matches_per_kernel_path(gpu, small, monkeypatch):
+    """The same tokens through both paths of one model: logits within TOL of
+    each other and of the oracle, and the same state afterwards."""
+    w, buf, path = small
+    print("small fp32: persistent vs per-kernel, 40 steps", flush=True)
+    hp = _model(path, SMALL)
+    monkeypatch.setenv("SNHIP_PERSIST", "0")
+    hk = _model(path, SMALL)
+    assert hp.persistent_grid > 0 and hk.persistent_grid == 0
+    orc = oracle.SnOracle(buf)
+    for t in np.random.default_rng(5).integers(0, SMALL.vocab_size, 40):
+        a = np.asarray(hp.step(int(t)), np.float32)
+        b = np.asarray(hk.step(int(t)), np.float32)
+        r = orc.step([t])[0]
+        assert np.abs(a - r).max() < TOL and np.abs(a - b).max() < TOL
+        assert a.argmax() == r.argmax()
+    sp, hpst = hp.get_state(1)
+    sk, hkst = hk.get_state(1)
+    assert float((sp - sk).abs().max()) < 1e-5 and float((hpst - hkst).abs().max()) < 1e-5
+
+
+@pytest.mark.parametrize("grid", [1, 3, 8, 64, 512])
+def test_grid_sizes(gpu, tiny, monkeypatch, grid):
+    """Any grid size gives the same tokens: one workgroup doing every phase,
+    grids that are not a multiple of the 8 barrier groups, fewer workgroups
+    than channel groups, two workgroups per CU."""
+    w, buf, path = tiny
+    print(f"tiny fp32 persistent grid={grid}", flush=True)
+    monkeypatch.setenv("SNHIP_PERSIST_WG", str(grid))
+    hm = _model(path, TINY)
+    assert 0 < hm.persistent_grid <= grid
+    _greedy_vs_oracle(gpu, hm, oracle.SnOracle(buf), 7, 48)
+
+
+def test_long_greedy_tiny(gpu, tiny):
+    """300 greedy steps in one launch (14 700 grid barriers on TINY)."""
+    w, buf, path = tiny
+    print("tiny fp32 persistent greedy 300", flush=True)
+    _greedy_vs_oracle(gpu, _model(path, TINY), oracle.SnOracle(buf), 11, 300)
+
+
+def test_prefill_then_persistent_greedy(gpu, small):
+    """Chunked prefill (matrix-core path) hands its state to the persistent
+    greedy decode; then single steps continue from the greedy state."""
+    w, buf, path = small
+    print("small fp32: prefill 100 + persistent greedy 32 + 4 steps", flush=True)
+    hm = _model(path, SMALL)
+    orc = oracle.SnOracle(buf)
+    prompt = np.random.default_rng(2).integers(0, SMALL.vocab_size, 100).astype(np.int32)
+    lg = hm.prefill_batch(torch.from_numpy(prompt[None]).to(gpu))[0].cpu().numpy()
+    for t in prompt:
+        ref = orc.step([t])[0]
+    assert np.abs(lg - ref).max() < TOL
+    out = _greedy_vs_oracle(gpu, hm, orc, int(ref.argmax()), 32)
+    cur = int(out[-1])
+    for _ in range(4):
+        a = np.asarray(hm.step(cur), np.float32)
+        r = orc.step([cur])[0]
+        assert np.abs(a - r).max() < TOL
+        cur = int(r.argmax())
+
+
+@pytest.mark.parametrize("block", [32, 64])
+def test_int4_greedy(gpu, tmp_path_factory, block):
+    print(f"small int4 g{block} persistent greedy 40", flush=True)
+    w = gaussian_matmuls(init_sunnynet(SMALL, 0), seed=3)
+    path = _blob(tmp_path_factory, f"small_g{block}.bin", pack_sunny_blob(w))
+    hm = _model(path, SMALL, weights="int4", block=block)
+    assert hm.persistent_grid > 0
+    _greedy_vs_oracle(gpu, hm, oracle.SnOracle(dequant_blob(w, block)), 3, 40)
+
+
+def test_100m_fp32_and_int4(gpu, tmp_path_factory):
+    """SunnyNet-100M (12 layers, D=1024, V=32000): fp32 seed 1 and INT4 g32 on
+    N(0, 0.02) matmuls (seed 3), 16 greedy steps each."""
+    cfg = SUNNY_100M
+    print("100M fp32 persistent greedy 16", flush=True)
+    w = init_sunnynet(cfg, 1)
+    buf = pack_sunny_blob(w)
+    path = _blob(tmp_path_factory, "m100.bin", buf)
+    _greedy_vs_oracle(gpu, _model(path, cfg), oracle.SnOracle(buf), 17, 16)
+    print("100M int4 g32 persistent greedy 16", flush=True)
+    wq = gaussian_matmuls(w, seed=3)
+    pq = _blob(tmp_path_factory, "m100q.bin", pack_sunny_blob(wq))
+    _greedy_vs_oracle(gpu, _model(pq, cfg, weights="int4", block=32),
+                      oracle.SnOracle(dequant_blob(wq, 32)), 17, 16)
+
+
+def test_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
+    """A barrier target the host raised out of reach: every workgroup gives up
+    after its poll limit and leaves the kernel, the call reports an error, and
+    the handle keeps working once the target is normal again."""
+    w, buf, path = tiny
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
+    hm = _model(path, TINY)
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.step_batch_host([3])
+    monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
+    hm2 = _model(path, TINY)
+    orc = oracle.SnOracle(buf)
+    a = hm2.step_batch_host([3])[0]
+    assert np.abs(a - orc.step([3])[0]).max() < TOL
