@@ -5,10 +5,17 @@
 
 namespace snhip {
 
-// Largest dim / inner / rank the persistent kernel handles (LDS staging and
-// register batches are sized for it); larger models use the per-kernel path.
-constexpr int kPersistMaxDim = 2048;
-constexpr int kPersistMaxTaps = 8;
+// Row order of the low-rank output q = U v (2 dim values) on this backend:
+// the 8 value rows and the 8 gate rows of each channel group are adjacent, so
+// one group's 16 rows of U are contiguous (U's rows are permuted at load).
+__host__ __device__ inline int qrow_u(int i) { return 16 * (i >> 3) + (i & 7); }
+__host__ __device__ inline int qrow_g(int i) { return 16 * (i >> 3) + 8 + (i & 7); }
+
+// Largest dim, and inner / rank, the persistent kernel handles (LDS staging
+// and per-thread register arrays are sized for them); larger models use the
+// per-kernel path.
+constexpr int kPersistMaxD = 1024;
+constexpr int kPersistMaxK = 1536;
 
 // A weight matrix, row-major (M, Kd): fp32 rows in w, or INT4 codes in q
 // ((M, Kd/2) bytes, quant.c packing) with per-group scales sc ((M, Kd/block)).
@@ -22,7 +29,8 @@ struct PMat {
 struct PLayer {
     const float *ni_g, *ni_c, *nm_g, *nm_c, *dw, *delta;
     float a_tanh, b_gain;
-    PMat V, U, Wz, Wc, Ws;
+    PMat VW;                // V (rank rows) followed by W_eff (dim rows), both (., dim)
+    PMat U, Wz, Wc;         // U rows in the qrow_u / qrow_g order
 };
 
 struct PersistArgs {
@@ -33,6 +41,7 @@ struct PersistArgs {
     PMat head;
     float* s;               // (L, D) state of the sequence
     float* hist;            // (L, kh, D) conv history, newest first
+    float* hd;              // (L, kh, D) hist[k] * dw[K-2-k], kept by the kernel
     float *x, *v, *sfb, *u, *z;   // exchange buffers: D, R, D, D, I floats
     unsigned long long* part;     // per-workgroup argmax keys (grid size)
     unsigned* bar;                // barrier words (kPersistBarWords), zeroed before launch
@@ -48,6 +57,11 @@ struct PersistArgs {
 // time-out flag.
 constexpr int kPersistBarWords = 320;
 constexpr int kPersistBarErr = 288;
+
+// Conv taps the kernel is built for (the history loads are straight-line
+// code), and its largest grid.
+constexpr int kPersistTaps = 4;
+constexpr int kPersistMaxGrid = 1024;
 
 // Workgroups per CU the kernel can keep resident (0 if it cannot run).
 int persist_occupancy(int blk);

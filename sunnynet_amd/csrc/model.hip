@@ -155,6 +155,7 @@ __global__ __launch_bounds__(256) void k_ln(const float* __restrict__ x, int ldx
 
 // Competitive gate, decay gate and state update for every (b, channel):
 // sunnynet.c:252-266 (groups of 8, state update after the feedback GEMV).
+// q rows are in the qrow_u / qrow_g order.
 __global__ void k_compete_state(const float* __restrict__ q, const float* __restrict__ delta,
                                 float* __restrict__ s, size_t s_bstride, float* __restrict__ u,
                                 int B, int D, int clamp, float p_floor) {
@@ -162,11 +163,10 @@ __global__ void k_compete_state(const float* __restrict__ q, const float* __rest
     if (idx >= (long)B * D) return;
     const int b = (int)(idx / D), i = (int)(idx - (long)b * D);
     const float* qb = q + (size_t)b * 2 * D;
-    const float* gate = qb + D;
     const int base = i & ~7, off = i - base;
-    const float gi = gate[i];
-    const float uu = qb[i] * (sgm(gi - gate[base + ((off + 1) & 7)]) *
-                              sgm(gi - gate[base + ((off + 2) & 7)]));
+    const float gi = qb[qrow_g(i)];
+    const float uu = qb[qrow_u(i)] * (sgm(gi - qb[qrow_g(base + ((off + 1) & 7))]) *
+                                      sgm(gi - qb[qrow_g(base + ((off + 2) & 7))]));
     float p = 1.0f - delta[i] * (1.0f - sgm(gi));
     if (clamp && p < p_floor) p = p_floor;
     float* sp = s + (size_t)b * s_bstride + i;
@@ -421,6 +421,15 @@ __global__ void k_transpose(const float* __restrict__ src, float* __restrict__ d
     }
 }
 
+// Rows of U (2D, R) into the qrow_u / qrow_g order: dst[perm(o)] = src[o].
+__global__ void k_permute_u(const float* __restrict__ src, float* __restrict__ dst, int D, int R) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= 2L * D * R) return;
+    const int o = (int)(idx / R), k = (int)(idx % R);
+    const int po = o < D ? qrow_u(o) : qrow_g(o - D);
+    dst[(size_t)po * R + k] = src[idx];
+}
+
 // ------------------------------------------------------------------- host
 struct Mat {
     int M = 0, Kd = 0;
@@ -515,8 +524,8 @@ __global__ __launch_bounds__(64 * W) void k_core_scan(
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
             const long r = row0 + min(t0 + k, T - 1);
-            ur[k] = q[r * 2 * D + i];
-            gt[k] = q[r * 2 * D + D + i];
+            ur[k] = q[r * 2 * D + qrow_u(i)];
+            gt[k] = q[r * 2 * D + qrow_g(i)];
         }
     };
     auto prep = [&](int tile) {
@@ -635,6 +644,7 @@ struct SnHipModel {
     int persist_wg = 0;
     snhip::PLayer* dlayers = nullptr;     // device copy of the layer table
     unsigned* pbar = nullptr;             // grid barrier words
+    float* hd = nullptr;                  // conv-history products of sequence 0
     unsigned* h_err = nullptr;            // pinned copy of the barrier time-out flag
     unsigned persist_spin = 1u << 22;     // barrier poll limit (SNHIP_PERSIST_SPIN)
     unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests)
@@ -691,25 +701,61 @@ bool upload(SnHipModel* m, float*& dst, const float* src, size_t n) {
     return dst && hipMemcpy(dst, src, n * sizeof(float), hipMemcpyHostToDevice) == hipSuccess;
 }
 
-// Upload an (in,out) blob matrix as (out,in), optionally quantizing to INT4.
+// Storage of one weight matrix, (out, in) rows: fp32 w, or INT4 q + sc.
+struct MatStore {
+    float* w = nullptr;
+    uint8_t* q = nullptr;
+    float* sc = nullptr;
+};
+
+MatStore alloc_mat(SnHipModel* m, size_t rows, size_t in) {
+    MatStore S;
+    if (m->wfmt == SNHIP_WEIGHTS_F32) {
+        S.w = dalloc<float>(m, rows * in);
+    } else {
+        S.q = dalloc<uint8_t>(m, rows * in / 2);
+        S.sc = dalloc<float>(m, rows * in / m->block);
+    }
+    return S;
+}
+
+bool store_ok(const SnHipModel* m, const MatStore& S) {
+    return m->wfmt == SNHIP_WEIGHTS_F32 ? S.w != nullptr : (S.q && S.sc);
+}
+
+// Upload an (in,out) blob matrix as (out,in) rows starting at row `row0` of
+// the storage S (quantized to INT4 for that format). perm_u: U's rows go to
+// the qrow_u / qrow_g order (in = R, out = 2D).
 bool upload_mat(SnHipModel* m, Mat& M, const float* src, int in, int out, float* tmp_in,
-                float* tmp_out) {
+                float* tmp_out, const MatStore& S, size_t row0, bool perm_u = false) {
     M.M = out;
     M.Kd = in;
     const size_t n = (size_t)in * out;
     if (hipMemcpy(tmp_in, src, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) return false;
-    float* dst = m->wfmt == SNHIP_WEIGHTS_F32 ? (M.w = dalloc<float>(m, n)) : tmp_out;
-    if (!dst) return false;
     dim3 grid((out + 31) / 32, (in + 31) / 32);
-    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, nullptr, tmp_in, dst, in, out);
+    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, nullptr, tmp_in, tmp_out, in, out);
+    const float* rows = tmp_out;
+    if (perm_u) {
+        hipLaunchKernelGGL(k_permute_u, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr,
+                           tmp_out, tmp_in, out / 2, in);
+        rows = tmp_in;
+    }
     if (hipGetLastError() != hipSuccess) return false;
-    if (m->wfmt == SNHIP_WEIGHTS_INT4) {
-        M.q = dalloc<uint8_t>(m, n / 2);
-        M.sc = dalloc<float>(m, n / m->block);
-        if (!M.q || !M.sc) return false;
-        if (launch_quant_i4(tmp_out, M.q, M.sc, out, in, m->block, nullptr) != SNHIP_OK) return false;
+    if (m->wfmt == SNHIP_WEIGHTS_F32) {
+        M.w = S.w + row0 * in;
+        if (hipMemcpy(M.w, rows, n * sizeof(float), hipMemcpyDeviceToDevice) != hipSuccess) return false;
+    } else {
+        M.q = S.q + row0 * in / 2;
+        M.sc = S.sc + row0 * in / m->block;
+        if (launch_quant_i4(rows, M.q, M.sc, out, in, m->block, nullptr) != SNHIP_OK) return false;
     }
     return hipDeviceSynchronize() == hipSuccess;
+}
+
+bool upload_new(SnHipModel* m, Mat& M, const float* src, int in, int out, float* tmp_in,
+                float* tmp_out, bool perm_u = false) {
+    const MatStore S = alloc_mat(m, out, in);
+    return store_ok(m, S) && upload_mat(m, M, src, in, out, tmp_in, tmp_out, S, 0, perm_u);
 }
 
 PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M}; }
@@ -720,8 +766,8 @@ PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M}; }
 void setup_persist(SnHipModel* m) {
     if (const char* e = getenv("SNHIP_PERSIST"))
         if (e[0] == '0') return;
-    if (m->D > kPersistMaxDim || m->I > kPersistMaxDim || m->R > kPersistMaxDim ||
-        m->K > kPersistMaxTaps || m->D % 8)
+    if (m->D > kPersistMaxD || m->I > kPersistMaxK || m->R > kPersistMaxK ||
+        m->K != kPersistTaps || m->D % 8)
         return;
     int dev = 0, coop = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -732,7 +778,7 @@ void setup_persist(SnHipModel* m) {
     if (occ < 1) return;
     int nwg = ncu;
     if (const char* e = getenv("SNHIP_PERSIST_WG")) nwg = atoi(e);
-    nwg = std::min(std::min(nwg, ncu * occ), 1024);
+    nwg = std::min(std::min(nwg, ncu * occ), kPersistMaxGrid);
     if (nwg < 1) return;
     if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->persist_spin = (unsigned)std::max(1, atoi(e));
     if (const char* e = getenv("SNHIP_PERSIST_STALL")) m->persist_stall = (unsigned)std::max(0, atoi(e));
@@ -742,11 +788,14 @@ void setup_persist(SnHipModel* m) {
         PLayer& P = hl[l];
         P.ni_g = A.ni_g; P.ni_c = A.ni_c; P.nm_g = A.nm_g; P.nm_c = A.nm_c;
         P.dw = A.dw; P.delta = A.delta; P.a_tanh = A.a_tanh; P.b_gain = A.b_gain;
-        P.V = pmat(A.V); P.U = pmat(A.U); P.Wz = pmat(A.Wz); P.Wc = pmat(A.Wc); P.Ws = pmat(A.Ws);
+        P.VW = pmat(A.V);
+        P.VW.M = A.V.M + A.Ws.M;      // W_eff's rows follow V's in one storage
+        P.U = pmat(A.U); P.Wz = pmat(A.Wz); P.Wc = pmat(A.Wc);
     }
     m->dlayers = dalloc<PLayer>(m, m->L);
     m->pbar = dalloc<unsigned>(m, kPersistBarWords);
-    if (!m->dlayers || !m->pbar || hipHostMalloc((void**)&m->h_err, sizeof(unsigned), 0) != hipSuccess)
+    m->hd = dalloc<float>(m, (size_t)m->L * (m->kh ? m->kh : 1) * m->D);
+    if (!m->dlayers || !m->pbar || !m->hd || hipHostMalloc((void**)&m->h_err, sizeof(unsigned), 0) != hipSuccess)
         return;
     *m->h_err = 0;
     if (hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PLayer), hipMemcpyHostToDevice) != hipSuccess)
@@ -790,8 +839,8 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     const size_t D = dim, I = inner, R = rank, K = taps, V = vocab;
     const size_t big = std::max(std::max(D * R, R * 2 * D), std::max(D * I, std::max(D * D, D * V)));
     float* tmp_in = dalloc<float>(m, big);
-    float* tmp_out = wfmt == SNHIP_WEIGHTS_INT4 ? dalloc<float>(m, big) : nullptr;
-    if (!tmp_in || (wfmt == SNHIP_WEIGHTS_INT4 && !tmp_out)) { free_model(m); set_last_error("out of device memory"); return nullptr; }
+    float* tmp_out = dalloc<float>(m, big);
+    if (!tmp_in || !tmp_out) { free_model(m); set_last_error("out of device memory"); return nullptr; }
 
     const float* p = P.data();
     bool ok = true;
@@ -804,11 +853,14 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         ok &= upload(m, t, p, I); A.nm_g = t; p += I;
         ok &= upload(m, t, p, I); A.nm_c = t; p += I;
         ok &= upload(m, t, p, K * D); A.dw = t; p += K * D;
-        ok = ok && upload_mat(m, A.V, p, dim, rank, tmp_in, tmp_out); p += D * R;
-        ok = ok && upload_mat(m, A.U, p, rank, 2 * dim, tmp_in, tmp_out); p += R * 2 * D;
-        ok = ok && upload_mat(m, A.Wz, p, dim, inner, tmp_in, tmp_out); p += D * I;
-        ok = ok && upload_mat(m, A.Wc, p, inner, dim, tmp_in, tmp_out); p += I * D;
-        ok = ok && upload_mat(m, A.Ws, p, dim, dim, tmp_in, tmp_out); p += D * D;
+        // V and W_eff share one (R + D, D) storage: V's rows, then W_eff's.
+        const MatStore vw = alloc_mat(m, R + D, D);
+        ok = ok && store_ok(m, vw);
+        ok = ok && upload_mat(m, A.V, p, dim, rank, tmp_in, tmp_out, vw, 0); p += D * R;
+        ok = ok && upload_new(m, A.U, p, rank, 2 * dim, tmp_in, tmp_out, true); p += R * 2 * D;
+        ok = ok && upload_new(m, A.Wz, p, dim, inner, tmp_in, tmp_out); p += D * I;
+        ok = ok && upload_new(m, A.Wc, p, inner, dim, tmp_in, tmp_out); p += I * D;
+        ok = ok && upload_mat(m, A.Ws, p, dim, dim, tmp_in, tmp_out, vw, R); p += D * D;
         ok &= upload(m, t, p, D); A.delta = t; p += D;
         A.a_tanh = p[0]; A.b_gain = p[1]; p += 2;
     }
@@ -818,7 +870,7 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         ok &= upload(m, t, p, D); m->no_g = t; p += D;
         ok &= upload(m, t, p, D); m->no_c = t; p += D;
         ok &= upload(m, t, p, V * D); m->embed = t; p += V * D;
-        ok = ok && upload_mat(m, m->head, p, dim, vocab, tmp_in, tmp_out);
+        ok = ok && upload_new(m, m->head, p, dim, vocab, tmp_in, tmp_out);
     }
     const size_t B = max_batch;
     if (ok) {
@@ -848,7 +900,7 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     }
     // The transpose staging buffers are no longer needed.
     for (auto it = m->allocs.begin(); it != m->allocs.end();) {
-        if (*it == tmp_in || (tmp_out && *it == tmp_out)) { (void)hipFree(*it); it = m->allocs.erase(it); }
+        if (*it == tmp_in || *it == tmp_out) { (void)hipFree(*it); it = m->allocs.erase(it); }
         else ++it;
     }
     if (hipMemset(m->s, 0, B * layers * D * sizeof(float)) != hipSuccess ||
@@ -1223,7 +1275,7 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
     a.vocab = m->vocab; a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
     a.embed = m->embed; a.no_g = m->no_g; a.no_c = m->no_c;
     a.head = pmat(m->head);
-    a.s = m->s; a.hist = m->hist;
+    a.s = m->s; a.hist = m->hist; a.hd = m->hd;
     a.x = m->x; a.v = m->v; a.sfb = m->sfb; a.u = m->u; a.z = m->z;
     a.part = m->best;
     a.bar = m->pbar;

@@ -4,23 +4,32 @@
 // The math is the decode step of sunnynet/runtime/sunnynet.c:212-334, in the
 // same operation order as the per-kernel path (model.hip). A step is a chain
 // of small matrix-vector products, each too short to fill the chip as its own
-// launch; here the whole grid (one or two workgroups per CU) walks through the
-// step in phases separated by grid barriers:
+// launch; here the whole grid (one workgroup per CU) walks through the step in
+// phases separated by grid barriers:
 //
 //   A  LN_in(x), depthwise conv -> at;  v = V at,  sfb = W_eff s      (all WGs)
-//   B  q = U v for one group of 8 channels per WG (16 rows: 8 value, 8 gate),
+//   B  q = U v for one group of 8 channels per WG (16 contiguous rows of U:
+//      8 value, 8 gate),
 //      competitive + decay gate, s' = p s + (1 - p) u, conv history shift
 //   C  z = wedge(W_z u)
 //   D  y = LN_I(z);  x = W_c y + b s' + sfb + x
 //   H  logits = E LN_out(x), per-WG argmax key;  then every WG reduces the
 //      keys to the same greedy token, the next step's input.
 //
-// 4 L + 1 barriers per step. Before waiting at a barrier each wave issues the
-// weight loads of its first batch of rows of the next phase (they do not depend
-// on the activations), so weight streaming overlaps the barrier.
+// 4 L + 1 barriers per step. A barrier is split into arrive and wait; between
+// the two, the loads that do not depend on the phase that just ended are
+// issued: the dot waves load the weights of their first two batches of rows
+// of the next phase (and b s' + sfb + x for phase D), the staging wave the
+// inputs produced two or more phases earlier (the state s and conv-history
+// products for phase A, the old state and history for phase B) and the next
+// LayerNorm's gain and bias. After the wait only the previous phase's output
+// is fetched. Conv history: the phase-B owner of a channel also stores
+// hd[k] = hist'[k] * dw[K-2-k] for the next step, so phase A forms
+// acc = raw * dw[K-1] + hd[0] + hd[1] + ... in the reference's order
+// (sunnynet.c:227-233) with the products already rounded, bit-identical.
 //
-// Values exchanged between workgroups (x, v, sfb, u, z, s, the conv history,
-// the argmax keys) are written and read with agent-scope atomic accesses
+// Values exchanged between workgroups (x, v, sfb, u, z, s, hist, hd, the
+// argmax keys) are written and read with agent-scope atomic accesses
 // (global_load / global_store with sc1 on gfx950): the per-XCD L2 caches are
 // not coherent with each other, and plain loads would see stale lines. Each
 // wave drains its stores (s_waitcnt 0) before the workgroup arrives at a
@@ -38,11 +47,49 @@ namespace snhip {
 namespace {
 
 constexpr int NT = 256;                      // threads per workgroup (4 waves)
-constexpr int kMaxK = kPersistMaxDim;
-constexpr int PER = kMaxK / NT;              // values per thread in the LayerNorms
-constexpr int MR = 2;                        // fp32: rows per wave batch
-constexpr int NK = kMaxK / 256;              // fp32: float4 per lane per row
-constexpr int MU = 8;                        // INT4: units per wave batch
+constexpr int kMaxD = kPersistMaxD;          // dim
+constexpr int kMaxK = kPersistMaxK;          // inner, rank
+constexpr int PD = kMaxD / NT;               // values per thread of a dim-wide vector
+constexpr int PI = kMaxK / NT;               // of an inner- or rank-wide vector
+constexpr int PH = 8;                        // fp32: float4 per lane in one batch
+constexpr int MUH_MAX = 8;                   // INT4: units in one batch (32-wide groups;
+template <int BLK> constexpr int muh() { return BLK == 64 ? 4 : MUH_MAX; }   // half for 64)
+
+// Read-only data through global-address-space pointers: global_load (counted
+// by vmcnt only). Through a generic pointer the compiler emits flat loads,
+// which also count against lgkmcnt, so the first LDS wait after a prefetch
+// would stall until every prefetched weight had arrived.
+// (Native vector types: HIP's float4 / uint4 are classes whose copy goes
+// through a generic reference and would lose the address space.)
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const float g_f32;
+typedef __attribute__((address_space(1))) const f32x4v g_f32x4;
+typedef __attribute__((address_space(1))) const u32x4v g_u32x4;
+__device__ __forceinline__ float ldg(const float* p) { return *(g_f32*)p; }
+__device__ __forceinline__ float4 ldg4(const float* p) {
+    const f32x4v v = *(g_f32x4*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ldgq(const uint8_t* p) {
+    const u32x4v v = *(g_u32x4*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// The layer table never changes during a launch: read through the constant
+// address space it becomes scalar loads (counted by lgkmcnt), so fetching a
+// layer's pointers does not wait for the vector loads in flight.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __attribute__((address_space(4))) const PLayer c_layer;
+#else
+typedef const PLayer c_layer;   // host pass of the kernel source
+#endif
+// LDS activations are addressed the same way (ds_read, not flat).
+typedef __attribute__((address_space(3))) const float l_f32;
+typedef __attribute__((address_space(3))) const f32x4v l_f32x4;
+__device__ __forceinline__ float4 lds4(l_f32x4* p) {
+    const f32x4v v = *p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float ldc(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -53,15 +100,36 @@ __device__ __forceinline__ void stc(float* p, float v) {
 
 __device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-__device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// The same value, opaque to the optimizer. Applied to the thread index at
+// every phase boundary so per-lane addresses are formed inside each phase
+// instead of being hoisted out of the step loop (where hundreds of them
+// would stay live and spill).
+__device__ __forceinline__ int opq(int v) {
+    asm volatile("" : "+v"(v));
     return v;
 }
 
-__device__ __forceinline__ float ssum(float v, int seg) {
-    for (int o = seg >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Sum over the lane's 16-lane row, in every lane of the row: a rotation
+// butterfly with DPP row_ror 8, 4, 2, 1 (pairs are symmetric and the adds
+// commutative, so every lane ends with the same value).
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v += dppf<0x128>(v);   // row_ror:8
+    v += dppf<0x124>(v);   // row_ror:4
+    v += dppf<0x122>(v);   // row_ror:2
+    v += dppf<0x121>(v);   // row_ror:1
     return v;
+}
+__device__ __forceinline__ float lane_val(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Whole-wave sum (wave-uniform result).
+__device__ __forceinline__ float wsum(float v) {
+    v = row_sum(v);
+    return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
 }
 
 __device__ __forceinline__ unsigned long long kmax_wave(unsigned long long k) {
@@ -94,122 +162,253 @@ __device__ __forceinline__ float bsum(float v, float* red) {
 
 // Two-pass LayerNorm statistics (sunnynet.c:198-210 form) over n values,
 // element k * NT + tid held in xv[k].
-__device__ __forceinline__ void ln_stats(const float (&xv)[PER], int n, float eps, float* red,
+template <int N>
+__device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps, int tid, float* red,
                                          float& mean, float& rstd) {
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < PER; ++k)
-        if (k * NT + (int)threadIdx.x < n) sum += xv[k];
+    for (int k = 0; k < N; ++k)
+        if (k * NT + tid < n) sum += xv[k];
     mean = bsum(sum, red) / (float)n;
     float vs = 0.0f;
 #pragma unroll
-    for (int k = 0; k < PER; ++k)
-        if (k * NT + (int)threadIdx.x < n) {
+    for (int k = 0; k < N; ++k)
+        if (k * NT + tid < n) {
             const float d = xv[k] - mean;
             vs += d * d;
         }
     rstd = 1.0f / sqrtf(bsum(vs, red) / (float)n + eps);
 }
 
-// One phase's matrix-vector work: up to two matrices with the same
-// contraction length Kd, split in units (fp32: one row; INT4: rpp rows, one
-// per segment of seg lanes, each lane one group of BLK inputs). This wave
-// takes units u0, u0 + ustride, ...
+// Issue agent-scope loads of n values (element k * NT + tid in v[k]); the
+// caller consumes them later.
+template <int N>
+__device__ __forceinline__ void issue_ldc(float (&v)[N], const float* src, int n, int tid) {
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        if (k * NT < n) v[k] = ldc(src + min(k * NT + tid, n - 1));
+}
+template <int N>
+__device__ __forceinline__ void issue_ldg(float (&v)[N], const float* src, int n, int tid) {
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        if (k * NT < n) v[k] = ldg(src + min(k * NT + tid, n - 1));
+}
+
+// Keeps the scheduler from moving instructions across this point, so loads
+// stay in the issue order the kernel relies on (vmcnt drains in order).
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// One phase's matrix-vector work: rows of one matrix W with contraction
+// length Kd, split in units; rows below `split` multiply x0, the others x1.
+// fp32: a unit is one row; a lane holds float4 i of a row at k = i * 256 +
+// 4 * lane (nk4 of them, rounded up to a power of two), a batch holds
+// PH / nk4 rows. INT4: a unit is rpp rows, one per segment of seg lanes, each
+// lane one group of BLK inputs; a batch holds MUH units. This wave takes units
+// u0, u0 + ustride, ... in batches; two batches are in registers at a time.
 struct PhaseDesc {
-    PMat j0, j1;
-    int nu0, nu1;
-    int Kd, ng, seg, rpp;
-    const float* x0;        // LDS activation of job 0 (staged layout)
-    const float* x1;        // of job 1
+    PMat W;
+    int nu, split;
+    int Kd, nk4, lg4, ng, seg, rpp, rpb;
+    l_f32* x0;              // LDS activation of rows < split (staged layout)
+    l_f32* x1;              // of rows >= split
     int u0, ustride, nb;    // first unit, stride, batches
 };
 
-template <int BLK>
-struct Batch {
-    static constexpr int MB = BLK ? MU : MR;
-    static constexpr int QW = BLK ? BLK / 32 : 1;    // uint4 per INT4 group
-    float4 wf[BLK ? 1 : MR][NK];
-    uint4 wq[BLK ? MU : 1][QW];
-    float wsc[BLK ? MU : 1];
-    int job[MB], unit[MB];
+// A row's epilogue pre-loads (phase D: s', sfb, x).
+struct Pre3 {
+    float s, f, x;
+};
 
-    __device__ __forceinline__ void load(const PhaseDesc& P, int b, int lane) {
-        const int lrow = lane / P.seg, lg = lane - lrow * P.seg;
+// Epilogue inputs read with the weights (phase D): s', sfb and x per row.
+struct EpiPre {
+    const float* s;         // s' (new state) of the layer, or NULL: no pre-loads
+    const float* sfb;
+    const float* x;         // residual input
+};
+
+constexpr int EPS = 2;                       // slots per batch with epilogue pre-loads
+
+template <int BLK>
+struct Pool {
+    static constexpr int MUH = muh<BLK>();
+    static constexpr int QW = BLK ? BLK / 32 : 1;    // uint4 per INT4 group
+    static constexpr int MS = BLK ? MUH : PH;        // slots (rows / units) per batch
+    float4 wf[2][BLK ? 1 : PH];
+    uint4 wq[2][BLK ? MUH : 1][QW];
+    float wsc[2][BLK ? MUH : 1];
+    float ep[2][EPS][3];
+    bool ep_on[2];
+    int unit[2][MS];                                 // -1: empty slot
+
+    // Batch b of P into half h. Straight-line code with the same loads on
+    // every path (empty slots and lanes read element 0 of the matrix), so the
+    // compiler's wait counts for earlier loads stay exact. EP: also s', sfb,
+    // x of the batch's first EPS rows.
+    template <bool EP>
+    __device__ __forceinline__ void load(const PhaseDesc& P, int h, int b, int lane, const EpiPre& E) {
+        const bool bok = b < P.nb;
+        ep_on[h] = EP;
+        if constexpr (BLK == 0) {
+            const int sh = P.lg4;
 #pragma unroll
-        for (int s = 0; s < MB; ++s) {
-            const int u = P.u0 + (b * MB + s) * P.ustride;
-            int j = -1, ul = 0;
-            if (u < P.nu0) { j = 0; ul = u; }
-            else if (u < P.nu0 + P.nu1) { j = 1; ul = u - P.nu0; }
-            job[s] = j;
-            unit[s] = ul;
-            if (j < 0) continue;
-            if constexpr (BLK == 0) {
-                const float* row = (j ? P.j1.w : P.j0.w) + (size_t)ul * P.Kd;
+            for (int j = 0; j < PH; ++j) {
+                const int r = j >> sh, i = j & ((1 << sh) - 1);
+                const int u = P.u0 + (b * P.rpb + r) * P.ustride;
+                const bool ok = bok && r < P.rpb && u < P.nu;
+                const int k = i * 256 + lane * 4;
+                wf[h][j] = ldg4(P.W.w + ((ok && k < P.Kd) ? (size_t)u * P.Kd + k : 0));
+            }
 #pragma unroll
-                for (int i = 0; i < NK; ++i) {
-                    const int k = i * 256 + lane * 4;
-                    if (k < P.Kd) wf[s][i] = *reinterpret_cast<const float4*>(row + k);
+            for (int r = 0; r < PH; ++r) {
+                const int u = P.u0 + (b * P.rpb + r) * P.ustride;
+                unit[h][r] = (bok && r < P.rpb && u < P.nu) ? u : -1;
+            }
+            if constexpr (EP) {
+#pragma unroll
+                for (int r = 0; r < EPS; ++r) {
+                    const int u = unit[h][r] < 0 ? 0 : unit[h][r];
+                    ep[h][r][0] = ldc(E.s + u);
+                    ep[h][r][1] = ldc(E.sfb + u);
+                    ep[h][r][2] = ldc(E.x + u);
                 }
-            } else {
-                const int r = ul * P.rpp + lrow;
-                if (r < (j ? P.j1.M : P.j0.M) && lg < P.ng) {
-                    const uint8_t* qr = (j ? P.j1.q : P.j0.q) + (size_t)r * (P.Kd / 2) + lg * (BLK / 2);
+            }
+        } else {
+            const int lrow = lane / P.seg, lg = lane - lrow * P.seg;
 #pragma unroll
-                    for (int h = 0; h < QW; ++h) wq[s][h] = *reinterpret_cast<const uint4*>(qr + 16 * h);
-                    wsc[s] = (j ? P.j1.sc : P.j0.sc)[(size_t)r * P.ng + lg];
+            for (int s = 0; s < MUH; ++s) {
+                const int u = P.u0 + (b * MUH + s) * P.ustride;
+                const bool uok = bok && u < P.nu;
+                unit[h][s] = uok ? u : -1;
+                const int r = u * P.rpp + lrow;
+                const bool ok = uok && r < P.W.M && lg < P.ng;
+                const uint8_t* qr = P.W.q + (ok ? (size_t)r * (P.Kd / 2) + lg * (BLK / 2) : 0);
+#pragma unroll
+                for (int q = 0; q < QW; ++q) wq[h][s][q] = ldgq(qr + 16 * q);
+                wsc[h][s] = ldg(P.W.sc + (ok ? (size_t)r * P.ng + lg : 0));
+                if constexpr (EP) {
+                    if (s < EPS) {
+                        const int rr = (uok && r < P.W.M) ? r : 0;
+                        ep[h][s][0] = ldc(E.s + rr);
+                        ep[h][s][1] = ldc(E.sfb + rr);
+                        ep[h][s][2] = ldc(E.x + rr);
+                    }
                 }
             }
         }
     }
 
-    // epi(job, row, value, writer): the row's dot product; `writer` is true
-    // on exactly one lane per row.
-    template <class Epi>
-    __device__ __forceinline__ void compute(const PhaseDesc& P, int lane, Epi&& epi) {
-        const int lrow = lane / P.seg, lg = lane - lrow * P.seg;
+    // epi(row, value, writer, pre, has_pre): the row's dot product; `writer`
+    // is true on exactly one lane per row; pre = the row's epilogue pre-loads
+    // when has_pre.
+    template <int NK4, class Epi>
+    __device__ __forceinline__ void compute_f32(const PhaseDesc& P, int h, int lane, Epi&& epi) {
+        constexpr int RPB = PH / NK4;
+        float acc[RPB];
 #pragma unroll
-        for (int s = 0; s < MB; ++s) {
-            if (job[s] < 0) continue;
-            const float* xs = job[s] ? P.x1 : P.x0;
-            if constexpr (BLK == 0) {
-                float acc = 0.0f;
+        for (int r = 0; r < RPB; ++r) {
+            acc[r] = 0.0f;
+            if (unit[h][r] < 0) continue;
+            l_f32* xs = unit[h][r] < P.split ? P.x0 : P.x1;
 #pragma unroll
-                for (int i = 0; i < NK; ++i) {
-                    const int k = i * 256 + lane * 4;
-                    if (k < P.Kd) {
-                        const float4 x4 = *reinterpret_cast<const float4*>(xs + k);
-                        acc = fmaf(wf[s][i].x, x4.x, acc);
-                        acc = fmaf(wf[s][i].y, x4.y, acc);
-                        acc = fmaf(wf[s][i].z, x4.z, acc);
-                        acc = fmaf(wf[s][i].w, x4.w, acc);
-                    }
+            for (int i = 0; i < NK4; ++i) {
+                const int k = i * 256 + lane * 4;
+                if (k < P.Kd) {
+                    const float4 x4 = lds4((l_f32x4*)(xs + k));
+                    const float4 w4 = wf[h][r * NK4 + i];
+                    acc[r] = fmaf(w4.x, x4.x, acc[r]);
+                    acc[r] = fmaf(w4.y, x4.y, acc[r]);
+                    acc[r] = fmaf(w4.z, x4.z, acc[r]);
+                    acc[r] = fmaf(w4.w, x4.w, acc[r]);
                 }
-                acc = wsum(acc);
-                epi(job[s], unit[s], acc, lane == 0);
-            } else {
-                const int M = job[s] ? P.j1.M : P.j0.M;
-                const int r = unit[s] * P.rpp + lrow;
-                const bool live = r < M && lg < P.ng;
-                float acc = 0.0f;
-                if (live) {
-                    const float sc = wsc[s];
-#pragma unroll
-                    for (int j = 0; j < BLK / 2; ++j) {
-                        const uint4& qq = wq[s][j >> 4];
-                        const int wi = (j >> 2) & 3;
-                        const uint32_t word = wi == 0 ? qq.x : wi == 1 ? qq.y : wi == 2 ? qq.z : qq.w;
-                        const uint32_t byte = (word >> ((j & 3) * 8)) & 0xFFu;
-                        // quant.c:82-83, bit-identical dequantization
-                        const float wl = (float)((int)(byte & 0x0Fu) - 8) * sc;
-                        const float wh = (float)((int)(byte >> 4) - 8) * sc;
-                        acc = fmaf(wl, xs[j * P.ng + lg], acc);
-                        acc = fmaf(wh, xs[(j + BLK / 2) * P.ng + lg], acc);
-                    }
-                }
-                acc = ssum(acc, P.seg);
-                epi(job[s], r, acc, live && lg == 0);
             }
+        }
+#pragma unroll
+        for (int r = 0; r < RPB; ++r) acc[r] = row_sum(acc[r]);
+#pragma unroll
+        for (int r = 0; r < RPB; ++r)
+            acc[r] = (lane_val(acc[r], 0) + lane_val(acc[r], 16)) + (lane_val(acc[r], 32) + lane_val(acc[r], 48));
+#pragma unroll
+        for (int r = 0; r < RPB; ++r)
+            if (unit[h][r] >= 0) {
+                const bool hp = ep_on[h] && r < EPS;
+                const int re = r < EPS ? r : 0;
+                epi(unit[h][r], acc[r], lane == 0, Pre3{ep[h][re][0], ep[h][re][1], ep[h][re][2]}, hp);
+            }
+    }
+
+    template <class Epi>
+    __device__ __forceinline__ void compute_i4(const PhaseDesc& P, int h, int lane, Epi&& epi) {
+        const int lrow = lane / P.seg, lg = lane - lrow * P.seg;
+        constexpr int NW = BLK / 8;                  // 32-bit words of codes per group
+        float acc[MUH];
+#pragma unroll
+        for (int s = 0; s < MUH; ++s) {
+            acc[s] = 0.0f;
+            const int r = unit[h][s] * P.rpp + lrow;
+            if (unit[h][s] < 0 || r >= P.W.M || lg >= P.ng) continue;
+            l_f32x4* x4 = (l_f32x4*)(r < P.split ? P.x0 : P.x1);
+            const float sc = wsc[h][s];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const uint4& qq = wq[h][s][w >> 2];
+                const int wi = w & 3;
+                const uint32_t word = wi == 0 ? qq.x : wi == 1 ? qq.y : wi == 2 ? qq.z : qq.w;
+                // Byte 4w + e holds element 4w + e (low nibble) and
+                // 4w + e + BLK/2 (high nibble); quant.c:82-83 dequantization.
+                const float4 xl = lds4(x4 + w * P.ng + lg);
+                const float4 xh = lds4(x4 + (w + NW) * P.ng + lg);
+                const float xlo[4] = {xl.x, xl.y, xl.z, xl.w};
+                const float xhi[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t byte = (word >> (8 * e)) & 0xFFu;
+                    const float wl = (float)((int)(byte & 0x0Fu) - 8) * sc;
+                    const float wh = (float)((int)(byte >> 4) - 8) * sc;
+                    acc[s] = fmaf(wl, xlo[e], acc[s]);
+                    acc[s] = fmaf(wh, xhi[e], acc[s]);
+                }
+            }
+        }
+        if (P.seg >= 16) {
+            // rows of 16 lanes by DPP, then the rows of each segment
+#pragma unroll
+            for (int s = 0; s < MUH; ++s) acc[s] = row_sum(acc[s]);
+#pragma unroll
+            for (int s = 0; s < MUH; ++s) {
+                const float r0 = lane_val(acc[s], 0), r1 = lane_val(acc[s], 16);
+                const float r2 = lane_val(acc[s], 32), r3 = lane_val(acc[s], 48);
+                acc[s] = P.seg == 64 ? (r0 + r1) + (r2 + r3)
+                       : P.seg == 32 ? (lane < 32 ? r0 + r1 : r2 + r3)
+                                     : acc[s];
+            }
+        } else {
+            for (int o = P.seg >> 1; o > 0; o >>= 1)
+#pragma unroll
+                for (int s = 0; s < MUH; ++s) acc[s] += __shfl_xor(acc[s], o, 64);
+        }
+#pragma unroll
+        for (int s = 0; s < MUH; ++s) {
+            if (unit[h][s] < 0) continue;
+            const int r = unit[h][s] * P.rpp + lrow;
+            const bool hp = ep_on[h] && s < EPS;
+            const int se = s < EPS ? s : 0;
+            epi(r, acc[s], r < P.W.M && lg < P.ng && lg == 0,
+                Pre3{ep[h][se][0], ep[h][se][1], ep[h][se][2]}, hp);
+        }
+    }
+
+    template <class Epi>
+    __device__ __forceinline__ void compute(const PhaseDesc& P, int h, int lane, Epi&& epi) {
+        if constexpr (BLK == 0) {
+            switch (P.nk4) {
+                case 1: compute_f32<1>(P, h, lane, epi); break;
+                case 2: compute_f32<2>(P, h, lane, epi); break;
+                case 4: compute_f32<4>(P, h, lane, epi); break;
+                default: compute_f32<8>(P, h, lane, epi); break;
+            }
+        } else {
+            compute_i4(P, h, lane, epi);
         }
     }
 };
@@ -258,22 +457,40 @@ __device__ __forceinline__ bool bar_wait(GridBar& g, int* flag) {
     return *flag != 0;
 }
 
-template <int BLK>
+// Order of loads. vmcnt drains in issue order per wave, so a value can only
+// be consumed once everything issued before it has arrived, and the compiler
+// computes exact waits only across straight-line code that issues the same
+// loads on every path. Each phase therefore issues, in this order and without
+// branches: its own inputs (the previous phase's output, LayerNorm
+// parameters), then the next phase's inputs produced earlier (state, history
+// products), then the next phase's weights into the register half the current
+// phase does not use. Phases alternate halves: A and C use half 0, B and D
+// half 1; the LM head streams through both. A phase's weights are issued a
+// full phase ahead and are in registers when it starts (arriving at a barrier
+// drains every outstanding access: gfx9 counts stores and loads together).
+// KHT: conv-history entries (taps - 1), a compile-time count so the history
+// loads are straight-line too.
+template <int BLK, int KHT>
 __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
-    __shared__ __align__(16) float xs[kMaxK];
-    __shared__ __align__(16) float xs2[kMaxK];
-    __shared__ float raw[kMaxK];
+    __shared__ __align__(16) float xs[kMaxK];     // activation of the current products
+    __shared__ __align__(16) float xs2[kMaxD];    // old state s (phase A, W_eff's rows)
+    __shared__ float raw[kMaxD];                  // LN_in(x) of the layer: history input
+    __shared__ float hdl[KHT * kMaxD];            // conv-history products of the layer
     __shared__ float q16[16];
     __shared__ float red[4];
     __shared__ unsigned long long kred[4];
     __shared__ int flag;
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    auto fresh = [&]() {
+        tid = opq(tid);
+        lane = tid & 63;
+    };
     const int nwg = gridDim.x, wg = blockIdx.x;
     const int NW = nwg * 4, gw = wg * 4 + wv;
-    const int D = a.D, I = a.I, R = a.R, K = a.K, kh = a.kh;
-    constexpr int MB = Batch<BLK>::MB;
+    const int D = a.D, I = a.I, R = a.R, K = KHT + 1, L = a.L;
+    constexpr int kh = KHT;
 
     GridBar bar;
     {
@@ -290,229 +507,332 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
 
     auto sidx = [&](int i, int Kd) -> int {
         if constexpr (BLK == 0) return i;
-        else return (i % BLK) * (Kd / BLK) + i / BLK;
+        else return ((((i % BLK) >> 2) * (Kd / BLK) + i / BLK) << 2) + (i & 3);
     };
     auto geom = [&](PhaseDesc& P, int Kd) {
         P.Kd = Kd;
         if constexpr (BLK == 0) {
+            const int n = (Kd + 255) / 256;
+            P.lg4 = n <= 1 ? 0 : n <= 2 ? 1 : n <= 4 ? 2 : 3;
+            P.nk4 = 1 << P.lg4;
             P.ng = 0; P.seg = 64; P.rpp = 1;
+            P.rpb = PH / P.nk4;
         } else {
+            P.nk4 = 0; P.lg4 = 0;
             P.ng = Kd / BLK;
             P.seg = (P.ng < 64 && 64 % P.ng == 0) ? P.ng : 64;
             P.rpp = 64 / P.seg;
+            P.rpb = muh<BLK>();
         }
     };
     auto finish = [&](PhaseDesc& P, int u0, int stride) {
         P.u0 = u0;
         P.ustride = stride;
-        const int total = P.nu0 + P.nu1;
-        const int cnt = u0 < total ? (total - u0 + stride - 1) / stride : 0;
-        P.nb = (cnt + MB - 1) / MB;
+        const int cnt = u0 < P.nu ? (P.nu - u0 + stride - 1) / stride : 0;
+        P.nb = (cnt + P.rpb - 1) / P.rpb;
     };
-    auto one = [&](const PMat& W, int Kd, const float* x) {
+    auto desc = [&](const PMat& W, int Kd, const float* x0, const float* x1, int split) {
+        // x0 / x1 are this workgroup's LDS arrays
         PhaseDesc P;
         geom(P, Kd);
-        P.j0 = W; P.j1 = W;
-        P.nu0 = (W.M + P.rpp - 1) / P.rpp; P.nu1 = 0;
-        P.x0 = x; P.x1 = x;
+        P.W = W;
+        P.nu = (W.M + P.rpp - 1) / P.rpp;
+        P.split = split;
+        P.x0 = (l_f32*)x0; P.x1 = (l_f32*)x1;
         finish(P, gw, NW);
         return P;
     };
-    auto descA = [&](int l) {
-        const PLayer& Ly = a.layers[l];
-        PhaseDesc P;
-        geom(P, D);
-        P.j0 = Ly.V; P.j1 = Ly.Ws;
-        P.nu0 = (Ly.V.M + P.rpp - 1) / P.rpp;
-        P.nu1 = (Ly.Ws.M + P.rpp - 1) / P.rpp;
-        P.x0 = xs; P.x1 = xs2;
-        finish(P, gw, NW);
-        return P;
-    };
-    // Group c: rows 8c.. (values) and D + 8c.. (gates) of U, split over the
-    // workgroup's four waves.
+    // V's rows multiply at, W_eff's rows (from row R on) the old state.
+    auto layer = [&](int l) -> PLayer { return ((c_layer*)a.layers)[l]; };
+    auto descA = [&](int l) { return desc(layer(l).VW, D, xs, xs2, R); };
+    const int ngroups = D / 8;
+    // Group c: the 16 contiguous rows 16c.. of U (8 values, 8 gates), split
+    // over the workgroup's four waves. (A workgroup without a group loads
+    // the last group's rows and leaves them unused.)
     auto descB = [&](int l, int c) {
-        const PMat& U = a.layers[l].U;
+        const PMat U = layer(l).U;
         PhaseDesc P;
         geom(P, R);
-        const size_t r0 = (size_t)8 * c, r1 = (size_t)D + 8 * c;
-        if constexpr (BLK == 0) {
-            P.j0 = PMat{U.w + r0 * R, nullptr, nullptr, 8};
-            P.j1 = PMat{U.w + r1 * R, nullptr, nullptr, 8};
-        } else {
-            P.j0 = PMat{nullptr, U.q + r0 * (R / 2), U.sc + r0 * P.ng, 8};
-            P.j1 = PMat{nullptr, U.q + r1 * (R / 2), U.sc + r1 * P.ng, 8};
-        }
-        P.nu0 = P.nu1 = (8 + P.rpp - 1) / P.rpp;
-        P.x0 = xs; P.x1 = xs;
+        const size_t r0 = (size_t)16 * min(c, ngroups - 1);
+        if constexpr (BLK == 0) P.W = PMat{U.w + r0 * R, nullptr, nullptr, 16};
+        else P.W = PMat{nullptr, U.q + r0 * (R / 2), U.sc + r0 * P.ng, 16};
+        P.nu = (16 + P.rpp - 1) / P.rpp;
+        P.split = 16;
+        P.x0 = (l_f32*)xs; P.x1 = (l_f32*)xs;
         finish(P, wv, 4);
         return P;
     };
-    auto descC = [&](int l) { return one(a.layers[l].Wz, D, xs); };
-    auto descD = [&](int l) { return one(a.layers[l].Wc, I, xs); };
-    auto descH = [&]() { return one(a.head, D, xs); };
+    auto descC = [&](int l) {
+        const PMat W = layer(l).Wz;
+        return desc(W, D, xs, xs, W.M);
+    };
+    auto descD = [&](int l) {
+        const PMat W = layer(l).Wc;
+        return desc(W, I, xs, xs, W.M);
+    };
+    auto descH = [&]() { return desc(a.head, D, xs, xs, a.head.M); };
+    const EpiPre none{nullptr, nullptr, nullptr};
 
-    Batch<BLK> bt;
-    auto run = [&](const PhaseDesc& P, auto&& epi) {
+    Pool<BLK> pool;
+    // All batches of a phase from one half (batch 0 loaded a phase earlier).
+    auto run0 = [&](const PhaseDesc& P, const EpiPre& E, auto&& epi) {
         for (int b = 0; b < P.nb; ++b) {
-            if (b > 0) bt.load(P, b, lane);   // batch 0 was loaded before the barrier
-            bt.compute(P, lane, epi);
+            if (b > 0) pool.template load<false>(P, 0, b, lane, E);
+            pool.compute(P, 0, lane, epi);
+        }
+    };
+    auto run1 = [&](const PhaseDesc& P, const EpiPre& E, auto&& epi) {
+        for (int b = 0; b < P.nb; ++b) {
+            if (b > 0) pool.template load<false>(P, 1, b, lane, E);
+            pool.compute(P, 1, lane, epi);
+        }
+    };
+    // Double-buffered through both halves (batches 0 and 1 loaded before).
+    auto run_stream = [&](const PhaseDesc& P, const EpiPre& E, auto&& epi) {
+        for (int b = 0; b < P.nb; b += 2) {
+            pool.compute(P, 0, lane, epi);
+            pool.template load<false>(P, 0, b + 2, lane, E);
+            if (b + 1 < P.nb) {
+                pool.compute(P, 1, lane, epi);
+                pool.template load<false>(P, 1, b + 3, lane, E);
+            }
         }
     };
 
-    const int ngroups = D / 8;
+    // Phase A inputs produced earlier: s -> xs2, conv-history products -> hdl.
+    float sv[PD], hv[PD][KHT > 0 ? KHT : 1];
+    auto prestage_issue = [&](int l) {
+        const float* s_l = a.s + (size_t)l * D;
+        const float* hd_l = a.hd + (size_t)l * (kh ? kh : 1) * D;
+#pragma unroll
+        for (int k = 0; k < PD; ++k) {
+            const int i = min(k * NT + tid, D - 1);
+            sv[k] = ldc(s_l + i);
+#pragma unroll
+            for (int t = 0; t < KHT; ++t) hv[k][t] = ldc(hd_l + (size_t)t * D + i);
+        }
+    };
+    auto prestage_store = [&]() {
+#pragma unroll
+        for (int k = 0; k < PD; ++k) {
+            const int i = k * NT + tid;
+            if (i >= D) continue;
+            xs2[sidx(i, D)] = sv[k];
+#pragma unroll
+            for (int t = 0; t < KHT; ++t) hdl[t * D + i] = hv[k][t];
+        }
+    };
+    // Phase B inputs for channel group c: old s and history of channel
+    // 8 c + (tid & 7) (used by tid < 8).
+    float pb_s = 0.0f, pb_h[KHT > 1 ? KHT - 1 : 1];
+    auto preload_B = [&](int l, int c) {
+        const int i = min(c, ngroups - 1) * 8 + (tid & 7);
+        pb_s = ldc(a.s + (size_t)l * D + i);
+        const float* h_l = a.hist + (size_t)l * (kh ? kh : 1) * D;
+#pragma unroll
+        for (int t = 0; t + 1 < KHT; ++t) pb_h[t] = ldc(h_l + (size_t)t * D + i);
+    };
+
+    // ---- phases (A of layer 0 differs: it also issues its own weights)
+    auto phaseA = [&](int l, bool tok_ok, const float* erow) {
+        const PLayer Ly = layer(l);
+        float xv[PD], gv[PD], cv[PD], dv[PD];
+        if (l == 0) issue_ldg(xv, erow, D, tid);
+        else issue_ldc(xv, a.x, D, tid);
+        issue_ldg(gv, Ly.ni_g, D, tid);
+        issue_ldg(cv, Ly.ni_c, D, tid);
+        issue_ldg(dv, Ly.dw + (size_t)(K - 1) * D, D, tid);
+        issue_fence();
+        if (l == 0) {
+            prestage_issue(0);
+            issue_fence();
+            pool.template load<false>(descA(0), 0, 0, lane, none);
+            issue_fence();
+        }
+        preload_B(l, wg);
+        issue_fence();
+        pool.template load<false>(descB(l, wg), 1, 0, lane, none);
+        issue_fence();
+        if (l == 0) prestage_store();
+#pragma unroll
+        for (int k = 0; k < PD; ++k)
+            if (k * NT + tid >= D) xv[k] = 0.0f;
+            else if (l == 0 && !tok_ok) xv[k] = __builtin_nanf("");
+        float mean, rstd;
+        ln_stats(xv, D, a.eps, tid, red, mean, rstd);
+#pragma unroll
+        for (int k = 0; k < PD; ++k) {
+            const int i = k * NT + tid;
+            if (i >= D) continue;
+            const float r = (xv[k] - mean) * rstd * gv[k] + cv[k];
+            raw[i] = r;
+            float acc = r * dv[k];
+#pragma unroll
+            for (int t = 0; t < KHT; ++t) acc = acc + hdl[t * D + i];
+            xs[sidx(i, D)] = KHT > 0 ? r + acc : r;
+        }
+        __syncthreads();
+        run0(descA(l), none, [&](int r, float v, bool w, Pre3, bool) {
+            if (w) stc(r < R ? a.v + r : a.sfb + (r - R), v);
+        });
+    };
+    auto phaseB = [&](int l) {
+        const PLayer Ly = layer(l);
+        float* s_l = a.s + (size_t)l * D;
+        float* h_l = a.hist + (size_t)l * (kh ? kh : 1) * D;
+        float* hd_l = a.hd + (size_t)l * (kh ? kh : 1) * D;
+        float vv[PI];
+        issue_ldc(vv, a.v, R, tid);
+        issue_fence();
+        pool.template load<false>(descC(l), 0, 0, lane, none);
+        issue_fence();
+#pragma unroll
+        for (int k = 0; k < PI; ++k)
+            if (k * NT + tid < R) xs[sidx(k * NT + tid, R)] = vv[k];
+        __syncthreads();
+        for (int c = wg; c < ngroups; c += nwg) {
+            const PhaseDesc P = descB(l, c);
+            if (c != wg) {
+                preload_B(l, c);
+                pool.template load<false>(P, 1, 0, lane, none);
+            }
+            run1(P, none, [&](int r, float v, bool w, Pre3, bool) {
+                if (w) q16[r] = v;
+            });
+            __syncthreads();
+            if (tid < 8) {
+                const int i = c * 8 + tid;
+                const float gi = q16[8 + tid];
+                const float uu = q16[tid] * (sgm(gi - q16[8 + ((tid + 1) & 7)]) *
+                                             sgm(gi - q16[8 + ((tid + 2) & 7)]));
+                float p = 1.0f - ldg(Ly.delta + i) * (1.0f - sgm(gi));
+                if (a.clamp && p < a.p_floor) p = a.p_floor;
+                stc(s_l + i, p * pb_s + (1.0f - p) * uu);
+                stc(a.u + i, uu);
+                if (KHT > 0) {
+                    // hist' = [raw, hist[0], ..., hist[kh-2]]; hd' = hist' * dw
+                    const float r = raw[i];
+                    stc(h_l + i, r);
+                    stc(hd_l + i, r * ldg(Ly.dw + (size_t)(K - 2) * D + i));
+#pragma unroll
+                    for (int t = 1; t < KHT; ++t) {
+                        stc(h_l + (size_t)t * D + i, pb_h[t - 1]);
+                        stc(hd_l + (size_t)t * D + i, pb_h[t - 1] * ldg(Ly.dw + (size_t)(K - 2 - t) * D + i));
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    };
+    auto phaseC = [&](int l, const EpiPre& preD) {
+        const PLayer Ly = layer(l);
+        float uv[PD];
+        issue_ldc(uv, a.u, D, tid);
+        issue_fence();
+        pool.template load<true>(descD(l), 1, 0, lane, preD);
+        issue_fence();
+#pragma unroll
+        for (int k = 0; k < PD; ++k)
+            if (k * NT + tid < D) xs[sidx(k * NT + tid, D)] = uv[k];
+        __syncthreads();
+        const float at = Ly.a_tanh;
+        run0(descC(l), none, [&](int r, float v, bool w, Pre3, bool) {
+            if (w) stc(a.z + r, v * (1.0f + 0.5f * at / (1.0f + fabsf(v))));
+        });
+    };
+    auto phaseD = [&](int l, bool bad_tok, const EpiPre& preD) {
+        const PLayer Ly = layer(l);
+        float zv[PI], gv[PI], cv[PI];
+        issue_ldc(zv, a.z, I, tid);
+        issue_ldg(gv, Ly.nm_g, I, tid);
+        issue_ldg(cv, Ly.nm_c, I, tid);
+        issue_fence();
+        const bool more = l + 1 < L;
+        prestage_issue(more ? l + 1 : l);
+        issue_fence();
+        pool.template load<false>(more ? descA(l + 1) : descH(), 0, 0, lane, none);
+        issue_fence();
+#pragma unroll
+        for (int k = 0; k < PI; ++k)
+            if (k * NT + tid >= I) zv[k] = 0.0f;
+        float mean, rstd;
+        ln_stats(zv, I, a.eps, tid, red, mean, rstd);
+#pragma unroll
+        for (int k = 0; k < PI; ++k) {
+            const int i = k * NT + tid;
+            if (i < I) xs[sidx(i, I)] = (zv[k] - mean) * rstd * gv[k] + cv[k];
+        }
+        __syncthreads();
+        const float bg = Ly.b_gain;
+        run1(descD(l), preD, [&](int r, float v, bool w, Pre3 pre, bool hp) {
+            if (w) {
+                if (!hp) pre = Pre3{ldc(preD.s + r), ldc(preD.sfb + r), ldc(preD.x + r)};
+                const float xr = bad_tok ? __builtin_nanf("") : pre.x;
+                stc(a.x + r, v + (bg * pre.s + pre.f + xr));
+            }
+        });
+        if (more) prestage_store();
+        else pool.template load<false>(descH(), 1, 1, lane, none);
+    };
+    auto barrier = [&]() -> bool {
+        bar_arrive(bar);
+        fresh();
+        const bool ok = bar_wait(bar, &flag);
+        fresh();
+        return ok;
+    };
+
+    // Conv-history products of the stored history, for the first step: each
+    // channel group's owner (the phase-B assignment) writes its channels.
+    if (KHT > 0)
+        for (int c = wg; c < ngroups; c += nwg)
+            for (int idx = tid; idx < L * kh * 8; idx += NT) {
+                const int l = idx / (kh * 8), t = (idx / 8) % kh, i = c * 8 + (idx & 7);
+                const size_t off = ((size_t)l * kh + t) * D + i;
+                stc(a.hd + off, ldc(a.hist + off) * ldg(layer(l).dw + (size_t)(K - 2 - t) * D + i));
+            }
+    if (!barrier()) return;
+
     int tok = a.tok_in[0];
-    bt.load(descA(0), 0, lane);
     for (int step = 0; step < a.n_steps; ++step) {
         const bool last = step + 1 == a.n_steps;
         const bool tok_ok = tok >= 0 && tok < a.vocab;
         const float* erow = a.embed + (size_t)(tok_ok ? tok : 0) * D;
-        for (int l = 0; l < a.L; ++l) {
-            const PLayer& Ly = a.layers[l];
-            float* s_l = a.s + (size_t)l * D;
-            float* h_l = a.hist + (size_t)l * (kh ? kh : 1) * D;
-
-            // ---- A: raw = LN_in(x), at = raw + conv(raw, hist) (sunnynet.c:221-237);
-            //         v = V at, sfb = W_eff s (old state)
-            {
-                float xv[PER];
-#pragma unroll
-                for (int k = 0; k < PER; ++k) {
-                    const int i = k * NT + tid;
-                    float v = 0.0f;
-                    if (i < D) v = l == 0 ? (tok_ok ? erow[i] : __builtin_nanf("")) : ldc(a.x + i);
-                    xv[k] = v;
-                }
-                float mean, rstd;
-                ln_stats(xv, D, a.eps, red, mean, rstd);
-#pragma unroll
-                for (int k = 0; k < PER; ++k) {
-                    const int i = k * NT + tid;
-                    if (i >= D) continue;
-                    const float r = (xv[k] - mean) * rstd * Ly.ni_g[i] + Ly.ni_c[i];
-                    raw[i] = r;
-                    float at = r;
-                    if (K > 1) {
-                        float acc = r * Ly.dw[(size_t)(K - 1) * D + i];
-#pragma unroll
-                        for (int k2 = 0; k2 < kPersistMaxTaps - 1; ++k2)
-                            if (k2 < kh) acc = acc + ldc(h_l + (size_t)k2 * D + i) * Ly.dw[(size_t)(K - 2 - k2) * D + i];
-                        at = r + acc;
-                    }
-                    const int si = sidx(i, D);
-                    xs[si] = at;
-                    xs2[si] = ldc(s_l + i);
-                }
-                __syncthreads();
-                run(descA(l), [&](int j, int r, float v, bool w) {
-                    if (w) stc((j ? a.sfb : a.v) + r, v);
-                });
-            }
-            bar_arrive(bar);
-            if (wg < ngroups) bt.load(descB(l, wg), 0, lane);
-            if (!bar_wait(bar, &flag)) return;
-
-            // ---- B: q = U v for this workgroup's channel groups; gates, state
-            //         update and conv history shift (sunnynet.c:238-266)
-            if (wg < ngroups) {
-                for (int i = tid; i < R; i += NT) xs[sidx(i, R)] = ldc(a.v + i);
-                __syncthreads();
-                for (int c = wg; c < ngroups; c += nwg) {
-                    const PhaseDesc P = descB(l, c);
-                    for (int b = 0; b < P.nb; ++b) {
-                        if (b > 0 || c != wg) bt.load(P, b, lane);
-                        bt.compute(P, lane, [&](int j, int r, float v, bool w) {
-                            if (w) q16[j * 8 + r] = v;
-                        });
-                    }
-                    __syncthreads();
-                    if (tid < 8) {
-                        const int i = c * 8 + tid;
-                        const float gi = q16[8 + tid];
-                        const float uu = q16[tid] * (sgm(gi - q16[8 + ((tid + 1) & 7)]) *
-                                                     sgm(gi - q16[8 + ((tid + 2) & 7)]));
-                        float p = 1.0f - Ly.delta[i] * (1.0f - sgm(gi));
-                        if (a.clamp && p < a.p_floor) p = a.p_floor;
-                        const float so = ldc(s_l + i);
-                        stc(s_l + i, p * so + (1.0f - p) * uu);
-                        stc(a.u + i, uu);
-                        if (kh) {
-                            float h[kPersistMaxTaps - 1];
-#pragma unroll
-                            for (int k2 = 0; k2 < kPersistMaxTaps - 1; ++k2)
-                                h[k2] = k2 + 1 < kh ? ldc(h_l + (size_t)k2 * D + i) : 0.0f;
-#pragma unroll
-                            for (int k2 = kPersistMaxTaps - 2; k2 >= 1; --k2)
-                                if (k2 < kh) stc(h_l + (size_t)k2 * D + i, h[k2 - 1]);
-                            stc(h_l + i, raw[i]);
-                        }
-                    }
-                    __syncthreads();
-                }
-            }
-            bar_arrive(bar);
-            bt.load(descC(l), 0, lane);
-            if (!bar_wait(bar, &flag)) return;
-
-            // ---- C: z = wedge(W_z u) (sunnynet.c:268-271)
-            for (int i = tid; i < D; i += NT) xs[sidx(i, D)] = ldc(a.u + i);
-            __syncthreads();
-            run(descC(l), [&](int, int r, float v, bool w) {
-                if (w) stc(a.z + r, v * (1.0f + 0.5f * Ly.a_tanh / (1.0f + fabsf(v))));
-            });
-            bar_arrive(bar);
-            bt.load(descD(l), 0, lane);
-            if (!bar_wait(bar, &flag)) return;
-
-            // ---- D: y = LN_I(z); x = W_c y + b s' + sfb + x (sunnynet.c:272-277)
-            {
-                float zv[PER];
-#pragma unroll
-                for (int k = 0; k < PER; ++k) {
-                    const int i = k * NT + tid;
-                    zv[k] = i < I ? ldc(a.z + i) : 0.0f;
-                }
-                float mean, rstd;
-                ln_stats(zv, I, a.eps, red, mean, rstd);
-#pragma unroll
-                for (int k = 0; k < PER; ++k) {
-                    const int i = k * NT + tid;
-                    if (i < I) xs[sidx(i, I)] = (zv[k] - mean) * rstd * Ly.nm_g[i] + Ly.nm_c[i];
-                }
-                __syncthreads();
-                run(descD(l), [&](int, int r, float v, bool w) {
-                    if (w) {
-                        const float xr = l == 0 ? (tok_ok ? erow[r] : __builtin_nanf("")) : ldc(a.x + r);
-                        stc(a.x + r, v + (Ly.b_gain * ldc(s_l + r) + ldc(a.sfb + r) + xr));
-                    }
-                });
-            }
-            bar_arrive(bar);
-            if (l + 1 < a.L) bt.load(descA(l + 1), 0, lane);
-            else bt.load(descH(), 0, lane);
-            if (!bar_wait(bar, &flag)) return;
+        // Layer 0 (peeled: its phase A issues its own weights), then the rest.
+        for (int l = 0; l < L; ++l) {
+            const EpiPre preD{a.s + (size_t)l * D, a.sfb, l == 0 ? erow : a.x};
+            if (l == 0) phaseA(0, tok_ok, erow);
+            else phaseA(l, true, erow);
+            if (!barrier()) return;
+            phaseB(l);
+            if (!barrier()) return;
+            phaseC(l, preD);
+            if (!barrier()) return;
+            phaseD(l, l == 0 && !tok_ok, preD);
+            if (!barrier()) return;
         }
 
         // ---- H: logits = E LN_out(x) (sunnynet.c:280-333), argmax key per workgroup
         {
-            float xv[PER];
+            float xv[PD], gv[PD], cv[PD];
+            issue_ldc(xv, a.x, D, tid);
+            issue_ldg(gv, a.no_g, D, tid);
+            issue_ldg(cv, a.no_c, D, tid);
 #pragma unroll
-            for (int k = 0; k < PER; ++k) {
-                const int i = k * NT + tid;
-                xv[k] = i < D ? ldc(a.x + i) : 0.0f;
-            }
+            for (int k = 0; k < PD; ++k)
+                if (k * NT + tid >= D) xv[k] = 0.0f;
             float mean, rstd;
-            ln_stats(xv, D, a.eps, red, mean, rstd);
+            ln_stats(xv, D, a.eps, tid, red, mean, rstd);
 #pragma unroll
-            for (int k = 0; k < PER; ++k) {
+            for (int k = 0; k < PD; ++k) {
                 const int i = k * NT + tid;
-                if (i < D) xs[sidx(i, D)] = (xv[k] - mean) * rstd * a.no_g[i] + a.no_c[i];
+                if (i < D) xs[sidx(i, D)] = (xv[k] - mean) * rstd * gv[k] + cv[k];
             }
             __syncthreads();
             unsigned long long best = 0ull;
             float* lg = last ? a.logits : nullptr;
             const bool greedy = a.greedy != 0;
-            run(descH(), [&](int, int r, float v, bool w) {
+            run_stream(descH(), none, [&](int r, float v, bool w, Pre3, bool) {
                 if (w) {
                     if (lg) lg[r] = v;
                     if (greedy) best = max(best, argmax_key(v, r));
@@ -528,47 +848,49 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
             }
         }
         if (!a.greedy) break;
-        bar_arrive(bar);
-        if (!last) bt.load(descA(0), 0, lane);
-        if (!bar_wait(bar, &flag)) return;
+        if (!barrier()) return;
         // Every workgroup reduces the same keys to the same token.
         {
             unsigned long long k = 0ull;
-            for (int i = tid; i < nwg; i += NT)
-                k = max(k, __hip_atomic_load(a.part + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+            for (int j = 0; j < kPersistMaxGrid / NT; ++j)
+                k = max(k, __hip_atomic_load(a.part + min(j * NT + tid, nwg - 1), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
             k = kmax_wave(k);
             if (lane == 0) kred[wv] = k;
             __syncthreads();
             k = max(max(kred[0], kred[1]), max(kred[2], kred[3]));
             tok = (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
             if (wg == 0 && tid == 0) a.out_tok[step] = tok;
+            __syncthreads();
         }
     }
+}
+
+const void* kernel_for(int blk) {
+    return blk == 0 ? (const void*)k_decode_persist<0, kPersistTaps - 1>
+         : blk == 32 ? (const void*)k_decode_persist<32, kPersistTaps - 1>
+                     : (const void*)k_decode_persist<64, kPersistTaps - 1>;
 }
 
 }  // namespace
 
 int persist_occupancy(int blk) {
     int nb = 0;
-    hipError_t e;
-    if (blk == 0) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_decode_persist<0>, NT, 0);
-    else if (blk == 32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_decode_persist<32>, NT, 0);
-    else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_decode_persist<64>, NT, 0);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel_for(blk), NT, 0);
     return e == hipSuccess ? nb : 0;
 }
 
 snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipStream_t st) {
-    if (a.D > kMaxK || a.I > kMaxK || a.R > kMaxK || a.K > kPersistMaxTaps || a.D % 8 || nwg < 1 ||
-        a.n_steps < 1 || (a.greedy && !a.out_tok) || (!a.greedy && a.n_steps != 1)) {
+    if (a.D > kMaxD || a.I > kMaxK || a.R > kMaxK || a.K != kPersistTaps || a.D % 8 || nwg < 1 ||
+        nwg > kPersistMaxGrid || a.n_steps < 1 || (a.greedy && !a.out_tok) ||
+        (!a.greedy && a.n_steps != 1)) {
         set_last_error("persistent decode: unsupported shape or arguments");
         return SNHIP_E_INVAL;
     }
     PersistArgs args = a;
     void* kargs[] = {&args};
-    const void* fn = blk == 0 ? (const void*)k_decode_persist<0>
-                   : blk == 32 ? (const void*)k_decode_persist<32>
-                               : (const void*)k_decode_persist<64>;
-    SNHIP_CHECK(hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(NT), kargs, 0, st));
+    SNHIP_CHECK(hipLaunchCooperativeKernel(kernel_for(blk), dim3(nwg), dim3(NT), kargs, 0, st));
     return SNHIP_OK;
 }
 
