@@ -8,7 +8,13 @@
 
 namespace snhip {
 
-enum GemmEpi { GEPI_STORE = 0, GEPI_WEDGE = 1, GEPI_RESID = 2 };
+enum GemmEpi {
+    GEPI_STORE = 0,   // Y = acc
+    GEPI_WEDGE = 1,   // Y = acc (1 + a/2 / (1 + |acc|))
+    GEPI_RESID = 2,   // Y = acc + (b_gain s + sfb + Y)
+    GEPI_ADD = 3,     // Y = Y + acc
+    GEPI_RELU2 = 4,   // Y = max(acc, 0)^2
+};
 
 struct GemmArgs {
     // X rows. If shift_T > 0, row m reads X[m - 1] except when m % shift_T == 0,

@@ -38,8 +38,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, int m, int n, f
         *y = acc;
     } else if (g.epi == GEPI_WEDGE) {
         *y = acc * (1.0f + 0.5f * g.a_tanh / (1.0f + fabsf(acc)));       // sunnynet.c:270-271
-    } else {
+    } else if (g.epi == GEPI_RESID) {
         *y = acc + (g.b_gain * g.s[(long)m * g.lds + n] + g.sfb[(long)m * g.ldf + n] + *y);  // :276
+    } else if (g.epi == GEPI_ADD) {
+        *y = *y + acc;                                                    // rwkv7.c:300,314
+    } else {
+        const float t = acc > 0.0f ? acc : 0.0f;                          // rwkv7.c:308-312
+        *y = t * t;
     }
 }
 

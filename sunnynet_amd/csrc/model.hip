@@ -25,6 +25,7 @@
 #include "common.h"
 #include "decode.h"
 #include "gemm.h"
+#include "gemv.h"
 #include "snhip.h"
 
 namespace snhip {
@@ -172,203 +173,6 @@ __global__ void k_compete_state(const float* __restrict__ q, const float* __rest
     float* sp = s + (size_t)b * s_bstride + i;
     *sp = p * *sp + (1.0f - p) * uu;
     u[(size_t)b * D + i] = uu;
-}
-
-// ------------------------------------------------------------------- GEMV
-enum { EPI_STORE = 0, EPI_WEDGE = 1, EPI_RESID = 2, EPI_ARGMAX = 3 };
-
-struct GemvJob {
-    const float* w;       // fp32 (M, Kd) or nullptr
-    const uint8_t* q;     // int4 (M, Kd/2)
-    const float* sc;      // int4 scales (M, Kd/BLK)
-    int M, Kd, B;
-    const float* X; int ldx;
-    float* Y; int ldy;
-    int epi;
-    float a_tanh, b_gain;
-    const float* s; int lds;
-    const float* sfb; int ldf;
-    unsigned long long* best;   // EPI_ARGMAX: per-block packed maxima, [b * nblk + blk]
-    int nblk;
-};
-
-// Orderable key of (value, index): larger value wins, then smaller index,
-// so the maximum key is torch.argmax's first maximal index.
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-    const uint32_t u = __float_as_uint(v);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
-}
-
-__device__ __forceinline__ void epilogue(const GemvJob& J, int b, int m, float acc) {
-    float* y = J.Y + (size_t)b * J.ldy + m;
-    if (J.epi == EPI_STORE) {
-        *y = acc;
-    } else if (J.epi == EPI_ARGMAX) {
-        *y = acc;   // the maximum is reduced by the caller (k_gemv)
-    } else if (J.epi == EPI_WEDGE) {
-        // sunnynet.c:270-271
-        *y = acc * (1.0f + 0.5f * J.a_tanh / (1.0f + fabsf(acc)));
-    } else {
-        // sunnynet.c:276: out += b_gain * s + sfb + x (x is Y itself)
-        *y = acc + (J.b_gain * J.s[(size_t)b * J.lds + m] + J.sfb[(size_t)b * J.ldf + m] + *y);
-    }
-}
-
-// Y[b, m] = sum_k W[m, k] X[b, k] for up to two independent jobs in one
-// launch (blocks [0, j0.nblk) run job 0, the rest job 1).
-// BLK = 0: fp32 weights; BLK = 32 / 64: INT4 groups of BLK inputs.
-// X is staged in LDS in chunks of BT sequences. fp32: plain rows, read as
-// float4 at the lane's columns. INT4: transposed inside each group
-// (xs[j * ngroups + g] = x[g * BLK + j]) so lanes reading the same in-group
-// position of different groups hit different banks. Each wave streams whole
-// weight rows (fp32: two rows in flight; INT4: 64/ngroups rows per pass when
-// the group count divides 64).
-template <int BLK, int BT>
-__global__ __launch_bounds__(256) void k_gemv(GemvJob j0, GemvJob j1) {
-    extern __shared__ float xs[];
-    const bool second = (int)blockIdx.x >= j0.nblk;
-    const GemvJob& J = second ? j1 : j0;
-    const int blk = second ? (int)blockIdx.x - j0.nblk : (int)blockIdx.x;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int M = J.M, Kd = J.Kd, B = J.B;
-    const int nw = J.nblk * 4;
-    const int gw = blk * 4 + wv;
-
-    const bool amax = J.epi == EPI_ARGMAX;
-    __shared__ unsigned long long kbest[4][BT];
-    for (int b0 = 0; b0 < B; b0 += BT) {
-        const int nb = min(BT, B - b0);
-        unsigned long long best[BT];
-#pragma unroll
-        for (int bb = 0; bb < BT; ++bb) best[bb] = 0ull;
-        __syncthreads();
-        if constexpr (BLK == 0) {
-            for (int i = threadIdx.x; i < nb * Kd; i += 256) {
-                const int bb = i / Kd, k = i - bb * Kd;
-                xs[i] = J.X[(size_t)(b0 + bb) * J.ldx + k];
-            }
-        } else {
-            const int ng = Kd / BLK;
-            for (int i = threadIdx.x; i < nb * Kd; i += 256) {
-                const int bb = i / Kd, k = i - bb * Kd;
-                const int g = k / BLK, j = k - g * BLK;
-                xs[bb * Kd + j * ng + g] = J.X[(size_t)(b0 + bb) * J.ldx + k];
-            }
-        }
-        __syncthreads();
-
-        if constexpr (BLK == 0) {
-            for (int r = gw * 2; r < M; r += nw * 2) {
-                const bool two = r + 1 < M;
-                const float* w0 = J.w + (size_t)r * Kd;
-                const float* w1 = two ? w0 + Kd : w0;
-                float a0[BT], a1[BT];
-#pragma unroll
-                for (int bb = 0; bb < BT; ++bb) { a0[bb] = 0.0f; a1[bb] = 0.0f; }
-                for (int k = lane * 4; k < Kd; k += 256) {
-                    const float4 x0 = *reinterpret_cast<const float4*>(w0 + k);
-                    const float4 x1 = *reinterpret_cast<const float4*>(w1 + k);
-#pragma unroll
-                    for (int bb = 0; bb < BT; ++bb) {
-                        if (bb < nb) {
-                            const float4 xv = *reinterpret_cast<const float4*>(xs + bb * Kd + k);
-                            a0[bb] = fmaf(x0.x, xv.x, a0[bb]); a0[bb] = fmaf(x0.y, xv.y, a0[bb]);
-                            a0[bb] = fmaf(x0.z, xv.z, a0[bb]); a0[bb] = fmaf(x0.w, xv.w, a0[bb]);
-                            a1[bb] = fmaf(x1.x, xv.x, a1[bb]); a1[bb] = fmaf(x1.y, xv.y, a1[bb]);
-                            a1[bb] = fmaf(x1.z, xv.z, a1[bb]); a1[bb] = fmaf(x1.w, xv.w, a1[bb]);
-                        }
-                    }
-                }
-#pragma unroll
-                for (int bb = 0; bb < BT; ++bb) {
-                    if (bb < nb) {
-                        const float s0 = wave_sum(a0[bb]);
-                        const float s1 = wave_sum(a1[bb]);
-                        if (lane == 0) {
-                            epilogue(J, b0 + bb, r, s0);
-                            if (two) epilogue(J, b0 + bb, r + 1, s1);
-                        }
-                        if (amax) {
-                            unsigned long long k = argmax_key(s0, r);
-                            if (two) k = max(k, argmax_key(s1, r + 1));
-                            best[bb] = max(best[bb], k);
-                        }
-                    }
-                }
-            }
-        } else {
-            constexpr int HB = BLK / 2;              // bytes per group
-            const int ng = Kd / BLK;
-            const int seg = (ng < 64 && (64 % ng) == 0) ? ng : 64;
-            const int rpi = 64 / seg;                // rows per wave pass
-            const int lrow = lane / seg, lg = lane - lrow * seg;
-            for (int r0 = gw * rpi; r0 < M; r0 += nw * rpi) {
-                const int r = r0 + lrow;
-                const bool live = r < M;
-                float acc[BT];
-#pragma unroll
-                for (int bb = 0; bb < BT; ++bb) acc[bb] = 0.0f;
-                if (live) {
-                    const uint8_t* qr = J.q + (size_t)r * (Kd / 2);
-                    const float* sr = J.sc + (size_t)r * ng;
-                    for (int g = lg; g < ng; g += seg) {
-                        uint4 qv[HB / 16];
-#pragma unroll
-                        for (int h = 0; h < HB / 16; ++h)
-                            qv[h] = *reinterpret_cast<const uint4*>(qr + (size_t)g * HB + h * 16);
-                        const float sc = sr[g];
-#pragma unroll
-                        for (int j = 0; j < HB; ++j) {
-                            const uint32_t word = reinterpret_cast<const uint32_t*>(qv)[j >> 2];
-                            const uint32_t byte = (word >> ((j & 3) * 8)) & 0xFFu;
-                            // quant.c:82-83, bit-identical dequantization
-                            const float wl = (float)((int)(byte & 0x0Fu) - 8) * sc;
-                            const float wh = (float)((int)(byte >> 4) - 8) * sc;
-#pragma unroll
-                            for (int bb = 0; bb < BT; ++bb) {
-                                if (bb < nb) {
-                                    const float* xb = xs + bb * Kd;
-                                    acc[bb] = fmaf(wl, xb[j * ng + g], acc[bb]);
-                                    acc[bb] = fmaf(wh, xb[(j + HB) * ng + g], acc[bb]);
-                                }
-                            }
-                        }
-                    }
-                }
-#pragma unroll
-                for (int bb = 0; bb < BT; ++bb) {
-                    if (bb < nb) {
-                        const float t = seg_sum(acc[bb], seg);
-                        if (live && lg == 0) epilogue(J, b0 + bb, r, t);
-                        if (amax && live && lg == 0) best[bb] = max(best[bb], argmax_key(t, r));
-                    }
-                }
-            }
-        }
-        if (amax) {
-            // Per-wave maximum (int4 keeps one candidate per row segment),
-            // then per block; one plain store per (sequence, block).
-#pragma unroll
-            for (int bb = 0; bb < BT; ++bb) {
-                unsigned long long k = best[bb];
-                for (int o = 32; o > 0; o >>= 1) {
-                    const unsigned long long other =
-                        ((unsigned long long)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
-                        (uint32_t)__shfl_xor((int)(k & 0xFFFFFFFFull), o, 64);
-                    k = max(k, other);
-                }
-                if (lane == 0) kbest[wv][bb] = k;
-            }
-            __syncthreads();
-            if (threadIdx.x < (unsigned)nb) {
-                const int bb = threadIdx.x;
-                const unsigned long long k = max(max(kbest[0][bb], kbest[1][bb]),
-                                                 max(kbest[2][bb], kbest[3][bb]));
-                J.best[(size_t)(b0 + bb) * J.nblk + blk] = k;
-            }
-        }
-    }
 }
 
 // Greedy token from the per-block maxima (first maximal index, the
@@ -936,38 +740,10 @@ GemvJob make_job(const Mat& W, int B, const float* X, int ldx, float* Y, int ldy
     return j;
 }
 
-int gemv_blocks(const GemvJob& j, int wfmt, int block) {
-    int rows_per_wave = 2;
-    if (wfmt == SNHIP_WEIGHTS_INT4) {
-        const int ng = j.Kd / block;
-        rows_per_wave = (ng < 64 && 64 % ng == 0) ? 64 / ng : 1;
-    }
-    const int rows_per_block = 4 * rows_per_wave;
-    int nb = (j.M + rows_per_block - 1) / rows_per_block;
-    return nb > 4096 ? 4096 : nb;
-}
-
-template <int BLK>
-hipError_t launch_gemv_fmt(GemvJob j0, GemvJob j1, int bt, hipStream_t st) {
-    const int kd = std::max(j0.Kd, j1.nblk ? j1.Kd : 0);
-    const dim3 grid(j0.nblk + j1.nblk), blk(256);
-    if (bt == 1)
-        hipLaunchKernelGGL((k_gemv<BLK, 1>), grid, blk, (size_t)kd * 4, st, j0, j1);
-    else
-        hipLaunchKernelGGL((k_gemv<BLK, 8>), grid, blk, (size_t)kd * 4 * 8, st, j0, j1);
-    return hipGetLastError();
-}
-
-// Launch one or two GEMV jobs (pass j1.nblk = 0 for a single job).
+// One or two GEMV jobs in one launch (j1.M == 0: one job).
 hipError_t launch_gemv(const SnHipModel* m, GemvJob j0, GemvJob j1, hipStream_t st) {
-    j0.nblk = gemv_blocks(j0, m->wfmt, m->block);
-    if (j1.M > 0) j1.nblk = gemv_blocks(j1, m->wfmt, m->block);
-    else j1.nblk = 0;
-    const int kd = std::max(j0.Kd, j1.nblk ? j1.Kd : 0);
-    const int bt = (j0.B > 1 && (size_t)kd * 4 * 8 <= 65536) ? 8 : 1;
-    if (m->wfmt == SNHIP_WEIGHTS_F32) return launch_gemv_fmt<0>(j0, j1, bt, st);
-    if (m->block == 32) return launch_gemv_fmt<32>(j0, j1, bt, st);
-    return launch_gemv_fmt<64>(j0, j1, bt, st);
+    GemvJob js[2] = {j0, j1};
+    return launch_gemv(js, j1.M > 0 ? 2 : 1, m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0, st);
 }
 
 GemmArgs gemm_for(const SnHipModel* m, const Mat& W, const float* X, long ldx, int M, float* Y,
@@ -1018,7 +794,7 @@ snhip_status enqueue_head(SnHipModel* m, int B, const float* x, float* logits_ou
         SNHIP_CHECK(launch_gemv(m, jh, none, st));
         if (greedy)
             hipLaunchKernelGGL(k_finalize_tok, dim3(B), dim3(256), 0, st, m->best,
-                               gemv_blocks(jh, m->wfmt, m->block), B, m->tok, m->tok_hist,
+                               gemv_blocks(jh, m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0), B, m->tok, m->tok_hist,
                                m->counter, m->done, m->hist_cap);
     }
     SNHIP_CHECK(hipGetLastError());
