@@ -1,0 +1,87 @@
+/* RWKV-7 decode handle on the HIP backend.
+ *
+ * Mirrors the reference's sunnynet/runtime/rwkv7.h:14-28 (sn_rk_load /
+ * sn_rk_step / sn_rk_prefill / sn_rk_reset / sn_rk_free / sn_rk_vocab /
+ * sn_rk_ready) with the prefix snhip_rk_ and the same argument order, meaning
+ * and error behaviour: the loader reads the reference's v3 blob
+ * (experiments/_export_rwkv7.py format) and returns NULL on an IO, magic,
+ * version, dimension or allocation failure; void functions tolerate a NULL
+ * handle; logits buffers of the mirrored calls are caller-owned HOST memory of
+ * length vocab; prefill feeds the tokens in order (rwkv7.c:362-364).
+ *
+ * Weights: INT4-tagged matrices of the blob (group 64) stay INT4 and are
+ * dequantized in registers, bit-identically to sn_dequant_i4; fp32 matrices
+ * stay fp32 unless snhip_rk_load_ex asks for INT4 (then every fp32 matrix whose
+ * input length is a multiple of `block` is quantized at load). The reference
+ * runs INT4 matrices as W4A8; this backend keeps activations fp32 (W4A32).
+ *
+ * Extensions: max_batch independent sequences, device-pointer entry points on a
+ * caller stream, on-device greedy decoding, state import/export:
+ *   S     (B, layers, n_head, head_size, head_size)  fp32, S[.., i, j] row i
+ *   shift (B, layers, 2, dim)                         fp32 (time mix, channel mix)
+ */
+#ifndef SNHIP_RWKV7_H
+#define SNHIP_RWKV7_H
+
+#include <stdint.h>
+
+#include "snhip_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct SnHipRwkv7 SnHipRwkv7;
+
+/* Weight format for snhip_rk_load_ex besides SNHIP_WEIGHTS_F32 (0) and
+ * SNHIP_WEIGHTS_INT4 (1) of snhip.h: every matrix as the blob stores it. */
+#define SNHIP_WEIGHTS_STORED 2
+
+/* rwkv7.h:16: B = 1, each matrix as stored in the blob. */
+SnHipRwkv7* snhip_rk_load(const char* path);
+/* Same checks; max_batch sequences; weight_format SNHIP_WEIGHTS_STORED,
+ * SNHIP_WEIGHTS_F32 (INT4 blob matrices dequantized at load) or
+ * SNHIP_WEIGHTS_INT4 (fp32 blob matrices quantized at load with group `block`,
+ * 32 or 64, where block divides their input length). */
+SnHipRwkv7* snhip_rk_load_ex(const char* path, int32_t max_batch, int32_t weight_format,
+                             int32_t block);
+/* rwkv7.h:17-18 */
+void snhip_rk_free(SnHipRwkv7* m);
+void snhip_rk_reset(SnHipRwkv7* m);
+/* rwkv7.h:21-22: sequence 0; logits host, length vocab. */
+void snhip_rk_step(SnHipRwkv7* m, int token, float* logits);
+void snhip_rk_prefill(SnHipRwkv7* m, const int* tokens, int n, float* logits);
+/* rwkv7.h:27-28 */
+int snhip_rk_vocab(const SnHipRwkv7* m);
+int snhip_rk_ready(const SnHipRwkv7* m);
+
+/* ---- extensions ---------------------------------------------------------- */
+snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream);
+int32_t snhip_rk_max_batch(const SnHipRwkv7* m);
+/* One step of sequences [0, B): tokens_dev (B) int32, logits_dev (B, vocab). */
+snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
+                                     float* logits_dev);
+/* Greedy decoding on the device (first maximal logit): feeds tokens_dev (B),
+ * out_tokens_dev (n_steps, B) receives each step's choice; logits_dev (B,
+ * vocab), if not NULL, the last step's logits. */
+snhip_status snhip_rk_decode_greedy_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
+                                        int32_t n_steps, int32_t* out_tokens_dev,
+                                        float* logits_dev);
+snhip_status snhip_rk_get_state_dev(SnHipRwkv7* m, float* S_dev, float* shift_dev, int32_t B);
+snhip_status snhip_rk_set_state_dev(SnHipRwkv7* m, const float* S_dev, const float* shift_dev,
+                                    int32_t B);
+
+/* Stable-ABI mirror of sn_abi.h:88-100 (sn_abi_rwkv7_*): status codes of
+ * snhip_abi.h; logits host memory of at least snhip_abi_rwkv7_vocab floats. */
+SnHipRwkv7* snhip_abi_rwkv7_load(const char* blob_path);
+snhip_status snhip_abi_rwkv7_step(SnHipRwkv7* m, int32_t token, float* logits);
+snhip_status snhip_abi_rwkv7_prefill(SnHipRwkv7* m, const int32_t* tokens, int32_t n,
+                                     float* logits);
+snhip_status snhip_abi_rwkv7_reset(SnHipRwkv7* m);
+void snhip_abi_rwkv7_free(SnHipRwkv7* m);
+int32_t snhip_abi_rwkv7_vocab(const SnHipRwkv7* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SNHIP_RWKV7_H */

@@ -81,6 +81,27 @@ _SIGS = {
     "snhip_prefill_batch_dev": (I32, [V, V, I32, I32, V]),
     "snhip_get_state_dev": (I32, [V, V, V, I32]),
     "snhip_set_state_dev": (I32, [V, V, V, I32]),
+    # include/snhip_rwkv7.h
+    "snhip_rk_load": (V, [CP]),
+    "snhip_rk_load_ex": (V, [CP, I32, I32, I32]),
+    "snhip_rk_free": (None, [V]),
+    "snhip_rk_reset": (None, [V]),
+    "snhip_rk_step": (None, [V, INT, V]),
+    "snhip_rk_prefill": (None, [V, V, INT, V]),
+    "snhip_rk_vocab": (INT, [V]),
+    "snhip_rk_ready": (INT, [V]),
+    "snhip_rk_set_stream": (I32, [V, V]),
+    "snhip_rk_max_batch": (I32, [V]),
+    "snhip_rk_step_batch_dev": (I32, [V, V, I32, V]),
+    "snhip_rk_decode_greedy_dev": (I32, [V, V, I32, I32, V, V]),
+    "snhip_rk_get_state_dev": (I32, [V, V, V, I32]),
+    "snhip_rk_set_state_dev": (I32, [V, V, V, I32]),
+    "snhip_abi_rwkv7_load": (V, [CP]),
+    "snhip_abi_rwkv7_step": (I32, [V, I32, V]),
+    "snhip_abi_rwkv7_prefill": (I32, [V, V, I32, V]),
+    "snhip_abi_rwkv7_reset": (I32, [V]),
+    "snhip_abi_rwkv7_free": (None, [V]),
+    "snhip_abi_rwkv7_vocab": (I32, [V]),
 }
 
 

@@ -47,8 +47,9 @@ extern "C" {
 int32_t snhip_abi_version(void) { return SNHIP_ABI_VERSION; }
 
 uint32_t snhip_abi_caps(void) {
-    return SNHIP_CAP_RECUR_SCAN | SNHIP_CAP_RECUR_STEP | SNHIP_CAP_THREADS |
-           SNHIP_CAP_DEVICE_PTR | SNHIP_CAP_INT4;
+    return SNHIP_CAP_RECUR_SCAN | SNHIP_CAP_RECUR_STEP | SNHIP_CAP_RWKV7 | SNHIP_CAP_THREADS |
+           SNHIP_CAP_DEVICE_PTR | SNHIP_CAP_SUNNY_MODEL | SNHIP_CAP_INT4 | SNHIP_CAP_BATCH |
+           SNHIP_CAP_PREFILL;
 }
 
 snhip_status snhip_abi_check(int32_t caller_major) {

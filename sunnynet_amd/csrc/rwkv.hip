@@ -1,0 +1,977 @@
+// RWKV-7 decode on gfx950 (include/snhip_rwkv7.h).
+//
+// The math is the reference's C runtime, sunnynet/runtime/rwkv7.c:143-360:
+//   x = LN_0(E[token]); per layer:
+//     xn = LN_1(x); d = shift_0 - xn; x_{r,w,k,v,a,g} = xn + lerp_* d
+//     r, k, v = W_r x_r, W_k x_k, W_v x_v
+//     w = exp(-sig(W_2 tanh(W_1 x_w) + w_0) / sqrt(e))
+//     v = v + (v_first - v) sig(V_2 V_1 x_v + v_0)   (layer 0: v_first = v)
+//     a = sig(A_2 A_1 x_a + a_0);  g = G_2 sig(G_1 x_g)
+//     kk = k kk_w;  k = k + k (a - 1) ka_w
+//     per head: S = S diag(w) - (S kk^) (kk^ a)^T + v k^T;  y = S r
+//               y = (GroupNorm(y) + (r . k rk_w) v) g
+//     x += W_o y;  shift_0 = xn
+//     xn2 = LN_2(x);  x += W_cv relu(W_ck (xn2 + cmk_lerp (shift_1 - xn2)))^2;  shift_1 = xn2
+//   logits = W_head LN_out(x)
+//
+// One step is a short sequence of kernels on the handle's stream (captured
+// into a HIP graph and replayed); every kernel processes all B sequences.
+// Matrix-vector products use the shared GEMV (gemv.hip) below 8 sequences
+// and the MFMA GEMM (gemm.hip) from 8 on; everything between them is fused
+// per sequence (token-shift mixes) or per head (k_rk_heads: decay, mixes,
+// normalized kk, the 64 x 64 state update and read-out, group norm, bonus,
+// gate), keeping each head's state tile in registers for one pass over HBM.
+// Weights live row-major (out, in), fp32 or INT4.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "common.h"
+#include "gemm.h"
+#include "gemv.h"
+#include "snhip.h"
+#include "snhip_rwkv7.h"
+
+namespace snhip {
+namespace {
+
+constexpr int kRkMagic = 0x4B57524B;   // rwkv7.c:36
+constexpr int kRkVersion = 3;
+constexpr int kRkBlobBlock = 64;       // INT4 group of the v3 blob (rwkv7.c:40)
+constexpr float kR2 = 0.6065306597126334f;   // 1/sqrt(e), rwkv7.c:38
+constexpr float kEpsGroup = 6.4e-4f;          // rwkv7.c:39
+constexpr int kHS = 64;                        // head size this backend runs
+constexpr int kMaxRank = 256;                  // rwkv7.c: LoRA scratch of 256
+constexpr int kLnPer = 16;                     // LayerNorm values per thread (dim <= 4096)
+
+__device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Two-pass LayerNorm over n <= 4096 values (rwkv7.c:127-140 form), element
+// k * 256 + tid in xv[k].
+__device__ __forceinline__ void ln_stats(const float (&xv)[kLnPer], int n, float eps, float* red,
+                                         float& mean, float& rstd) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k)
+        if (k * 256 + (int)threadIdx.x < n) sum += xv[k];
+    mean = block_sum256(sum, red) / (float)n;
+    float vs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k)
+        if (k * 256 + (int)threadIdx.x < n) {
+            const float d = xv[k] - mean;
+            vs += d * d;
+        }
+    rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
+}
+
+__device__ __forceinline__ void load_row(float (&xv)[kLnPer], const float* x, int n) {
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        xv[k] = i < n ? x[i] : 0.0f;
+    }
+}
+
+// x[b] = LN_0(E[tok[b]]) (rwkv7.c:351-352); NaN rows for out-of-range ids.
+__global__ __launch_bounds__(256) void k_rk_embed(const int32_t* __restrict__ tok,
+                                                  const float* __restrict__ embed,
+                                                  const float* __restrict__ g,
+                                                  const float* __restrict__ c, float* __restrict__ x,
+                                                  int D, int vocab, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    const int t = tok[b];
+    const bool ok = t >= 0 && t < vocab;
+    float xv[kLnPer];
+    load_row(xv, embed + (size_t)(ok ? t : 0) * D, D);
+    if (!ok)
+#pragma unroll
+        for (int k = 0; k < kLnPer; ++k) xv[k] = __builtin_nanf("");
+    float mean, rstd;
+    ln_stats(xv, D, eps, red, mean, rstd);
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        if (i < D) x[(size_t)b * D + i] = (xv[k] - mean) * rstd * g[i] + c[i];
+    }
+}
+
+// y[b] = LN(x[b]) (the output norm, rwkv7.c:358).
+__global__ __launch_bounds__(256) void k_rk_ln(const float* __restrict__ x, const float* __restrict__ g,
+                                               const float* __restrict__ c, float* __restrict__ y,
+                                               int D, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    float xv[kLnPer];
+    load_row(xv, x + (size_t)b * D, D);
+    float mean, rstd;
+    ln_stats(xv, D, eps, red, mean, rstd);
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        if (i < D) y[(size_t)b * D + i] = (xv[k] - mean) * rstd * g[i] + c[i];
+    }
+}
+
+// Time-mix inputs (rwkv7.c:213-227): xn = LN_1(x); d = shift_0 - xn;
+// X6[b][s] = xn + lerp[s] d for s = r, w, k, v, a, g; shift_0 <- xn.
+__global__ __launch_bounds__(256) void k_rk_mix1(const float* __restrict__ x,
+                                                 const float* __restrict__ g,
+                                                 const float* __restrict__ c,
+                                                 const float* __restrict__ lerp,
+                                                 float* __restrict__ shift, size_t shift_bstride,
+                                                 float* __restrict__ X6, int D, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    float xv[kLnPer];
+    load_row(xv, x + (size_t)b * D, D);
+    float mean, rstd;
+    ln_stats(xv, D, eps, red, mean, rstd);
+    float* sh = shift + (size_t)b * shift_bstride;
+    float* o = X6 + (size_t)b * 6 * D;
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        if (i >= D) continue;
+        const float xn = (xv[k] - mean) * rstd * g[i] + c[i];
+        const float d = sh[i] - xn;
+#pragma unroll
+        for (int s = 0; s < 6; ++s) o[(size_t)s * D + i] = xn + lerp[(size_t)s * D + i] * d;
+        sh[i] = xn;
+    }
+}
+
+// Channel-mix input (rwkv7.c:303-305,315): xn2 = LN_2(x);
+// xk2 = xn2 + cmk_lerp (shift_1 - xn2); shift_1 <- xn2.
+__global__ __launch_bounds__(256) void k_rk_mix2(const float* __restrict__ x,
+                                                 const float* __restrict__ g,
+                                                 const float* __restrict__ c,
+                                                 const float* __restrict__ lerp,
+                                                 float* __restrict__ shift1, size_t shift_bstride,
+                                                 float* __restrict__ xk2, int D, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    float xv[kLnPer];
+    load_row(xv, x + (size_t)b * D, D);
+    float mean, rstd;
+    ln_stats(xv, D, eps, red, mean, rstd);
+    float* sh = shift1 + (size_t)b * shift_bstride;
+#pragma unroll
+    for (int k = 0; k < kLnPer; ++k) {
+        const int i = k * 256 + threadIdx.x;
+        if (i >= D) continue;
+        const float xn = (xv[k] - mean) * rstd * g[i] + c[i];
+        xk2[(size_t)b * D + i] = xn + lerp[i] * (sh[i] - xn);
+        sh[i] = xn;
+    }
+}
+
+// LoRA middle activations (rwkv7.c:235,256): lw = tanh(lw), lg = sig(lg).
+__global__ void k_rk_lora_act(float* __restrict__ lw, int Rw, float* __restrict__ lg, int Rg,
+                              int ld) {
+    const int b = blockIdx.x;
+    for (int i = threadIdx.x; i < Rw; i += blockDim.x) lw[(size_t)b * ld + i] = tanhf(lw[(size_t)b * ld + i]);
+    for (int i = threadIdx.x; i < Rg; i += blockDim.x) lg[(size_t)b * ld + i] = sgm(lg[(size_t)b * ld + i]);
+}
+
+struct HeadArgs {
+    const float *r, *k, *v, *dw, *da, *dv, *g;   // (B, D) each
+    float* vfirst;                                // (B, D)
+    const float *w0, *a0, *v0, *kk_w, *ka_w, *rk_w, *lnx_w, *lnx_b;
+    float* S;            // layer base; sequence b at S + b * s_bstride, head h at + h * HS*HS
+    size_t s_bstride;
+    float* y;            // (B, D)
+    int D, first;
+};
+
+// One head of one sequence per workgroup (rwkv7.c:143-189 and :236-299).
+// Channel work by the first wave; the 64 x 64 state by all 256 threads,
+// thread t owning row i = t / 4, columns 16 (t % 4) .. 16 (t % 4) + 15.
+__global__ __launch_bounds__(256) void k_rk_heads(HeadArgs A) {
+    __shared__ float w_[kHS], k_[kHS], v_[kHS], a_[kHS], kn_[kHS], r_[kHS], y_[kHS];
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const size_t row = (size_t)b * A.D;
+    if (t < kHS) {
+        const int c = h * kHS + t;
+        const float ww = expf(-sgm(A.dw[row + c] + A.w0[c]) * kR2);          // :236-237
+        float vv = A.v[row + c];
+        if (A.first) {
+            A.vfirst[row + c] = vv;                                            // :240
+        } else {
+            const float mix = sgm(A.dv[row + c] + A.v0[c]);                    // :244-246
+            vv = vv + (A.vfirst[row + c] - vv) * mix;
+        }
+        const float av = sgm(A.da[row + c] + A.a0[c]);                        // :251-252
+        const float kv = A.k[row + c];
+        const float kkv = kv * A.kk_w[c];                                      // :259
+        const float k2 = kv + kv * (av - 1.0f) * A.ka_w[c];                   // :260
+        // |kk| of the head, floored at 1e-12 (:158-162)
+        float nrm = sqrtf(wave_sum(kkv * kkv));
+        if (!(nrm > 1e-12f)) nrm = 1e-12f;
+        const float inv = 1.0f / nrm;
+        w_[t] = ww; k_[t] = k2; v_[t] = vv; a_[t] = av; kn_[t] = kkv * inv; r_[t] = A.r[row + c];
+    }
+    __syncthreads();
+    const int i = t >> 2, j0 = (t & 3) * 16;
+    float* Sr = A.S + (size_t)b * A.s_bstride + (size_t)h * kHS * kHS + (size_t)i * kHS + j0;
+    float s[16];
+#pragma unroll
+    for (int q = 0; q < 16; q += 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(Sr + q);
+        s[q] = v4.x; s[q + 1] = v4.y; s[q + 2] = v4.z; s[q + 3] = v4.w;
+    }
+    float pv = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
+    pv += __shfl_xor(pv, 1, 64);
+    pv += __shfl_xor(pv, 2, 64);
+    const float vi = v_[i];
+    float yacc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int j = j0 + q;
+        const float kka = kn_[j] * a_[j];
+        const float vk = vi * k_[j];
+        const float ns = fmaf(s[q], w_[j], vk - pv * kka);                    // :180-181
+        s[q] = ns;
+        yacc = fmaf(ns, r_[j], yacc);
+    }
+#pragma unroll
+    for (int q = 0; q < 16; q += 4)
+        *reinterpret_cast<float4*>(Sr + q) = make_float4(s[q], s[q + 1], s[q + 2], s[q + 3]);
+    yacc += __shfl_xor(yacc, 1, 64);
+    yacc += __shfl_xor(yacc, 2, 64);
+    if ((t & 3) == 0) y_[i] = yacc;
+    __syncthreads();
+    if (t < kHS) {
+        // group norm, bonus and gate (:266-288)
+        const int c = h * kHS + t;
+        const float yy = y_[t];
+        const float mean = wave_sum(yy) / (float)kHS;
+        const float d = yy - mean;
+        const float rstd = 1.0f / sqrtf(wave_sum(d * d) / (float)kHS + kEpsGroup);
+        const float dot = wave_sum(r_[t] * k_[t] * A.rk_w[c]);
+        const float n = (yy - mean) * rstd * A.lnx_w[c] + A.lnx_b[c];
+        A.y[row + c] = (n + dot * v_[t]) * A.g[row + c];
+    }
+}
+
+// (in, out) row-major -> (out, in) row-major, 32x32 tiles through LDS.
+__global__ void k_rk_transpose(const float* __restrict__ src, float* __restrict__ dst, int in, int out) {
+    __shared__ float tile[32][33];
+    const int bo = blockIdx.x * 32, bi = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int r = ty; r < 32; r += 8) {
+        const int i = bi + r, o = bo + tx;
+        if (i < in && o < out) tile[r][tx] = src[(size_t)i * out + o];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int o = bo + r, i = bi + tx;
+        if (o < out && i < in) dst[(size_t)o * in + i] = tile[tx][r];
+    }
+}
+
+// Per-block partial maxima of logits rows (GEMM head): grid (nblk, B).
+__global__ __launch_bounds__(256) void k_rk_argmax_partial(const float* __restrict__ logits, int V,
+                                                           unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[256];
+    const int b = blockIdx.y, nblk = gridDim.x;
+    const int chunk = (V + nblk - 1) / nblk;
+    const int lo = blockIdx.x * chunk, hi = min(V, lo + chunk);
+    unsigned long long k = 0ull;
+    for (int i = lo + (int)threadIdx.x; i < hi; i += 256) k = max(k, argmax_key(logits[(size_t)b * V + i], i));
+    red[threadIdx.x] = k;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + o]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[(size_t)b * nblk + blockIdx.x] = red[0];
+}
+
+// Greedy token of each sequence from the per-block maxima (first maximal
+// index); writes it to tok (the next step's input) and to out at the device
+// step counter; the last block to finish advances the counter.
+__global__ __launch_bounds__(256) void k_rk_finalize(const unsigned long long* __restrict__ part,
+                                                     int nblk, int B, int32_t* __restrict__ tok,
+                                                     int32_t* __restrict__ out,
+                                                     int32_t* __restrict__ counter,
+                                                     int32_t* __restrict__ done, int cap) {
+    __shared__ unsigned long long red[256];
+    const int b = blockIdx.x;
+    unsigned long long k = 0ull;
+    for (int i = threadIdx.x; i < nblk; i += 256) k = max(k, part[(size_t)b * nblk + i]);
+    red[threadIdx.x] = k;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + o]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int32_t tk = (int32_t)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFull));
+        const int step = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        tok[b] = tk;
+        if ((long)step * B + b < (long)cap) out[(size_t)step * B + b] = tk;
+        __threadfence();
+        if (atomicAdd(done, 1) == B - 1) {
+            *done = 0;
+            __hip_atomic_store(counter, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// A weight matrix, row-major (M, Kd): fp32 w, or INT4 q + sc with group block.
+struct RMat {
+    int M = 0, Kd = 0;
+    float* w = nullptr;
+    uint8_t* q = nullptr;
+    float* sc = nullptr;
+    int block = 0;
+};
+
+struct RkLayer {
+    const float *ln1w, *ln1b, *ln2w, *ln2b, *lerp, *w0, *a0, *v0, *kk, *ka, *rk, *lnxw, *lnxb, *cmk_lerp;
+    int Rw, Ra, Rv, Rg;
+    RMat r, k, v, o, w1, w2, a1, a2, v1, v2, g1, g2, cmk, cmv;
+};
+
+}  // namespace
+}  // namespace snhip
+
+struct SnHipRwkv7 {
+    int L = 0, D = 0, HS = 0, NH = 0, F = 0, vocab = 0, max_batch = 1, wfmt = 0, block = 32;
+    float eps = 0.f;
+    std::vector<snhip::RkLayer> layers;
+    const float *en_w = nullptr, *en_b = nullptr, *on_w = nullptr, *on_b = nullptr, *embed = nullptr;
+    snhip::RMat head;
+    float *S = nullptr, *shift = nullptr;
+    float *x = nullptr, *X6 = nullptr, *r = nullptr, *k = nullptr, *v = nullptr, *lo = nullptr,
+          *dw = nullptr, *da = nullptr, *dv = nullptr, *g = nullptr, *y = nullptr, *vfirst = nullptr,
+          *xk2 = nullptr, *ck = nullptr, *nrm = nullptr, *logits = nullptr;
+    int32_t* tok = nullptr;
+    unsigned long long* best = nullptr;
+    int32_t *counter = nullptr, *done = nullptr, *tok_hist = nullptr;
+    int hist_cap = 0;
+    std::vector<void*> allocs;
+    hipStream_t stream = nullptr, work = nullptr;
+    hipEvent_t ev_in = nullptr, ev_out = nullptr;
+    std::map<std::tuple<int, const void*, int>, hipGraphExec_t> graphs;
+    bool use_graphs = true;
+    int gemm_min_batch = 8;
+    float* gemm_work = nullptr;
+    size_t gemm_work_floats = 0;
+    int ready = 0;
+};
+
+namespace snhip {
+namespace {
+
+template <typename T>
+T* ralloc(SnHipRwkv7* m, size_t n) {
+    void* p = nullptr;
+    if (hipMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 4) != hipSuccess) return nullptr;
+    m->allocs.push_back(p);
+    return static_cast<T*>(p);
+}
+
+void free_rk(SnHipRwkv7* m) {
+    if (!m) return;
+    for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+    if (m->ev_in) (void)hipEventDestroy(m->ev_in);
+    if (m->ev_out) (void)hipEventDestroy(m->ev_out);
+    if (m->work) (void)hipStreamDestroy(m->work);
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+// Tag-prefixed tensor stream of the v3 blob (rwkv7.c:380-420).
+struct Cur {
+    const uint8_t* p;
+    const uint8_t* end;
+    bool ok;
+};
+
+const float* take_vec(Cur& c, size_t n) {
+    if (!c.ok || (size_t)(c.end - c.p) < 4 + n * sizeof(float)) { c.ok = false; return nullptr; }
+    int32_t tag;
+    memcpy(&tag, c.p, 4);
+    if (tag != 0) { c.ok = false; return nullptr; }
+    c.p += 4;
+    const float* r = reinterpret_cast<const float*>(c.p);
+    c.p += n * sizeof(float);
+    return r;
+}
+
+bool upload(SnHipRwkv7* m, const float*& dst, const float* src, size_t n) {
+    float* d = ralloc<float>(m, n);
+    if (!d || hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) return false;
+    dst = d;
+    return true;
+}
+
+// A matrix y = M x with `in` inputs and `out` outputs, into (out, in) rows:
+// tag 0 (fp32 M^T) is transposed on the device and, for INT4, quantized when
+// block divides in; tag 1 (INT4, group 64) stays INT4 or is dequantized.
+bool take_mat(SnHipRwkv7* m, Cur& c, RMat& M, int in, int out, float* tmp0, float* tmp1) {
+    M.M = out;
+    M.Kd = in;
+    if (!c.ok || (size_t)(c.end - c.p) < 4) { c.ok = false; return false; }
+    int32_t tag;
+    memcpy(&tag, c.p, 4);
+    c.p += 4;
+    const size_t n = (size_t)in * out;
+    if (tag == 0) {
+        if ((size_t)(c.end - c.p) < n * sizeof(float)) { c.ok = false; return false; }
+        if (hipMemcpy(tmp0, c.p, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) return false;
+        c.p += n * sizeof(float);
+        hipLaunchKernelGGL(k_rk_transpose, dim3((out + 31) / 32, (in + 31) / 32), dim3(256), 0, nullptr,
+                           tmp0, tmp1, in, out);
+        if (hipGetLastError() != hipSuccess) return false;
+        if (m->wfmt == SNHIP_WEIGHTS_INT4 && in % m->block == 0) {
+            M.block = m->block;
+            M.q = ralloc<uint8_t>(m, n / 2);
+            M.sc = ralloc<float>(m, n / M.block);
+            if (!M.q || !M.sc) return false;
+            if (launch_quant_i4(tmp1, M.q, M.sc, out, in, M.block, nullptr) != SNHIP_OK) return false;
+        } else {
+            M.w = ralloc<float>(m, n);
+            if (!M.w || hipMemcpy(M.w, tmp1, n * sizeof(float), hipMemcpyDeviceToDevice) != hipSuccess)
+                return false;
+        }
+    } else if (tag == 1) {
+        if (in % kRkBlobBlock) { c.ok = false; return false; }
+        const size_t qb = n / 2, sb = n / kRkBlobBlock * sizeof(float);
+        if ((size_t)(c.end - c.p) < qb + sb) { c.ok = false; return false; }
+        uint8_t* q = ralloc<uint8_t>(m, qb);
+        float* sc = ralloc<float>(m, n / kRkBlobBlock);
+        if (!q || !sc) return false;
+        // (scales may sit unaligned in the stream; hipMemcpy takes bytes)
+        if (hipMemcpy(q, c.p, qb, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(sc, c.p + qb, sb, hipMemcpyHostToDevice) != hipSuccess)
+            return false;
+        c.p += qb + sb;
+        if (m->wfmt != SNHIP_WEIGHTS_F32) {
+            M.q = q; M.sc = sc; M.block = kRkBlobBlock;
+        } else {
+            M.w = ralloc<float>(m, n);
+            if (!M.w || launch_dequant_i4(q, sc, M.w, out, in, kRkBlobBlock, nullptr) != SNHIP_OK)
+                return false;
+        }
+    } else {
+        c.ok = false;
+        return false;
+    }
+    return hipDeviceSynchronize() == hipSuccess;
+}
+
+SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
+    if (!path || max_batch <= 0 || max_batch > 1024) { set_last_error("invalid arguments"); return nullptr; }
+    if (wfmt != SNHIP_WEIGHTS_F32 && wfmt != SNHIP_WEIGHTS_INT4 && wfmt != SNHIP_WEIGHTS_STORED) {
+        set_last_error("unknown weight format");
+        return nullptr;
+    }
+    if (wfmt == SNHIP_WEIGHTS_INT4 && block != 32 && block != 64) { set_last_error("INT4 block must be 32 or 64"); return nullptr; }
+    FILE* f = fopen(path, "rb");
+    if (!f) { set_last_error(std::string("cannot open ") + path); return nullptr; }
+    std::vector<uint8_t> buf;
+    {
+        fseek(f, 0, SEEK_END);
+        const long sz = ftell(f);
+        fseek(f, 0, SEEK_SET);
+        if (sz < 44) { fclose(f); set_last_error("blob too short"); return nullptr; }
+        buf.resize((size_t)sz);
+        const size_t got = fread(buf.data(), 1, buf.size(), f);
+        fclose(f);
+        if (got != buf.size()) { set_last_error("blob read failed"); return nullptr; }
+    }
+    int32_t h[10];
+    memcpy(h, buf.data(), sizeof h);
+    if (h[0] != kRkMagic || h[1] != kRkVersion) { set_last_error("bad RWKV-7 blob header (magic/version)"); return nullptr; }
+    const int L = h[2], D = h[3], HS = h[4], NH = h[5], F = h[6], V = h[8];
+    if (L <= 0 || D <= 0 || HS != kHS || NH * HS != D || F <= 0 || V <= 0 || D > kLnPer * 256 ||
+        D % 32 || F % 4) {
+        set_last_error("unsupported RWKV-7 shape (head size must be 64, dim <= 4096)");
+        return nullptr;
+    }
+    const uint8_t* p = buf.data() + 40;
+    float eps;
+    memcpy(&eps, p, 4);
+    p += 4;
+    if ((size_t)(buf.data() + buf.size() - p) < (size_t)16 * L) { set_last_error("blob is truncated"); return nullptr; }
+    std::vector<int32_t> ranks(4 * (size_t)L);
+    memcpy(ranks.data(), p, ranks.size() * sizeof(int32_t));
+    p += ranks.size() * sizeof(int32_t);
+
+    SnHipRwkv7* m = new SnHipRwkv7();
+    m->L = L; m->D = D; m->HS = HS; m->NH = NH; m->F = F; m->vocab = V; m->eps = eps;
+    m->max_batch = max_batch; m->wfmt = wfmt; m->block = block;
+    const size_t big = std::max((size_t)D * V, std::max((size_t)D * F, (size_t)D * D));
+    float* tmp0 = ralloc<float>(m, big);
+    float* tmp1 = ralloc<float>(m, big);
+    if (!tmp0 || !tmp1) { free_rk(m); set_last_error("out of device memory"); return nullptr; }
+    Cur c{p, buf.data() + buf.size(), true};
+    bool ok = true;
+    m->layers.resize(L);
+    for (int l = 0; l < L && ok && c.ok; ++l) {
+        RkLayer& A = m->layers[l];
+        A.Rw = ranks[4 * l]; A.Ra = ranks[4 * l + 1]; A.Rv = ranks[4 * l + 2]; A.Rg = ranks[4 * l + 3];
+        if (A.Rw <= 0 || A.Ra <= 0 || A.Rv <= 0 || A.Rg <= 0 || A.Rw > kMaxRank || A.Ra > kMaxRank ||
+            A.Rv > kMaxRank || A.Rg > kMaxRank || A.Rw % 4 || A.Ra % 4 || A.Rv % 4 || A.Rg % 4) {
+            c.ok = false;
+            break;
+        }
+        const float* t;
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.ln1w, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.ln1b, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.ln2w, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.ln2b, t, D);
+        ok = ok && (t = take_vec(c, (size_t)6 * D)) && upload(m, A.lerp, t, (size_t)6 * D);
+        ok = ok && take_mat(m, c, A.r, D, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.k, D, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.v, D, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.o, D, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.w1, D, A.Rw, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.w2, A.Rw, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.a1, D, A.Ra, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.a2, A.Ra, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.v1, D, A.Rv, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.v2, A.Rv, D, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.g1, D, A.Rg, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.g2, A.Rg, D, tmp0, tmp1);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.w0, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.a0, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.v0, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.kk, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.ka, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.rk, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.lnxw, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.lnxb, t, D);
+        ok = ok && take_mat(m, c, A.cmk, D, F, tmp0, tmp1);
+        ok = ok && take_mat(m, c, A.cmv, F, D, tmp0, tmp1);
+        ok = ok && (t = take_vec(c, D)) && upload(m, A.cmk_lerp, t, D);
+    }
+    if (ok && c.ok) {
+        const float* t;
+        ok = ok && (t = take_vec(c, D)) && upload(m, m->en_w, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, m->en_b, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, m->on_w, t, D);
+        ok = ok && (t = take_vec(c, D)) && upload(m, m->on_b, t, D);
+        ok = ok && (t = take_vec(c, (size_t)V * D)) && upload(m, m->embed, t, (size_t)V * D);
+        ok = ok && take_mat(m, c, m->head, D, V, tmp0, tmp1);
+    }
+    if (!ok || !c.ok) {
+        if (last_error().empty() || !c.ok) set_last_error("RWKV-7 blob is malformed or truncated");
+        free_rk(m);
+        return nullptr;
+    }
+    for (auto it = m->allocs.begin(); it != m->allocs.end();) {
+        if (*it == tmp0 || *it == tmp1) { (void)hipFree(*it); it = m->allocs.erase(it); }
+        else ++it;
+    }
+    const size_t B = max_batch;
+    m->S = ralloc<float>(m, B * L * NH * HS * HS);
+    m->shift = ralloc<float>(m, B * L * 2 * D);
+    m->x = ralloc<float>(m, B * D);
+    m->X6 = ralloc<float>(m, B * 6 * D);
+    m->r = ralloc<float>(m, B * D);
+    m->k = ralloc<float>(m, B * D);
+    m->v = ralloc<float>(m, B * D);
+    m->lo = ralloc<float>(m, B * 4 * kMaxRank);
+    m->dw = ralloc<float>(m, B * D);
+    m->da = ralloc<float>(m, B * D);
+    m->dv = ralloc<float>(m, B * D);
+    m->g = ralloc<float>(m, B * D);
+    m->y = ralloc<float>(m, B * D);
+    m->vfirst = ralloc<float>(m, B * D);
+    m->xk2 = ralloc<float>(m, B * D);
+    m->ck = ralloc<float>(m, B * F);
+    m->nrm = ralloc<float>(m, B * D);
+    m->logits = ralloc<float>(m, B * V);
+    m->tok = ralloc<int32_t>(m, B);
+    m->best = ralloc<unsigned long long>(m, B * 4096);
+    m->counter = ralloc<int32_t>(m, 1);
+    m->done = ralloc<int32_t>(m, 1);
+    m->gemm_work_floats = (size_t)16 << 20;
+    m->gemm_work = ralloc<float>(m, m->gemm_work_floats);
+    if (!m->S || !m->shift || !m->x || !m->X6 || !m->r || !m->k || !m->v || !m->lo || !m->dw ||
+        !m->da || !m->dv || !m->g || !m->y || !m->vfirst || !m->xk2 || !m->ck || !m->nrm ||
+        !m->logits || !m->tok || !m->best || !m->counter || !m->done || !m->gemm_work ||
+        hipMemset(m->S, 0, B * L * NH * HS * HS * sizeof(float)) != hipSuccess ||
+        hipMemset(m->shift, 0, B * L * 2 * D * sizeof(float)) != hipSuccess ||
+        hipMemset(m->counter, 0, sizeof(int32_t)) != hipSuccess ||
+        hipMemset(m->done, 0, sizeof(int32_t)) != hipSuccess ||
+        hipStreamCreateWithFlags(&m->work, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming) != hipSuccess) {
+        set_last_error("device setup failed");
+        free_rk(m);
+        return nullptr;
+    }
+    if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
+    if (const char* e = getenv("SNHIP_GEMM_MIN_BATCH")) m->gemm_min_batch = std::max(1, atoi(e));
+    m->ready = 1;
+    return m;
+}
+
+// Matrix products of one dependency level: GEMV jobs grouped by weight
+// format (up to kGemvMaxJobs per launch); from gemm_min_batch sequences on,
+// the MFMA GEMM for every product whose contraction is a multiple of 32.
+struct MMList {
+    SnHipRwkv7* m;
+    int B;
+    GemvJob jobs[8];
+    int blk[8];
+    int n = 0;
+
+    snhip_status add(const RMat& W, const float* X, int ldx, float* Y, int ldy, int epi) {
+        if (B >= m->gemm_min_batch && W.Kd % 32 == 0) {
+            GemmArgs g{};
+            g.X = X; g.ldx = ldx;
+            g.w = W.w; g.q = W.q; g.sc = W.sc; g.block = W.q ? W.block : 0;
+            g.M = B; g.N = W.M; g.K = W.Kd;
+            g.Y = Y; g.ldy = ldy;
+            g.epi = epi == EPI_ADD ? GEPI_ADD : epi == EPI_RELU2 ? GEPI_RELU2 : GEPI_STORE;
+            return launch_gemm(g, m->gemm_work, m->gemm_work_floats, m->work);
+        }
+        GemvJob j{};
+        j.w = W.w; j.q = W.q; j.sc = W.sc;
+        j.M = W.M; j.Kd = W.Kd; j.B = B;
+        j.X = X; j.ldx = ldx; j.Y = Y; j.ldy = ldy;
+        j.epi = epi;
+        jobs[n] = j;
+        blk[n] = W.q ? W.block : 0;
+        ++n;
+        return SNHIP_OK;
+    }
+
+    snhip_status flush(hipStream_t st) {
+        bool used[8] = {false};
+        for (int i = 0; i < n; ++i) {
+            if (used[i]) continue;
+            GemvJob batch[kGemvMaxJobs];
+            int nb = 0;
+            for (int j = i; j < n && nb < kGemvMaxJobs; ++j)
+                if (!used[j] && blk[j] == blk[i]) { batch[nb++] = jobs[j]; used[j] = true; }
+            SNHIP_CHECK(launch_gemv(batch, nb, blk[i], st));
+        }
+        n = 0;
+        return SNHIP_OK;
+    }
+};
+
+snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, hipStream_t st) {
+    const int D = m->D, F = m->F, NH = m->NH, L = m->L, HS = m->HS;
+    const size_t s_bstride = (size_t)L * NH * HS * HS, sh_bstride = (size_t)L * 2 * D;
+    const int ldl = 4 * kMaxRank;
+    float* lw = m->lo;
+    float* la = m->lo + kMaxRank;
+    float* lv = m->lo + 2 * kMaxRank;
+    float* lg = m->lo + 3 * kMaxRank;
+    hipLaunchKernelGGL(k_rk_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->en_w, m->en_b,
+                       m->x, D, m->vocab, m->eps);
+    MMList mm{m, B};
+    snhip_status rc;
+    for (int l = 0; l < L; ++l) {
+        const RkLayer& A = m->layers[l];
+        float* sh = m->shift + (size_t)l * 2 * D;
+        hipLaunchKernelGGL(k_rk_mix1, dim3(B), dim3(256), 0, st, m->x, A.ln1w, A.ln1b, A.lerp, sh,
+                           sh_bstride, m->X6, D, m->eps);
+        const float* xr = m->X6;
+        const float* xw = m->X6 + D;
+        const float* xk = m->X6 + 2 * D;
+        const float* xv = m->X6 + 3 * D;
+        const float* xa = m->X6 + 4 * D;
+        const float* xg = m->X6 + 5 * D;
+        const int ld6 = 6 * D;
+        if ((rc = mm.add(A.r, xr, ld6, m->r, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.k, xk, ld6, m->k, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.v, xv, ld6, m->v, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.w1, xw, ld6, lw, ldl, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.a1, xa, ld6, la, ldl, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.g1, xg, ld6, lg, ldl, EPI_STORE)) != SNHIP_OK) return rc;
+        if (l > 0 && (rc = mm.add(A.v1, xv, ld6, lv, ldl, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        hipLaunchKernelGGL(k_rk_lora_act, dim3(B), dim3(256), 0, st, lw, A.Rw, lg, A.Rg, ldl);
+        if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.a2, la, ldl, m->da, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.g2, lg, ldl, m->g, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if (l > 0 && (rc = mm.add(A.v2, lv, ldl, m->dv, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        HeadArgs H{};
+        H.r = m->r; H.k = m->k; H.v = m->v; H.dw = m->dw; H.da = m->da; H.dv = m->dv; H.g = m->g;
+        H.vfirst = m->vfirst;
+        H.w0 = A.w0; H.a0 = A.a0; H.v0 = A.v0; H.kk_w = A.kk; H.ka_w = A.ka; H.rk_w = A.rk;
+        H.lnx_w = A.lnxw; H.lnx_b = A.lnxb;
+        H.S = m->S + (size_t)l * NH * HS * HS;
+        H.s_bstride = s_bstride;
+        H.y = m->y;
+        H.D = D;
+        H.first = l == 0;
+        hipLaunchKernelGGL(k_rk_heads, dim3(NH, B), dim3(256), 0, st, H);
+        if ((rc = mm.add(A.o, m->y, D, m->x, D, EPI_ADD)) != SNHIP_OK) return rc;
+        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        hipLaunchKernelGGL(k_rk_mix2, dim3(B), dim3(256), 0, st, m->x, A.ln2w, A.ln2b, A.cmk_lerp,
+                           sh + D, sh_bstride, m->xk2, D, m->eps);
+        if ((rc = mm.add(A.cmk, m->xk2, D, m->ck, F, EPI_RELU2)) != SNHIP_OK) return rc;
+        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.cmv, m->ck, F, m->x, D, EPI_ADD)) != SNHIP_OK) return rc;
+        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+    }
+    hipLaunchKernelGGL(k_rk_ln, dim3(B), dim3(256), 0, st, m->x, m->on_w, m->on_b, m->nrm, D, m->eps);
+    const RMat& Hm = m->head;
+    if (B >= m->gemm_min_batch) {
+        if ((rc = mm.add(Hm, m->nrm, D, logits_out, m->vocab, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        if (greedy) {
+            const int nblk = 64;
+            hipLaunchKernelGGL(k_rk_argmax_partial, dim3(nblk, B), dim3(256), 0, st, logits_out,
+                               m->vocab, m->best);
+            hipLaunchKernelGGL(k_rk_finalize, dim3(B), dim3(256), 0, st, m->best, nblk, B, m->tok,
+                               m->tok_hist, m->counter, m->done, m->hist_cap);
+        }
+    } else {
+        GemvJob j{};
+        j.w = Hm.w; j.q = Hm.q; j.sc = Hm.sc;
+        j.M = Hm.M; j.Kd = Hm.Kd; j.B = B;
+        j.X = m->nrm; j.ldx = D; j.Y = logits_out; j.ldy = m->vocab;
+        j.epi = greedy ? EPI_ARGMAX : EPI_STORE;
+        j.best = m->best;
+        SNHIP_CHECK(launch_gemv(&j, 1, Hm.q ? Hm.block : 0, st));
+        if (greedy)
+            hipLaunchKernelGGL(k_rk_finalize, dim3(B), dim3(256), 0, st, m->best, j.nblk, B, m->tok,
+                               m->tok_hist, m->counter, m->done, m->hist_cap);
+    }
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
+// reps steps on the internal stream, ordered after the caller's stream;
+// captured once per (B, logits, greedy) into a graph and replayed.
+snhip_status run_steps(SnHipRwkv7* m, int B, float* logits_out, bool greedy, int reps) {
+    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
+    SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
+    if (!m->use_graphs) {
+        for (int i = 0; i < reps; ++i) {
+            const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
+            if (rc != SNHIP_OK) return rc;
+        }
+    } else {
+        const auto key = std::make_tuple(B, (const void*)logits_out, greedy ? 1 : 0);
+        auto it = m->graphs.find(key);
+        if (it == m->graphs.end()) {
+            if (m->graphs.size() >= 16) {
+                for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+                m->graphs.clear();
+            }
+            hipGraph_t g = nullptr;
+            SNHIP_CHECK(hipStreamBeginCapture(m->work, hipStreamCaptureModeThreadLocal));
+            const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
+            const hipError_t ec = hipStreamEndCapture(m->work, &g);
+            if (rc != SNHIP_OK) { if (g) (void)hipGraphDestroy(g); return rc; }
+            SNHIP_CHECK(ec);
+            hipGraphExec_t ex = nullptr;
+            const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            SNHIP_CHECK(ei);
+            it = m->graphs.emplace(key, ex).first;
+        }
+        for (int i = 0; i < reps; ++i) SNHIP_CHECK(hipGraphLaunch(it->second, m->work));
+    }
+    SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
+    SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
+    return SNHIP_OK;
+}
+
+bool tokens_ok(const SnHipRwkv7* m, const int32_t* t, int n) {
+    for (int i = 0; i < n; ++i)
+        if (t[i] < 0 || t[i] >= m->vocab) return false;
+    return true;
+}
+
+snhip_status step_host(SnHipRwkv7* m, const int32_t* tokens, int B, float* logits) {
+    if (!m || !tokens || !logits || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    if (!tokens_ok(m, tokens, B)) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens, B * sizeof(int32_t), hipMemcpyHostToDevice, m->stream));
+    const snhip_status rc = run_steps(m, B, m->logits, false, 1);
+    if (rc != SNHIP_OK) return rc;
+    SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)B * m->vocab * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream));
+    SNHIP_CHECK(hipStreamSynchronize(m->stream));
+    return SNHIP_OK;
+}
+
+snhip_status prefill_host(SnHipRwkv7* m, const int32_t* tokens, int n, float* logits) {
+    if (!m || !tokens || n <= 0 || !logits) return SNHIP_E_INVAL;
+    if (!tokens_ok(m, tokens, n)) return SNHIP_E_INVAL;
+    // rwkv7.c:362-364: the step, once per token, in order.
+    for (int i = 0; i < n; ++i) {
+        SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens + i, sizeof(int32_t), hipMemcpyHostToDevice, m->stream));
+        const snhip_status rc = run_steps(m, 1, m->logits, false, 1);
+        if (rc != SNHIP_OK) return rc;
+    }
+    SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float),
+                               hipMemcpyDeviceToHost, m->stream));
+    SNHIP_CHECK(hipStreamSynchronize(m->stream));
+    return SNHIP_OK;
+}
+
+}  // namespace
+}  // namespace snhip
+
+using namespace snhip;
+
+extern "C" {
+
+SnHipRwkv7* snhip_rk_load(const char* path) {
+    return load_rk(path, 1, SNHIP_WEIGHTS_STORED, kRkBlobBlock);
+}
+
+SnHipRwkv7* snhip_rk_load_ex(const char* path, int32_t max_batch, int32_t weight_format,
+                             int32_t block) {
+    return load_rk(path, max_batch, weight_format, block);
+}
+
+void snhip_rk_free(SnHipRwkv7* m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    else (void)hipDeviceSynchronize();
+    free_rk(m);
+}
+
+void snhip_rk_reset(SnHipRwkv7* m) {
+    if (!m) return;
+    const size_t B = m->max_batch;
+    (void)hipMemsetAsync(m->S, 0, B * m->L * m->NH * m->HS * m->HS * sizeof(float), m->stream);
+    (void)hipMemsetAsync(m->shift, 0, B * m->L * 2 * m->D * sizeof(float), m->stream);
+    (void)hipStreamSynchronize(m->stream);
+}
+
+void snhip_rk_step(SnHipRwkv7* m, int token, float* logits) {
+    const int32_t t = token;
+    (void)step_host(m, &t, 1, logits);
+}
+
+void snhip_rk_prefill(SnHipRwkv7* m, const int* tokens, int n, float* logits) {
+    (void)prefill_host(m, tokens, n, logits);
+}
+
+int snhip_rk_vocab(const SnHipRwkv7* m) { return m ? m->vocab : 0; }
+int snhip_rk_ready(const SnHipRwkv7* m) { return m && m->ready; }
+
+snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream) {
+    if (!m) return SNHIP_E_INVAL;
+    m->stream = as_stream(stream);
+    return SNHIP_OK;
+}
+
+int32_t snhip_rk_max_batch(const SnHipRwkv7* m) { return m ? m->max_batch : 0; }
+
+snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
+                                     float* logits_dev) {
+    if (!m || !tokens_dev || !logits_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens_dev, B * sizeof(int32_t), hipMemcpyDeviceToDevice, m->stream));
+    return run_steps(m, B, logits_dev, false, 1);
+}
+
+snhip_status snhip_rk_decode_greedy_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
+                                        int32_t n_steps, int32_t* out_tokens_dev,
+                                        float* logits_dev) {
+    if (!m || !tokens_dev || !out_tokens_dev || B <= 0 || B > m->max_batch || n_steps <= 0)
+        return SNHIP_E_INVAL;
+    if ((long)n_steps * B > (long)m->hist_cap || !m->tok_hist) {
+        // Grow the token history; graphs bake its address, so drop them.
+        SNHIP_CHECK(hipStreamSynchronize(m->stream));
+        SNHIP_CHECK(hipStreamSynchronize(m->work));
+        for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+        m->graphs.clear();
+        long cap = 256L * m->max_batch;
+        while (cap < (long)n_steps * B) cap *= 2;
+        if (cap > (1L << 30)) return SNHIP_E_INVAL;
+        int32_t* hbuf = nullptr;
+        SNHIP_CHECK(hipMalloc(&hbuf, (size_t)cap * sizeof(int32_t)));
+        if (m->tok_hist) {
+            (void)hipFree(m->tok_hist);
+            for (auto it = m->allocs.begin(); it != m->allocs.end(); ++it)
+                if (*it == m->tok_hist) { m->allocs.erase(it); break; }
+        }
+        m->tok_hist = hbuf;
+        m->allocs.push_back(hbuf);
+        m->hist_cap = (int)cap;
+    }
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, tokens_dev, B * sizeof(int32_t), hipMemcpyDeviceToDevice, m->stream));
+    SNHIP_CHECK(hipMemsetAsync(m->counter, 0, sizeof(int32_t), m->stream));
+    const snhip_status rc = run_steps(m, B, logits_dev ? logits_dev : m->logits, true, n_steps);
+    if (rc != SNHIP_OK) return rc;
+    SNHIP_CHECK(hipMemcpyAsync(out_tokens_dev, m->tok_hist, (size_t)n_steps * B * sizeof(int32_t),
+                               hipMemcpyDeviceToDevice, m->stream));
+    return SNHIP_OK;
+}
+
+snhip_status snhip_rk_get_state_dev(SnHipRwkv7* m, float* S_dev, float* shift_dev, int32_t B) {
+    if (!m || !S_dev || !shift_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(S_dev, m->S, (size_t)B * m->L * m->NH * m->HS * m->HS * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->stream));
+    SNHIP_CHECK(hipMemcpyAsync(shift_dev, m->shift, (size_t)B * m->L * 2 * m->D * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->stream));
+    return SNHIP_OK;
+}
+
+snhip_status snhip_rk_set_state_dev(SnHipRwkv7* m, const float* S_dev, const float* shift_dev,
+                                    int32_t B) {
+    if (!m || !S_dev || !shift_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    SNHIP_CHECK(hipMemcpyAsync(m->S, S_dev, (size_t)B * m->L * m->NH * m->HS * m->HS * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->stream));
+    SNHIP_CHECK(hipMemcpyAsync(m->shift, shift_dev, (size_t)B * m->L * 2 * m->D * sizeof(float),
+                               hipMemcpyDeviceToDevice, m->stream));
+    return SNHIP_OK;
+}
+
+// sn_abi.c:94-134 mirror
+SnHipRwkv7* snhip_abi_rwkv7_load(const char* blob_path) {
+    if (!blob_path) return nullptr;
+    return snhip_rk_load(blob_path);
+}
+
+snhip_status snhip_abi_rwkv7_step(SnHipRwkv7* m, int32_t token, float* logits) {
+    if (!m || !logits || token < 0) return SNHIP_E_INVAL;
+    return step_host(m, &token, 1, logits);
+}
+
+snhip_status snhip_abi_rwkv7_prefill(SnHipRwkv7* m, const int32_t* tokens, int32_t n,
+                                     float* logits) {
+    if (!m || !tokens || !logits || n <= 0) return SNHIP_E_INVAL;
+    return prefill_host(m, tokens, n, logits);
+}
+
+snhip_status snhip_abi_rwkv7_reset(SnHipRwkv7* m) {
+    if (!m) return SNHIP_E_INVAL;
+    snhip_rk_reset(m);
+    return SNHIP_OK;
+}
+
+void snhip_abi_rwkv7_free(SnHipRwkv7* m) { snhip_rk_free(m); }
+
+int32_t snhip_abi_rwkv7_vocab(const SnHipRwkv7* m) { return m ? m->vocab : 0; }
+
+}  // extern "C"

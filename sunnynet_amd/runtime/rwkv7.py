@@ -1,0 +1,118 @@
+"""RWKV-7 decode handle on the GPU (include/snhip_rwkv7.h).
+
+``HipRwkv7(path)`` loads the reference's v3 runtime blob and offers the
+reference C handle's operations (sunnynet/runtime/rwkv7.h:16-28): ``reset()``,
+``step(token) -> list[float]`` and ``prefill(tokens) -> list[float]`` (host
+logits, one B=1 sequence). Extensions: ``max_batch`` sequences, weight format
+(``"stored"`` as in the blob, ``"fp32"``, ``"int4"`` with a group ``block``),
+``step_batch`` / ``decode_greedy`` on device tensors, and ``get_state`` /
+``set_state`` (S (B, L, H, 64, 64), shift (B, L, 2, D)).
+"""
+from __future__ import annotations
+
+import ctypes
+import struct
+
+import numpy as np
+import torch
+
+from .. import _native
+
+__all__ = ["HipRwkv7"]
+
+FORMATS = {"fp32": 0, "int4": 1, "stored": 2}
+
+
+class HipRwkv7:
+    def __init__(self, path, *, max_batch: int = 1, weights: str = "stored", block: int = 32,
+                 device=None):
+        self._lib = _native.lib()
+        self.device = torch.device(device or "cuda:0")
+        with open(path, "rb") as f:
+            h = struct.unpack("<10i", f.read(40))
+        self.layers, self.dim, self.head_size, self.n_head = h[2], h[3], h[4], h[5]
+        self.max_batch = int(max_batch)
+        with torch.cuda.device(self.device):
+            self._h = self._lib.snhip_rk_load_ex(str(path).encode(), self.max_batch,
+                                                 FORMATS[weights], int(block))
+        if not self._h:
+            raise RuntimeError(f"snhip_rk_load failed: {path}: {_native.last_error()}")
+        if not self._lib.snhip_rk_ready(self._h):
+            raise RuntimeError("snhip_rk_load returned a handle that is not ready")
+        self.vocab = int(self._lib.snhip_rk_vocab(self._h))
+        self._logits = (ctypes.c_float * self.vocab)()
+        self._bind_stream()
+
+    def _bind_stream(self):
+        _native.check(self._lib.snhip_rk_set_stream(self._h, _native.stream_handle(self.device)),
+                      "snhip_rk_set_stream")
+
+    # ---------------------------------------------- reference-shaped surface
+    def reset(self):
+        self._bind_stream()
+        self._lib.snhip_rk_reset(self._h)
+
+    def step(self, token: int) -> list:
+        self._bind_stream()
+        self._lib.snhip_rk_step(self._h, int(token), ctypes.byref(self._logits))
+        return np.frombuffer(self._logits, np.float32).tolist()
+
+    def prefill(self, tokens) -> list:
+        toks = [int(t) for t in tokens]
+        self._bind_stream()
+        buf = (ctypes.c_int * len(toks))(*toks)
+        self._lib.snhip_rk_prefill(self._h, buf, len(toks), ctypes.byref(self._logits))
+        return np.frombuffer(self._logits, np.float32).tolist()
+
+    # -------------------------------------------------------- device surface
+    def step_batch(self, tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        B = int(tokens.shape[0])
+        tokens = tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        if out is None:
+            out = torch.empty(B, self.vocab, device=self.device, dtype=torch.float32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_rk_step_batch_dev(self._h, tokens.data_ptr(), B,
+                                                        out.data_ptr()), "snhip_rk_step_batch_dev")
+        return out
+
+    def decode_greedy(self, tokens: torch.Tensor, n_steps: int, logits: torch.Tensor | None = None):
+        B = int(tokens.shape[0])
+        tokens = tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        out = torch.empty(n_steps, B, device=self.device, dtype=torch.int32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_rk_decode_greedy_dev(
+            self._h, tokens.data_ptr(), B, int(n_steps), out.data_ptr(),
+            logits.data_ptr() if logits is not None else None), "snhip_rk_decode_greedy_dev")
+        return out
+
+    def get_state(self, B: int | None = None):
+        B = self.max_batch if B is None else B
+        S = torch.empty(B, self.layers, self.n_head, self.head_size, self.head_size,
+                        device=self.device)
+        sh = torch.empty(B, self.layers, 2, self.dim, device=self.device)
+        self._bind_stream()
+        _native.check(self._lib.snhip_rk_get_state_dev(self._h, S.data_ptr(), sh.data_ptr(), B),
+                      "snhip_rk_get_state_dev")
+        return S, sh
+
+    def set_state(self, S: torch.Tensor, shift: torch.Tensor):
+        B = int(S.shape[0])
+        S = S.to(device=self.device, dtype=torch.float32).contiguous()
+        shift = shift.to(device=self.device, dtype=torch.float32).contiguous()
+        if S.shape != (B, self.layers, self.n_head, self.head_size, self.head_size) or \
+                shift.shape != (B, self.layers, 2, self.dim):
+            raise ValueError("state must be S (B,L,H,64,64) and shift (B,L,2,D)")
+        self._bind_stream()
+        _native.check(self._lib.snhip_rk_set_state_dev(self._h, S.data_ptr(), shift.data_ptr(), B),
+                      "snhip_rk_set_state_dev")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.snhip_rk_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

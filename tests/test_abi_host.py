@@ -29,7 +29,8 @@ def test_version_matches_header():
 
 def test_caps_include_core():
     names = abi.cap_names()
-    for want in ("recur_scan", "recur_step", "threads", "device_ptr", "int4"):
+    for want in ("recur_scan", "recur_step", "rwkv7", "threads", "device_ptr", "sunny_model",
+                 "int4", "batch", "prefill"):
         assert want in names
     assert "quant_i8" not in names
 
