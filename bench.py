@@ -16,6 +16,9 @@ steps on the device at B=1 and B=64, fp32; and the same shape with INT4 g32
 weights (matmuls ~ N(0, 0.02)) after a T=2048 prefill at B=1, 8, 32. Each
 entry gives tokens/s, us/step and the HBM roofline of the step's weight
 bytes; ``cpu_baseline`` there is the reference ``sn_step`` on host cores.
+``decode.rwkv7``: the RWKV-7 configuration (12 layers, D=768, vocab 65536,
+INT4 g32), 512-token prompt, 128 greedy steps at B=1 and B=64, with the
+reference ``sn_rk_step`` timed on its INT4 blob.
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -215,7 +218,82 @@ def bench_decode(cpu: bool):
             out["cases"].append(case)
     if cpu:
         out["cpu_baseline"] = cpu_decode_baseline(p32, cfg)
+    out["rwkv7"] = bench_rwkv7(cpu)
     return out
+
+
+def bench_rwkv7(cpu: bool):
+    """RWKV-7 12 layers, D=768, 12 heads of 64, F=3072, vocab 65536 (seed-2
+    synthetic weights), INT4 g32 quantized at load: a 512-token random prompt
+    by stepping, then 128 greedy steps on the device at B=1 and B=64."""
+    import tempfile
+
+    from sunnynet_amd.runtime.rwkv7 import HipRwkv7
+    from sunnynet_amd.rwkv7 import RWKV_CFG4, init_rwkv7, pack_rwkv7_blob
+    cfg = RWKV_CFG4
+    dev = torch.device("cuda:0")
+    tmp = tempfile.mkdtemp(prefix="snhip_bench_rk_")
+    log("[bench] RWKV-7 weights (seed 2)")
+    w = init_rwkv7(cfg, 2)
+    p32 = os.path.join(tmp, "rk_fp32.bin")
+    with open(p32, "wb") as f:
+        f.write(pack_rwkv7_blob(w))
+    n = cfg.matmul_params()
+    wbytes = n // 2 + (n // 32) * 4
+    sbytes = 2 * cfg.layers * cfg.n_head * cfg.head_size ** 2 * 4     # state read + write
+    out = {"model": "RWKV-7 L=12 D=768 H=12x64 F=3072 V=65536 ranks (64,64,32,128), INT4 g32",
+           "steps": 128, "prompt": 512, "cases": []}
+    g = torch.Generator(device="cpu").manual_seed(321)
+    for B in (1, 64):
+        hm = HipRwkv7(p32, weights="int4", block=32, max_batch=B)
+        prompts = torch.randint(0, cfg.vocab, (out["prompt"], B), generator=g, dtype=torch.int32).to(dev)
+        lg = torch.empty(B, cfg.vocab, device=dev)
+        for t in range(out["prompt"]):
+            hm.step_batch(prompts[t], out=lg)
+        tok = lg.argmax(1).int()
+        hm.decode_greedy(tok, 4)
+        torch.cuda.synchronize()
+        steps = out["steps"]
+        ms = _time_ms(lambda: hm.decode_greedy(tok, steps)) / steps
+        hm.close()
+        nb = wbytes + B * sbytes
+        case = {"weights": "int4-g32", "B": B, "us_per_step": round(ms * 1e3, 2),
+                "tok_s": round(B / ms * 1e3, 1), "bytes_per_step": nb,
+                "hbm_gbs": round(nb / (ms * 1e-3) / 1e9, 2),
+                "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"[bench] rwkv7 B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s")
+        out["cases"].append(case)
+    if cpu:
+        out["cpu_baseline"] = cpu_rwkv7_baseline(w, tmp)
+    return out
+
+
+def cpu_rwkv7_baseline(w, tmp):
+    """The reference sn_rk_step (B = 1) on the INT4 v3 blob (group 64, its
+    W4A8 path), single thread as rwkv7.c runs; bounded to ~10 s."""
+    import oracle
+    from sunnynet_amd.rwkv7 import pack_rwkv7_blob
+    if not oracle.ref_available():
+        return {"value": None, "unit": "tok/s (B=1)", "cores": 1, "kind": "reference",
+                "sample": "reference build absent"}
+    p4 = os.path.join(tmp, "rk_q4.bin")
+    with open(p4, "wb") as f:
+        f.write(pack_rwkv7_blob(w, int4=True))
+    m = oracle.RefRk(p4, w.cfg.vocab)
+    for t in range(4):
+        m.step(t)
+    times = []
+    deadline = time.perf_counter() + 10.0
+    while len(times) < 20 and time.perf_counter() < deadline:
+        t0 = time.perf_counter()
+        m.step(len(times) + 100)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    log(f"[bench] cpu reference sn_rk_step int4: {med*1e3:.2f} ms/token")
+    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": 1, "kind": "reference",
+            "ms_per_token": round(med * 1e3, 3),
+            "sample": f"RWKV-7 same shape, INT4 group-64 blob (W4A8), 4 warm-up steps then median "
+                      f"of {len(times)} single steps"}
 
 
 def cpu_decode_baseline(path, cfg):
