@@ -59,35 +59,8 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// Values per thread held in registers by the LayerNorm kernels (n <= 4096).
+// Largest LayerNorm row: 16 values per thread of a 256-thread block.
 constexpr int kLnPer = 16;
-
-// Two-pass LayerNorm statistics (sunnynet.c:198-210 form) over n values held
-// in registers, kLnPer per thread of a 256-thread block (element i*256+tid).
-__device__ __forceinline__ void ln_stats_reg(const float (&xv)[kLnPer], int n, float eps,
-                                             float* red, float& mean, float& rstd) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kLnPer; ++k)
-        if (k * 256 + (int)threadIdx.x < n) sum += xv[k];
-    mean = block_sum256(sum, red) / (float)n;
-    float vs = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kLnPer; ++k)
-        if (k * 256 + (int)threadIdx.x < n) {
-            const float d = xv[k] - mean;
-            vs += d * d;
-        }
-    rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
-}
-
-__device__ __forceinline__ void load_row(float (&xv)[kLnPer], const float* x, int n) {
-#pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        xv[k] = i < n ? x[i] : 0.0f;
-    }
-}
 
 __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
                         float* __restrict__ x, int D, int vocab) {
@@ -98,37 +71,73 @@ __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict
         x[(size_t)b * D + i] = ok ? embed[(size_t)t * D + i] : __builtin_nanf("");
 }
 
+// Two-pass LayerNorm statistics (sunnynet.c:198-210 form) over n values held
+// in registers, PER per thread of a 256-thread block (element k*256+tid).
+template <int PER>
+__device__ __forceinline__ void ln_stats_t(const float (&xv)[PER], int n, float eps, float* red,
+                                           float& mean, float& rstd) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+        if (k * 256 + (int)threadIdx.x < n) sum += xv[k];
+    mean = block_sum256(sum, red) / (float)n;
+    float vs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+        if (k * 256 + (int)threadIdx.x < n) {
+            const float d = xv[k] - mean;
+            vs += d * d;
+        }
+    rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
+}
+
 // raw = LN(x); at = raw + conv(raw, hist); hist <- [raw, hist[0..K-3]] in place.
-// One block per sequence; conv order as sunnynet.c:227-237.
+// One block per sequence; conv order as sunnynet.c:227-237. Every load (x,
+// gains, taps, history) is issued before the statistics are reduced.
+template <int PER>
 __global__ __launch_bounds__(256) void k_ln_conv(
         const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ c,
         const float* __restrict__ dw, float* __restrict__ hist, size_t hist_bstride,
         float* __restrict__ at, int D, int K, float eps) {
     __shared__ float red[4];
-    const int b = blockIdx.x;
+    const int b = blockIdx.x, tid = threadIdx.x;
     const float* xb = x + (size_t)b * D;
     float* hb = hist + (size_t)b * hist_bstride;
-    float xv[kLnPer];
-    load_row(xv, xb, D);
+    float xv[PER], gv[PER], cv[PER], h[kMaxTaps - 1][PER], dv[kMaxTaps][PER];
+#pragma unroll
+    for (int kk = 0; kk < PER; ++kk) {
+        const int i = min(kk * 256 + tid, D - 1);   // lanes past D load a valid element
+        xv[kk] = xb[i];
+        gv[kk] = g[i];
+        cv[kk] = c[i];
+#pragma unroll
+        for (int t = 0; t < kMaxTaps - 1; ++t) h[t][kk] = t < K - 1 ? hb[(size_t)t * D + i] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxTaps; ++t) dv[t][kk] = t < K ? dw[(size_t)t * D + i] : 0.0f;
+    }
     float mean, rstd;
-    ln_stats_reg(xv, D, eps, red, mean, rstd);
+    ln_stats_t<PER>(xv, D, eps, red, mean, rstd);
 #pragma unroll
-    for (int kk = 0; kk < kLnPer; ++kk) {
-        const int i = kk * 256 + threadIdx.x;
+    for (int kk = 0; kk < PER; ++kk) {
+        const int i = kk * 256 + tid;
         if (i >= D) continue;
-        const float raw = (xv[kk] - mean) * rstd * g[i] + c[i];
+        const float raw = (xv[kk] - mean) * rstd * gv[kk] + cv[kk];
         if (K > 1) {
-            float h[kMaxTaps - 1];
+            float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < kMaxTaps - 1; ++k) h[k] = k < K - 1 ? hb[(size_t)k * D + i] : 0.0f;
-            float acc = raw * dw[(size_t)(K - 1) * D + i];
+            for (int t = 0; t < kMaxTaps; ++t)
+                if (t == K - 1) acc = raw * dv[t][kk];
 #pragma unroll
-            for (int k = 0; k < kMaxTaps - 1; ++k)
-                if (k < K - 1) acc = acc + h[k] * dw[(size_t)(K - 2 - k) * D + i];
+            for (int t = 0; t < kMaxTaps - 1; ++t)
+                if (t < K - 1) {
+#pragma unroll
+                    for (int u = 0; u < kMaxTaps; ++u)
+                        if (u == K - 2 - t) acc = acc + h[t][kk] * dv[u][kk];
+                }
             at[(size_t)b * D + i] = raw + acc;
 #pragma unroll
-            for (int k = kMaxTaps - 2; k >= 1; --k)
-                if (k <= K - 2) hb[(size_t)k * D + i] = h[k - 1];
+            for (int t = kMaxTaps - 2; t >= 1; --t)
+                if (t <= K - 2) hb[(size_t)t * D + i] = h[t - 1][kk];
             hb[i] = raw;
         } else {
             at[(size_t)b * D + i] = raw;
@@ -136,22 +145,65 @@ __global__ __launch_bounds__(256) void k_ln_conv(
     }
 }
 
-// y = LN(x) per sequence (norm_mix and norm_out).
+// y = LN(x) per sequence (norm_mix and norm_out); loads issued up front.
+template <int PER>
 __global__ __launch_bounds__(256) void k_ln(const float* __restrict__ x, int ldx,
                                             const float* __restrict__ g,
                                             const float* __restrict__ c, float* __restrict__ y,
                                             int ldy, int n, float eps) {
     __shared__ float red[4];
-    const int b = blockIdx.x;
-    float xv[kLnPer];
-    load_row(xv, x + (size_t)b * ldx, n);
-    float mean, rstd;
-    ln_stats_reg(xv, n, eps, red, mean, rstd);
+    const int b = blockIdx.x, tid = threadIdx.x;
+    float xv[PER], gv[PER], cv[PER];
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        if (i < n) y[(size_t)b * ldy + i] = (xv[k] - mean) * rstd * g[i] + c[i];
+    for (int k = 0; k < PER; ++k) {
+        const int i = min(k * 256 + tid, n - 1);
+        xv[k] = x[(size_t)b * ldx + i];
+        gv[k] = g[i];
+        cv[k] = c[i];
     }
+    float mean, rstd;
+    ln_stats_t<PER>(xv, n, eps, red, mean, rstd);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = k * 256 + tid;
+        if (i < n) y[(size_t)b * ldy + i] = (xv[k] - mean) * rstd * gv[k] + cv[k];
+    }
+}
+
+// Per-thread element count for a row of n (<= 4096) values.
+int ln_per(int n) {
+    const int p = (n + 255) / 256;
+    return p <= 1 ? 1 : p <= 2 ? 2 : p <= 4 ? 4 : p <= 6 ? 6 : p <= 8 ? 8 : 16;
+}
+
+void launch_ln(int rows, const float* x, int ldx, const float* g, const float* c, float* y,
+               int ldy, int n, float eps, hipStream_t st) {
+    const dim3 grid((unsigned)rows), blk(256);
+    switch (ln_per(n)) {
+    case 1: hipLaunchKernelGGL(k_ln<1>, grid, blk, 0, st, x, ldx, g, c, y, ldy, n, eps); break;
+    case 2: hipLaunchKernelGGL(k_ln<2>, grid, blk, 0, st, x, ldx, g, c, y, ldy, n, eps); break;
+    case 4: hipLaunchKernelGGL(k_ln<4>, grid, blk, 0, st, x, ldx, g, c, y, ldy, n, eps); break;
+    case 6: hipLaunchKernelGGL(k_ln<6>, grid, blk, 0, st, x, ldx, g, c, y, ldy, n, eps); break;
+    case 8: hipLaunchKernelGGL(k_ln<8>, grid, blk, 0, st, x, ldx, g, c, y, ldy, n, eps); break;
+    default: hipLaunchKernelGGL(k_ln<16>, grid, blk, 0, st, x, ldx, g, c, y, ldy, n, eps); break;
+    }
+}
+
+void launch_ln_conv(int rows, const float* x, const float* g, const float* c, const float* dw,
+                    float* hist, size_t hist_bstride, float* at, int D, int K, float eps,
+                    hipStream_t st) {
+    const dim3 grid((unsigned)rows), blk(256);
+#define SNHIP_LNC(P) hipLaunchKernelGGL(k_ln_conv<P>, grid, blk, 0, st, x, g, c, dw, hist, \
+                                        hist_bstride, at, D, K, eps)
+    switch (ln_per(D)) {
+    case 1: SNHIP_LNC(1); break;
+    case 2: SNHIP_LNC(2); break;
+    case 4: SNHIP_LNC(4); break;
+    case 6: SNHIP_LNC(6); break;
+    case 8: SNHIP_LNC(8); break;
+    default: SNHIP_LNC(16); break;
+    }
+#undef SNHIP_LNC
 }
 
 // Competitive gate, decay gate and state update for every (b, channel):
@@ -437,6 +489,8 @@ struct SnHipModel {
     bool gemm_ok = true;
     float* gemm_work = nullptr;           // split-K partials
     size_t gemm_work_floats = 0;
+    unsigned* gemm_cnt = nullptr;         // skinny-GEMM tile counters (zero between launches)
+    int gemm_ncnt = 0;
     // Chunked prefill workspace for (max_batch x pf_chunk) rows, on first use.
     int pf_chunk = 0;
     float *pf_x = nullptr, *pf_raw = nullptr, *pf_at = nullptr, *pf_v = nullptr, *pf_q = nullptr,
@@ -725,7 +779,14 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     if (!m->gemm_ok) m->gemm_min_batch = 1 << 30;
     m->gemm_work_floats = (size_t)16 << 20;
     m->gemm_work = dalloc<float>(m, m->gemm_work_floats);
-    if (!m->gemm_work) { set_last_error("out of device memory"); free_model(m); return nullptr; }
+    m->gemm_ncnt = 4096;
+    m->gemm_cnt = dalloc<unsigned>(m, m->gemm_ncnt);
+    if (!m->gemm_work || !m->gemm_cnt ||
+        hipMemset(m->gemm_cnt, 0, m->gemm_ncnt * sizeof(unsigned)) != hipSuccess) {
+        set_last_error("out of device memory");
+        free_model(m);
+        return nullptr;
+    }
     setup_persist(m);
     m->ready = 1;
     return m;
@@ -758,8 +819,15 @@ GemmArgs gemm_for(const SnHipModel* m, const Mat& W, const float* X, long ldx, i
     return g;
 }
 
+GemmWork gemm_work(const SnHipModel* m) {
+    GemmWork w;
+    w.part = m->gemm_work; w.part_floats = m->gemm_work_floats;
+    w.cnt = m->gemm_cnt; w.ncnt = m->gemm_ncnt;
+    return w;
+}
+
 snhip_status run_gemm(SnHipModel* m, const GemmArgs& g, hipStream_t st) {
-    return launch_gemm(g, m->gemm_work, m->gemm_work_floats, st);
+    return launch_gemm(g, gemm_work(m), st);
 }
 
 __global__ void k_copy_rows(const float* __restrict__ src, long lds, float* __restrict__ dst,
@@ -772,8 +840,7 @@ __global__ void k_copy_rows(const float* __restrict__ src, long lds, float* __re
 snhip_status enqueue_head(SnHipModel* m, int B, const float* x, float* logits_out, bool greedy,
                           hipStream_t st) {
     const int D = m->D;
-    hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, x, D, m->no_g, m->no_c, m->nrm, D, D,
-                       m->eps);
+    launch_ln(B, x, D, m->no_g, m->no_c, m->nrm, D, D, m->eps, st);
     if (B >= m->gemm_min_batch) {
         const snhip_status rc = run_gemm(m, gemm_for(m, m->head, m->nrm, D, B, logits_out, m->vocab), st);
         if (rc != SNHIP_OK) return rc;
@@ -814,22 +881,33 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
         const Layer& A = m->layers[l];
         float* s_l = m->s + (size_t)l * D;
         float* h_l = m->hist + (size_t)l * (m->kh ? m->kh : 1) * D;
-        hipLaunchKernelGGL(k_ln_conv, dim3(B), dim3(256), 0, st, m->x, A.ni_g, A.ni_c, A.dw, h_l,
-                           hbs, m->at, D, m->K, m->eps);
+        launch_ln_conv(B, m->x, A.ni_g, A.ni_c, A.dw, h_l, hbs, m->at, D, m->K, m->eps, st);
         const long n = (long)B * D;
         if (mm) {
             snhip_status rc;
-            if ((rc = run_gemm(m, gemm_for(m, A.V, m->at, D, B, m->v, R), st)) != SNHIP_OK) return rc;
-            if ((rc = run_gemm(m, gemm_for(m, A.Ws, s_l, (long)sbs, B, m->sfb, D), st)) != SNHIP_OK) return rc;
-            if ((rc = run_gemm(m, gemm_for(m, A.U, m->v, R, B, m->q, 2 * D), st)) != SNHIP_OK) return rc;
-            hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                               m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
+            // v = V at and sfb = W_eff s (old state) in one launch.
+            if ((rc = launch_gemm2(gemm_for(m, A.V, m->at, D, B, m->v, R),
+                                   gemm_for(m, A.Ws, s_l, (long)sbs, B, m->sfb, D), gemm_work(m),
+                                   st)) != SNHIP_OK)
+                return rc;
+            GemmArgs gu = gemm_for(m, A.U, m->v, R, B, m->q, 2 * D);
+            if (gemm_fuses_compete(gu, gemm_work(m))) {
+                // Gate and state update in the U product's epilogue.
+                gu.epi = GEPI_COMPETE;
+                gu.Y = m->u; gu.ldy = D;
+                gu.s = s_l; gu.lds = (long)sbs;
+                gu.delta = A.delta; gu.clamp = m->clamp; gu.p_floor = m->p_floor;
+                if ((rc = run_gemm(m, gu, st)) != SNHIP_OK) return rc;
+            } else {
+                if ((rc = run_gemm(m, gu, st)) != SNHIP_OK) return rc;
+                hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                                   st, m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
+            }
             GemmArgs gz = gemm_for(m, A.Wz, m->u, D, B, m->z, I);
             gz.epi = GEPI_WEDGE;
             gz.a_tanh = A.a_tanh;
             if ((rc = run_gemm(m, gz, st)) != SNHIP_OK) return rc;
-            hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->z, I, A.nm_g, A.nm_c, m->yn, I, I,
-                               m->eps);
+            launch_ln(B, m->z, I, A.nm_g, A.nm_c, m->yn, I, I, m->eps, st);
             GemmArgs gc = gemm_for(m, A.Wc, m->yn, I, B, m->x, D);
             gc.epi = GEPI_RESID;
             gc.b_gain = A.b_gain;
@@ -851,8 +929,7 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
         jz.epi = EPI_WEDGE;
         jz.a_tanh = A.a_tanh;
         SNHIP_CHECK(launch_gemv(m, jz, none, st));
-        hipLaunchKernelGGL(k_ln, dim3(B), dim3(256), 0, st, m->z, I, A.nm_g, A.nm_c, m->yn, I, I,
-                           m->eps);
+        launch_ln(B, m->z, I, A.nm_g, A.nm_c, m->yn, I, I, m->eps, st);
         GemvJob jc = make_job(A.Wc, B, m->yn, I, m->x, D);
         jc.epi = EPI_RESID;
         jc.b_gain = A.b_gain;
@@ -964,8 +1041,7 @@ snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_o
         const Layer& A = m->layers[l];
         float* s_l = m->s + (size_t)l * D;
         float* h_l = m->hist + (size_t)l * (m->kh ? m->kh : 1) * D;
-        hipLaunchKernelGGL(k_ln, dim3((unsigned)rows), dim3(256), 0, st, m->pf_x, D, A.ni_g, A.ni_c,
-                           m->pf_raw, D, D, m->eps);
+        launch_ln((int)rows, m->pf_x, D, A.ni_g, A.ni_c, m->pf_raw, D, D, m->eps, st);
         const float* at = m->pf_raw;
         if (m->K > 1) {
             const long n = rows * D;
@@ -984,8 +1060,7 @@ snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_o
         gz.epi = GEPI_WEDGE;
         gz.a_tanh = A.a_tanh;
         if ((rc = run_gemm(m, gz, st)) != SNHIP_OK) return rc;
-        hipLaunchKernelGGL(k_ln, dim3((unsigned)rows), dim3(256), 0, st, m->pf_z, I, A.nm_g, A.nm_c,
-                           m->pf_yn, I, I, m->eps);
+        launch_ln((int)rows, m->pf_z, I, A.nm_g, A.nm_c, m->pf_yn, I, I, m->eps, st);
         // sfb_t = W_eff s_{t-1}, with s_{-1} the carried state (layers.py:208-217,243-250)
         GemmArgs gs = gemm_for(m, A.Ws, m->pf_st, D, (int)rows, m->pf_sfb, D);
         gs.X0 = s_l; gs.ldx0 = (long)sbs; gs.shift_T = Tc;

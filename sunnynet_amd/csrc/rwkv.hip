@@ -381,6 +381,8 @@ struct SnHipRwkv7 {
     int gemm_min_batch = 8;
     float* gemm_work = nullptr;
     size_t gemm_work_floats = 0;
+    unsigned* gemm_cnt = nullptr;      // skinny-GEMM tile counters (zero between launches)
+    int gemm_ncnt = 0;
     int ready = 0;
 };
 
@@ -614,9 +616,12 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
     m->done = ralloc<int32_t>(m, 1);
     m->gemm_work_floats = (size_t)16 << 20;
     m->gemm_work = ralloc<float>(m, m->gemm_work_floats);
+    m->gemm_ncnt = 4096;
+    m->gemm_cnt = ralloc<unsigned>(m, m->gemm_ncnt);
     if (!m->S || !m->shift || !m->x || !m->X6 || !m->r || !m->k || !m->v || !m->lo || !m->dw ||
         !m->da || !m->dv || !m->g || !m->y || !m->vfirst || !m->xk2 || !m->ck || !m->nrm ||
         !m->logits || !m->tok || !m->best || !m->counter || !m->done || !m->gemm_work ||
+        !m->gemm_cnt || hipMemset(m->gemm_cnt, 0, m->gemm_ncnt * sizeof(unsigned)) != hipSuccess ||
         hipMemset(m->S, 0, B * L * NH * HS * HS * sizeof(float)) != hipSuccess ||
         hipMemset(m->shift, 0, B * L * 2 * D * sizeof(float)) != hipSuccess ||
         hipMemset(m->counter, 0, sizeof(int32_t)) != hipSuccess ||
@@ -652,7 +657,10 @@ struct MMList {
             g.M = B; g.N = W.M; g.K = W.Kd;
             g.Y = Y; g.ldy = ldy;
             g.epi = epi == EPI_ADD ? GEPI_ADD : epi == EPI_RELU2 ? GEPI_RELU2 : GEPI_STORE;
-            return launch_gemm(g, m->gemm_work, m->gemm_work_floats, m->work);
+            GemmWork gw;
+            gw.part = m->gemm_work; gw.part_floats = m->gemm_work_floats;
+            gw.cnt = m->gemm_cnt; gw.ncnt = m->gemm_ncnt;
+            return launch_gemm(g, gw, m->work);
         }
         GemvJob j{};
         j.w = W.w; j.q = W.q; j.sc = W.sc;

@@ -175,18 +175,19 @@ def test_greedy_decode_on_device(gpu, small):
         cur = nxt
 
 
-@pytest.mark.parametrize("block", [32, 64])
-def test_int4_matches_dequantized_oracle(gpu, tmp_path_factory, block):
+@pytest.mark.parametrize("block,B", [(32, 4), (64, 4), (32, 16), (64, 16)])
+def test_int4_matches_dequantized_oracle(gpu, tmp_path_factory, block, B):
     """INT4 group-quantized weights (N(0, 0.02) matmuls): HIP dequantizes in
-    registers; the oracle runs fp32 on the bit-identical dequantized blob."""
-    print(f"small int4 block={block}", flush=True)
+    registers (GEMV below 8 sequences, MFMA GEMM from 8); the oracle runs fp32
+    on the bit-identical dequantized blob."""
+    print(f"small int4 block={block} B={B}", flush=True)
     w = gaussian_matmuls(init_sunnynet(SMALL, 0), seed=3)
     path = _write(tmp_path_factory, f"small_g{block}.bin", pack_sunny_blob(w))
-    hm = _model(path, SMALL, weights="int4", block=block, max_batch=4)
-    orc = oracle.SnOracle(dequant_blob(w, block), batch=4)
-    rng = np.random.default_rng(block)
+    hm = _model(path, SMALL, weights="int4", block=block, max_batch=B)
+    orc = oracle.SnOracle(dequant_blob(w, block), batch=B)
+    rng = np.random.default_rng(block + B)
     for _ in range(24):
-        toks = rng.integers(0, SMALL.vocab_size, 4).astype(np.int32)
+        toks = rng.integers(0, SMALL.vocab_size, B).astype(np.int32)
         a = hm.step_batch(torch.from_numpy(toks).to(gpu)).cpu().numpy()
         b = orc.step(toks)
         assert np.abs(a - b).max() < TOL
@@ -263,12 +264,14 @@ def test_100m_b64_matches_oracle_on_sampled_sequences(gpu, m100):
         assert np.array_equal(a[pick].argmax(1), b.argmax(1))
 
 
-def test_graph_replays_match_eager(gpu, small, monkeypatch):
+@pytest.mark.parametrize("B", [4, 16])
+def test_graph_replays_match_eager(gpu, small, monkeypatch, B):
     """The step runs as a captured HIP graph; replay it many times with host
     work and synchronization in between and compare every replay with the
-    eager (uncaptured) launch sequence."""
+    eager (uncaptured) launch sequence, bit for bit (B = 16: the MFMA GEMMs,
+    whose split-K tile counters are re-armed by every launch)."""
     w, buf, path = small
-    B = 4
+    print(f"small graph vs eager B={B}", flush=True)
     rng = np.random.default_rng(11)
     seqs = [rng.integers(0, SMALL.vocab_size, B).astype(np.int32) for _ in range(10)]
     hg = _model(path, SMALL, max_batch=B)
