@@ -1,9 +1,11 @@
 """RWKV-7 decode handle on the GPU (include/snhip_rwkv7.h).
 
-``HipRwkv7(path)`` loads the reference's v3 runtime blob and offers the
-reference C handle's operations (sunnynet/runtime/rwkv7.h:16-28): ``reset()``,
-``step(token) -> list[float]`` and ``prefill(tokens) -> list[float]`` (host
-logits, one B=1 sequence). Extensions: ``max_batch`` sequences, weight format
+``HipRwkv7(path[, vocab])`` loads the reference's v3 runtime blob and offers
+the reference handle's operations (sunnynet/runtime/rwkv7.h:16-28 and the
+ctypes class ``SnRWKV7``, sunnynet/runtime/rwkv7_c.py:65-104): ``reset()``,
+``step(token) -> list[float]``, ``step_raw(token)``, ``logits()`` and
+``prefill(tokens) -> list[float]`` (host logits, one B=1 sequence); a
+``vocab`` given positionally must equal the blob's. Extensions: ``max_batch`` sequences, weight format
 (``"stored"`` as in the blob, ``"fp32"``, ``"int4"`` with a group ``block``),
 ``step_batch`` / ``decode_greedy`` on device tensors, and ``get_state`` /
 ``set_state`` (S (B, L, H, 64, 64), shift (B, L, 2, D)).
@@ -24,8 +26,8 @@ FORMATS = {"fp32": 0, "int4": 1, "stored": 2}
 
 
 class HipRwkv7:
-    def __init__(self, path, *, max_batch: int = 1, weights: str = "stored", block: int = 32,
-                 device=None):
+    def __init__(self, path, vocab: int | None = None, *, max_batch: int = 1,
+                 weights: str = "stored", block: int = 32, device=None):
         self._lib = _native.lib()
         self.device = torch.device(device or "cuda:0")
         with open(path, "rb") as f:
@@ -40,6 +42,9 @@ class HipRwkv7:
         if not self._lib.snhip_rk_ready(self._h):
             raise RuntimeError("snhip_rk_load returned a handle that is not ready")
         self.vocab = int(self._lib.snhip_rk_vocab(self._h))
+        if vocab is not None and int(vocab) != self.vocab:
+            self.close()
+            raise ValueError(f"vocab {vocab} does not match the blob's {self.vocab}")
         self._logits = (ctypes.c_float * self.vocab)()
         self._bind_stream()
 
@@ -55,6 +60,14 @@ class HipRwkv7:
     def step(self, token: int) -> list:
         self._bind_stream()
         self._lib.snhip_rk_step(self._h, int(token), ctypes.byref(self._logits))
+        return np.frombuffer(self._logits, np.float32).tolist()
+
+    def step_raw(self, token: int) -> None:
+        """Advance the state; the logits stay in the handle's buffer."""
+        self._bind_stream()
+        self._lib.snhip_rk_step(self._h, int(token), ctypes.byref(self._logits))
+
+    def logits(self) -> list:
         return np.frombuffer(self._logits, np.float32).tolist()
 
     def prefill(self, tokens) -> list:

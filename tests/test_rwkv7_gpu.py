@@ -86,6 +86,30 @@ def test_tiny_fp32_b1(gpu, tiny):
     assert np.abs(S.cpu().numpy() - So).max() < 1e-4 and np.abs(sh.cpu().numpy() - sho).max() < 1e-5
 
 
+def test_reference_class_surface(gpu, tiny):
+    """Constructed and driven like the reference's SnRWKV7(path, vocab)
+    (rwkv7_c.py:65-104): step_raw advances the state, logits() returns the
+    last step's logits, prefill feeds tokens in order; a vocab that does not
+    match the blob is rejected."""
+    w, p32, _ = tiny
+    print("rwkv7 tiny reference class surface", flush=True)
+    hm = HipRwkv7(p32, RWKV_TINY.vocab)
+    orc = oracle.RkOracle(p32.read_bytes())
+    toks = [5, 77, 300, 2]
+    for t in toks[:-1]:
+        hm.step_raw(t)
+        orc.step([t])
+    a = np.asarray(hm.step(toks[-1]), np.float32)
+    b = orc.step([toks[-1]])[0]
+    assert np.abs(a - b).max() < TOL
+    assert np.array_equal(np.asarray(hm.logits(), np.float32), a)
+    hm.reset()
+    c = np.asarray(hm.prefill(toks), np.float32)
+    assert np.array_equal(c, a)
+    with pytest.raises(ValueError):
+        HipRwkv7(p32, RWKV_TINY.vocab + 1)
+
+
 @pytest.mark.parametrize("B", [3, 9])
 def test_tiny_batched(gpu, tiny, B):
     """B=9 runs the matrix products on the MFMA GEMM."""
