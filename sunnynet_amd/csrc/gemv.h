@@ -32,9 +32,17 @@ struct GemvJob {
     const float* sfb; int ldf;
     unsigned long long* best;   // EPI_ARGMAX: per-block packed maxima, [b * nblk + blk]
     int nblk;                   // set by launch_gemv
+    int xact;                   // activation applied to X as it is staged (GemvAct)
 };
 
-constexpr int kGemvMaxJobs = 4;
+// Elementwise activation of a job's input vector, applied while staging it.
+enum GemvAct {
+    ACT_NONE = 0,
+    ACT_TANH = 1,      // tanhf(x)                       (rwkv7.c:235)
+    ACT_SIGMOID = 2,   // 1 / (1 + expf(-x))             (rwkv7.c:256)
+};
+
+constexpr int kGemvMaxJobs = 8;
 
 // Orderable key of (value, index): larger value wins, then smaller index,
 // so the maximum key is torch.argmax's first maximal index.

@@ -87,17 +87,21 @@ __global__ __launch_bounds__(256) void k_gemv(GemvJobs JS) {
 #pragma unroll
         for (int bb = 0; bb < BT; ++bb) best[bb] = 0ull;
         __syncthreads();
+        const int xact = J.xact;
+        auto xval = [&](float v) {
+            return xact == ACT_TANH ? tanhf(v) : xact == ACT_SIGMOID ? 1.0f / (1.0f + expf(-v)) : v;
+        };
         if constexpr (BLK == 0) {
             for (int i = threadIdx.x; i < nb * Kd; i += 256) {
                 const int bb = i / Kd, k = i - bb * Kd;
-                xs[i] = J.X[(size_t)(b0 + bb) * J.ldx + k];
+                xs[i] = xval(J.X[(size_t)(b0 + bb) * J.ldx + k]);
             }
         } else {
             const int ng = Kd / BLK;
             for (int i = threadIdx.x; i < nb * Kd; i += 256) {
                 const int bb = i / Kd, k = i - bb * Kd;
                 const int g = k / BLK, j = k - g * BLK;
-                xs[bb * Kd + j * ng + g] = J.X[(size_t)(b0 + bb) * J.ldx + k];
+                xs[bb * Kd + j * ng + g] = xval(J.X[(size_t)(b0 + bb) * J.ldx + k]);
             }
         }
         __syncthreads();

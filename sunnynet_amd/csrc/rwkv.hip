@@ -66,17 +66,18 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // Two-pass LayerNorm over n <= 4096 values (rwkv7.c:127-140 form), element
-// k * 256 + tid in xv[k].
-__device__ __forceinline__ void ln_stats(const float (&xv)[kLnPer], int n, float eps, float* red,
+// k * 256 + tid in xv[k], PER per thread.
+template <int PER>
+__device__ __forceinline__ void ln_stats(const float (&xv)[PER], int n, float eps, float* red,
                                          float& mean, float& rstd) {
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k)
+    for (int k = 0; k < PER; ++k)
         if (k * 256 + (int)threadIdx.x < n) sum += xv[k];
     mean = block_sum256(sum, red) / (float)n;
     float vs = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k)
+    for (int k = 0; k < PER; ++k)
         if (k * 256 + (int)threadIdx.x < n) {
             const float d = xv[k] - mean;
             vs += d * d;
@@ -84,15 +85,12 @@ __device__ __forceinline__ void ln_stats(const float (&xv)[kLnPer], int n, float
     rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
 }
 
-__device__ __forceinline__ void load_row(float (&xv)[kLnPer], const float* x, int n) {
-#pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        xv[k] = i < n ? x[i] : 0.0f;
-    }
-}
+// Element index of slot k of this thread, clamped so every load is valid
+// (slots past n are loaded but never used).
+__device__ __forceinline__ int ln_idx(int k, int n) { return min(k * 256 + (int)threadIdx.x, n - 1); }
 
 // x[b] = LN_0(E[tok[b]]) (rwkv7.c:351-352); NaN rows for out-of-range ids.
+template <int PER>
 __global__ __launch_bounds__(256) void k_rk_embed(const int32_t* __restrict__ tok,
                                                   const float* __restrict__ embed,
                                                   const float* __restrict__ g,
@@ -102,39 +100,51 @@ __global__ __launch_bounds__(256) void k_rk_embed(const int32_t* __restrict__ to
     const int b = blockIdx.x;
     const int t = tok[b];
     const bool ok = t >= 0 && t < vocab;
-    float xv[kLnPer];
-    load_row(xv, embed + (size_t)(ok ? t : 0) * D, D);
-    if (!ok)
+    const float* er = embed + (size_t)(ok ? t : 0) * D;
+    float xv[PER], gv[PER], cv[PER];
 #pragma unroll
-        for (int k = 0; k < kLnPer; ++k) xv[k] = __builtin_nanf("");
+    for (int k = 0; k < PER; ++k) {
+        const int i = ln_idx(k, D);
+        xv[k] = ok ? er[i] : __builtin_nanf("");
+        gv[k] = g[i];
+        cv[k] = c[i];
+    }
     float mean, rstd;
-    ln_stats(xv, D, eps, red, mean, rstd);
+    ln_stats<PER>(xv, D, eps, red, mean, rstd);
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
+    for (int k = 0; k < PER; ++k) {
         const int i = k * 256 + threadIdx.x;
-        if (i < D) x[(size_t)b * D + i] = (xv[k] - mean) * rstd * g[i] + c[i];
+        if (i < D) x[(size_t)b * D + i] = (xv[k] - mean) * rstd * gv[k] + cv[k];
     }
 }
 
 // y[b] = LN(x[b]) (the output norm, rwkv7.c:358).
+template <int PER>
 __global__ __launch_bounds__(256) void k_rk_ln(const float* __restrict__ x, const float* __restrict__ g,
                                                const float* __restrict__ c, float* __restrict__ y,
                                                int D, float eps) {
     __shared__ float red[4];
     const int b = blockIdx.x;
-    float xv[kLnPer];
-    load_row(xv, x + (size_t)b * D, D);
-    float mean, rstd;
-    ln_stats(xv, D, eps, red, mean, rstd);
+    float xv[PER], gv[PER], cv[PER];
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
+    for (int k = 0; k < PER; ++k) {
+        const int i = ln_idx(k, D);
+        xv[k] = x[(size_t)b * D + i];
+        gv[k] = g[i];
+        cv[k] = c[i];
+    }
+    float mean, rstd;
+    ln_stats<PER>(xv, D, eps, red, mean, rstd);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
         const int i = k * 256 + threadIdx.x;
-        if (i < D) y[(size_t)b * D + i] = (xv[k] - mean) * rstd * g[i] + c[i];
+        if (i < D) y[(size_t)b * D + i] = (xv[k] - mean) * rstd * gv[k] + cv[k];
     }
 }
 
 // Time-mix inputs (rwkv7.c:213-227): xn = LN_1(x); d = shift_0 - xn;
 // X6[b][s] = xn + lerp[s] d for s = r, w, k, v, a, g; shift_0 <- xn.
+template <int PER>
 __global__ __launch_bounds__(256) void k_rk_mix1(const float* __restrict__ x,
                                                  const float* __restrict__ g,
                                                  const float* __restrict__ c,
@@ -143,26 +153,36 @@ __global__ __launch_bounds__(256) void k_rk_mix1(const float* __restrict__ x,
                                                  float* __restrict__ X6, int D, float eps) {
     __shared__ float red[4];
     const int b = blockIdx.x;
-    float xv[kLnPer];
-    load_row(xv, x + (size_t)b * D, D);
-    float mean, rstd;
-    ln_stats(xv, D, eps, red, mean, rstd);
     float* sh = shift + (size_t)b * shift_bstride;
+    float xv[PER], gv[PER], cv[PER], sv[PER], lv[6][PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = ln_idx(k, D);
+        xv[k] = x[(size_t)b * D + i];
+        gv[k] = g[i];
+        cv[k] = c[i];
+        sv[k] = sh[i];
+#pragma unroll
+        for (int s6 = 0; s6 < 6; ++s6) lv[s6][k] = lerp[(size_t)s6 * D + i];
+    }
+    float mean, rstd;
+    ln_stats<PER>(xv, D, eps, red, mean, rstd);
     float* o = X6 + (size_t)b * 6 * D;
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
+    for (int k = 0; k < PER; ++k) {
         const int i = k * 256 + threadIdx.x;
         if (i >= D) continue;
-        const float xn = (xv[k] - mean) * rstd * g[i] + c[i];
-        const float d = sh[i] - xn;
+        const float xn = (xv[k] - mean) * rstd * gv[k] + cv[k];
+        const float d = sv[k] - xn;
 #pragma unroll
-        for (int s = 0; s < 6; ++s) o[(size_t)s * D + i] = xn + lerp[(size_t)s * D + i] * d;
+        for (int s6 = 0; s6 < 6; ++s6) o[(size_t)s6 * D + i] = xn + lv[s6][k] * d;
         sh[i] = xn;
     }
 }
 
 // Channel-mix input (rwkv7.c:303-305,315): xn2 = LN_2(x);
 // xk2 = xn2 + cmk_lerp (shift_1 - xn2); shift_1 <- xn2.
+template <int PER>
 __global__ __launch_bounds__(256) void k_rk_mix2(const float* __restrict__ x,
                                                  const float* __restrict__ g,
                                                  const float* __restrict__ c,
@@ -171,20 +191,47 @@ __global__ __launch_bounds__(256) void k_rk_mix2(const float* __restrict__ x,
                                                  float* __restrict__ xk2, int D, float eps) {
     __shared__ float red[4];
     const int b = blockIdx.x;
-    float xv[kLnPer];
-    load_row(xv, x + (size_t)b * D, D);
-    float mean, rstd;
-    ln_stats(xv, D, eps, red, mean, rstd);
     float* sh = shift1 + (size_t)b * shift_bstride;
+    float xv[PER], gv[PER], cv[PER], sv[PER], lv[PER];
 #pragma unroll
-    for (int k = 0; k < kLnPer; ++k) {
+    for (int k = 0; k < PER; ++k) {
+        const int i = ln_idx(k, D);
+        xv[k] = x[(size_t)b * D + i];
+        gv[k] = g[i];
+        cv[k] = c[i];
+        sv[k] = sh[i];
+        lv[k] = lerp[i];
+    }
+    float mean, rstd;
+    ln_stats<PER>(xv, D, eps, red, mean, rstd);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
         const int i = k * 256 + threadIdx.x;
         if (i >= D) continue;
-        const float xn = (xv[k] - mean) * rstd * g[i] + c[i];
-        xk2[(size_t)b * D + i] = xn + lerp[i] * (sh[i] - xn);
+        const float xn = (xv[k] - mean) * rstd * gv[k] + cv[k];
+        xk2[(size_t)b * D + i] = xn + lv[k] * (sv[k] - xn);
         sh[i] = xn;
     }
 }
+
+// Per-thread slot count of the row kernels for a row of D values.
+int rk_per(int D) {
+    const int p = (D + 255) / 256;
+    return p <= 1 ? 1 : p <= 2 ? 2 : p <= 3 ? 3 : p <= 4 ? 4 : p <= 8 ? 8 : 16;
+}
+
+// Launches K<PER> for the row length's slot count.
+#define SNHIP_RK_ROWS(K, D, grid, st, ...)                                                    \
+    do {                                                                                      \
+        switch (rk_per(D)) {                                                                  \
+        case 1: hipLaunchKernelGGL(K<1>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
+        case 2: hipLaunchKernelGGL(K<2>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
+        case 3: hipLaunchKernelGGL(K<3>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
+        case 4: hipLaunchKernelGGL(K<4>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
+        case 8: hipLaunchKernelGGL(K<8>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
+        default: hipLaunchKernelGGL(K<16>, grid, dim3(256), 0, st, __VA_ARGS__); break;        \
+        }                                                                                     \
+    } while (0)
 
 // LoRA middle activations (rwkv7.c:235,256): lw = tanh(lw), lg = sig(lg).
 __global__ void k_rk_lora_act(float* __restrict__ lw, int Rw, float* __restrict__ lg, int Rg,
@@ -649,7 +696,9 @@ struct MMList {
     int blk[8];
     int n = 0;
 
-    snhip_status add(const RMat& W, const float* X, int ldx, float* Y, int ldy, int epi) {
+    // xact (GEMV path only): activation applied to X as it is staged.
+    snhip_status add(const RMat& W, const float* X, int ldx, float* Y, int ldy, int epi,
+                     int xact = ACT_NONE) {
         if (B >= m->gemm_min_batch && W.Kd % 32 == 0) {
             GemmArgs g{};
             g.X = X; g.ldx = ldx;
@@ -667,6 +716,7 @@ struct MMList {
         j.M = W.M; j.Kd = W.Kd; j.B = B;
         j.X = X; j.ldx = ldx; j.Y = Y; j.ldy = ldy;
         j.epi = epi;
+        j.xact = xact;
         jobs[n] = j;
         blk[n] = W.q ? W.block : 0;
         ++n;
@@ -696,15 +746,15 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
     float* la = m->lo + kMaxRank;
     float* lv = m->lo + 2 * kMaxRank;
     float* lg = m->lo + 3 * kMaxRank;
-    hipLaunchKernelGGL(k_rk_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->en_w, m->en_b,
-                       m->x, D, m->vocab, m->eps);
+    SNHIP_RK_ROWS(k_rk_embed, D, dim3(B), st, m->tok, m->embed, m->en_w, m->en_b, m->x, D, m->vocab,
+                  m->eps);
     MMList mm{m, B};
     snhip_status rc;
     for (int l = 0; l < L; ++l) {
         const RkLayer& A = m->layers[l];
         float* sh = m->shift + (size_t)l * 2 * D;
-        hipLaunchKernelGGL(k_rk_mix1, dim3(B), dim3(256), 0, st, m->x, A.ln1w, A.ln1b, A.lerp, sh,
-                           sh_bstride, m->X6, D, m->eps);
+        SNHIP_RK_ROWS(k_rk_mix1, D, dim3(B), st, m->x, A.ln1w, A.ln1b, A.lerp, sh, sh_bstride, m->X6, D,
+                      m->eps);
         const float* xr = m->X6;
         const float* xw = m->X6 + D;
         const float* xk = m->X6 + 2 * D;
@@ -720,10 +770,16 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         if ((rc = mm.add(A.g1, xg, ld6, lg, ldl, EPI_STORE)) != SNHIP_OK) return rc;
         if (l > 0 && (rc = mm.add(A.v1, xv, ld6, lv, ldl, EPI_STORE)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        hipLaunchKernelGGL(k_rk_lora_act, dim3(B), dim3(256), 0, st, lw, A.Rw, lg, A.Rg, ldl);
-        if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, EPI_STORE)) != SNHIP_OK) return rc;
+        // tanh / sigmoid of the LoRA middles: in the GEMV's input staging below
+        // gemm_min_batch sequences, else one small kernel.
+        const bool gemv = B < m->gemm_min_batch;
+        if (!gemv)
+            hipLaunchKernelGGL(k_rk_lora_act, dim3(B), dim3(256), 0, st, lw, A.Rw, lg, A.Rg, ldl);
+        if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, EPI_STORE, gemv ? ACT_TANH : ACT_NONE)) != SNHIP_OK)
+            return rc;
         if ((rc = mm.add(A.a2, la, ldl, m->da, D, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.g2, lg, ldl, m->g, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.g2, lg, ldl, m->g, D, EPI_STORE, gemv ? ACT_SIGMOID : ACT_NONE)) != SNHIP_OK)
+            return rc;
         if (l > 0 && (rc = mm.add(A.v2, lv, ldl, m->dv, D, EPI_STORE)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
         HeadArgs H{};
@@ -739,14 +795,14 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         hipLaunchKernelGGL(k_rk_heads, dim3(NH, B), dim3(256), 0, st, H);
         if ((rc = mm.add(A.o, m->y, D, m->x, D, EPI_ADD)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        hipLaunchKernelGGL(k_rk_mix2, dim3(B), dim3(256), 0, st, m->x, A.ln2w, A.ln2b, A.cmk_lerp,
-                           sh + D, sh_bstride, m->xk2, D, m->eps);
+        SNHIP_RK_ROWS(k_rk_mix2, D, dim3(B), st, m->x, A.ln2w, A.ln2b, A.cmk_lerp, sh + D, sh_bstride,
+                      m->xk2, D, m->eps);
         if ((rc = mm.add(A.cmk, m->xk2, D, m->ck, F, EPI_RELU2)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
         if ((rc = mm.add(A.cmv, m->ck, F, m->x, D, EPI_ADD)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
     }
-    hipLaunchKernelGGL(k_rk_ln, dim3(B), dim3(256), 0, st, m->x, m->on_w, m->on_b, m->nrm, D, m->eps);
+    SNHIP_RK_ROWS(k_rk_ln, D, dim3(B), st, m->x, m->on_w, m->on_b, m->nrm, D, m->eps);
     const RMat& Hm = m->head;
     if (B >= m->gemm_min_batch) {
         if ((rc = mm.add(Hm, m->nrm, D, logits_out, m->vocab, EPI_STORE)) != SNHIP_OK) return rc;
