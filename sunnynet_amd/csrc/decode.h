@@ -16,6 +16,7 @@ __host__ __device__ inline int qrow_g(int i) { return 16 * (i >> 3) + 8 + (i & 7
 // per-kernel path.
 constexpr int kPersistMaxD = 1024;
 constexpr int kPersistMaxK = 1536;
+constexpr int kPersistMaxL = 32;             // layers (the layer table is staged in LDS)
 
 // A weight matrix, row-major (M, Kd): fp32 rows in w, or INT4 codes in q
 // ((M, Kd/2) bytes, quant.c packing) with per-group scales sc ((M, Kd/block)).
@@ -39,32 +40,33 @@ struct PersistArgs {
     float eps, p_floor;
     const float *embed, *no_g, *no_c;
     PMat head;
-    float* s;               // (L, D) state of the sequence
-    float* hist;            // (L, kh, D) conv history, newest first
-    float* hd;              // (L, kh, D) hist[k] * dw[K-2-k], kept by the kernel
-    float *x, *v, *sfb, *u, *z;   // exchange buffers: D, R, D, D, I floats
-    unsigned long long* part;     // per-workgroup argmax keys (grid size)
-    unsigned* bar;                // barrier words (kPersistBarWords), zeroed before launch
-    const int32_t* tok_in;        // first input token (device)
-    int32_t* out_tok;             // greedy: token chosen after each step (n_steps)
-    float* logits;                // if not NULL: logits of the last step (vocab)
+    float* s;               // (L, D) state: read at the first step, written back after the last
+    float* hist;            // (L, kh, D) conv history, newest first: same
+    float* ring;            // (grid, L, kh, D) each workgroup's recent LN_in outputs
+    unsigned long long* ex; // (2, kPersistExWords) exchange words, zeroed before the launch
+    unsigned long long* sx; // (L, 2, D) new-state words, zeroed before the launch
+    unsigned* err;          // set on a poll time-out
+    const int32_t* tok_in;  // first input token (device)
+    int32_t* out_tok;       // greedy: token chosen after each step (n_steps)
+    float* logits;          // if not NULL: logits of the last step (vocab)
     int n_steps, greedy;
-    unsigned spin_limit;    // polls before a barrier wait gives up
-    unsigned stall;         // added to every barrier target: > 0 only to test the time-out path
+    unsigned spin_limit;    // polls before a wait gives up
+    unsigned stall;         // added to every awaited epoch: > 0 only to test the time-out path
 };
 
-// Barrier words: 8 group counters 128 bytes apart, the top counter, the
-// time-out flag.
-constexpr int kPersistBarWords = 320;
-constexpr int kPersistBarErr = 288;
+// Exchange words per epoch slot (>= inner, rank, dim and two per workgroup).
+constexpr int kPersistExWords = 2048;
 
-// Conv taps the kernel is built for (the history loads are straight-line
-// code), and its largest grid.
+// Conv taps the kernel is built for, and its largest grid.
 constexpr int kPersistTaps = 4;
 constexpr int kPersistMaxGrid = 1024;
 
 // Workgroups per CU the kernel can keep resident (0 if it cannot run).
 int persist_occupancy(int blk);
+// Grid sizes the kernel accepts for a shape: G divides dim, each workgroup's
+// dim / G channels are whole channel groups of 8 or an equal part of one, and
+// every workgroup gets rows of V, W_z and the head.
+bool persist_grid_ok(int G, int D, int I, int R, int vocab);
 snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipStream_t st);
 
 }  // namespace snhip

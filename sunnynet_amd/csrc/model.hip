@@ -501,10 +501,12 @@ struct SnHipModel {
     // model's shape or the device does not allow it.
     int persist_wg = 0;
     snhip::PLayer* dlayers = nullptr;     // device copy of the layer table
-    unsigned* pbar = nullptr;             // grid barrier words
-    float* hd = nullptr;                  // conv-history products of sequence 0
-    unsigned* h_err = nullptr;            // pinned copy of the barrier time-out flag
-    unsigned persist_spin = 1u << 22;     // barrier poll limit (SNHIP_PERSIST_SPIN)
+    unsigned long long* pex = nullptr;    // exchange words (2 x kPersistExWords)
+    unsigned long long* psx = nullptr;    // new-state words (L x 2 x D)
+    float* pring = nullptr;               // per-workgroup LN_in history rings
+    unsigned* perr = nullptr;             // time-out flag
+    unsigned* h_err = nullptr;            // pinned copy of the time-out flag
+    unsigned persist_spin = 1u << 22;     // poll limit (SNHIP_PERSIST_SPIN)
     unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests)
     int ready = 0;
 };
@@ -620,12 +622,14 @@ PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M}; }
 
 // Enables the persistent single-sequence decode when the shape fits it and the
 // device supports cooperative launches (SNHIP_PERSIST=0 turns it off;
-// SNHIP_PERSIST_WG sets the grid size, default one workgroup per CU).
+// SNHIP_PERSIST_WG caps the grid size). The grid is the largest size the
+// kernel accepts for the shape (persist_grid_ok) up to one workgroup per
+// four channels and per CU (measured fastest at dim 1024: 256 workgroups).
 void setup_persist(SnHipModel* m) {
     if (const char* e = getenv("SNHIP_PERSIST"))
         if (e[0] == '0') return;
     if (m->D > kPersistMaxD || m->I > kPersistMaxK || m->R > kPersistMaxK ||
-        m->K != kPersistTaps || m->D % 8)
+        m->K != kPersistTaps || m->D % 8 || m->L > kPersistMaxL)
         return;
     int dev = 0, coop = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -634,9 +638,12 @@ void setup_persist(SnHipModel* m) {
         return;
     const int occ = persist_occupancy(m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0);
     if (occ < 1) return;
-    int nwg = ncu;
-    if (const char* e = getenv("SNHIP_PERSIST_WG")) nwg = atoi(e);
-    nwg = std::min(std::min(nwg, ncu * occ), kPersistMaxGrid);
+    int cap = std::min(m->D / 4, ncu);
+    if (const char* e = getenv("SNHIP_PERSIST_WG")) cap = atoi(e);
+    cap = std::min(std::min(cap, ncu * occ), kPersistMaxGrid);
+    int nwg = 0;
+    for (int g = cap; g >= 1 && !nwg; --g)
+        if (persist_grid_ok(g, m->D, m->I, m->R, m->vocab)) nwg = g;
     if (nwg < 1) return;
     if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->persist_spin = (unsigned)std::max(1, atoi(e));
     if (const char* e = getenv("SNHIP_PERSIST_STALL")) m->persist_stall = (unsigned)std::max(0, atoi(e));
@@ -651,9 +658,12 @@ void setup_persist(SnHipModel* m) {
         P.U = pmat(A.U); P.Wz = pmat(A.Wz); P.Wc = pmat(A.Wc);
     }
     m->dlayers = dalloc<PLayer>(m, m->L);
-    m->pbar = dalloc<unsigned>(m, kPersistBarWords);
-    m->hd = dalloc<float>(m, (size_t)m->L * (m->kh ? m->kh : 1) * m->D);
-    if (!m->dlayers || !m->pbar || !m->hd || hipHostMalloc((void**)&m->h_err, sizeof(unsigned), 0) != hipSuccess)
+    m->pex = dalloc<unsigned long long>(m, 2 * (size_t)kPersistExWords);
+    m->psx = dalloc<unsigned long long>(m, (size_t)m->L * 2 * m->D);
+    m->pring = dalloc<float>(m, (size_t)nwg * m->L * m->kh * m->D);
+    m->perr = dalloc<unsigned>(m, 1);
+    if (!m->dlayers || !m->pex || !m->psx || !m->pring || !m->perr ||
+        hipHostMalloc((void**)&m->h_err, sizeof(unsigned), 0) != hipSuccess)
         return;
     *m->h_err = 0;
     if (hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PLayer), hipMemcpyHostToDevice) != hipSuccess)
@@ -1116,28 +1126,27 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
 // step's logits.
 snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_tok,
                          float* logits) {
-    constexpr int kMaxStepsPerLaunch = 1 << 20;   // keeps barrier counters far from wrapping
+    constexpr int kMaxStepsPerLaunch = 1 << 20;   // keeps exchange epochs far from wrapping
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
     SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
-    SNHIP_CHECK(hipMemsetAsync(m->pbar, 0, kPersistBarWords * sizeof(unsigned), m->work));
+    SNHIP_CHECK(hipMemsetAsync(m->perr, 0, sizeof(unsigned), m->work));
     PersistArgs a{};
     a.layers = m->dlayers;
     a.L = m->L; a.D = m->D; a.I = m->I; a.R = m->R; a.K = m->K; a.kh = m->kh;
     a.vocab = m->vocab; a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
     a.embed = m->embed; a.no_g = m->no_g; a.no_c = m->no_c;
     a.head = pmat(m->head);
-    a.s = m->s; a.hist = m->hist; a.hd = m->hd;
-    a.x = m->x; a.v = m->v; a.sfb = m->sfb; a.u = m->u; a.z = m->z;
-    a.part = m->best;
-    a.bar = m->pbar;
+    a.s = m->s; a.hist = m->hist;
+    a.ring = m->pring; a.ex = m->pex; a.sx = m->psx; a.err = m->perr;
     a.greedy = greedy ? 1 : 0;
     a.spin_limit = m->persist_spin;
     a.stall = m->persist_stall;
     const int blk = m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0;
     for (int done = 0; done < n_steps;) {
         const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
-        if (done > 0)   // counters only; the time-out flag accumulates
-            SNHIP_CHECK(hipMemsetAsync(m->pbar, 0, kPersistBarErr * sizeof(unsigned), m->work));
+        // Epochs restart at 1 in every launch: clear the words of the last one.
+        SNHIP_CHECK(hipMemsetAsync(m->pex, 0, 2 * (size_t)kPersistExWords * sizeof(unsigned long long), m->work));
+        SNHIP_CHECK(hipMemsetAsync(m->psx, 0, (size_t)m->L * 2 * m->D * sizeof(unsigned long long), m->work));
         a.tok_in = done == 0 ? m->tok : out_tok + done - 1;
         a.out_tok = greedy ? out_tok + done : nullptr;
         a.logits = done + n == n_steps ? logits : nullptr;
@@ -1146,8 +1155,7 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
         if (rc != SNHIP_OK) return rc;
         done += n;
     }
-    SNHIP_CHECK(hipMemcpyAsync(m->h_err, m->pbar + kPersistBarErr, sizeof(unsigned),
-                               hipMemcpyDeviceToHost, m->work));
+    SNHIP_CHECK(hipMemcpyAsync(m->h_err, m->perr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
     SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
     SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
     return SNHIP_OK;
@@ -1157,7 +1165,7 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
 snhip_status persist_status(SnHipModel* m) {
     if (m->h_err && *m->h_err) {
         *m->h_err = 0;
-        set_last_error("persistent decode: grid barrier timed out");
+        set_last_error("persistent decode: exchange wait timed out");
         return SNHIP_E_DEVICE;
     }
     return SNHIP_OK;

@@ -1,66 +1,71 @@
-// Persistent decode of one sequence: every layer of every step in one
+// Persistent decode of one sequence: every layer of every greedy step in one
 // cooperative launch (the B = 1 path of snhip_step / snhip_decode_greedy_dev).
 //
-// The math is the decode step of sunnynet/runtime/sunnynet.c:212-334, in the
-// same operation order as the per-kernel path (model.hip). A step is a chain
-// of small matrix-vector products, each too short to fill the chip as its own
-// launch; here the whole grid (one workgroup per CU) walks through the step in
-// phases separated by grid barriers:
+// The math is the decode step of sunnynet/runtime/sunnynet.c:212-334 (LayerNorm,
+// depthwise conv, low-rank U V product, competitive and decay gates, state
+// update, W_z read-out with the wedge, LN over inner, W_c + b s' + W_eff s + x,
+// final LN and head). A step is a chain of small matrix-vector products, each
+// too short to fill the chip as its own launch; here the whole grid walks
+// through the step in phases:
 //
-//   A  LN_in(x), depthwise conv -> at;  v = V at,  sfb = W_eff s      (all WGs)
-//   B  q = U v for one group of 8 channels per WG (16 contiguous rows of U:
-//      8 value, 8 gate),
-//      competitive + decay gate, s' = p s + (1 - p) u, conv history shift
-//   C  z = wedge(W_z u)
-//   D  y = LN_I(z);  x = W_c y + b s' + sfb + x
-//   H  logits = E LN_out(x), per-WG argmax key;  then every WG reduces the
-//      keys to the same greedy token, the next step's input.
+//   A(l)  x -> LN_in -> conv -> at;  v = V at (rows spread over the grid),
+//         sfb = W_eff s_old for the workgroup's own channels
+//   B(l)  q = U v for the workgroup's channel group(s) (16 contiguous rows of U
+//         per group: 8 values, 8 gates), competitive + decay gate,
+//         s' = p s + (1 - p) u for its own channels
+//   C(l)  z = wedge(W_z u)
+//   D(l)  y = LN_I(z);  x' = W_c y + b s' + sfb + x for its own channels
+//   H     logits = E LN_out(x), per-workgroup argmax key
+//   T     every workgroup reduces the keys to the same greedy token
 //
-// 4 L + 1 barriers per step. A barrier is split into arrive and wait; between
-// the two, the loads that do not depend on the phase that just ended are
-// issued: the dot waves load the weights of their first two batches of rows
-// of the next phase (and b s' + sfb + x for phase D), the staging wave the
-// inputs produced two or more phases earlier (the state s and conv-history
-// products for phase A, the old state and history for phase B) and the next
-// LayerNorm's gain and bias. After the wait only the previous phase's output
-// is fetched. Conv history: the phase-B owner of a channel also stores
-// hd[k] = hist'[k] * dw[K-2-k] for the next step, so phase A forms
-// acc = raw * dw[K-1] + hd[0] + hd[1] + ... in the reference's order
-// (sunnynet.c:227-233) with the products already rounded, bit-identical.
+// Exchange. Each vector a phase produces (v, u, z, x, the keys) is published as
+// 64-bit words (epoch << 32 | float bits) with agent-scope stores; the next
+// phase's readers poll those words until every epoch matches. Data and flag
+// travel in one single-copy-atomic word, so a reader needs no barrier and no
+// second round trip: a phase costs one store-to-load latency across XCDs.
+// Words are double-buffered by epoch parity. A writer of epoch e + 2 has read
+// epoch e + 1 from every workgroup, and each of those read all of epoch e
+// before writing e + 1, so no reader is still on the slot being overwritten
+// (every workgroup produces and reads every exchange). Buffers are zeroed
+// before each launch and epochs start at 1.
 //
-// Values exchanged between workgroups (x, v, sfb, u, z, s, hist, hd, the
-// argmax keys) are written and read with agent-scope atomic accesses
-// (global_load / global_store with sc1 on gfx950): the per-XCD L2 caches are
-// not coherent with each other, and plain loads would see stale lines. Each
-// wave drains its stores (s_waitcnt 0) before the workgroup arrives at a
-// barrier. Weights and other read-only data use ordinary cached loads.
+// Ownership. Workgroup w owns channels [w cpw, (w + 1) cpw): their state s,
+// the W_eff and W_c rows, and the residual x. Everything a channel needs in
+// phase D (s', sfb, x) is therefore produced inside the workgroup and never
+// exchanged; s' is also published (one word per channel, by step parity) for
+// every workgroup's W_eff product in the next step. Every workgroup forms the
+// full LN_in(x) of each layer, so each keeps its own copy of the last three
+// (a ring in global memory, read and written by the same thread) and computes
+// the conv in the reference's order, bit-identical. The handle's s / hist are
+// read at the first step and written back by the owners after the last.
 //
-// The barrier is two-level: workgroup g counts on group counter g & 7 (128
-// bytes apart, one per XCD under round-robin dispatch); the last arrival of a
-// group bumps the top counter that every workgroup polls. Counters only grow
-// (targets are epoch multiples), so no reset is needed inside the launch. Every
-// poll loop is bounded: on time-out the flag word is set and every workgroup
-// leaves the kernel at its next barrier.
+// Weights stream through two register pools per wave: while one batch of rows
+// is multiplied, the next batch (or the next phase's first batch) is in
+// flight, so a phase starts with its first weights already loaded. Every poll
+// loop is bounded: on time-out the error word is set and every workgroup
+// leaves at its next poll.
 #include "decode.h"
 
 namespace snhip {
 namespace {
 
-constexpr int NT = 256;                      // threads per workgroup (4 waves)
+constexpr int NT = 1024;                     // threads per workgroup (16 waves, 4 per SIMD)
+constexpr int NWV = NT / 64;
 constexpr int kMaxD = kPersistMaxD;          // dim
 constexpr int kMaxK = kPersistMaxK;          // inner, rank
-constexpr int PD = kMaxD / NT;               // values per thread of a dim-wide vector
-constexpr int PI = kMaxK / NT;               // of an inner- or rank-wide vector
-constexpr int PH = 8;                        // fp32: float4 per lane in one batch
-constexpr int MUH_MAX = 8;                   // INT4: units in one batch (32-wide groups;
-template <int BLK> constexpr int muh() { return BLK == 64 ? 4 : MUH_MAX; }   // half for 64)
+constexpr int PD = (kMaxD + NT - 1) / NT;   // values per thread of a dim-wide vector
+constexpr int PK = (kMaxK + NT - 1) / NT;   // of an inner- or rank-wide vector
+constexpr int CAPF = 4;                      // fp32: float4 per lane in one batch
+constexpr int KPT = (kPersistMaxGrid + NT - 1) / NT;   // argmax keys per thread
+constexpr int KT = kPersistTaps;             // conv taps
+constexpr int KH = KT - 1;                   // history entries
+
+typedef unsigned long long u64;
 
 // Read-only data through global-address-space pointers: global_load (counted
-// by vmcnt only). Through a generic pointer the compiler emits flat loads,
-// which also count against lgkmcnt, so the first LDS wait after a prefetch
-// would stall until every prefetched weight had arrived.
-// (Native vector types: HIP's float4 / uint4 are classes whose copy goes
-// through a generic reference and would lose the address space.)
+// by vmcnt only); through a generic pointer the compiler emits flat loads,
+// which also count against lgkmcnt and would make the first LDS wait after a
+// prefetch wait for every prefetched weight.
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const float g_f32;
@@ -75,96 +80,126 @@ __device__ __forceinline__ uint4 ldgq(const uint8_t* p) {
     const u32x4v v = *(g_u32x4*)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-// The layer table never changes during a launch: read through the constant
-// address space it becomes scalar loads (counted by lgkmcnt), so fetching a
-// layer's pointers does not wait for the vector loads in flight.
-#if defined(__HIP_DEVICE_COMPILE__)
-typedef __attribute__((address_space(4))) const PLayer c_layer;
-#else
-typedef const PLayer c_layer;   // host pass of the kernel source
-#endif
-// LDS activations are addressed the same way (ds_read, not flat).
-typedef __attribute__((address_space(3))) const float l_f32;
+typedef __attribute__((address_space(3))) float l_f32;
 typedef __attribute__((address_space(3))) const f32x4v l_f32x4;
-__device__ __forceinline__ float4 lds4(l_f32x4* p) {
-    const f32x4v v = *p;
+__device__ __forceinline__ float4 lds4(const l_f32* p) {
+    const f32x4v v = *(l_f32x4*)p;
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ float ldc(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// ---- exchange words
+__device__ __forceinline__ void ll_put(u64* p, uint32_t bits, unsigned ep) {
+    __hip_atomic_store(p, ((u64)ep << 32) | (u64)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void stc(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void ll_putf(u64* p, float v, unsigned ep) { ll_put(p, __float_as_uint(v), ep); }
+__device__ __forceinline__ u64 ll_get(const u64* p) {
+    return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool ll_ok(u64 w, unsigned ep) { return (uint32_t)(w >> 32) == ep; }
+__device__ __forceinline__ float ll_f(u64 w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ u64 ll_ready(float v, unsigned ep) { return ((u64)ep << 32) | __float_as_uint(v); }
+
+struct PollCtl {
+    unsigned* err;
+    unsigned limit;
+};
+
+// Re-polls the words of w that do not carry their epoch yet (word k from
+// addr(k), expected epoch want(k)) until all do. False on time-out (this
+// thread then sets the error word) or when another workgroup reported one.
+template <int W, class Addr, class Want>
+__device__ __forceinline__ bool ll_spin(u64 (&w)[W], Addr&& addr, Want&& want, const PollCtl& pc) {
+    unsigned spins = 0;
+    while (true) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < W; ++k) all = all && ll_ok(w[k], want(k));
+        if (all) return true;
+        if ((++spins & 255) == 0) {
+            if (__hip_atomic_load(pc.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+            if (spins > pc.limit) {
+                __hip_atomic_store(pc.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < W; ++k)
+            if (!ll_ok(w[k], want(k))) w[k] = ll_get(addr(k));
+    }
 }
 
 __device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // The same value, opaque to the optimizer. Applied to the thread index at
-// every phase boundary so per-lane addresses are formed inside each phase
-// instead of being hoisted out of the step loop (where hundreds of them
-// would stay live and spill).
+// every phase so per-lane addresses are formed inside the phase instead of
+// being hoisted out of the step loop (hundreds would stay live and spill).
 __device__ __forceinline__ int opq(int v) {
     asm volatile("" : "+v"(v));
     return v;
 }
 
-// Sum over the lane's 16-lane row, in every lane of the row: a rotation
-// butterfly with DPP row_ror 8, 4, 2, 1 (pairs are symmetric and the adds
-// commutative, so every lane ends with the same value).
+// ---- wave / block reductions
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+// Sum over the lane's 16-lane row, in every lane of the row (rotations by 8,
+// 4, 2, 1: pairs are symmetric, so every lane ends with the same value).
 __device__ __forceinline__ float row_sum(float v) {
-    v += dppf<0x128>(v);   // row_ror:8
-    v += dppf<0x124>(v);   // row_ror:4
-    v += dppf<0x122>(v);   // row_ror:2
-    v += dppf<0x121>(v);   // row_ror:1
+    v += dppf<0x128>(v);
+    v += dppf<0x124>(v);
+    v += dppf<0x122>(v);
+    v += dppf<0x121>(v);
     return v;
 }
 __device__ __forceinline__ float lane_val(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
-// Whole-wave sum (wave-uniform result).
 __device__ __forceinline__ float wsum(float v) {
     v = row_sum(v);
     return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
 }
-
-__device__ __forceinline__ unsigned long long kmax_wave(unsigned long long k) {
+__device__ __forceinline__ u64 kmax_wave(u64 k) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        const unsigned long long other =
-            ((unsigned long long)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
-            (uint32_t)__shfl_xor((int)(k & 0xFFFFFFFFull), o, 64);
+        const u64 other = ((u64)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
+                          (uint32_t)__shfl_xor((int)(k & 0xFFFFFFFFull), o, 64);
         k = max(k, other);
     }
     return k;
 }
-
-// Orderable key of (value, index): larger value wins, then smaller index
+// Orderable key of (value, index): larger value wins, then the smaller index
 // (torch.argmax's first maximal index, sunnynet/cli.py:41).
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+__device__ __forceinline__ u64 argmax_key(float v, int idx) {
     const uint32_t u = __float_as_uint(v);
     const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+    return ((u64)ord << 32) | (u64)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+// Block sum (wave-uniform result in every thread) through the NWV floats at
+// red: one barrier. Consecutive sums use different red buffers, and any two
+// uses of one buffer are separated by other barriers.
 __device__ __forceinline__ float bsum(float v, float* red) {
     v = wsum(v);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    __syncthreads();
     if (lane == 0) red[w] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
+    barrier_lds();
+    float r[NWV];
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) r[i] = red[i];
+#pragma unroll
+    for (int h = NWV / 2; h > 0; h >>= 1)
+#pragma unroll
+        for (int i = 0; i < h; ++i) r[i] = r[i] + r[i + h];
+    return r[0];
 }
 
-// Two-pass LayerNorm statistics (sunnynet.c:198-210 form) over n values,
-// element k * NT + tid held in xv[k].
+// Two-pass LayerNorm statistics (sunnynet.c:198-210) over n values, element
+// k * NT + tid in xv[k] (0 beyond n); red holds 2 NWV floats.
 template <int N>
-__device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps, int tid, float* red,
-                                         float& mean, float& rstd) {
+__device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps, float* red, float& mean,
+                                         float& rstd) {
+    const int tid = threadIdx.x;
     float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < N; ++k)
@@ -177,703 +212,588 @@ __device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps,
             const float d = xv[k] - mean;
             vs += d * d;
         }
-    rstd = 1.0f / sqrtf(bsum(vs, red) / (float)n + eps);
+    rstd = 1.0f / sqrtf(bsum(vs, red + NWV) / (float)n + eps);
 }
 
-// Issue agent-scope loads of n values (element k * NT + tid in v[k]); the
-// caller consumes them later.
-template <int N>
-__device__ __forceinline__ void issue_ldc(float (&v)[N], const float* src, int n, int tid) {
-#pragma unroll
-    for (int k = 0; k < N; ++k)
-        if (k * NT < n) v[k] = ldc(src + min(k * NT + tid, n - 1));
+// ---- jobs: the rows of one matrix a workgroup multiplies in one phase
+//
+// Rows j < n1 are r0 + j s0 and multiply x0; rows n1 <= j < n are r1 + (j - n1)
+// and multiply x1 (LDS vectors in the staged layout). With two parts, waves
+// 0-1 take the first and waves 2-3 the second, so each wave multiplies one
+// vector and keeps its slice of it in registers for the whole job.
+// fp32: lane l holds float4 i of a row at k = 256 i + 4 l; the wave's rows
+// form a flat list of items (row, i), nk4 = ceil(K / 256) items per row, and
+// a batch is CAPF consecutive items (a row may straddle two batches: its
+// per-lane partial sum carries over).
+// INT4: a row is split over seg lanes (the next power of two >= its ng
+// groups), one group of codes per lane; a unit is rpp = 64 / seg rows, a
+// batch MU units.
+struct Job {
+    const float* w;
+    const uint8_t* q;
+    const float* sc;
+    int K, n1, n, r0, s0, r1;
+    const l_f32* x0;
+    const l_f32* x1;
+};
+
+__device__ __forceinline__ Job make_job(const PMat& W, int K, int n1, int n, int r0, int s0, int r1,
+                                        const l_f32* x0, const l_f32* x1) {
+    Job J;
+    J.w = W.w; J.q = W.q; J.sc = W.sc;
+    J.K = K; J.n1 = n1; J.n = n; J.r0 = r0; J.s0 = s0; J.r1 = r1;
+    J.x0 = x0; J.x1 = x1;
+    return J;
 }
-template <int N>
-__device__ __forceinline__ void issue_ldg(float (&v)[N], const float* src, int n, int tid) {
-#pragma unroll
-    for (int k = 0; k < N; ++k)
-        if (k * NT < n) v[k] = ldg(src + min(k * NT + tid, n - 1));
+
+__device__ __forceinline__ int job_row(const Job& J, int j) { return j < J.n1 ? J.r0 + j * J.s0 : J.r1 + (j - J.n1); }
+
+// The wave's part of a job: job rows base + (wl + nwp m), m = 0, 1, ...
+struct Share {
+    int base, cnt, wl, nwp;
+    const l_f32* x;
+};
+__device__ __forceinline__ Share share_of(const Job& J, int wv) {
+    const bool two = J.n1 > 0 && J.n1 < J.n;
+    const bool hi = two && wv >= NWV / 2;
+    Share S;
+    S.nwp = two ? NWV / 2 : NWV;
+    S.wl = hi ? wv - NWV / 2 : wv;
+    S.base = hi ? J.n1 : 0;
+    S.cnt = two ? (hi ? J.n - J.n1 : J.n1) : J.n;
+    S.x = hi ? J.x1 : J.x0;
+    return S;
 }
-
-// Keeps the scheduler from moving instructions across this point, so loads
-// stay in the issue order the kernel relies on (vmcnt drains in order).
-__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// One phase's matrix-vector work: rows of one matrix W with contraction
-// length Kd, split in units; rows below `split` multiply x0, the others x1.
-// fp32: a unit is one row; a lane holds float4 i of a row at k = i * 256 +
-// 4 * lane (nk4 of them, rounded up to a power of two), a batch holds
-// PH / nk4 rows. INT4: a unit is rpp rows, one per segment of seg lanes, each
-// lane one group of BLK inputs; a batch holds MUH units. This wave takes units
-// u0, u0 + ustride, ... in batches; two batches are in registers at a time.
-struct PhaseDesc {
-    PMat W;
-    int nu, split;
-    int Kd, nk4, lg4, ng, seg, rpp, rpb;
-    l_f32* x0;              // LDS activation of rows < split (staged layout)
-    l_f32* x1;              // of rows >= split
-    int u0, ustride, nb;    // first unit, stride, batches
-};
-
-// A row's epilogue pre-loads (phase D: s', sfb, x).
-struct Pre3 {
-    float s, f, x;
-};
-
-// Epilogue inputs read with the weights (phase D): s', sfb and x per row.
-struct EpiPre {
-    const float* s;         // s' (new state) of the layer, or NULL: no pre-loads
-    const float* sfb;
-    const float* x;         // residual input
-};
-
-constexpr int EPS = 2;                       // slots per batch with epilogue pre-loads
 
 template <int BLK>
 struct Pool {
-    static constexpr int MUH = muh<BLK>();
     static constexpr int QW = BLK ? BLK / 32 : 1;    // uint4 per INT4 group
-    static constexpr int MS = BLK ? MUH : PH;        // slots (rows / units) per batch
-    float4 wf[2][BLK ? 1 : PH];
-    uint4 wq[2][BLK ? MUH : 1][QW];
-    float wsc[2][BLK ? MUH : 1];
-    float ep[2][EPS][3];
-    bool ep_on[2];
-    int unit[2][MS];                                 // -1: empty slot
+    static constexpr int MU = 2;                     // INT4 units per batch
+    float4 wf[BLK ? 1 : CAPF];
+    uint4 wq[BLK ? MU : 1][QW];
+    float wsc[BLK ? MU : 1];
+};
 
-    // Batch b of P into half h. Straight-line code with the same loads on
-    // every path (empty slots and lanes read element 0 of the matrix), so the
-    // compiler's wait counts for earlier loads stay exact. EP: also s', sfb,
-    // x of the batch's first EPS rows.
-    template <bool EP>
-    __device__ __forceinline__ void load(const PhaseDesc& P, int h, int b, int lane, const EpiPre& E) {
-        const bool bok = b < P.nb;
-        ep_on[h] = EP;
-        if constexpr (BLK == 0) {
-            const int sh = P.lg4;
+// The lane's slice of the job's input vector: fp32 nothing (read per item);
+// INT4 the quads of its group (low and high halves), zero past the row.
+template <int BLK>
+struct XCache {
+    float4 q[BLK ? BLK / 4 : 1];
+};
+
+// INT4 row geometry: log2 of the lanes per row.
+template <int BLK>
+__device__ __forceinline__ int i4_lseg(int K) {
+    const int ng = K / BLK;
+    return ng <= 1 ? 0 : 32 - __clz(ng - 1);
+}
+
+template <int BLK>
+__device__ __forceinline__ int job_batches(const Job& J, int wv) {
+    const Share S = share_of(J, wv);
+    const int nw = S.cnt > S.wl ? (S.cnt - S.wl + S.nwp - 1) / S.nwp : 0;   // the wave's rows
+    if constexpr (BLK == 0) {
+        return (nw * ((J.K + 255) >> 8) + CAPF - 1) / CAPF;
+    } else {
+        const int rpp = 64 >> i4_lseg<BLK>(J.K);
+        const int nu = (S.cnt + rpp - 1) / rpp;
+        const int nwu = nu > S.wl ? (nu - S.wl + S.nwp - 1) / S.nwp : 0;
+        return (nwu + Pool<BLK>::MU - 1) / Pool<BLK>::MU;
+    }
+}
+
+// Batch b of J into P. Straight-line: every slot issues its loads (empty ones
+// read element 0 of the matrix), so wait counts stay exact.
+template <int BLK>
+__device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int wv, int lane) {
+    const Share S = share_of(J, wv);
+    if constexpr (BLK == 0) {
+        const int nk4 = (J.K + 255) >> 8;
 #pragma unroll
-            for (int j = 0; j < PH; ++j) {
-                const int r = j >> sh, i = j & ((1 << sh) - 1);
-                const int u = P.u0 + (b * P.rpb + r) * P.ustride;
-                const bool ok = bok && r < P.rpb && u < P.nu;
-                const int k = i * 256 + lane * 4;
-                wf[h][j] = ldg4(P.W.w + ((ok && k < P.Kd) ? (size_t)u * P.Kd + k : 0));
-            }
+        for (int s = 0; s < CAPF; ++s) {
+            const int m = b * CAPF + s, mr = m / nk4, i = m - mr * nk4;
+            const int jl = S.wl + S.nwp * mr;
+            const int k = i * 256 + lane * 4;
+            const bool ok = jl < S.cnt && k < J.K;
+            const size_t off = (size_t)job_row(J, S.base + jl) * J.K + k;
+            P.wf[s] = ldg4(J.w + (ok ? off : 0));
+        }
+    } else {
+        constexpr int MU = Pool<BLK>::MU;
+        const int ng = J.K / BLK, ls = i4_lseg<BLK>(J.K), rpp = 64 >> ls;
+        const int lrow = lane >> ls, lg = lane & ((1 << ls) - 1);
 #pragma unroll
-            for (int r = 0; r < PH; ++r) {
-                const int u = P.u0 + (b * P.rpb + r) * P.ustride;
-                unit[h][r] = (bok && r < P.rpb && u < P.nu) ? u : -1;
-            }
-            if constexpr (EP) {
+        for (int s = 0; s < MU; ++s) {
+            const int jl = (S.wl + S.nwp * (b * MU + s)) * rpp + lrow;
+            const bool ok = jl < S.cnt && lg < ng;
+            const int row = job_row(J, S.base + jl);
+            const size_t qo = (size_t)row * (J.K / 2) + lg * (BLK / 2);
+            const size_t so = (size_t)row * ng + lg;
 #pragma unroll
-                for (int r = 0; r < EPS; ++r) {
-                    const int u = unit[h][r] < 0 ? 0 : unit[h][r];
-                    ep[h][r][0] = ldc(E.s + u);
-                    ep[h][r][1] = ldc(E.sfb + u);
-                    ep[h][r][2] = ldc(E.x + u);
-                }
-            }
-        } else {
-            const int lrow = lane / P.seg, lg = lane - lrow * P.seg;
-#pragma unroll
-            for (int s = 0; s < MUH; ++s) {
-                const int u = P.u0 + (b * MUH + s) * P.ustride;
-                const bool uok = bok && u < P.nu;
-                unit[h][s] = uok ? u : -1;
-                const int r = u * P.rpp + lrow;
-                const bool ok = uok && r < P.W.M && lg < P.ng;
-                const uint8_t* qr = P.W.q + (ok ? (size_t)r * (P.Kd / 2) + lg * (BLK / 2) : 0);
-#pragma unroll
-                for (int q = 0; q < QW; ++q) wq[h][s][q] = ldgq(qr + 16 * q);
-                wsc[h][s] = ldg(P.W.sc + (ok ? (size_t)r * P.ng + lg : 0));
-                if constexpr (EP) {
-                    if (s < EPS) {
-                        const int rr = (uok && r < P.W.M) ? r : 0;
-                        ep[h][s][0] = ldc(E.s + rr);
-                        ep[h][s][1] = ldc(E.sfb + rr);
-                        ep[h][s][2] = ldc(E.x + rr);
-                    }
-                }
-            }
+            for (int qq = 0; qq < Pool<BLK>::QW; ++qq) P.wq[s][qq] = ldgq(J.q + (ok ? qo + 16 * qq : 0));
+            P.wsc[s] = ldg(J.sc + (ok ? so : 0));
         }
     }
+}
 
-    // epi(row, value, writer, pre, has_pre): the row's dot product; `writer`
-    // is true on exactly one lane per row; pre = the row's epilogue pre-loads
-    // when has_pre.
-    template <int NK4, class Epi>
-    __device__ __forceinline__ void compute_f32(const PhaseDesc& P, int h, int lane, Epi&& epi) {
-        constexpr int RPB = PH / NK4;
-        float acc[RPB];
+template <int BLK>
+__device__ __forceinline__ void xcache_load(const Job& J, XCache<BLK>& X, int wv, int lane) {
+    if constexpr (BLK != 0) {
+        const Share S = share_of(J, wv);
+        const int ng = J.K / BLK, ls = i4_lseg<BLK>(J.K);
+        const int lg = min(lane & ((1 << ls) - 1), ng - 1);
 #pragma unroll
-        for (int r = 0; r < RPB; ++r) {
-            acc[r] = 0.0f;
-            if (unit[h][r] < 0) continue;
-            l_f32* xs = unit[h][r] < P.split ? P.x0 : P.x1;
-#pragma unroll
-            for (int i = 0; i < NK4; ++i) {
-                const int k = i * 256 + lane * 4;
-                if (k < P.Kd) {
-                    const float4 x4 = lds4((l_f32x4*)(xs + k));
-                    const float4 w4 = wf[h][r * NK4 + i];
-                    acc[r] = fmaf(w4.x, x4.x, acc[r]);
-                    acc[r] = fmaf(w4.y, x4.y, acc[r]);
-                    acc[r] = fmaf(w4.z, x4.z, acc[r]);
-                    acc[r] = fmaf(w4.w, x4.w, acc[r]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < RPB; ++r) acc[r] = row_sum(acc[r]);
-#pragma unroll
-        for (int r = 0; r < RPB; ++r)
-            acc[r] = (lane_val(acc[r], 0) + lane_val(acc[r], 16)) + (lane_val(acc[r], 32) + lane_val(acc[r], 48));
-#pragma unroll
-        for (int r = 0; r < RPB; ++r)
-            if (unit[h][r] >= 0) {
-                const bool hp = ep_on[h] && r < EPS;
-                const int re = r < EPS ? r : 0;
-                epi(unit[h][r], acc[r], lane == 0, Pre3{ep[h][re][0], ep[h][re][1], ep[h][re][2]}, hp);
-            }
+        for (int q = 0; q < BLK / 4; ++q) X.q[q] = lds4(S.x + 4 * (q * ng + lg));
     }
+}
 
-    template <class Epi>
-    __device__ __forceinline__ void compute_i4(const PhaseDesc& P, int h, int lane, Epi&& epi) {
-        const int lrow = lane / P.seg, lg = lane - lrow * P.seg;
-        constexpr int NW = BLK / 8;                  // 32-bit words of codes per group
-        float acc[MUH];
+// epi(j, row, value, writer): `writer` is true on exactly one lane per row.
+// Every slot is computed (the loads of empty slots are valid addresses);
+// only rows of the job are handed to epi.
+template <class Epi>
+__device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<0>& P, int wv, int lane, float& pacc,
+                                            Epi&& epi) {
+    const Share S = share_of(J, wv);
+    const int nk4 = (J.K + 255) >> 8;
+    float4 xs[CAPF];
 #pragma unroll
-        for (int s = 0; s < MUH; ++s) {
-            acc[s] = 0.0f;
-            const int r = unit[h][s] * P.rpp + lrow;
-            if (unit[h][s] < 0 || r >= P.W.M || lg >= P.ng) continue;
-            l_f32x4* x4 = (l_f32x4*)(r < P.split ? P.x0 : P.x1);
-            const float sc = wsc[h][s];
+    for (int s = 0; s < CAPF; ++s) {
+        const int m = b * CAPF + s, mr = m / nk4, i = m - mr * nk4;
+        xs[s] = lds4(S.x + min(i * 256 + lane * 4, J.K - 4));
+    }
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const uint4& qq = wq[h][s][w >> 2];
-                const int wi = w & 3;
-                const uint32_t word = wi == 0 ? qq.x : wi == 1 ? qq.y : wi == 2 ? qq.z : qq.w;
-                // Byte 4w + e holds element 4w + e (low nibble) and
-                // 4w + e + BLK/2 (high nibble); quant.c:82-83 dequantization.
-                const float4 xl = lds4(x4 + w * P.ng + lg);
-                const float4 xh = lds4(x4 + (w + NW) * P.ng + lg);
-                const float xlo[4] = {xl.x, xl.y, xl.z, xl.w};
-                const float xhi[4] = {xh.x, xh.y, xh.z, xh.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t byte = (word >> (8 * e)) & 0xFFu;
-                    const float wl = (float)((int)(byte & 0x0Fu) - 8) * sc;
-                    const float wh = (float)((int)(byte >> 4) - 8) * sc;
-                    acc[s] = fmaf(wl, xlo[e], acc[s]);
-                    acc[s] = fmaf(wh, xhi[e], acc[s]);
-                }
-            }
+    for (int s = 0; s < CAPF; ++s) {
+        const int m = b * CAPF + s, mr = m / nk4, i = m - mr * nk4;
+        const int jl = S.wl + S.nwp * mr;
+        if (i * 256 + lane * 4 < J.K) {
+            const float4 w4 = P.wf[s];
+            pacc = fmaf(w4.x, xs[s].x, pacc);
+            pacc = fmaf(w4.y, xs[s].y, pacc);
+            pacc = fmaf(w4.z, xs[s].z, pacc);
+            pacc = fmaf(w4.w, xs[s].w, pacc);
         }
-        if (P.seg >= 16) {
-            // rows of 16 lanes by DPP, then the rows of each segment
+        if (i == nk4 - 1) {
+            const float v = wsum(pacc);
+            pacc = 0.0f;
+            if (jl < S.cnt) epi(S.base + jl, job_row(J, S.base + jl), v, lane == 0);
+        }
+    }
+}
+
+template <int BLK, class Epi>
+__device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int wv,
+                                           int lane, Epi&& epi) {
+    constexpr int MU = Pool<BLK>::MU;
+    constexpr int NW = BLK / 8;                  // 32-bit words of codes per group
+    const Share S = share_of(J, wv);
+    const int ng = J.K / BLK, ls = i4_lseg<BLK>(J.K), rpp = 64 >> ls, seg = 1 << ls;
+    const int lrow = lane >> ls, lg = lane & (seg - 1);
+    const bool lane_ok = lg < ng;
+    // Units of this batch that hold rows (the rest are skipped, uniformly).
+    const int nu = (S.cnt + rpp - 1) / rpp;
+    const int u0 = S.wl + S.nwp * b * MU;
+    const int nvu = u0 < nu ? min(MU, (nu - u0 + S.nwp - 1) / S.nwp) : 0;
+    float acc[MU];
 #pragma unroll
-            for (int s = 0; s < MUH; ++s) acc[s] = row_sum(acc[s]);
+    for (int s = 0; s < MU; ++s) {
+        acc[s] = 0.0f;
+        if (s >= nvu) continue;
+        // (q - 8) * scale as one rounding: fma(q, scale, -8 scale), with
+        // -8 scale exact (quant.c:82-83 dequantization, bit-identical).
+        const float sc = P.wsc[s], m8 = -8.0f * sc;
+        float a = 0.0f;
 #pragma unroll
-            for (int s = 0; s < MUH; ++s) {
+        for (int w = 0; w < NW; ++w) {
+            const uint4& qq = P.wq[s][w >> 2];
+            const int wi = w & 3;
+            const uint32_t word = wi == 0 ? qq.x : wi == 1 ? qq.y : wi == 2 ? qq.z : qq.w;
+            // Byte 4w + e holds element 4w + e (low nibble) and 4w + e + BLK/2
+            // (high nibble).
+            const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+            const float4 xl = X.q[w], xh = X.q[w + NW];
+            a = fmaf(fmaf((float)(lo & 0xFFu), sc, m8), xl.x, a);
+            a = fmaf(fmaf((float)(hi & 0xFFu), sc, m8), xh.x, a);
+            a = fmaf(fmaf((float)((lo >> 8) & 0xFFu), sc, m8), xl.y, a);
+            a = fmaf(fmaf((float)((hi >> 8) & 0xFFu), sc, m8), xh.y, a);
+            a = fmaf(fmaf((float)((lo >> 16) & 0xFFu), sc, m8), xl.z, a);
+            a = fmaf(fmaf((float)((hi >> 16) & 0xFFu), sc, m8), xh.z, a);
+            a = fmaf(fmaf((float)(lo >> 24), sc, m8), xl.w, a);
+            a = fmaf(fmaf((float)(hi >> 24), sc, m8), xh.w, a);
+        }
+        acc[s] = lane_ok ? a : 0.0f;
+    }
+    if (seg >= 16) {
+#pragma unroll
+        for (int s = 0; s < MU; ++s) acc[s] = row_sum(acc[s]);
+        if (seg > 16) {
+#pragma unroll
+            for (int s = 0; s < MU; ++s) {
                 const float r0 = lane_val(acc[s], 0), r1 = lane_val(acc[s], 16);
                 const float r2 = lane_val(acc[s], 32), r3 = lane_val(acc[s], 48);
-                acc[s] = P.seg == 64 ? (r0 + r1) + (r2 + r3)
-                       : P.seg == 32 ? (lane < 32 ? r0 + r1 : r2 + r3)
-                                     : acc[s];
+                acc[s] = seg == 64 ? (r0 + r1) + (r2 + r3) : (lane < 32 ? r0 + r1 : r2 + r3);
             }
-        } else {
-            for (int o = P.seg >> 1; o > 0; o >>= 1)
+        }
+    } else {
+        for (int o = seg >> 1; o > 0; o >>= 1)
 #pragma unroll
-                for (int s = 0; s < MUH; ++s) acc[s] += __shfl_xor(acc[s], o, 64);
-        }
+            for (int s = 0; s < MU; ++s) acc[s] += __shfl_xor(acc[s], o, 64);
+    }
 #pragma unroll
-        for (int s = 0; s < MUH; ++s) {
-            if (unit[h][s] < 0) continue;
-            const int r = unit[h][s] * P.rpp + lrow;
-            const bool hp = ep_on[h] && s < EPS;
-            const int se = s < EPS ? s : 0;
-            epi(r, acc[s], r < P.W.M && lg < P.ng && lg == 0,
-                Pre3{ep[h][se][0], ep[h][se][1], ep[h][se][2]}, hp);
-        }
-    }
-
-    template <class Epi>
-    __device__ __forceinline__ void compute(const PhaseDesc& P, int h, int lane, Epi&& epi) {
-        if constexpr (BLK == 0) {
-            switch (P.nk4) {
-                case 1: compute_f32<1>(P, h, lane, epi); break;
-                case 2: compute_f32<2>(P, h, lane, epi); break;
-                case 4: compute_f32<4>(P, h, lane, epi); break;
-                default: compute_f32<8>(P, h, lane, epi); break;
-            }
-        } else {
-            compute_i4(P, h, lane, epi);
-        }
-    }
-};
-
-struct GridBar {
-    unsigned* sub;
-    unsigned* top;
-    unsigned* err;
-    unsigned cnt, ngrp, epoch, stall, limit;
-};
-
-// All of this workgroup's global stores have completed; count it in.
-__device__ __forceinline__ void bar_arrive(GridBar& g) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    ++g.epoch;
-    if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(g.sub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1 == g.cnt * g.epoch)
-            __hip_atomic_fetch_add(g.top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int s = 0; s < MU; ++s) {
+        const int jl = (S.wl + S.nwp * (b * MU + s)) * rpp + lrow;
+        if (jl < S.cnt) epi(S.base + jl, job_row(J, S.base + jl), acc[s], lg == 0);
     }
 }
 
-// Waits until every workgroup has arrived; false on time-out (or another
-// workgroup's time-out), after which the caller leaves the kernel.
-__device__ __forceinline__ bool bar_wait(GridBar& g, int* flag) {
-    if (threadIdx.x == 0) {
-        const unsigned want = g.ngrp * g.epoch + g.stall;
-        int ok = 1;
-        unsigned spins = 0;
-        while ((int)(__hip_atomic_load(g.top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - want) < 0) {
-            if ((++spins & 255) == 0) {
-                if (__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) { ok = 0; break; }
-                if (spins > g.limit) {
-                    __hip_atomic_store(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok = 0;
-                    break;
-                }
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        *flag = ok;
-    }
-    __syncthreads();
-    return *flag != 0;
+template <int BLK, class Epi>
+__device__ __forceinline__ void compute(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int wv,
+                                        int lane, float& pacc, Epi&& epi) {
+    if constexpr (BLK == 0) compute_f32(J, b, P, wv, lane, pacc, epi);
+    else compute_i4<BLK>(J, b, P, X, wv, lane, epi);
 }
 
-// Order of loads. vmcnt drains in issue order per wave, so a value can only
-// be consumed once everything issued before it has arrived, and the compiler
-// computes exact waits only across straight-line code that issues the same
-// loads on every path. Each phase therefore issues, in this order and without
-// branches: its own inputs (the previous phase's output, LayerNorm
-// parameters), then the next phase's inputs produced earlier (state, history
-// products), then the next phase's weights into the register half the current
-// phase does not use. Phases alternate halves: A and C use half 0, B and D
-// half 1; the LM head streams through both. A phase's weights are issued a
-// full phase ahead and are in registers when it starts (arriving at a barrier
-// drains every outstanding access: gfx9 counts stores and loads together).
-// KHT: conv-history entries (taps - 1), a compile-time count so the history
-// loads are straight-line too.
-template <int BLK, int KHT>
+// Runs every batch of J (batch 0 is already in p0): batches alternate between
+// the pools, and each is issued before the previous one is multiplied. The
+// loads of a batch past the last read element 0 of the matrix (unused), so
+// every path issues the same loads and the wait counts stay exact.
+template <int BLK, class Epi>
+__device__ __forceinline__ void run_job(const Job& J, Pool<BLK>& p0, Pool<BLK>& p1, int wv, int lane, Epi&& epi) {
+    const int nb = job_batches<BLK>(J, wv);
+    XCache<BLK> X;
+    xcache_load<BLK>(J, X, wv, lane);
+    float pacc = 0.0f;
+    for (int b = 0; b < nb; b += 2) {
+        pool_load<BLK>(J, b + 1, p1, wv, lane);
+        compute<BLK>(J, b, p0, X, wv, lane, pacc, epi);
+        pool_load<BLK>(J, b + 2, p0, wv, lane);
+        if (b + 1 < nb) compute<BLK>(J, b + 1, p1, X, wv, lane, pacc, epi);
+    }
+}
+
+// Index of element i of a K-long vector in the staged LDS layout: fp32 plain;
+// INT4 quad-major, so lane g of a row reads its group's quads q at
+// (q ng + g) * 4 (consecutive lanes, consecutive 16 bytes).
+template <int BLK>
+__device__ __forceinline__ int sidx(int i, int K) {
+    if constexpr (BLK == 0) return i;
+    else return ((((i % BLK) >> 2) * (K / BLK) + i / BLK) << 2) + (i & 3);
+}
+
+#ifdef SNHIP_PERSIST_PROF
+// Phase timestamps of workgroup 0 (wall clock), for profiling builds only.
+__device__ unsigned long long g_prof[2048];
+#define PROF(idx) do { if (wg == 0 && lane == 0 && step == 3) g_prof[(idx) * 4 + wv] = wall_clock64(); } while (0)
+#else
+#define PROF(idx) do { } while (0)
+#endif
+
+// One code path serves every phase (the instruction cache holds the whole
+// step loop): phase p of a step is A, B, C, D of layer p / 4 for p < 4 L, then
+// the head H; per-phase differences are uniform branches on the phase type.
+template <int BLK>
 __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
-    __shared__ __align__(16) float xs[kMaxK];     // activation of the current products
-    __shared__ __align__(16) float xs2[kMaxD];    // old state s (phase A, W_eff's rows)
-    __shared__ float raw[kMaxD];                  // LN_in(x) of the layer: history input
-    __shared__ float hdl[KHT * kMaxD];            // conv-history products of the layer
-    __shared__ float q16[16];
-    __shared__ float red[4];
-    __shared__ unsigned long long kred[4];
-    __shared__ int flag;
+    __shared__ __align__(16) float xin[kMaxK];    // input vector of the current products
+    __shared__ __align__(16) float xs2[kMaxD];    // old state s (W_eff's input in phase A)
+    __shared__ float xres[kMaxD];                 // x of the layer (residual)
+    __shared__ float res[kMaxK + kMaxD];          // products of the current phase, by job row
+    __shared__ float sown[kMaxD];                 // s' of the owned channels
+    __shared__ float sfbl[kMaxD];                 // W_eff s_old of the owned channels
+    __shared__ float red[2 * NWV];
+    __shared__ u64 kred[NWV];
+    __shared__ int sflag;
+    __shared__ PLayer ltab[kPersistMaxL];          // the layer table (LDS reads, no scalar misses)
 
     int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     auto fresh = [&]() {
         tid = opq(tid);
         lane = tid & 63;
     };
-    const int nwg = gridDim.x, wg = blockIdx.x;
-    const int NW = nwg * 4, gw = wg * 4 + wv;
-    const int D = a.D, I = a.I, R = a.R, K = KHT + 1, L = a.L;
-    constexpr int kh = KHT;
+    const int G = gridDim.x, wg = blockIdx.x;
+    const int D = a.D, I = a.I, R = a.R, L = a.L;
+    const int cpw = D / G, c0 = wg * cpw;                     // owned channels
+    const int grp0 = c0 >> 3, ngrp = cpw >= 8 ? cpw >> 3 : 1; // owned channel groups
+    const PollCtl pc{a.err, a.spin_limit};
+    for (int i = tid; i < L * (int)sizeof(PLayer) / 4; i += NT)
+        ((uint32_t*)ltab)[i] = ((const uint32_t*)a.layers)[i];
+    const PLayer* lt = ltab;
+    u64* ex0 = a.ex;
+    auto exs = [&](unsigned e) -> u64* { return ex0 + (size_t)(e & 1u) * kPersistExWords; };
 
-    GridBar bar;
-    {
-        const int g = wg & 7;
-        bar.sub = a.bar + g * 32;
-        bar.top = a.bar + 256;
-        bar.err = a.bar + kPersistBarErr;
-        bar.cnt = (unsigned)((nwg - g + 7) / 8);
-        bar.ngrp = (unsigned)min(nwg, 8);
-        bar.epoch = 0;
-        bar.stall = a.stall;
-        bar.limit = a.spin_limit;
-    }
+    if (tid == 0) sflag = 0;
+    barrier_lds();
+    // Leaves the kernel (in every thread of the workgroup) when any thread's
+    // poll failed.
+    auto agree = [&](bool ok) -> bool {
+        if (!ok) sflag = 1;
+        barrier_lds();
+        return sflag == 0;
+    };
 
-    auto sidx = [&](int i, int Kd) -> int {
-        if constexpr (BLK == 0) return i;
-        else return ((((i % BLK) >> 2) * (Kd / BLK) + i / BLK) << 2) + (i & 3);
-    };
-    auto geom = [&](PhaseDesc& P, int Kd) {
-        P.Kd = Kd;
-        if constexpr (BLK == 0) {
-            const int n = (Kd + 255) / 256;
-            P.lg4 = n <= 1 ? 0 : n <= 2 ? 1 : n <= 4 ? 2 : 3;
-            P.nk4 = 1 << P.lg4;
-            P.ng = 0; P.seg = 64; P.rpp = 1;
-            P.rpb = PH / P.nk4;
-        } else {
-            P.nk4 = 0; P.lg4 = 0;
-            P.ng = Kd / BLK;
-            P.seg = (P.ng < 64 && 64 % P.ng == 0) ? P.ng : 64;
-            P.rpp = 64 / P.seg;
-            P.rpb = muh<BLK>();
-        }
-    };
-    auto finish = [&](PhaseDesc& P, int u0, int stride) {
-        P.u0 = u0;
-        P.ustride = stride;
-        const int cnt = u0 < P.nu ? (P.nu - u0 + stride - 1) / stride : 0;
-        P.nb = (cnt + P.rpb - 1) / P.rpb;
-    };
-    auto desc = [&](const PMat& W, int Kd, const float* x0, const float* x1, int split) {
-        // x0 / x1 are this workgroup's LDS arrays
-        PhaseDesc P;
-        geom(P, Kd);
-        P.W = W;
-        P.nu = (W.M + P.rpp - 1) / P.rpp;
-        P.split = split;
-        P.x0 = (l_f32*)x0; P.x1 = (l_f32*)x1;
-        finish(P, gw, NW);
-        return P;
-    };
-    // V's rows multiply at, W_eff's rows (from row R on) the old state.
-    auto layer = [&](int l) -> PLayer { return ((c_layer*)a.layers)[l]; };
-    auto descA = [&](int l) { return desc(layer(l).VW, D, xs, xs2, R); };
-    const int ngroups = D / 8;
-    // Group c: the 16 contiguous rows 16c.. of U (8 values, 8 gates), split
-    // over the workgroup's four waves. (A workgroup without a group loads
-    // the last group's rows and leaves them unused.)
-    auto descB = [&](int l, int c) {
-        const PMat U = layer(l).U;
-        PhaseDesc P;
-        geom(P, R);
-        const size_t r0 = (size_t)16 * min(c, ngroups - 1);
-        if constexpr (BLK == 0) P.W = PMat{U.w + r0 * R, nullptr, nullptr, 16};
-        else P.W = PMat{nullptr, U.q + r0 * (R / 2), U.sc + r0 * P.ng, 16};
-        P.nu = (16 + P.rpp - 1) / P.rpp;
-        P.split = 16;
-        P.x0 = (l_f32*)xs; P.x1 = (l_f32*)xs;
-        finish(P, wv, 4);
-        return P;
-    };
-    auto descC = [&](int l) {
-        const PMat W = layer(l).Wz;
-        return desc(W, D, xs, xs, W.M);
-    };
-    auto descD = [&](int l) {
-        const PMat W = layer(l).Wc;
-        return desc(W, I, xs, xs, W.M);
-    };
-    auto descH = [&]() { return desc(a.head, D, xs, xs, a.head.M); };
-    const EpiPre none{nullptr, nullptr, nullptr};
-
-    Pool<BLK> pool;
-    // All batches of a phase from one half (batch 0 loaded a phase earlier).
-    auto run0 = [&](const PhaseDesc& P, const EpiPre& E, auto&& epi) {
-        for (int b = 0; b < P.nb; ++b) {
-            if (b > 0) pool.template load<false>(P, 0, b, lane, E);
-            pool.compute(P, 0, lane, epi);
-        }
-    };
-    auto run1 = [&](const PhaseDesc& P, const EpiPre& E, auto&& epi) {
-        for (int b = 0; b < P.nb; ++b) {
-            if (b > 0) pool.template load<false>(P, 1, b, lane, E);
-            pool.compute(P, 1, lane, epi);
-        }
-    };
-    // Double-buffered through both halves (batches 0 and 1 loaded before).
-    auto run_stream = [&](const PhaseDesc& P, const EpiPre& E, auto&& epi) {
-        for (int b = 0; b < P.nb; b += 2) {
-            pool.compute(P, 0, lane, epi);
-            pool.template load<false>(P, 0, b + 2, lane, E);
-            if (b + 1 < P.nb) {
-                pool.compute(P, 1, lane, epi);
-                pool.template load<false>(P, 1, b + 3, lane, E);
-            }
+    const int nV = R > wg ? (R - wg + G - 1) / G : 0;
+    const int nZ = I > wg ? (I - wg + G - 1) / G : 0;
+    const int nH = a.vocab > wg ? (a.vocab - wg + G - 1) / G : 0;
+    const l_f32* lx = (const l_f32*)xin;
+    const l_f32* ls = (const l_f32*)xs2;
+    const int NP = 4 * L + 1;
+    // The rows this workgroup multiplies in phase p (A: its V rows, then the
+    // W_eff rows of its channels; B: the U rows of its channel groups; C: its
+    // W_z rows; D: the W_c rows of its channels; H: its head rows).
+    auto job = [&](int p) -> Job {
+        if (p >= 4 * L) return make_job(a.head, D, nH, nH, wg, G, 0, lx, lx);
+        const PLayer* Ly = lt + (p >> 2);
+        switch (p & 3) {
+            case 0: return make_job(Ly->VW, D, nV, nV + cpw, wg, G, R + c0, lx, ls);
+            case 1: return make_job(Ly->U, R, 16 * ngrp, 16 * ngrp, 16 * grp0, 1, 0, lx, lx);
+            case 2: return make_job(Ly->Wz, D, nZ, nZ, wg, G, 0, lx, lx);
+            default: return make_job(Ly->Wc, I, cpw, cpw, c0, 1, 0, lx, lx);
         }
     };
 
-    // Phase A inputs produced earlier: s -> xs2, conv-history products -> hdl.
-    float sv[PD], hv[PD][KHT > 0 ? KHT : 1];
-    auto prestage_issue = [&](int l) {
-        const float* s_l = a.s + (size_t)l * D;
-        const float* hd_l = a.hd + (size_t)l * (kh ? kh : 1) * D;
-#pragma unroll
-        for (int k = 0; k < PD; ++k) {
-            const int i = min(k * NT + tid, D - 1);
-            sv[k] = ldc(s_l + i);
-#pragma unroll
-            for (int t = 0; t < KHT; ++t) hv[k][t] = ldc(hd_l + (size_t)t * D + i);
-        }
-    };
-    auto prestage_store = [&]() {
-#pragma unroll
-        for (int k = 0; k < PD; ++k) {
-            const int i = k * NT + tid;
-            if (i >= D) continue;
-            xs2[sidx(i, D)] = sv[k];
-#pragma unroll
-            for (int t = 0; t < KHT; ++t) hdl[t * D + i] = hv[k][t];
-        }
-    };
-    // Phase B inputs for channel group c: old s and history of channel
-    // 8 c + (tid & 7) (used by tid < 8).
-    float pb_s = 0.0f, pb_h[KHT > 1 ? KHT - 1 : 1];
-    auto preload_B = [&](int l, int c) {
-        const int i = min(c, ngroups - 1) * 8 + (tid & 7);
-        pb_s = ldc(a.s + (size_t)l * D + i);
-        const float* h_l = a.hist + (size_t)l * (kh ? kh : 1) * D;
-#pragma unroll
-        for (int t = 0; t + 1 < KHT; ++t) pb_h[t] = ldc(h_l + (size_t)t * D + i);
-    };
+    Pool<BLK> p0, p1;
+    pool_load<BLK>(job(0), 0, p0, wv, lane);
 
-    // ---- phases (A of layer 0 differs: it also issues its own weights)
-    auto phaseA = [&](int l, bool tok_ok, const float* erow) {
-        const PLayer Ly = layer(l);
-        float xv[PD], gv[PD], cv[PD], dv[PD];
-        if (l == 0) issue_ldg(xv, erow, D, tid);
-        else issue_ldc(xv, a.x, D, tid);
-        issue_ldg(gv, Ly.ni_g, D, tid);
-        issue_ldg(cv, Ly.ni_c, D, tid);
-        issue_ldg(dv, Ly.dw + (size_t)(K - 1) * D, D, tid);
-        issue_fence();
-        if (l == 0) {
-            prestage_issue(0);
-            issue_fence();
-            pool.template load<false>(descA(0), 0, 0, lane, none);
-            issue_fence();
-        }
-        preload_B(l, wg);
-        issue_fence();
-        pool.template load<false>(descB(l, wg), 1, 0, lane, none);
-        issue_fence();
-        if (l == 0) prestage_store();
-#pragma unroll
-        for (int k = 0; k < PD; ++k)
-            if (k * NT + tid >= D) xv[k] = 0.0f;
-            else if (l == 0 && !tok_ok) xv[k] = __builtin_nanf("");
-        float mean, rstd;
-        ln_stats(xv, D, a.eps, tid, red, mean, rstd);
-#pragma unroll
-        for (int k = 0; k < PD; ++k) {
-            const int i = k * NT + tid;
-            if (i >= D) continue;
-            const float r = (xv[k] - mean) * rstd * gv[k] + cv[k];
-            raw[i] = r;
-            float acc = r * dv[k];
-#pragma unroll
-            for (int t = 0; t < KHT; ++t) acc = acc + hdl[t * D + i];
-            xs[sidx(i, D)] = KHT > 0 ? r + acc : r;
-        }
-        __syncthreads();
-        run0(descA(l), none, [&](int r, float v, bool w, Pre3, bool) {
-            if (w) stc(r < R ? a.v + r : a.sfb + (r - R), v);
-        });
-    };
-    auto phaseB = [&](int l) {
-        const PLayer Ly = layer(l);
-        float* s_l = a.s + (size_t)l * D;
-        float* h_l = a.hist + (size_t)l * (kh ? kh : 1) * D;
-        float* hd_l = a.hd + (size_t)l * (kh ? kh : 1) * D;
-        float vv[PI];
-        issue_ldc(vv, a.v, R, tid);
-        issue_fence();
-        pool.template load<false>(descC(l), 0, 0, lane, none);
-        issue_fence();
-#pragma unroll
-        for (int k = 0; k < PI; ++k)
-            if (k * NT + tid < R) xs[sidx(k * NT + tid, R)] = vv[k];
-        __syncthreads();
-        for (int c = wg; c < ngroups; c += nwg) {
-            const PhaseDesc P = descB(l, c);
-            if (c != wg) {
-                preload_B(l, c);
-                pool.template load<false>(P, 1, 0, lane, none);
-            }
-            run1(P, none, [&](int r, float v, bool w, Pre3, bool) {
-                if (w) q16[r] = v;
-            });
-            __syncthreads();
-            if (tid < 8) {
-                const int i = c * 8 + tid;
-                const float gi = q16[8 + tid];
-                const float uu = q16[tid] * (sgm(gi - q16[8 + ((tid + 1) & 7)]) *
-                                             sgm(gi - q16[8 + ((tid + 2) & 7)]));
-                float p = 1.0f - ldg(Ly.delta + i) * (1.0f - sgm(gi));
-                if (a.clamp && p < a.p_floor) p = a.p_floor;
-                stc(s_l + i, p * pb_s + (1.0f - p) * uu);
-                stc(a.u + i, uu);
-                if (KHT > 0) {
-                    // hist' = [raw, hist[0], ..., hist[kh-2]]; hd' = hist' * dw
-                    const float r = raw[i];
-                    stc(h_l + i, r);
-                    stc(hd_l + i, r * ldg(Ly.dw + (size_t)(K - 2) * D + i));
-#pragma unroll
-                    for (int t = 1; t < KHT; ++t) {
-                        stc(h_l + (size_t)t * D + i, pb_h[t - 1]);
-                        stc(hd_l + (size_t)t * D + i, pb_h[t - 1] * ldg(Ly.dw + (size_t)(K - 2 - t) * D + i));
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    };
-    auto phaseC = [&](int l, const EpiPre& preD) {
-        const PLayer Ly = layer(l);
-        float uv[PD];
-        issue_ldc(uv, a.u, D, tid);
-        issue_fence();
-        pool.template load<true>(descD(l), 1, 0, lane, preD);
-        issue_fence();
-#pragma unroll
-        for (int k = 0; k < PD; ++k)
-            if (k * NT + tid < D) xs[sidx(k * NT + tid, D)] = uv[k];
-        __syncthreads();
-        const float at = Ly.a_tanh;
-        run0(descC(l), none, [&](int r, float v, bool w, Pre3, bool) {
-            if (w) stc(a.z + r, v * (1.0f + 0.5f * at / (1.0f + fabsf(v))));
-        });
-    };
-    auto phaseD = [&](int l, bool bad_tok, const EpiPre& preD) {
-        const PLayer Ly = layer(l);
-        float zv[PI], gv[PI], cv[PI];
-        issue_ldc(zv, a.z, I, tid);
-        issue_ldg(gv, Ly.nm_g, I, tid);
-        issue_ldg(cv, Ly.nm_c, I, tid);
-        issue_fence();
-        const bool more = l + 1 < L;
-        prestage_issue(more ? l + 1 : l);
-        issue_fence();
-        pool.template load<false>(more ? descA(l + 1) : descH(), 0, 0, lane, none);
-        issue_fence();
-#pragma unroll
-        for (int k = 0; k < PI; ++k)
-            if (k * NT + tid >= I) zv[k] = 0.0f;
-        float mean, rstd;
-        ln_stats(zv, I, a.eps, tid, red, mean, rstd);
-#pragma unroll
-        for (int k = 0; k < PI; ++k) {
-            const int i = k * NT + tid;
-            if (i < I) xs[sidx(i, I)] = (zv[k] - mean) * rstd * gv[k] + cv[k];
-        }
-        __syncthreads();
-        const float bg = Ly.b_gain;
-        run1(descD(l), preD, [&](int r, float v, bool w, Pre3 pre, bool hp) {
-            if (w) {
-                if (!hp) pre = Pre3{ldc(preD.s + r), ldc(preD.sfb + r), ldc(preD.x + r)};
-                const float xr = bad_tok ? __builtin_nanf("") : pre.x;
-                stc(a.x + r, v + (bg * pre.s + pre.f + xr));
-            }
-        });
-        if (more) prestage_store();
-        else pool.template load<false>(descH(), 1, 1, lane, none);
-    };
-    auto barrier = [&]() -> bool {
-        bar_arrive(bar);
-        fresh();
-        const bool ok = bar_wait(bar, &flag);
-        fresh();
-        return ok;
-    };
-
-    // Conv-history products of the stored history, for the first step: each
-    // channel group's owner (the phase-B assignment) writes its channels.
-    if (KHT > 0)
-        for (int c = wg; c < ngroups; c += nwg)
-            for (int idx = tid; idx < L * kh * 8; idx += NT) {
-                const int l = idx / (kh * 8), t = (idx / 8) % kh, i = c * 8 + (idx & 7);
-                const size_t off = ((size_t)l * kh + t) * D + i;
-                stc(a.hd + off, ldc(a.hist + off) * ldg(layer(l).dw + (size_t)(K - 2 - t) * D + i));
-            }
-    if (!barrier()) return;
-
+    unsigned ep = 0;                  // epoch of the last exchange produced
+    const unsigned stall = a.stall;   // > 0 only to test the time-out path
     int tok = a.tok_in[0];
+    float* ring_wg = a.ring + (size_t)wg * L * KH * D;
+    constexpr int WMAX = 2 * PD;      // exchange words per thread (A: x and s)
+    static_assert(WMAX >= PK, "gather words");
+
     for (int step = 0; step < a.n_steps; ++step) {
         const bool last = step + 1 == a.n_steps;
         const bool tok_ok = tok >= 0 && tok < a.vocab;
         const float* erow = a.embed + (size_t)(tok_ok ? tok : 0) * D;
-        // Layer 0 (peeled: its phase A issues its own weights), then the rest.
-        for (int l = 0; l < L; ++l) {
-            const EpiPre preD{a.s + (size_t)l * D, a.sfb, l == 0 ? erow : a.x};
-            if (l == 0) phaseA(0, tok_ok, erow);
-            else phaseA(l, true, erow);
-            if (!barrier()) return;
-            phaseB(l);
-            if (!barrier()) return;
-            phaseC(l, preD);
-            if (!barrier()) return;
-            phaseD(l, l == 0 && !tok_ok, preD);
-            if (!barrier()) return;
-        }
-
-        // ---- H: logits = E LN_out(x) (sunnynet.c:280-333), argmax key per workgroup
-        {
-            float xv[PD], gv[PD], cv[PD];
-            issue_ldc(xv, a.x, D, tid);
-            issue_ldg(gv, a.no_g, D, tid);
-            issue_ldg(cv, a.no_c, D, tid);
+        u64 best = 0ull;
+        for (int p = 0; p < NP; ++p) {
+            fresh();
+            const int t = p < 4 * L ? (p & 3) : 4;        // 0 A, 1 B, 2 C, 3 D, 4 H
+            const int l = min(p >> 2, L - 1);
+            const PLayer* Ly = lt + l;
+            // ---- the phase's input: the vector it multiplies (A: x, B: v,
+            // C: u, D: z, H: x), for A also the old state s (words PD..)
+            const int n0 = t == 1 ? R : t == 3 ? I : D;
+            const unsigned e0 = ep + stall, e1 = (unsigned)step + stall;
+            const u64* s0 = exs(ep);
+            const u64* s1 = a.sx + ((size_t)l * 2 + ((step - 1) & 1)) * D;
+            const bool plain0 = t == 0 && l == 0;          // x = the token's embedding row
+            const bool plain1 = step == 0;                 // s = the handle's state
+            const bool ln = t == 0 || t >= 3;
+            const float* gp = t == 0 ? Ly->ni_g : t == 3 ? Ly->nm_g : a.no_g;
+            const float* cp = t == 0 ? Ly->ni_c : t == 3 ? Ly->nm_c : a.no_c;
+            u64 w[WMAX];
+            float gv[PK], cv[PK], dv[KT][PD], hv[KH][PD], dl[PD];
+            float* ring_l = ring_wg + (size_t)l * KH * D;
+            auto word_in = [&](int k) -> bool {            // word k holds an element
+                if (t == 0) return (k % PD) * NT + tid < D;
+                return k < PK && k * NT + tid < n0;
+            };
+            auto addr = [&](int k) -> const u64* {
+                if (t == 0 && k >= PD) return s1 + min((k - PD) * NT + tid, D - 1);
+                return s0 + min(k * NT + tid, n0 - 1);
+            };
+            auto want = [&](int k) { return t == 0 && k >= PD ? e1 : e0; };
 #pragma unroll
-            for (int k = 0; k < PD; ++k)
-                if (k * NT + tid >= D) xv[k] = 0.0f;
-            float mean, rstd;
-            ln_stats(xv, D, a.eps, tid, red, mean, rstd);
-#pragma unroll
-            for (int k = 0; k < PD; ++k) {
-                const int i = k * NT + tid;
-                if (i < D) xs[sidx(i, D)] = (xv[k] - mean) * rstd * gv[k] + cv[k];
+            for (int k = 0; k < WMAX; ++k) {
+                const bool s_word = t == 0 && k >= PD;
+                const int i = min((s_word ? k - PD : k) * NT + tid, (s_word ? D : n0) - 1);
+                if (!word_in(k)) w[k] = ll_ready(0.0f, want(k));
+                else if (s_word ? plain1 : plain0)
+                    w[k] = ll_ready(ldg((s_word ? a.s + (size_t)l * D : erow) + i), want(k));
+                else w[k] = ll_get(addr(k));
             }
-            __syncthreads();
-            unsigned long long best = 0ull;
-            float* lg = last ? a.logits : nullptr;
-            const bool greedy = a.greedy != 0;
-            run_stream(descH(), none, [&](int r, float v, bool w, Pre3, bool) {
-                if (w) {
-                    if (lg) lg[r] = v;
-                    if (greedy) best = max(best, argmax_key(v, r));
+            if (ln) {
+#pragma unroll
+                for (int k = 0; k < PK; ++k) {
+                    const int i = min(k * NT + tid, n0 - 1);
+                    gv[k] = ldg(gp + i);
+                    cv[k] = ldg(cp + i);
+                }
+            }
+            if (t == 0) {
+#pragma unroll
+                for (int k = 0; k < PD; ++k) {
+                    const int i = min(k * NT + tid, D - 1);
+#pragma unroll
+                    for (int u = 0; u < KT; ++u) dv[u][k] = ldg(Ly->dw + (size_t)u * D + i);
+#pragma unroll
+                    for (int u = 0; u < KH; ++u) {
+                        // raw of step - 1 - u: this workgroup's ring, or the
+                        // handle's history (newest first) before the launch
+                        const int age = step - 1 - u;
+                        hv[u][k] = age >= 0 ? ring_l[(size_t)(age % KH) * D + i]
+                                            : ldg(a.hist + ((size_t)l * KH + (u - step)) * D + i);
+                    }
+                }
+            }
+            if (t == 1) {
+#pragma unroll
+                for (int k = 0; k < PD; ++k) dl[k] = ldg(Ly->delta + min(c0 + k * NT + tid, D - 1));
+            }
+            PROF(p * 8 + 0);
+            if (!agree(ll_spin(w, addr, want, pc))) return;
+            PROF(p * 8 + 1);
+            float xv[PK];
+#pragma unroll
+            for (int k = 0; k < PK; ++k) {
+                const bool in = k * NT + tid < n0 && (t != 0 || k < PD);
+                xv[k] = !in ? 0.0f : (plain0 && !tok_ok) ? __builtin_nanf("") : ll_f(w[k]);
+            }
+            float mean = 0.0f, rstd = 0.0f;
+            if (ln) ln_stats(xv, n0, a.eps, red, mean, rstd);
+            PROF(p * 8 + 2);
+#pragma unroll
+            for (int k = 0; k < PK; ++k) {
+                const int i = k * NT + tid;
+                if (i >= n0 || (t == 0 && k >= PD)) continue;
+                float y = ln ? (xv[k] - mean) * rstd * gv[k] + cv[k] : xv[k];
+                if (k < PD && t == 0) {
+                    // sunnynet.c:227-233: acc = raw w[K-1] + hist[0] w[K-2] + ...
+                    float acc = y * dv[KT - 1][k];
+#pragma unroll
+                    for (int u = 0; u < KH; ++u) acc = acc + hv[u][k] * dv[KT - 2 - u][k];
+                    ring_l[(size_t)(step % KH) * D + i] = y;
+                    xs2[sidx<BLK>(i, D)] = ll_f(w[PD + k]);
+                    xres[i] = xv[k];
+                    y = y + acc;
+                }
+                xin[sidx<BLK>(i, n0)] = y;
+            }
+            barrier_lds();
+            PROF(p * 8 + 3);
+            // ---- the products; every phase but H leaves them in res by job row
+            const bool head = t == 4;
+            float* lgp = head && last ? a.logits : nullptr;
+            run_job<BLK>(job(p), p0, p1, wv, lane, [&](int j, int row, float v, bool wr) {
+                if (!wr) return;
+                if (!head) {
+                    res[j] = v;
+                } else {
+                    if (lgp) lgp[row] = v;
+                    best = max(best, argmax_key(v, row));
                 }
             });
-            if (greedy) {
+            PROF(p * 8 + 4);
+            barrier_lds();
+            PROF(p * 8 + 5);
+            // ---- the phase's outputs
+            const unsigned epv = ++ep;
+            u64* out = exs(epv);
+            if (t == 0) {
+                for (int j = tid; j < nV + cpw; j += NT) {
+                    if (j < nV) ll_putf(out + wg + j * G, res[j], epv);
+                    else sfbl[j - nV] = res[j];
+                }
+            } else if (t == 1) {
+                // sunnynet.c:248-262: competitive gate within the group of 8,
+                // decay gate, state update
+                u64* sout = a.sx + ((size_t)l * 2 + (step & 1)) * D;
+#pragma unroll
+                for (int k = 0; k < PD; ++k) {
+                    const int c = k * NT + tid;
+                    if (c >= cpw) continue;
+                    const int i = c0 + c, jj = i & 7, base = ((i >> 3) - grp0) * 16;
+                    const float gi = res[base + 8 + jj];
+                    const float uu = res[base + jj] * (sgm(gi - res[base + 8 + ((jj + 1) & 7)]) *
+                                                       sgm(gi - res[base + 8 + ((jj + 2) & 7)]));
+                    float pg = 1.0f - dl[k] * (1.0f - sgm(gi));
+                    if (a.clamp && pg < a.p_floor) pg = a.p_floor;
+                    const float sn = pg * xs2[sidx<BLK>(i, D)] + (1.0f - pg) * uu;
+                    ll_putf(out + i, uu, epv);
+                    ll_putf(sout + i, sn, (unsigned)step + 1);
+                    sown[c] = sn;
+                }
+            } else if (t == 2) {
+                const float at = Ly->a_tanh;
+                for (int j = tid; j < nZ; j += NT) {
+                    const float v = res[j];
+                    ll_putf(out + wg + j * G, v * (1.0f + 0.5f * at / (1.0f + fabsf(v))), epv);
+                }
+            } else if (t == 3) {
+                const float bg = Ly->b_gain;
+                for (int c = tid; c < cpw; c += NT)
+                    ll_putf(out + c0 + c, res[c] + (bg * sown[c] + sfbl[c] + xres[c0 + c]), epv);
+            } else if (a.greedy) {
                 best = kmax_wave(best);
                 if (lane == 0) kred[wv] = best;
-                __syncthreads();
-                if (tid == 0)
-                    __hip_atomic_store(a.part + wg, max(max(kred[0], kred[1]), max(kred[2], kred[3])),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                barrier_lds();
+                if (tid < 2) {
+                    u64 kk = kred[0];
+#pragma unroll
+                    for (int i = 1; i < NWV; ++i) kk = max(kk, kred[i]);
+                    ll_put(out + 2 * wg + tid, tid == 0 ? (uint32_t)(kk >> 32) : (uint32_t)kk, epv);
+                }
             }
+            PROF(p * 8 + 6);
+            // ---- the next phase's first weights (the next step's first phase
+            // after H)
+            pool_load<BLK>(job(p + 1 < NP ? p + 1 : 0), 0, p0, wv, lane);
+            PROF(p * 8 + 7);
         }
         if (!a.greedy) break;
-        if (!barrier()) return;
-        // Every workgroup reduces the same keys to the same token.
+        fresh();
+        // ---------------- T: every workgroup reduces the keys to the same token
         {
-            unsigned long long k = 0ull;
+            const unsigned epx = ep + stall;
+            const u64* ksrc = exs(ep);
+            u64 w[2 * KPT];
+            auto addr = [&](int k) { return ksrc + 2 * min((k >> 1) * NT + tid, G - 1) + (k & 1); };
 #pragma unroll
-            for (int j = 0; j < kPersistMaxGrid / NT; ++j)
-                k = max(k, __hip_atomic_load(a.part + min(j * NT + tid, nwg - 1), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT));
-            k = kmax_wave(k);
-            if (lane == 0) kred[wv] = k;
-            __syncthreads();
-            k = max(max(kred[0], kred[1]), max(kred[2], kred[3]));
-            tok = (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+            for (int k = 0; k < 2 * KPT; ++k)
+                w[k] = (k >> 1) * NT + tid < G ? ll_get(addr(k)) : ll_ready(0.0f, epx);
+            if (!agree(ll_spin(w, addr, [&](int) { return epx; }, pc))) return;
+            u64 kk = 0ull;
+#pragma unroll
+            for (int q = 0; q < KPT; ++q)
+                if (q * NT + tid < G) kk = max(kk, ((u64)(uint32_t)w[2 * q] << 32) | (uint32_t)w[2 * q + 1]);
+            kk = kmax_wave(kk);
+            if (lane == 0) kred[wv] = kk;
+            barrier_lds();
+            kk = kred[0];
+#pragma unroll
+            for (int i = 1; i < NWV; ++i) kk = max(kk, kred[i]);
+            tok = (int)(0xFFFFFFFFu - (uint32_t)(kk & 0xFFFFFFFFull));
             if (wg == 0 && tid == 0) a.out_tok[step] = tok;
-            __syncthreads();
+            barrier_lds();
+        }
+    }
+
+    // Owners write back the state and the history (newest first) of their
+    // channels, for every layer. The ring entries are this thread's own
+    // stores; a history entry older than the launch comes from the handle's
+    // history, read before the entry it would overwrite.
+    const int T = a.n_steps;
+    for (int l = 0; l < L; ++l) {
+        const float* ring_l = ring_wg + (size_t)l * KH * D;
+        const u64* sl = a.sx + ((size_t)l * 2 + ((T - 1) & 1)) * D;
+#pragma unroll
+        for (int k = 0; k < PD; ++k) {
+            const int i = k * NT + tid;
+            if (i >= D || i < c0 || i >= c0 + cpw) continue;
+            a.s[(size_t)l * D + i] = ll_f(ll_get(sl + i));
+#pragma unroll
+            for (int j = KH - 1; j >= 0; --j) {
+                const int age = T - 1 - j;
+                float* hj = a.hist + ((size_t)l * KH + j) * D + i;
+                *hj = age >= 0 ? ring_l[(size_t)(age % KH) * D + i] : a.hist[((size_t)l * KH + (j - T)) * D + i];
+            }
         }
     }
 }
 
 const void* kernel_for(int blk) {
-    return blk == 0 ? (const void*)k_decode_persist<0, kPersistTaps - 1>
-         : blk == 32 ? (const void*)k_decode_persist<32, kPersistTaps - 1>
-                     : (const void*)k_decode_persist<64, kPersistTaps - 1>;
+    return blk == 0 ? (const void*)k_decode_persist<0>
+         : blk == 32 ? (const void*)k_decode_persist<32>
+                     : (const void*)k_decode_persist<64>;
 }
 
 }  // namespace
+
+#ifdef SNHIP_PERSIST_PROF
+extern "C" int snhip_persist_prof(unsigned long long* out, int n) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(unsigned long long) * n) == hipSuccess;
+}
+#endif
 
 int persist_occupancy(int blk) {
     int nb = 0;
@@ -881,10 +801,17 @@ int persist_occupancy(int blk) {
     return e == hipSuccess ? nb : 0;
 }
 
+bool persist_grid_ok(int G, int D, int I, int R, int vocab) {
+    if (G < 1 || G > kPersistMaxGrid || D % G) return false;
+    const int cpw = D / G;
+    if (cpw % 8 != 0 && 8 % cpw != 0) return false;
+    return G <= R && G <= I && G <= vocab;
+}
+
 snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipStream_t st) {
-    if (a.D > kMaxD || a.I > kMaxK || a.R > kMaxK || a.K != kPersistTaps || a.D % 8 || nwg < 1 ||
-        nwg > kPersistMaxGrid || a.n_steps < 1 || (a.greedy && !a.out_tok) ||
-        (!a.greedy && a.n_steps != 1)) {
+    if (a.D > kMaxD || a.I > kMaxK || a.R > kMaxK || a.K != kPersistTaps || a.D % 8 || a.L > kPersistMaxL ||
+        !persist_grid_ok(nwg, a.D, a.I, a.R, a.vocab) || a.n_steps < 1 ||
+        (a.greedy && !a.out_tok) || (!a.greedy && a.n_steps != 1)) {
         set_last_error("persistent decode: unsupported shape or arguments");
         return SNHIP_E_INVAL;
     }
