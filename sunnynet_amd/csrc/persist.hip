@@ -49,7 +49,10 @@
 namespace snhip {
 namespace {
 
-constexpr int NT = 1024;                     // threads per workgroup (16 waves, 4 per SIMD)
+#ifndef SNHIP_PERSIST_NT
+#define SNHIP_PERSIST_NT 1024
+#endif
+constexpr int NT = SNHIP_PERSIST_NT;         // threads per workgroup (16 waves, 4 per SIMD)
 constexpr int NWV = NT / 64;
 constexpr int kMaxD = kPersistMaxD;          // dim
 constexpr int kMaxK = kPersistMaxK;          // inner, rank
@@ -204,7 +207,7 @@ __device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps,
 #pragma unroll
     for (int k = 0; k < N; ++k)
         if (k * NT + tid < n) sum += xv[k];
-    mean = bsum(sum, red) / (float)n;
+    mean = bsum(sum, red) * (1.0f / (float)n);
     float vs = 0.0f;
 #pragma unroll
     for (int k = 0; k < N; ++k)
@@ -212,7 +215,7 @@ __device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps,
             const float d = xv[k] - mean;
             vs += d * d;
         }
-    rstd = 1.0f / sqrtf(bsum(vs, red + NWV) / (float)n + eps);
+    rstd = rsqrtf(bsum(vs, red + NWV) * (1.0f / (float)n) + eps);
 }
 
 // ---- jobs: the rows of one matrix a workgroup multiplies in one phase
