@@ -222,51 +222,42 @@ __device__ __forceinline__ void ln_stats(const float (&xv)[N], int n, float eps,
 //
 // Rows j < n1 are r0 + j s0 and multiply x0; rows n1 <= j < n are r1 + (j - n1)
 // and multiply x1 (LDS vectors in the staged layout). With two parts, waves
-// 0-1 take the first and waves 2-3 the second, so each wave multiplies one
-// vector and keeps its slice of it in registers for the whole job.
-// fp32: lane l holds float4 i of a row at k = 256 i + 4 l; the wave's rows
-// form a flat list of items (row, i), nk4 = ceil(K / 256) items per row, and
-// a batch is CAPF consecutive items (a row may straddle two batches: its
-// per-lane partial sum carries over).
-// INT4: a row is split over seg lanes (the next power of two >= its ng
-// groups), one group of codes per lane; a unit is rpp = 64 / seg rows, a
-// batch MU units.
+// 0 .. NWV/2-1 take the first and the others the second, so each wave
+// multiplies one vector and keeps its slice of it in registers for the whole
+// job. fp32: lane l holds float4 i of a row at k = 256 i + 4 l; the wave's
+// rows form a flat list of items (row, i), nk4 = ceil(K / 256) items per row,
+// and a batch is CAPF consecutive items (a row may straddle two batches: its
+// per-lane partial sum carries over). INT4: a row is split over seg lanes
+// (the next power of two >= its ng groups), one group of codes per lane; a
+// unit is rpp = 64 / seg rows, a batch MU units.
+//
+// Everything but the weight pointers is the same in every layer, so each
+// wave computes its share of each phase type once per launch (Geo, kept in
+// LDS) and a phase only reads it back: the scalar unit, shared by the 16
+// waves of a CU, is otherwise the bottleneck of a phase.
+struct Geo {
+    int K, n1, r0, s0, r1;   // job rows -> weight rows
+    int base, cnt, wl, nwp;  // this wave's rows: base + wl + nwp m (cnt rows in its part)
+    int nb;                  // batches of this wave
+    int ng, lseg, rpp;       // INT4: groups per row, log2 lanes per row, rows per unit
+    int nk4;                 // fp32: float4 items per row
+    int xsel;                // multiplies x1 (1) or x0 (0)
+    int pad;
+};
+static_assert(sizeof(Geo) == 64, "Geo is read as four 16-byte words");
+
 struct Job {
     const float* w;
     const uint8_t* q;
     const float* sc;
-    int K, n1, n, r0, s0, r1;
-    const l_f32* x0;
-    const l_f32* x1;
-};
-
-__device__ __forceinline__ Job make_job(const PMat& W, int K, int n1, int n, int r0, int s0, int r1,
-                                        const l_f32* x0, const l_f32* x1) {
-    Job J;
-    J.w = W.w; J.q = W.q; J.sc = W.sc;
-    J.K = K; J.n1 = n1; J.n = n; J.r0 = r0; J.s0 = s0; J.r1 = r1;
-    J.x0 = x0; J.x1 = x1;
-    return J;
-}
-
-__device__ __forceinline__ int job_row(const Job& J, int j) { return j < J.n1 ? J.r0 + j * J.s0 : J.r1 + (j - J.n1); }
-
-// The wave's part of a job: job rows base + (wl + nwp m), m = 0, 1, ...
-struct Share {
-    int base, cnt, wl, nwp;
     const l_f32* x;
+    Geo g;
 };
-__device__ __forceinline__ Share share_of(const Job& J, int wv) {
-    const bool two = J.n1 > 0 && J.n1 < J.n;
-    const bool hi = two && wv >= NWV / 2;
-    Share S;
-    S.nwp = two ? NWV / 2 : NWV;
-    S.wl = hi ? wv - NWV / 2 : wv;
-    S.base = hi ? J.n1 : 0;
-    S.cnt = two ? (hi ? J.n - J.n1 : J.n1) : J.n;
-    S.x = hi ? J.x1 : J.x0;
-    return S;
-}
+
+template <int BLK>
+__device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, int r1, int wv);
+
+__device__ __forceinline__ int job_row(const Geo& g, int j) { return j < g.n1 ? g.r0 + j * g.s0 : g.r1 + (j - g.n1); }
 
 template <int BLK>
 struct Pool {
@@ -284,54 +275,60 @@ struct XCache {
     float4 q[BLK ? BLK / 4 : 1];
 };
 
-// INT4 row geometry: log2 of the lanes per row.
 template <int BLK>
-__device__ __forceinline__ int i4_lseg(int K) {
-    const int ng = K / BLK;
-    return ng <= 1 ? 0 : 32 - __clz(ng - 1);
-}
-
-template <int BLK>
-__device__ __forceinline__ int job_batches(const Job& J, int wv) {
-    const Share S = share_of(J, wv);
-    const int nw = S.cnt > S.wl ? (S.cnt - S.wl + S.nwp - 1) / S.nwp : 0;   // the wave's rows
+__device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, int r1, int wv) {
+    Geo g;
+    g.K = K; g.n1 = n1; g.r0 = r0; g.s0 = s0; g.r1 = r1;
+    const bool two = n1 > 0 && n1 < n;
+    const bool hi = two && wv >= NWV / 2;
+    g.nwp = two ? NWV / 2 : NWV;
+    g.wl = hi ? wv - NWV / 2 : wv;
+    g.base = hi ? n1 : 0;
+    g.cnt = two ? (hi ? n - n1 : n1) : n;
+    g.xsel = hi ? 1 : 0;
+    g.pad = 0;
+    const int nw = g.cnt > g.wl ? (g.cnt - g.wl + g.nwp - 1) / g.nwp : 0;   // the wave's rows
     if constexpr (BLK == 0) {
-        return (nw * ((J.K + 255) >> 8) + CAPF - 1) / CAPF;
+        g.nk4 = (K + 255) >> 8;
+        g.ng = 0; g.lseg = 6; g.rpp = 1;
+        g.nb = (nw * g.nk4 + CAPF - 1) / CAPF;
     } else {
-        const int rpp = 64 >> i4_lseg<BLK>(J.K);
-        const int nu = (S.cnt + rpp - 1) / rpp;
-        const int nwu = nu > S.wl ? (nu - S.wl + S.nwp - 1) / S.nwp : 0;
-        return (nwu + Pool<BLK>::MU - 1) / Pool<BLK>::MU;
+        g.nk4 = 0;
+        g.ng = K / BLK;
+        g.lseg = g.ng <= 1 ? 0 : 32 - __clz(g.ng - 1);
+        g.rpp = 64 >> g.lseg;
+        const int nu = (g.cnt + g.rpp - 1) / g.rpp;
+        const int nwu = nu > g.wl ? (nu - g.wl + g.nwp - 1) / g.nwp : 0;
+        g.nb = (nwu + Pool<BLK>::MU - 1) / Pool<BLK>::MU;
     }
+    return g;
 }
 
 // Batch b of J into P. Straight-line: every slot issues its loads (empty ones
 // read element 0 of the matrix), so wait counts stay exact.
 template <int BLK>
-__device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int wv, int lane) {
-    const Share S = share_of(J, wv);
+__device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int lane) {
+    const Geo& g = J.g;
     if constexpr (BLK == 0) {
-        const int nk4 = (J.K + 255) >> 8;
 #pragma unroll
         for (int s = 0; s < CAPF; ++s) {
-            const int m = b * CAPF + s, mr = m / nk4, i = m - mr * nk4;
-            const int jl = S.wl + S.nwp * mr;
+            const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
+            const int jl = g.wl + g.nwp * mr;
             const int k = i * 256 + lane * 4;
-            const bool ok = jl < S.cnt && k < J.K;
-            const size_t off = (size_t)job_row(J, S.base + jl) * J.K + k;
-            P.wf[s] = ldg4(J.w + (ok ? off : 0));
+            const bool ok = jl < g.cnt && k < g.K;
+            const int row = job_row(g, g.base + jl);
+            P.wf[s] = ldg4(J.w + (ok ? (size_t)(uint32_t)(row * g.K + k) : 0));
         }
     } else {
         constexpr int MU = Pool<BLK>::MU;
-        const int ng = J.K / BLK, ls = i4_lseg<BLK>(J.K), rpp = 64 >> ls;
-        const int lrow = lane >> ls, lg = lane & ((1 << ls) - 1);
+        const int lrow = lane >> g.lseg, lg = lane & ((1 << g.lseg) - 1);
 #pragma unroll
         for (int s = 0; s < MU; ++s) {
-            const int jl = (S.wl + S.nwp * (b * MU + s)) * rpp + lrow;
-            const bool ok = jl < S.cnt && lg < ng;
-            const int row = job_row(J, S.base + jl);
-            const size_t qo = (size_t)row * (J.K / 2) + lg * (BLK / 2);
-            const size_t so = (size_t)row * ng + lg;
+            const int jl = (g.wl + g.nwp * (b * MU + s)) * g.rpp + lrow;
+            const bool ok = jl < g.cnt && lg < g.ng;
+            const int row = job_row(g, g.base + jl);
+            const uint32_t qo = (uint32_t)(row * (g.K / 2) + lg * (BLK / 2));
+            const uint32_t so = (uint32_t)(row * g.ng + lg);
 #pragma unroll
             for (int qq = 0; qq < Pool<BLK>::QW; ++qq) P.wq[s][qq] = ldgq(J.q + (ok ? qo + 16 * qq : 0));
             P.wsc[s] = ldg(J.sc + (ok ? so : 0));
@@ -340,62 +337,59 @@ __device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int
 }
 
 template <int BLK>
-__device__ __forceinline__ void xcache_load(const Job& J, XCache<BLK>& X, int wv, int lane) {
+__device__ __forceinline__ void xcache_load(const Job& J, XCache<BLK>& X, int lane) {
     if constexpr (BLK != 0) {
-        const Share S = share_of(J, wv);
-        const int ng = J.K / BLK, ls = i4_lseg<BLK>(J.K);
-        const int lg = min(lane & ((1 << ls) - 1), ng - 1);
+        const Geo& g = J.g;
+        const int lg = min(lane & ((1 << g.lseg) - 1), g.ng - 1);
 #pragma unroll
-        for (int q = 0; q < BLK / 4; ++q) X.q[q] = lds4(S.x + 4 * (q * ng + lg));
+        for (int q = 0; q < BLK / 4; ++q) X.q[q] = lds4(J.x + 4 * (q * g.ng + lg));
     }
 }
 
 // epi(j, row, value, writer): `writer` is true on exactly one lane per row.
-// Every slot is computed (the loads of empty slots are valid addresses);
-// only rows of the job are handed to epi.
+// Every slot's loads are valid addresses; only rows of the job reach epi.
 template <class Epi>
-__device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<0>& P, int wv, int lane, float& pacc,
+__device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<0>& P, int lane, float& pacc,
                                             Epi&& epi) {
-    const Share S = share_of(J, wv);
-    const int nk4 = (J.K + 255) >> 8;
+    const Geo& g = J.g;
     float4 xs[CAPF];
 #pragma unroll
     for (int s = 0; s < CAPF; ++s) {
-        const int m = b * CAPF + s, mr = m / nk4, i = m - mr * nk4;
-        xs[s] = lds4(S.x + min(i * 256 + lane * 4, J.K - 4));
+        const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
+        xs[s] = lds4(J.x + min(i * 256 + lane * 4, g.K - 4));
     }
 #pragma unroll
     for (int s = 0; s < CAPF; ++s) {
-        const int m = b * CAPF + s, mr = m / nk4, i = m - mr * nk4;
-        const int jl = S.wl + S.nwp * mr;
-        if (i * 256 + lane * 4 < J.K) {
+        const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
+        const int jl = g.wl + g.nwp * mr;
+        if (i * 256 + lane * 4 < g.K) {
             const float4 w4 = P.wf[s];
             pacc = fmaf(w4.x, xs[s].x, pacc);
             pacc = fmaf(w4.y, xs[s].y, pacc);
             pacc = fmaf(w4.z, xs[s].z, pacc);
             pacc = fmaf(w4.w, xs[s].w, pacc);
         }
-        if (i == nk4 - 1) {
+        if (i == g.nk4 - 1) {
             const float v = wsum(pacc);
             pacc = 0.0f;
-            if (jl < S.cnt) epi(S.base + jl, job_row(J, S.base + jl), v, lane == 0);
+            if (jl < g.cnt) epi(g.base + jl, job_row(g, g.base + jl), v, lane == 0);
         }
     }
 }
 
 template <int BLK, class Epi>
-__device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int wv,
-                                           int lane, Epi&& epi) {
+__device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int lane,
+                                           Epi&& epi) {
     constexpr int MU = Pool<BLK>::MU;
     constexpr int NW = BLK / 8;                  // 32-bit words of codes per group
-    const Share S = share_of(J, wv);
-    const int ng = J.K / BLK, ls = i4_lseg<BLK>(J.K), rpp = 64 >> ls, seg = 1 << ls;
-    const int lrow = lane >> ls, lg = lane & (seg - 1);
-    const bool lane_ok = lg < ng;
+    const Geo& g = J.g;
+    const int seg = 1 << g.lseg;
+    const int lrow = lane >> g.lseg, lg = lane & (seg - 1);
+    const bool lane_ok = lg < g.ng;
     // Units of this batch that hold rows (the rest are skipped, uniformly).
-    const int nu = (S.cnt + rpp - 1) / rpp;
-    const int u0 = S.wl + S.nwp * b * MU;
-    const int nvu = u0 < nu ? min(MU, (nu - u0 + S.nwp - 1) / S.nwp) : 0;
+    const int nu = (g.cnt + g.rpp - 1) >> (6 - g.lseg);
+    const int u0 = g.wl + g.nwp * b * MU;
+    const int nvu = u0 < nu ? min(MU, (nu - u0 + g.nwp - 1) / g.nwp) : 0;
     float acc[MU];
 #pragma unroll
     for (int s = 0; s < MU; ++s) {
@@ -443,34 +437,53 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
     }
 #pragma unroll
     for (int s = 0; s < MU; ++s) {
-        const int jl = (S.wl + S.nwp * (b * MU + s)) * rpp + lrow;
-        if (jl < S.cnt) epi(S.base + jl, job_row(J, S.base + jl), acc[s], lg == 0);
+        const int jl = (g.wl + g.nwp * (b * MU + s)) * g.rpp + lrow;
+        if (jl < g.cnt) epi(g.base + jl, job_row(g, g.base + jl), acc[s], lg == 0);
     }
 }
 
 template <int BLK, class Epi>
-__device__ __forceinline__ void compute(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int wv,
-                                        int lane, float& pacc, Epi&& epi) {
-    if constexpr (BLK == 0) compute_f32(J, b, P, wv, lane, pacc, epi);
-    else compute_i4<BLK>(J, b, P, X, wv, lane, epi);
+__device__ __forceinline__ void compute(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int lane,
+                                        float& pacc, Epi&& epi) {
+    if constexpr (BLK == 0) compute_f32(J, b, P, lane, pacc, epi);
+    else compute_i4<BLK>(J, b, P, X, lane, epi);
 }
 
 // Runs every batch of J (batch 0 is already in p0): batches alternate between
 // the pools, and each is issued before the previous one is multiplied. The
 // loads of a batch past the last read element 0 of the matrix (unused), so
-// every path issues the same loads and the wait counts stay exact.
+// every path issues the same loads and the wait counts stay exact. A wave
+// with no rows does nothing.
+#ifdef SNHIP_PERSIST_PROF
+__device__ unsigned long long g_jprof[64 * 4];
+#define JPROF(i) do { if (probe && lane == 0) g_jprof[(i) * 16 + wv] = wall_clock64(); } while (0)
+#else
+#define JPROF(i) do { } while (0)
+#endif
 template <int BLK, class Epi>
-__device__ __forceinline__ void run_job(const Job& J, Pool<BLK>& p0, Pool<BLK>& p1, int wv, int lane, Epi&& epi) {
-    const int nb = job_batches<BLK>(J, wv);
+__device__ __forceinline__ void run_job(const Job& J, Pool<BLK>& p0, Pool<BLK>& p1, int wv, int lane, Epi&& epi,
+                                        bool probe = false) {
+    JPROF(0);
+    const int nb = J.g.nb;
+    if (nb == 0) return;
     XCache<BLK> X;
-    xcache_load<BLK>(J, X, wv, lane);
+    xcache_load<BLK>(J, X, lane);
+    JPROF(1);
     float pacc = 0.0f;
     for (int b = 0; b < nb; b += 2) {
-        pool_load<BLK>(J, b + 1, p1, wv, lane);
-        compute<BLK>(J, b, p0, X, wv, lane, pacc, epi);
-        pool_load<BLK>(J, b + 2, p0, wv, lane);
-        if (b + 1 < nb) compute<BLK>(J, b + 1, p1, X, wv, lane, pacc, epi);
+        pool_load<BLK>(J, b + 1, p1, lane);
+        JPROF(2);
+        compute<BLK>(J, b, p0, X, lane, pacc, epi);
+        JPROF(3);
+        pool_load<BLK>(J, b + 2, p0, lane);
+        if (b + 1 < nb) compute<BLK>(J, b + 1, p1, X, lane, pacc, epi);
     }
+}
+
+// Batch 0 of the next job into p0 (nothing for a wave with no rows in it).
+template <int BLK>
+__device__ __forceinline__ void prefetch_job(const Job& J, Pool<BLK>& p0, int lane) {
+    if (J.g.nb > 0) pool_load<BLK>(J, 0, p0, lane);
 }
 
 // Index of element i of a K-long vector in the staged LDS layout: fp32 plain;
@@ -485,7 +498,10 @@ __device__ __forceinline__ int sidx(int i, int K) {
 #ifdef SNHIP_PERSIST_PROF
 // Phase timestamps of workgroup 0 (wall clock), for profiling builds only.
 __device__ unsigned long long g_prof[2048];
-#define PROF(idx) do { if (wg == 0 && lane == 0 && step == 3) g_prof[(idx) * 4 + wv] = wall_clock64(); } while (0)
+__device__ unsigned long long g_clk[4];
+#define PROF(idx) do { if (wg == 0 && lane == 0 && step == 3) g_prof[(idx) * 4 + wv] = wall_clock64(); \
+    if (wg == 0 && tid == 0 && step == 3 && (idx) == 1) { g_clk[0] = wall_clock64(); g_clk[1] = clock64(); } \
+    if (wg == 0 && tid == 0 && step == 3 && (idx) == 8 * 48 + 1) { g_clk[2] = wall_clock64(); g_clk[3] = clock64(); } } while (0)
 #else
 #define PROF(idx) do { } while (0)
 #endif
@@ -505,6 +521,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
     __shared__ u64 kred[NWV];
     __shared__ int sflag;
     __shared__ PLayer ltab[kPersistMaxL];          // the layer table (LDS reads, no scalar misses)
+    __shared__ Geo geo[5][NWV];                   // each wave's share of each phase type
 
     int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -541,20 +558,32 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
     const int NP = 4 * L + 1;
     // The rows this workgroup multiplies in phase p (A: its V rows, then the
     // W_eff rows of its channels; B: the U rows of its channel groups; C: its
-    // W_z rows; D: the W_c rows of its channels; H: its head rows).
+    // W_z rows; D: the W_c rows of its channels; H: its head rows): this
+    // wave's geometry of each phase type, once per launch.
+    if (lane == 0) {
+        geo[0][wv] = make_geo<BLK>(D, nV, nV + cpw, wg, G, R + c0, wv);
+        geo[1][wv] = make_geo<BLK>(R, 16 * ngrp, 16 * ngrp, 16 * grp0, 1, 0, wv);
+        geo[2][wv] = make_geo<BLK>(D, nZ, nZ, wg, G, 0, wv);
+        geo[3][wv] = make_geo<BLK>(I, cpw, cpw, c0, 1, 0, wv);
+        geo[4][wv] = make_geo<BLK>(D, nH, nH, wg, G, 0, wv);
+    }
+    barrier_lds();
     auto job = [&](int p) -> Job {
-        if (p >= 4 * L) return make_job(a.head, D, nH, nH, wg, G, 0, lx, lx);
-        const PLayer* Ly = lt + (p >> 2);
-        switch (p & 3) {
-            case 0: return make_job(Ly->VW, D, nV, nV + cpw, wg, G, R + c0, lx, ls);
-            case 1: return make_job(Ly->U, R, 16 * ngrp, 16 * ngrp, 16 * grp0, 1, 0, lx, lx);
-            case 2: return make_job(Ly->Wz, D, nZ, nZ, wg, G, 0, lx, lx);
-            default: return make_job(Ly->Wc, I, cpw, cpw, c0, 1, 0, lx, lx);
+        const int t = p < 4 * L ? (p & 3) : 4;
+        Job J;
+        J.g = geo[t][wv];
+        J.x = J.g.xsel ? ls : lx;
+        PMat W = a.head;
+        if (t < 4) {
+            const PLayer* Ly = lt + (p >> 2);
+            W = t == 0 ? Ly->VW : t == 1 ? Ly->U : t == 2 ? Ly->Wz : Ly->Wc;
         }
+        J.w = W.w; J.q = W.q; J.sc = W.sc;
+        return J;
     };
 
     Pool<BLK> p0, p1;
-    pool_load<BLK>(job(0), 0, p0, wv, lane);
+    prefetch_job<BLK>(job(0), p0, lane);
 
     unsigned ep = 0;                  // epoch of the last exchange produced
     const unsigned stall = a.stall;   // > 0 only to test the time-out path
@@ -675,7 +704,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
                     if (lgp) lgp[row] = v;
                     best = max(best, argmax_key(v, row));
                 }
-            });
+            }, wg == 0 && step == 3 && p == 4);
             PROF(p * 8 + 4);
             barrier_lds();
             PROF(p * 8 + 5);
@@ -730,7 +759,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
             PROF(p * 8 + 6);
             // ---- the next phase's first weights (the next step's first phase
             // after H)
-            pool_load<BLK>(job(p + 1 < NP ? p + 1 : 0), 0, p0, wv, lane);
+            prefetch_job<BLK>(job(p + 1 < NP ? p + 1 : 0), p0, lane);
             PROF(p * 8 + 7);
         }
         if (!a.greedy) break;
@@ -795,6 +824,12 @@ const void* kernel_for(int blk) {
 #ifdef SNHIP_PERSIST_PROF
 extern "C" int snhip_persist_prof(unsigned long long* out, int n) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(unsigned long long) * n) == hipSuccess;
+}
+extern "C" int snhip_persist_jprof(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_jprof), sizeof(unsigned long long) * 64) == hipSuccess;
+}
+extern "C" int snhip_persist_clk(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_clk), sizeof(unsigned long long) * 4) == hipSuccess;
 }
 #endif
 
