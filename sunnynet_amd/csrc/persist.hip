@@ -364,10 +364,7 @@ __device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<0>& 
         const int jl = g.wl + g.nwp * mr;
         if (i * 256 + lane * 4 < g.K) {
             const float4 w4 = P.wf[s];
-            pacc = fmaf(w4.x, xs[s].x, pacc);
-            pacc = fmaf(w4.y, xs[s].y, pacc);
-            pacc = fmaf(w4.z, xs[s].z, pacc);
-            pacc = fmaf(w4.w, xs[s].w, pacc);
+            pacc = pacc + (fmaf(w4.x, xs[s].x, w4.y * xs[s].y) + fmaf(w4.z, xs[s].z, w4.w * xs[s].w));
         }
         if (i == g.nk4 - 1) {
             const float v = wsum(pacc);
@@ -398,7 +395,9 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
         // (q - 8) * scale as one rounding: fma(q, scale, -8 scale), with
         // -8 scale exact (quant.c:82-83 dequantization, bit-identical).
         const float sc = P.wsc[s], m8 = -8.0f * sc;
-        float a = 0.0f;
+        // Four independent partial sums (one per byte of a code word) keep
+        // the FMA dependency chains short.
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
             const uint4& qq = P.wq[s][w >> 2];
@@ -408,16 +407,16 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
             // (high nibble).
             const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
             const float4 xl = X.q[w], xh = X.q[w + NW];
-            a = fmaf(fmaf((float)(lo & 0xFFu), sc, m8), xl.x, a);
-            a = fmaf(fmaf((float)(hi & 0xFFu), sc, m8), xh.x, a);
-            a = fmaf(fmaf((float)((lo >> 8) & 0xFFu), sc, m8), xl.y, a);
-            a = fmaf(fmaf((float)((hi >> 8) & 0xFFu), sc, m8), xh.y, a);
-            a = fmaf(fmaf((float)((lo >> 16) & 0xFFu), sc, m8), xl.z, a);
-            a = fmaf(fmaf((float)((hi >> 16) & 0xFFu), sc, m8), xh.z, a);
-            a = fmaf(fmaf((float)(lo >> 24), sc, m8), xl.w, a);
-            a = fmaf(fmaf((float)(hi >> 24), sc, m8), xh.w, a);
+            a[0] = fmaf(fmaf((float)(lo & 0xFFu), sc, m8), xl.x, a[0]);
+            a[1] = fmaf(fmaf((float)((lo >> 8) & 0xFFu), sc, m8), xl.y, a[1]);
+            a[2] = fmaf(fmaf((float)((lo >> 16) & 0xFFu), sc, m8), xl.z, a[2]);
+            a[3] = fmaf(fmaf((float)(lo >> 24), sc, m8), xl.w, a[3]);
+            a[0] = fmaf(fmaf((float)(hi & 0xFFu), sc, m8), xh.x, a[0]);
+            a[1] = fmaf(fmaf((float)((hi >> 8) & 0xFFu), sc, m8), xh.y, a[1]);
+            a[2] = fmaf(fmaf((float)((hi >> 16) & 0xFFu), sc, m8), xh.z, a[2]);
+            a[3] = fmaf(fmaf((float)(hi >> 24), sc, m8), xh.w, a[3]);
         }
-        acc[s] = lane_ok ? a : 0.0f;
+        acc[s] = lane_ok ? (a[0] + a[1]) + (a[2] + a[3]) : 0.0f;
     }
     if (seg >= 16) {
 #pragma unroll
@@ -452,8 +451,8 @@ __device__ __forceinline__ void compute(const Job& J, int b, const Pool<BLK>& P,
 // Runs every batch of J (batch 0 is already in p0): batches alternate between
 // the pools, and each is issued before the previous one is multiplied. The
 // loads of a batch past the last read element 0 of the matrix (unused), so
-// every path issues the same loads and the wait counts stay exact. A wave
-// with no rows does nothing.
+// every path of the loop issues the same loads and the wait counts stay
+// exact. A wave with no rows does nothing.
 #ifdef SNHIP_PERSIST_PROF
 __device__ unsigned long long g_jprof[64 * 4];
 #define JPROF(i) do { if (probe && lane == 0) g_jprof[(i) * 16 + wv] = wall_clock64(); } while (0)
@@ -470,11 +469,17 @@ __device__ __forceinline__ void run_job(const Job& J, Pool<BLK>& p0, Pool<BLK>& 
     xcache_load<BLK>(J, X, lane);
     JPROF(1);
     float pacc = 0.0f;
+    if (nb == 1) {
+        // One batch (the common case in the layer phases): nothing else to
+        // issue, and its own copy of the product code waits for p0 alone.
+        JPROF(2);
+        compute<BLK>(J, 0, p0, X, lane, pacc, epi);
+        JPROF(3);
+        return;
+    }
     for (int b = 0; b < nb; b += 2) {
         pool_load<BLK>(J, b + 1, p1, lane);
-        JPROF(2);
         compute<BLK>(J, b, p0, X, lane, pacc, epi);
-        JPROF(3);
         pool_load<BLK>(J, b + 2, p0, lane);
         if (b + 1 < nb) compute<BLK>(J, b + 1, p1, X, lane, pacc, epi);
     }
