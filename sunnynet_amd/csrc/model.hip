@@ -61,6 +61,10 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 
 // Largest LayerNorm row: 16 values per thread of a 256-thread block.
 constexpr int kLnPer = 16;
+// Prefill: up to this many channels (max_batch x dim) the gates are computed
+// for every row in parallel and the scan only multiplies and adds
+// (k_gate_rows + k_scan_rows); above it k_core_scan fuses them.
+constexpr size_t kSplitScanChannels = 16384;
 
 __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
                         float* __restrict__ x, int D, int vocab) {
@@ -429,6 +433,89 @@ __global__ __launch_bounds__(64 * W) void k_core_scan(
     if (w == 0) s_out[(size_t)b * out_bstride + i] = carry[lane];
 }
 
+// The per-element part of k_core_scan for every row of a prefill chunk, for
+// batches too small to hide it behind the scan (sunnynet.c:248-262, same
+// arithmetic as k_core_scan's prep): u = u_raw sigmoid(g - g_{+1})
+// sigmoid(g - g_{+2}) within the group of 8, p = 1 - delta (1 - sigmoid(g))
+// (clamped), and the scan input b = (1 - p) u.
+__global__ __launch_bounds__(256) void k_gate_rows(const float* __restrict__ q, const float* __restrict__ delta,
+                                                   float* __restrict__ u_out, float* __restrict__ pa,
+                                                   float* __restrict__ pb, long n, int D, int clamp,
+                                                   float p_floor) {
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n) return;
+    const long r = idx / D;
+    const int i = (int)(idx - r * D);
+    const float* qr = q + r * 2 * D;
+    const int base = i & ~7, off = i & 7;
+    const float gi = qr[qrow_g(i)];
+    const float g1 = qr[qrow_g(base + ((off + 1) & 7))], g2 = qr[qrow_g(base + ((off + 2) & 7))];
+    const float uu = qr[qrow_u(i)] * (sgm(gi - g1) * sgm(gi - g2));
+    float p = 1.0f - delta[i] * (1.0f - sgm(gi));
+    if (clamp && p < p_floor) p = p_floor;
+    u_out[idx] = uu;
+    pa[idx] = p;
+    pb[idx] = (1.0f - p) * uu;
+}
+
+// s_t = p_t s_{t-1} + b_t per channel (two roundings, as the decode step) over
+// the T rows of each sequence, for 64 channels per block: in each tile of
+// W TC steps wave w holds steps [w TC, (w + 1) TC), loaded before the tile's
+// hand-off chain starts; the state passes wave to wave through LDS, and a wave
+// loads its slice of the next tile right after its turn.
+template <int W, int TC>
+__global__ __launch_bounds__(64 * W) void k_scan_rows(
+        const float* __restrict__ pa, const float* __restrict__ pb, const float* __restrict__ s_in,
+        size_t s_bstride, float* __restrict__ s_out, size_t out_bstride, float* __restrict__ states, int T,
+        int D) {
+    __shared__ float carry[64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gpr = D / 64;
+    const int b = __builtin_amdgcn_readfirstlane(blockIdx.x / gpr);
+    const int i = (blockIdx.x - b * gpr) * 64 + lane;
+    // This sequence's rows as buffer resources: 32-bit byte offsets from a
+    // scalar base (raw buffer addressing, dword 3 = 0x00020000 on gfx950).
+    const size_t o = (size_t)b * T * D;
+    const int bytes = T * D * 4;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(pa + o), (short)0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(pb + o), (short)0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(states + o, (short)0, bytes, 0x00020000);
+    constexpr int TILE = W * TC;
+    float P[TC], Bv[TC];
+    auto load = [&](int t0) {
+        const int ts = min(t0 + w * TC, T - 1);
+        const int kmax = T - 1 - ts;
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const int vo = ((ts + min(k, kmax)) * D + i) * 4;
+            P[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, vo, 0, 0));
+            Bv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, vo, 0, 0));
+        }
+    };
+    if (w == 0) carry[lane] = s_in[(size_t)b * s_bstride + i];
+    load(0);
+    for (int t0 = 0; t0 < T; t0 += TILE) {
+        const int ts = t0 + w * TC;
+        for (int j = 0; j < W; ++j) {
+            barrier_lds();
+            if (w == j) {
+                float s = carry[lane];
+#pragma unroll
+                for (int k = 0; k < TC; ++k)
+                    if (ts + k < T) {
+                        s = P[k] * s + Bv[k];
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rs, ((ts + k) * D + i) * 4, 0, 0);
+                    }
+                carry[lane] = s;
+                if (t0 + TILE < T) load(t0 + TILE);
+            }
+        }
+    }
+    barrier_lds();
+    if (w == 0) s_out[(size_t)b * out_bstride + i] = carry[lane];
+}
+
 // Rows t = T-1 of each sequence: dst[b] = src[b*T + T-1].
 __global__ void k_last_rows(const float* __restrict__ src, float* __restrict__ dst, int T, int D) {
     const int b = blockIdx.x;
@@ -495,7 +582,7 @@ struct SnHipModel {
     int pf_chunk = 0;
     float *pf_x = nullptr, *pf_raw = nullptr, *pf_at = nullptr, *pf_v = nullptr, *pf_q = nullptr,
           *pf_u = nullptr, *pf_st = nullptr, *pf_z = nullptr, *pf_yn = nullptr, *pf_sfb = nullptr,
-          *pf_send = nullptr;
+          *pf_send = nullptr, *pf_pa = nullptr, *pf_pb = nullptr;
     int32_t* pf_tok = nullptr;
     // Persistent single-sequence decode (persist.hip): grid size, 0 when the
     // model's shape or the device does not allow it.
@@ -1001,7 +1088,7 @@ snhip_status ensure_prefill_ws(SnHipModel* m, int chunk) {
     SNHIP_CHECK(hipStreamSynchronize(m->stream));
     SNHIP_CHECK(hipStreamSynchronize(m->work));
     float** bufs[] = {&m->pf_x, &m->pf_raw, &m->pf_at, &m->pf_v, &m->pf_q, &m->pf_u,
-                      &m->pf_st, &m->pf_z, &m->pf_yn, &m->pf_sfb, &m->pf_send};
+                      &m->pf_st, &m->pf_z, &m->pf_yn, &m->pf_sfb, &m->pf_send, &m->pf_pa, &m->pf_pb};
     for (float** b : bufs)
         if (*b) {
             (void)hipFree(*b);
@@ -1027,6 +1114,10 @@ snhip_status ensure_prefill_ws(SnHipModel* m, int chunk) {
     m->pf_yn = dalloc<float>(m, rows * I);
     m->pf_sfb = dalloc<float>(m, rows * D);
     m->pf_send = dalloc<float>(m, (size_t)m->max_batch * D);
+    // scan inputs of the small-batch path (kSplitScanChannels)
+    const size_t prow = (size_t)m->max_batch * D <= kSplitScanChannels ? rows * D : 1;
+    m->pf_pa = dalloc<float>(m, prow);
+    m->pf_pb = dalloc<float>(m, prow);
     m->pf_tok = dalloc<int32_t>(m, rows);
     for (float** b : bufs)
         if (!*b) { m->pf_chunk = 0; set_last_error("out of device memory (prefill)"); return SNHIP_E_NOMEM; }
@@ -1063,9 +1154,19 @@ snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_o
         }
         if ((rc = run_gemm(m, gemm_for(m, A.V, at, D, (int)rows, m->pf_v, R), st)) != SNHIP_OK) return rc;
         if ((rc = run_gemm(m, gemm_for(m, A.U, m->pf_v, R, (int)rows, m->pf_q, 2 * D), st)) != SNHIP_OK) return rc;
-        hipLaunchKernelGGL((k_core_scan<4, 16>), dim3((unsigned)(B * (D / 64))), dim3(256), 0, st,
-                           m->pf_q, A.delta, s_l, sbs, m->pf_send, (size_t)D, m->pf_u, m->pf_st,
-                           Tc, D, m->clamp, m->p_floor);
+        if ((size_t)m->max_batch * D <= kSplitScanChannels) {
+            // Few channels: the gates of every row in parallel, then a scan
+            // that only multiplies and adds.
+            const long n = rows * D;
+            hipLaunchKernelGGL(k_gate_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m->pf_q,
+                               A.delta, m->pf_u, m->pf_pa, m->pf_pb, n, D, m->clamp, m->p_floor);
+            hipLaunchKernelGGL((k_scan_rows<16, 16>), dim3((unsigned)(B * (D / 64))), dim3(1024), 0, st,
+                               m->pf_pa, m->pf_pb, s_l, sbs, m->pf_send, (size_t)D, m->pf_st, Tc, D);
+        } else {
+            hipLaunchKernelGGL((k_core_scan<4, 16>), dim3((unsigned)(B * (D / 64))), dim3(256), 0, st,
+                               m->pf_q, A.delta, s_l, sbs, m->pf_send, (size_t)D, m->pf_u, m->pf_st,
+                               Tc, D, m->clamp, m->p_floor);
+        }
         GemmArgs gz = gemm_for(m, A.Wz, m->pf_u, D, (int)rows, m->pf_z, I);
         gz.epi = GEPI_WEDGE;
         gz.a_tanh = A.a_tanh;
@@ -1099,7 +1200,9 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
         set_last_error("chunked prefill needs dim % 64 == 0 and dim, inner, rank % 32 == 0");
         return SNHIP_E_UNSUPPORTED;
     }
-    int chunk = 512;
+    // 512-token chunks, longer for small batches so the products have at
+    // least ~2048 rows (the workspace is sized for max_batch x chunk rows).
+    int chunk = std::max(512, std::min(2048, 2048 / std::max(1, m->max_batch)));
     if (const char* e = getenv("SNHIP_PREFILL_CHUNK")) chunk = std::max(1, atoi(e));
     chunk = std::min(chunk, T);
     snhip_status rc = ensure_prefill_ws(m, chunk);

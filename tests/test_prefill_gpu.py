@@ -63,8 +63,10 @@ def _oracle_prefill(buf, prompts, B):
     return orc, last
 
 
-@pytest.mark.parametrize("B,T", [(1, 300), (3, 77), (5, 1)])
+@pytest.mark.parametrize("B,T", [(1, 300), (1, 1100), (3, 77), (5, 1)])
 def test_prefill_matches_stepping(gpu, small, B, T):
+    """Small batches take the split gate/scan path (several 512-step scan
+    tiles at T = 1100); the 100M B=64 test below takes the fused one."""
     w, buf, path = small
     print(f"prefill small B={B} T={T}", flush=True)
     prompts = np.random.default_rng(B * 1000 + T).integers(0, SMALL.vocab_size, (B, T)).astype(np.int32)
