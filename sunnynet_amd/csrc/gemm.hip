@@ -566,10 +566,13 @@ snhip_status launch_gemm(const GemmArgs& g, float* work, size_t work_floats, hip
     }
     const int gx = (g.N + BN - 1) / BN, gy = (g.M + BM - 1) / BM;
     const int ktiles = g.K / BK;
+    // Fewer than ~4 tiles per CU leaves the LDS pipeline of each workgroup
+    // exposed: split K so that about 1024 workgroups run (at least 4 k-tiles
+    // each), within the partial buffer.
     int splits = 1;
-    if (work && gx * gy < 192) {
-        splits = (384 + gx * gy - 1) / (gx * gy);
-        splits = std::min(splits, std::max(1, ktiles / 2));
+    if (work && gx * gy < 1024) {
+        splits = (1024 + gx * gy - 1) / (gx * gy);
+        splits = std::min(splits, std::max(1, ktiles / 4));
         while (splits > 1 && (size_t)splits * g.M * g.N > work_floats) --splits;
     }
     const int kchunk = ((ktiles + splits - 1) / splits) * BK;
