@@ -75,6 +75,7 @@ _SIGS = {
     "snhip_set_stream": (I32, [V, V]),
     "snhip_max_batch": (I32, [V]),
     "snhip_persistent_grid": (I32, [V]),
+    "snhip_batch_grid": (I32, [V]),
     "snhip_step_batch_dev": (I32, [V, V, I32, V]),
     "snhip_step_batch": (I32, [V, V, I32, V]),
     "snhip_decode_greedy_dev": (I32, [V, V, I32, I32, V, V]),

@@ -69,4 +69,44 @@ int persist_occupancy(int blk);
 bool persist_grid_ok(int G, int D, int I, int R, int vocab);
 snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipStream_t st);
 
+// Persistent step of a batch of sequences (batch.hip): every layer of one
+// decode step in one cooperative launch, phases separated by grid barriers.
+// Each phase writes its outputs to buffers no other phase of the launch
+// writes (per-layer slabs), with agent-coherent stores, so a barrier needs no
+// cache fences: a line a workgroup reads after a barrier was not cached by
+// its XCD earlier in the launch.
+constexpr int kBatchMaxK = 1536;       // deepest product: 8 waves x 3 chunks of 64
+constexpr int kBatchMaxRow = 2048;     // longest LayerNorm row: 512 threads x 4
+constexpr int kBatchBarWords = 512;    // barrier words (zeroed before each launch)
+
+struct BatchArgs {
+    const PLayer* layers;   // device array of L layers
+    int L, B, D, I, R, K, kh, clamp;
+    float eps, p_floor;
+    const float *no_g, *no_c;
+    const float* x0;        // (B, D) embedding rows of the step's tokens
+    float* xs;              // (L, B, D) residual after each layer
+    float* at;              // (L, B, D) LN_in + conv
+    float* v;               // (L, B, R) V at
+    float* sfb;             // (L, B, D) W_eff s (old state)
+    float* u;               // (L, B, D) gated values
+    float* z;               // (L, B, I) W_z u with the wedge
+    float* sn;              // (L, B, D) new state
+    float* s;               // (B, L, D) state: old in, new out
+    float* hist;            // (B, L, kh, D) conv history, newest first
+    float* nrm;             // (B, D) LN_out of the last residual (the head's input)
+    unsigned long long* bar;  // kBatchBarWords barrier words
+    unsigned* err;          // set on a barrier time-out
+    unsigned spin_limit;    // polls before a barrier wait gives up
+    unsigned stall;         // added to every awaited generation: > 0 only to test the time-out path
+};
+
+// Shapes the batched kernel handles: products no deeper than kBatchMaxK in
+// whole chunks of 64, LayerNorm rows up to kBatchMaxRow, four conv taps.
+bool batch_shape_ok(int D, int I, int R, int K, int L);
+// Grid for the batched kernel on this device (a multiple of 8, one
+// workgroup per CU), 0 if it cannot run.
+int batch_grid(int blk, int D, int I, int R);
+snhip_status launch_decode_batch(const BatchArgs& a, int G, int blk, hipStream_t st);
+
 }  // namespace snhip

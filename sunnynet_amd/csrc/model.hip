@@ -66,6 +66,10 @@ constexpr int kLnPer = 16;
 // (k_gate_rows + k_scan_rows); above it k_core_scan fuses them.
 constexpr size_t kSplitScanChannels = 16384;
 
+__global__ void k_zero_words(unsigned long long* p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0ull;
+}
+
 __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
                         float* __restrict__ x, int D, int vocab) {
     const int b = blockIdx.x;
@@ -592,9 +596,16 @@ struct SnHipModel {
     unsigned long long* psx = nullptr;    // new-state words (L x 2 x D)
     float* pring = nullptr;               // per-workgroup LN_in history rings
     unsigned* perr = nullptr;             // time-out flag
-    unsigned* h_err = nullptr;            // pinned copy of the time-out flag
+    unsigned* h_err = nullptr;            // pinned copies of the time-out flags: [0] perr, [1] berr
     unsigned persist_spin = 1u << 22;     // poll limit (SNHIP_PERSIST_SPIN)
     unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests)
+    // Persistent batched step (batch.hip) for batches of gemm_min_batch ..
+    // batch_max sequences: grid size, 0 when the shape or device does not allow it.
+    int batch_wg = 0;
+    int batch_max = 64;
+    float* bbuf = nullptr;                // per-layer slabs: xs, at, v, sfb, u, z, sn
+    unsigned long long* bbar = nullptr;   // barrier words
+    unsigned* berr = nullptr;             // time-out flag
     int ready = 0;
 };
 
@@ -707,6 +718,37 @@ bool upload_new(SnHipModel* m, Mat& M, const float* src, int in, int out, float*
 
 PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M}; }
 
+// The device layer table of the persistent kernels (built once).
+bool layer_table(SnHipModel* m) {
+    if (m->dlayers) return true;
+    std::vector<PLayer> hl(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const Layer& A = m->layers[l];
+        PLayer& P = hl[l];
+        P.ni_g = A.ni_g; P.ni_c = A.ni_c; P.nm_g = A.nm_g; P.nm_c = A.nm_c;
+        P.dw = A.dw; P.delta = A.delta; P.a_tanh = A.a_tanh; P.b_gain = A.b_gain;
+        P.VW = pmat(A.V);
+        P.VW.M = A.V.M + A.Ws.M;      // W_eff's rows follow V's in one storage
+        P.U = pmat(A.U); P.Wz = pmat(A.Wz); P.Wc = pmat(A.Wc);
+    }
+    PLayer* d = dalloc<PLayer>(m, m->L);
+    if (!d || hipMemcpy(d, hl.data(), hl.size() * sizeof(PLayer), hipMemcpyHostToDevice) != hipSuccess)
+        return false;
+    m->dlayers = d;
+    return true;
+}
+
+// Pinned host copies of the persistent kernels' time-out flags.
+bool host_err(SnHipModel* m) {
+    if (m->h_err) return true;
+    if (hipHostMalloc((void**)&m->h_err, 2 * sizeof(unsigned), 0) != hipSuccess) {
+        m->h_err = nullptr;
+        return false;
+    }
+    m->h_err[0] = m->h_err[1] = 0;
+    return true;
+}
+
 // Enables the persistent single-sequence decode when the shape fits it and the
 // device supports cooperative launches (SNHIP_PERSIST=0 turns it off;
 // SNHIP_PERSIST_WG caps the grid size). The grid is the largest size the
@@ -732,30 +774,34 @@ void setup_persist(SnHipModel* m) {
     for (int g = cap; g >= 1 && !nwg; --g)
         if (persist_grid_ok(g, m->D, m->I, m->R, m->vocab)) nwg = g;
     if (nwg < 1) return;
-    if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->persist_spin = (unsigned)std::max(1, atoi(e));
-    if (const char* e = getenv("SNHIP_PERSIST_STALL")) m->persist_stall = (unsigned)std::max(0, atoi(e));
-    std::vector<PLayer> hl(m->L);
-    for (int l = 0; l < m->L; ++l) {
-        const Layer& A = m->layers[l];
-        PLayer& P = hl[l];
-        P.ni_g = A.ni_g; P.ni_c = A.ni_c; P.nm_g = A.nm_g; P.nm_c = A.nm_c;
-        P.dw = A.dw; P.delta = A.delta; P.a_tanh = A.a_tanh; P.b_gain = A.b_gain;
-        P.VW = pmat(A.V);
-        P.VW.M = A.V.M + A.Ws.M;      // W_eff's rows follow V's in one storage
-        P.U = pmat(A.U); P.Wz = pmat(A.Wz); P.Wc = pmat(A.Wc);
-    }
-    m->dlayers = dalloc<PLayer>(m, m->L);
     m->pex = dalloc<unsigned long long>(m, 2 * (size_t)kPersistExWords);
     m->psx = dalloc<unsigned long long>(m, (size_t)m->L * 2 * m->D);
     m->pring = dalloc<float>(m, (size_t)nwg * m->L * m->kh * m->D);
     m->perr = dalloc<unsigned>(m, 1);
-    if (!m->dlayers || !m->pex || !m->psx || !m->pring || !m->perr ||
-        hipHostMalloc((void**)&m->h_err, sizeof(unsigned), 0) != hipSuccess)
-        return;
-    *m->h_err = 0;
-    if (hipMemcpy(m->dlayers, hl.data(), hl.size() * sizeof(PLayer), hipMemcpyHostToDevice) != hipSuccess)
-        return;
+    if (!m->pex || !m->psx || !m->pring || !m->perr || !layer_table(m) || !host_err(m)) return;
     m->persist_wg = nwg;
+}
+
+// Enables the persistent batched step (batch.hip) when the shape fits it and
+// the device supports cooperative launches (SNHIP_BATCH_PERSIST=0 turns it
+// off). Its per-layer slabs are sized for min(max_batch, batch_max) rows.
+void setup_batch(SnHipModel* m) {
+    if (const char* e = getenv("SNHIP_BATCH_PERSIST"))
+        if (e[0] == '0') return;
+    if (!m->gemm_ok || m->max_batch < m->gemm_min_batch || !batch_shape_ok(m->D, m->I, m->R, m->K, m->L) ||
+        m->kh != kPersistTaps - 1)
+        return;
+    const int G = batch_grid(m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0, m->D, m->I, m->R);
+    if (G < 8) return;
+    const size_t B = (size_t)std::min(m->max_batch, m->batch_max);
+    const size_t per = (size_t)m->L * (5 * (size_t)m->D + m->R + m->I);
+    m->bbuf = dalloc<float>(m, B * per);
+    m->bbar = dalloc<unsigned long long>(m, kBatchBarWords);
+    m->berr = dalloc<unsigned>(m, 1);
+    if (!m->bbuf || !m->bbar || !m->berr || !layer_table(m) || !host_err(m) ||
+        hipMemset(m->berr, 0, sizeof(unsigned)) != hipSuccess)
+        return;
+    m->batch_wg = G;
 }
 
 SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank, int taps,
@@ -884,7 +930,10 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         free_model(m);
         return nullptr;
     }
+    if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->persist_spin = (unsigned)std::max(1, atoi(e));
+    if (const char* e = getenv("SNHIP_PERSIST_STALL")) m->persist_stall = (unsigned)std::max(0, atoi(e));
     setup_persist(m);
+    setup_batch(m);
     m->ready = 1;
     return m;
 }
@@ -934,10 +983,15 @@ __global__ void k_copy_rows(const float* __restrict__ src, long lds, float* __re
 }
 
 // Final norm, LM head and (greedy) token selection for B rows of x.
+// Does a step of B sequences run as the batched persistent kernel?
+bool uses_batch(const SnHipModel* m, int B) {
+    return m->batch_wg > 0 && B >= m->gemm_min_batch && B <= std::min(m->max_batch, m->batch_max);
+}
+
 snhip_status enqueue_head(SnHipModel* m, int B, const float* x, float* logits_out, bool greedy,
-                          hipStream_t st) {
+                          hipStream_t st, bool normed = false) {
     const int D = m->D;
-    launch_ln(B, x, D, m->no_g, m->no_c, m->nrm, D, D, m->eps, st);
+    if (!normed) launch_ln(B, x, D, m->no_g, m->no_c, m->nrm, D, D, m->eps, st);
     if (B >= m->gemm_min_batch) {
         const snhip_status rc = run_gemm(m, gemm_for(m, m->head, m->nrm, D, B, logits_out, m->vocab), st);
         if (rc != SNHIP_OK) return rc;
@@ -973,6 +1027,30 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
     const size_t sbs = (size_t)L * D;                               // s batch stride
     const size_t hbs = (size_t)L * (m->kh ? m->kh : 1) * D;         // hist batch stride
     hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->x, D, m->vocab);
+    if (uses_batch(m, B)) {
+        // Every layer in one cooperative launch, then the head.
+        hipLaunchKernelGGL(k_zero_words, dim3(1), dim3(256), 0, st, m->bbar, kBatchBarWords);
+        BatchArgs a{};
+        a.layers = m->dlayers;
+        a.L = L; a.B = B; a.D = D; a.I = I; a.R = R; a.K = m->K; a.kh = m->kh;
+        a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
+        a.no_g = m->no_g; a.no_c = m->no_c;
+        a.x0 = m->x;
+        float* p = m->bbuf;
+        const size_t LB = (size_t)L * B;
+        a.xs = p; p += LB * D;
+        a.at = p; p += LB * D;
+        a.v = p; p += LB * R;
+        a.sfb = p; p += LB * D;
+        a.u = p; p += LB * D;
+        a.z = p; p += LB * I;
+        a.sn = p;
+        a.s = m->s; a.hist = m->hist; a.nrm = m->nrm;
+        a.bar = m->bbar; a.err = m->berr; a.spin_limit = m->persist_spin; a.stall = m->persist_stall;
+        const snhip_status rc = launch_decode_batch(a, m->batch_wg, m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0, st);
+        if (rc != SNHIP_OK) return rc;
+        return enqueue_head(m, B, nullptr, logits_out, greedy, st, true);
+    }
     const bool mm = B >= m->gemm_min_batch;
     for (int l = 0; l < L; ++l) {
         const Layer& A = m->layers[l];
@@ -1044,11 +1122,17 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
 snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int reps) {
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
     SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
-    if (!m->use_graphs) {
+    const bool batch = uses_batch(m, B);
+    if (!m->use_graphs || batch) {
+        // The batched persistent step is a handful of launches per step: they
+        // are queued directly (a cooperative launch is not captured).
+        if (batch) SNHIP_CHECK(hipMemsetAsync(m->berr, 0, sizeof(unsigned), m->work));
         for (int i = 0; i < reps; ++i) {
             const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
             if (rc != SNHIP_OK) return rc;
         }
+        if (batch)
+            SNHIP_CHECK(hipMemcpyAsync(m->h_err + 1, m->berr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
     } else {
         const auto key = std::make_tuple(B, (const void*)logits_out, greedy ? 1 : 0);
         auto it = m->graphs.find(key);
@@ -1266,9 +1350,14 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
 
 // After a synchronization: did a persistent launch time out at a barrier?
 snhip_status persist_status(SnHipModel* m) {
-    if (m->h_err && *m->h_err) {
-        *m->h_err = 0;
+    if (m->h_err && m->h_err[0]) {
+        m->h_err[0] = 0;
         set_last_error("persistent decode: exchange wait timed out");
+        return SNHIP_E_DEVICE;
+    }
+    if (m->h_err && m->h_err[1]) {
+        m->h_err[1] = 0;
+        set_last_error("batched persistent decode: barrier wait timed out");
         return SNHIP_E_DEVICE;
     }
     return SNHIP_OK;
@@ -1333,6 +1422,8 @@ int snhip_vocab(const SnHipModel* m) { return m ? m->vocab : 0; }
 int snhip_ready(const SnHipModel* m) { return m && m->ready; }
 int32_t snhip_max_batch(const SnHipModel* m) { return m ? m->max_batch : 0; }
 int32_t snhip_persistent_grid(const SnHipModel* m) { return m ? m->persist_wg : 0; }
+
+int32_t snhip_batch_grid(const SnHipModel* m) { return m ? m->batch_wg : 0; }
 
 snhip_status snhip_set_stream(SnHipModel* m, void* stream) {
     if (!m) return SNHIP_E_INVAL;

@@ -120,6 +120,11 @@ class HipModel:
         return out
 
     @property
+    def batch_grid(self) -> int:
+        """Workgroups of the persistent batched step (0: per-kernel steps)."""
+        return int(self._lib.snhip_batch_grid(self._h))
+
+    @property
     def persistent_grid(self) -> int:
         """Workgroups of the persistent B=1 decode kernel (0: per-kernel steps)."""
         return int(self._lib.snhip_persistent_grid(self._h))
