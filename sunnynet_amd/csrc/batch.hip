@@ -328,8 +328,19 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
     const int mb = (B + 15) / 16;
     const size_t sbs = (size_t)L * D;                    // state row stride
     const size_t hbs = (size_t)L * a.kh * D;             // history row stride
-    unsigned gen = 0;
+    unsigned gen = a.gen0;
     bool last = false;
+    // Layer 0's input row b: the embedding row of token b (NaN for an id
+    // outside the vocabulary, as k_embed writes), later layers' the residual.
+    auto in_row = [&](int l, int b, bool& ok) -> const float* {
+        if (l > 0) {
+            ok = true;
+            return a.xs + ((size_t)(l - 1) * B + b) * D;
+        }
+        const int t = a.tok[b];
+        ok = t >= 0 && t < a.vocab;
+        return a.embed + (size_t)(ok ? t : 0) * D;
+    };
 
     for (int i = tid; i < L * (int)sizeof(PLayer) / 4; i += NT)
         reinterpret_cast<unsigned*>(ltab)[i] = reinterpret_cast<const unsigned*>(a.layers)[i];
@@ -345,7 +356,6 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
 
     for (int l = 0; l < L; ++l) {
         const PLayer* P = ltab + l;
-        const float* xl = l == 0 ? a.x0 : a.xs + (size_t)(l - 1) * B * D;
         float* atl = a.at + (size_t)l * B * D;
         float* vl = a.v + (size_t)l * B * R;
         float* sfbl = a.sfb + (size_t)l * B * D;
@@ -359,7 +369,8 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
         BPROF(5 * l, 0);
         for (int b = wg; b < B; b += G) {
             fresh();
-            const float* xr = xl + (size_t)b * D;
+            bool xok;
+            const float* xr = in_row(l, b, xok);
             const gptr<float> ng = glb(uni(P->ni_g));
             const gptr<float> nc = glb(uni(P->ni_c));
             const gptr<float> dw = glb(uni(P->dw));
@@ -368,7 +379,7 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
 #pragma unroll
             for (int k = 0; k < PERM; ++k) {
                 const int i = min(k * NT + tid, D - 1);
-                xv[k] = xr[i];
+                xv[k] = xok ? xr[i] : __builtin_nanf("");
                 gv[k] = ng[i];
                 cv[k] = nc[i];
 #pragma unroll
@@ -532,7 +543,9 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
                 const int em = tl.m0 + ((tid & 255) >> 4), en = tl.n0 + (tid & 15);
                 const bool eon = tid < 256 && em < B;
                 const size_t eo = (size_t)min(em, B - 1) * D + en;
-                const float e_sn = snl[eo], e_sfb = sfbl[eo], e_x = xl[eo];
+                bool xok;
+                const float* xr = in_row(l, min(em, B - 1), xok);
+                const float e_sn = snl[eo], e_sfb = sfbl[eo], e_x = xok ? xr[en] : __builtin_nanf("");
                 XF x[NCM];
                 load_x<NCI, FULL>(x, zl, I, tl.m0, B, I, wv, lane);
                 if (t == wg) BPROF_LOADED(5 * l + 4, 1);

@@ -84,7 +84,9 @@ struct BatchArgs {
     int L, B, D, I, R, K, kh, clamp;
     float eps, p_floor;
     const float *no_g, *no_c;
-    const float* x0;        // (B, D) embedding rows of the step's tokens
+    const int32_t* tok;     // (B) the step's token ids: layer 0's input is their embedding rows
+    const float* embed;     // (vocab, D); an id outside [0, vocab) gives a NaN row
+    int vocab;
     float* xs;              // (L, B, D) residual after each layer
     float* at;              // (L, B, D) LN_in + conv
     float* v;               // (L, B, R) V at
@@ -95,7 +97,8 @@ struct BatchArgs {
     float* s;               // (B, L, D) state: old in, new out
     float* hist;            // (B, L, kh, D) conv history, newest first
     float* nrm;             // (B, D) LN_out of the last residual (the head's input)
-    unsigned long long* bar;  // kBatchBarWords barrier words
+    unsigned long long* bar;  // kBatchBarWords barrier words, zero before the first launch of a call
+    unsigned gen0;          // barriers completed by the earlier launches since they were zeroed
     unsigned* err;          // set on a barrier time-out
     unsigned spin_limit;    // polls before a barrier wait gives up
     unsigned stall;         // added to every awaited generation: > 0 only to test the time-out path

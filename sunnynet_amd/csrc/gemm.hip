@@ -401,7 +401,7 @@ __device__ __forceinline__ void sk_run(const SkJob& J, int local, float* red, in
 }
 
 // ---------------------------------------------------------------------------
-// Tiny-tile path (M <= 64, N up to 8192, K a multiple of 64 up to 3072: the
+// Tiny-tile path (M <= 64 with N up to 8192, or M <= 16 with any N; K a multiple of 64 up to 3072: the
 // per-layer products of batched decode). A workgroup computes one 16 x 16
 // tile of Y (16 rows of X x 16 weight rows) with no exchange between
 // workgroups: its nw waves split K into 64-wide chunks (wave w takes chunks
@@ -657,7 +657,10 @@ struct TtPlan { bool ok; int mb, ntiles, nw, nc, xcd; };
 
 TtPlan tt_plan(const GemmArgs& g) {
     TtPlan p{};
-    if (g.M > 64 || g.shift_T != 0 || g.K % TT_CH || g.N > 8192) return p;
+    // Wide products (the LM head) take this path only for up to 16 rows of X
+    // (one row block, no padding to 64 rows); measured at vocab 32000:
+    // INT4 B=8 head step 424 -> 405 us, but fp32 B=64 603 -> 661 us.
+    if (g.M > 64 || g.shift_T != 0 || g.K % TT_CH || (g.N > 8192 && g.M > 16)) return p;
     const int nch = g.K / TT_CH;
     for (int nc : {1, 2, 3, 4, 6}) {
         if (nch % nc == 0 && nch / nc <= TT_MAXW) {

@@ -66,10 +66,6 @@ constexpr int kLnPer = 16;
 // (k_gate_rows + k_scan_rows); above it k_core_scan fuses them.
 constexpr size_t kSplitScanChannels = 16384;
 
-__global__ void k_zero_words(unsigned long long* p, int n) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0ull;
-}
-
 __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
                         float* __restrict__ x, int D, int vocab) {
     const int b = blockIdx.x;
@@ -606,6 +602,7 @@ struct SnHipModel {
     float* bbuf = nullptr;                // per-layer slabs: xs, at, v, sfb, u, z, sn
     unsigned long long* bbar = nullptr;   // barrier words
     unsigned* berr = nullptr;             // time-out flag
+    unsigned batch_gen = 0;               // barriers of the launches since bbar was zeroed
     int ready = 0;
 };
 
@@ -1026,16 +1023,15 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
     const int D = m->D, I = m->I, R = m->R, L = m->L;
     const size_t sbs = (size_t)L * D;                               // s batch stride
     const size_t hbs = (size_t)L * (m->kh ? m->kh : 1) * D;         // hist batch stride
-    hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->x, D, m->vocab);
     if (uses_batch(m, B)) {
-        // Every layer in one cooperative launch, then the head.
-        hipLaunchKernelGGL(k_zero_words, dim3(1), dim3(256), 0, st, m->bbar, kBatchBarWords);
+        // Every layer in one cooperative launch (the embedding rows gathered
+        // inside), then the head.
         BatchArgs a{};
         a.layers = m->dlayers;
         a.L = L; a.B = B; a.D = D; a.I = I; a.R = R; a.K = m->K; a.kh = m->kh;
         a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
         a.no_g = m->no_g; a.no_c = m->no_c;
-        a.x0 = m->x;
+        a.tok = m->tok; a.embed = m->embed; a.vocab = m->vocab;
         float* p = m->bbuf;
         const size_t LB = (size_t)L * B;
         a.xs = p; p += LB * D;
@@ -1047,10 +1043,13 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
         a.sn = p;
         a.s = m->s; a.hist = m->hist; a.nrm = m->nrm;
         a.bar = m->bbar; a.err = m->berr; a.spin_limit = m->persist_spin; a.stall = m->persist_stall;
+        a.gen0 = m->batch_gen;
+        m->batch_gen += 5 * (unsigned)L;
         const snhip_status rc = launch_decode_batch(a, m->batch_wg, m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0, st);
         if (rc != SNHIP_OK) return rc;
         return enqueue_head(m, B, nullptr, logits_out, greedy, st, true);
     }
+    hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, m->tok, m->embed, m->x, D, m->vocab);
     const bool mm = B >= m->gemm_min_batch;
     for (int l = 0; l < L; ++l) {
         const Layer& A = m->layers[l];
@@ -1126,7 +1125,12 @@ snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int
     if (!m->use_graphs || batch) {
         // The batched persistent step is a handful of launches per step: they
         // are queued directly (a cooperative launch is not captured).
-        if (batch) SNHIP_CHECK(hipMemsetAsync(m->berr, 0, sizeof(unsigned), m->work));
+        if (batch) {
+            // Barrier counters restart from zero for this call's launches.
+            SNHIP_CHECK(hipMemsetAsync(m->berr, 0, sizeof(unsigned), m->work));
+            SNHIP_CHECK(hipMemsetAsync(m->bbar, 0, kBatchBarWords * sizeof(unsigned long long), m->work));
+            m->batch_gen = 0;
+        }
         for (int i = 0; i < reps; ++i) {
             const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
             if (rc != SNHIP_OK) return rc;

@@ -136,3 +136,21 @@ def test_batched_barrier_timeout_reports_error(gpu, small, monkeypatch):
     orc = oracle.SnOracle(buf, batch=B)
     a = hm2.step_batch_host(toks)
     assert np.abs(a - orc.step(toks)).max() < TOL
+
+
+def test_batched_kernel_out_of_range_token_gives_nan_row(gpu, small):
+    """An id outside the vocabulary on the device path gives that sequence a
+    NaN embedding row (as the per-kernel path's gather does); sequences are
+    independent, so every other row still matches the oracle."""
+    w, buf, path = small
+    B = 8
+    hm = _model(path, SMALL, max_batch=B)
+    assert hm.batch_grid > 0
+    toks = np.arange(B, dtype=np.int32) * 37
+    bad = toks.copy()
+    bad[3] = SMALL.vocab_size + 5
+    a = hm.step_batch(torch.from_numpy(bad).to(gpu)).cpu().numpy()
+    b = oracle.SnOracle(buf, batch=B).step(toks)
+    assert np.isnan(a[3]).all()
+    keep = [i for i in range(B) if i != 3]
+    assert np.abs(a[keep] - b[keep]).max() < TOL
