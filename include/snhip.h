@@ -42,7 +42,11 @@ SnHipModel* snhip_load(const char* path, int vocab, int dim, int inner, int rank
                        int taps, int layers, int group, int tied);
 
 /* Same checks as snhip_load; max_batch sequences, weight_format SNHIP_WEIGHTS_*,
- * block = INT4 group size along the input dim (even, divides dim, inner, rank). */
+ * block = INT4 group size along the input dim (even, divides dim, inner, rank).
+ * path may also name an INT4 blob (magic 'SNQ4', written by
+ * `python -m sunnynet_amd.blob --int4`; no counterpart in the reference):
+ * its codes and scales load as stored, with weight_format SNHIP_WEIGHTS_INT4
+ * and block equal to the blob's group size; snhip_load refuses it. */
 SnHipModel* snhip_load_ex(const char* path, int vocab, int dim, int inner, int rank,
                           int taps, int layers, int group, int tied,
                           int32_t max_batch, int32_t weight_format, int32_t block);

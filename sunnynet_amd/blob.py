@@ -143,3 +143,121 @@ def parse_sunny_blob(buf) -> dict:
                p_floor=p_floor, no_g=take(D), no_c=take(D), embed=take(V * D, (V, D)))
     out["head"] = take(D * V, (D, V)).T.copy()
     return out
+
+
+# ---------------------------------------------------------------------------
+# INT4 blob: the same model with every matrix a decode step multiplies (V, U,
+# W_z, W_c, W_s_eff and the head) stored pre-quantized, so an INT4 handle loads
+# it without quantizing. The reference has no quantized SunnyNet file; its
+# INT4 arithmetic (quant.c:34-87, group size 32 or 64) is what is stored.
+#
+# Layout (little-endian): 12 x int32 header
+# ``magic=0x34514E53 ('SNQ4'), version=1, vocab, dim, inner, rank, taps,
+# layers, group=8, tied, clamp, block``
+# then, per layer, ``norm_in.gamma (D), norm_in.center (D), norm_mix.gamma (I),
+# norm_mix.center (I), dw^T (K,D)`` (fp32), the five matrices V (R,D), U (2D,R),
+# W_z (I,D), W_c (D,I), W_s_eff (D,D) (row-major (out, in); U's rows in the
+# model's order, values then gates), each as ``codes (out, in/2) uint8`` then
+# ``scales (out, in/block) float32``, then ``delta (D), tanh(a), b_gain``;
+# then ``eps, p_floor, norm_out.gamma (D), norm_out.center (D), embed (V,D)``
+# (fp32, the lookup table) and the head (V,D) as codes then scales.
+# Codes pack the quant.c way: byte k of a group holds q[k] | q[k + block/2] << 4.
+
+I4_MAGIC = 0x34514E53
+I4_VERSION = 1
+I4_HEADER_BYTES = 48
+
+
+def convert_blob_int4(buf, block: int = 32) -> bytes:
+    """The INT4 blob of an fp32 runtime blob (quantized as quant.c does)."""
+    from .rwkv7 import quant_i4_np
+    if block not in (32, 64):
+        raise ValueError("block must be 32 or 64")
+    b = parse_sunny_blob(buf)
+    cfg = b["cfg"]
+    D, I, R, K, L, V = cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers, cfg.vocab_size
+    for n in (D, I, R):
+        if n % block:
+            raise ValueError("block must divide dim, inner and rank")
+    parts = [struct.pack("<12i", I4_MAGIC, I4_VERSION, V, D, I, R, K, L, b["group"], b["tied"],
+                         b["clamp"], block)]
+
+    def mat(M):
+        q, s = quant_i4_np(np.ascontiguousarray(M, np.float32), block)
+        return [q.tobytes(), s.tobytes()]
+
+    for d in b["layers"]:
+        parts += [d[k].astype(np.float32).tobytes() for k in ("ni_g", "ni_c", "nm_g", "nm_c")]
+        parts.append(np.ascontiguousarray(d["dw_t"], np.float32).tobytes())
+        for k in ("V", "U", "W_z", "W_c", "W_s_eff"):
+            parts += mat(d[k])
+        parts += [d["delta"].astype(np.float32).tobytes(),
+                  struct.pack("<2f", d["a_tanh"], d["b_gain"])]
+    parts.append(struct.pack("<2f", b["eps"], b["p_floor"]))
+    parts += [b["no_g"].astype(np.float32).tobytes(), b["no_c"].astype(np.float32).tobytes(),
+              np.ascontiguousarray(b["embed"], np.float32).tobytes()]
+    parts += mat(b["head"])
+    return b"".join(parts)
+
+
+def parse_blob_int4(buf) -> dict:
+    """Header, small parameters and (codes, scales) pairs of an INT4 blob."""
+    raw = bytes(buf)
+    h = struct.unpack_from("<12i", raw, 0)
+    if h[0] != I4_MAGIC or h[1] != I4_VERSION:
+        raise ValueError("not an INT4 SunnyNet blob (magic or version)")
+    V, D, I, R, K, L, G, tied, clamp, block = h[2:]
+    o = I4_HEADER_BYTES
+
+    def f32(n):
+        nonlocal o
+        a = np.frombuffer(raw, np.float32, n, o)
+        o += 4 * n
+        return a
+
+    def mat(out, inn):
+        nonlocal o
+        q = np.frombuffer(raw, np.uint8, out * inn // 2, o).reshape(out, inn // 2)
+        o += out * inn // 2
+        s = np.frombuffer(raw, np.float32, out * inn // block, o).reshape(out, inn // block)
+        o += 4 * out * inn // block
+        return q, s
+
+    layers = []
+    for _ in range(L):
+        d = dict(ni_g=f32(D), ni_c=f32(D), nm_g=f32(I), nm_c=f32(I), dw_t=f32(K * D).reshape(K, D))
+        for k, (out, inn) in (("V", (R, D)), ("U", (2 * D, R)), ("W_z", (I, D)),
+                              ("W_c", (D, I)), ("W_s_eff", (D, D))):
+            d[k] = mat(out, inn)
+        d["delta"] = f32(D)
+        d["a_tanh"], d["b_gain"] = (float(x) for x in f32(2))
+        layers.append(d)
+    eps, p_floor = (float(x) for x in f32(2))
+    out = dict(cfg=SunnyConfig(vocab_size=V, dim=D, inner=I, rank=R, taps=K, layers=L), group=G,
+               tied=tied, clamp=clamp, block=block, layers=layers, eps=eps, p_floor=p_floor,
+               no_g=f32(D), no_c=f32(D), embed=f32(V * D).reshape(V, D))
+    out["head"] = mat(V, D)
+    if o != len(raw):
+        raise ValueError(f"INT4 blob has {len(raw) - o} trailing bytes")
+    return out
+
+
+def main(argv=None) -> int:
+    """python -m sunnynet_amd.blob --int4 IN.bin OUT.bin [--block 32|64]:
+    write the INT4 blob of an fp32 runtime blob."""
+    import argparse
+    ap = argparse.ArgumentParser(prog="python -m sunnynet_amd.blob")
+    ap.add_argument("--int4", nargs=2, metavar=("IN", "OUT"), required=True)
+    ap.add_argument("--block", type=int, default=32, choices=(32, 64))
+    a = ap.parse_args(argv)
+    with open(a.int4[0], "rb") as f:
+        buf = f.read()
+    out = convert_blob_int4(buf, a.block)
+    with open(a.int4[1], "wb") as f:
+        f.write(out)
+    print(f"{a.int4[1]}: {len(out)} bytes (fp32 blob {len(buf)}), INT4 group {a.block}")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -651,6 +651,48 @@ bool read_blob(const char* path, const int32_t want[9], std::vector<float>& payl
     return true;
 }
 
+// INT4 blob (no counterpart in the reference, which stores fp32 only):
+// 12 x int32 header (magic 'SNQ4', version 1, vocab, dim, inner, rank, taps,
+// layers, group, tied, clamp, block), then the fp32 blob's fields in its
+// order with V, U, W_z, W_c, W_s_eff and the head as (out, in) quant.c codes
+// followed by their scales; the lookup embedding stays fp32.
+constexpr int32_t kMagicI4 = 0x34514E53, kVersionI4 = 1;
+
+int32_t peek_magic(const char* path) {
+    FILE* f = fopen(path, "rb");
+    if (!f) return 0;
+    int32_t h = 0;
+    const bool ok = fread(&h, sizeof(int32_t), 1, f) == 1;
+    fclose(f);
+    return ok ? h : 0;
+}
+
+// Reads an INT4 blob whole and checks its header and size against the shape.
+bool read_blob_i4(const char* path, const int32_t want[8], int block, std::vector<uint8_t>& raw,
+                  int32_t& clamp) {
+    FILE* f = fopen(path, "rb");
+    if (!f) { set_last_error(std::string("cannot open ") + path); return false; }
+    int32_t h[12];
+    if (fread(h, sizeof(int32_t), 12, f) != 12 || h[0] != kMagicI4 || h[1] != kVersionI4) {
+        fclose(f); set_last_error("bad INT4 blob header (magic or version)"); return false;
+    }
+    for (int i = 0; i < 8; ++i)
+        if (h[i + 2] != want[i]) { fclose(f); set_last_error("INT4 blob header does not match the given dimensions"); return false; }
+    if (h[11] != block) { fclose(f); set_last_error("INT4 blob group size differs from the requested block"); return false; }
+    clamp = h[10];
+    const size_t V = want[0], D = want[1], I = want[2], R = want[3], K = want[4], L = want[5], B = block;
+    auto qbytes = [&](size_t out, size_t in) { return out * in / 2 + out * (in / B) * 4; };
+    const size_t per_layer = 4 * (2 * D + 2 * I + K * D + D + 2) + qbytes(R, D) + qbytes(2 * D, R) +
+                             qbytes(I, D) + qbytes(D, I) + qbytes(D, D);
+    const size_t total = L * per_layer + 4 * (2 + 2 * D + V * D) + qbytes(V, D);
+    raw.resize(total + 1);
+    const size_t got = fread(raw.data(), 1, total + 1, f);
+    fclose(f);
+    if (got != total) { set_last_error(got < total ? "INT4 blob is truncated" : "INT4 blob has trailing bytes"); return false; }
+    raw.resize(total);
+    return true;
+}
+
 bool upload(SnHipModel* m, float*& dst, const float* src, size_t n) {
     dst = dalloc<float>(m, n);
     return dst && hipMemcpy(dst, src, n * sizeof(float), hipMemcpyHostToDevice) == hipSuccess;
@@ -677,6 +719,31 @@ MatStore alloc_mat(SnHipModel* m, size_t rows, size_t in) {
 bool store_ok(const SnHipModel* m, const MatStore& S) {
     return m->wfmt == SNHIP_WEIGHTS_F32 ? S.w != nullptr : (S.q && S.sc);
 }
+
+// Codes and scales of an (out, in) INT4 matrix into rows row0.. of storage S;
+// perm_u: U's rows go to the qrow_u / qrow_g order.
+bool upload_q(SnHipModel* m, Mat& M, const uint8_t* codes, const float* scales, int in, int out,
+              const MatStore& S, size_t row0, bool perm_u = false) {
+    M.M = out;
+    M.Kd = in;
+    const size_t cb = (size_t)in / 2, sb = (size_t)in / m->block;
+    M.q = S.q + row0 * cb;
+    M.sc = S.sc + row0 * sb;
+    if (!perm_u)
+        return hipMemcpy(M.q, codes, (size_t)out * cb, hipMemcpyHostToDevice) == hipSuccess &&
+               hipMemcpy(M.sc, scales, (size_t)out * sb * sizeof(float), hipMemcpyHostToDevice) == hipSuccess;
+    std::vector<uint8_t> qc((size_t)out * cb);
+    std::vector<float> sc((size_t)out * sb);
+    const int half = out / 2;
+    for (int i = 0; i < out; ++i) {
+        const int r = i < half ? qrow_u(i) : qrow_g(i - half);
+        memcpy(qc.data() + (size_t)r * cb, codes + (size_t)i * cb, cb);
+        memcpy(sc.data() + (size_t)r * sb, scales + (size_t)i * sb, sb * sizeof(float));
+    }
+    return hipMemcpy(M.q, qc.data(), qc.size(), hipMemcpyHostToDevice) == hipSuccess &&
+           hipMemcpy(M.sc, sc.data(), sc.size() * sizeof(float), hipMemcpyHostToDevice) == hipSuccess;
+}
+
 
 // Upload an (in,out) blob matrix as (out,in) rows starting at row `row0` of
 // the storage S (quantized to INT4 for that format). perm_u: U's rows go to
@@ -801,6 +868,63 @@ void setup_batch(SnHipModel* m) {
     m->batch_wg = G;
 }
 
+// Every weight of an INT4 blob (past its header) onto the device.
+bool load_layers_i4(SnHipModel* m, const uint8_t* raw) {
+    const size_t D = m->D, I = m->I, R = m->R, K = m->K, V = m->vocab, BL = m->block;
+    const uint8_t* o = raw;
+    auto f32 = [&](size_t n) {
+        const float* a = reinterpret_cast<const float*>(o);
+        o += 4 * n;
+        return a;
+    };
+    auto mat = [&](size_t out, size_t in, const uint8_t*& q, const float*& sc) {
+        q = o;
+        o += out * in / 2;
+        sc = reinterpret_cast<const float*>(o);
+        o += out * (in / BL) * 4;
+    };
+    bool ok = true;
+    for (int l = 0; l < m->L && ok; ++l) {
+        Layer& A = m->layers[l];
+        float* t;
+        ok &= upload(m, t, f32(D), D); A.ni_g = t;
+        ok &= upload(m, t, f32(D), D); A.ni_c = t;
+        ok &= upload(m, t, f32(I), I); A.nm_g = t;
+        ok &= upload(m, t, f32(I), I); A.nm_c = t;
+        ok &= upload(m, t, f32(K * D), K * D); A.dw = t;
+        const uint8_t* q;
+        const float* sc;
+        const MatStore vw = alloc_mat(m, R + D, D);        // V's rows, then W_eff's
+        ok = ok && store_ok(m, vw);
+        mat(R, D, q, sc); ok = ok && upload_q(m, A.V, q, sc, (int)D, (int)R, vw, 0);
+        mat(2 * D, R, q, sc);
+        const MatStore us = alloc_mat(m, 2 * D, R);
+        ok = ok && store_ok(m, us) && upload_q(m, A.U, q, sc, (int)R, (int)(2 * D), us, 0, true);
+        mat(I, D, q, sc);
+        const MatStore zs = alloc_mat(m, I, D);
+        ok = ok && store_ok(m, zs) && upload_q(m, A.Wz, q, sc, (int)D, (int)I, zs, 0);
+        mat(D, I, q, sc);
+        const MatStore cs = alloc_mat(m, D, I);
+        ok = ok && store_ok(m, cs) && upload_q(m, A.Wc, q, sc, (int)I, (int)D, cs, 0);
+        mat(D, D, q, sc); ok = ok && upload_q(m, A.Ws, q, sc, (int)D, (int)D, vw, R);
+        ok &= upload(m, t, f32(D), D); A.delta = t;
+        const float* ab = f32(2);
+        A.a_tanh = ab[0]; A.b_gain = ab[1];
+    }
+    if (!ok) return false;
+    const float* ep = f32(2);
+    m->eps = ep[0]; m->p_floor = ep[1];
+    float* t;
+    ok &= upload(m, t, f32(D), D); m->no_g = t;
+    ok &= upload(m, t, f32(D), D); m->no_c = t;
+    ok &= upload(m, t, f32(V * D), V * D); m->embed = t;
+    const uint8_t* q;
+    const float* sc;
+    mat(V, D, q, sc);
+    const MatStore hs = alloc_mat(m, V, D);
+    return ok && store_ok(m, hs) && upload_q(m, m->head, q, sc, (int)D, (int)V, hs, 0);
+}
+
 SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank, int taps,
                        int layers, int group, int tied, int max_batch, int wfmt, int block) {
     if (!path || vocab <= 0 || dim <= 0 || inner <= 0 || rank <= 0 || taps <= 0 || layers <= 0 ||
@@ -827,8 +951,18 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     }
     const int32_t want[9] = {vocab, dim, inner, rank, taps, layers, group, tied, 0};
     std::vector<float> P;
+    std::vector<uint8_t> Q;                  // an INT4 blob, read whole
     int32_t clamp = 0;
-    if (!read_blob(path, want, P, clamp)) return nullptr;
+    const bool i4blob = peek_magic(path) == kMagicI4;
+    if (i4blob) {
+        if (wfmt != SNHIP_WEIGHTS_INT4) {
+            set_last_error("an INT4 blob needs weight format SNHIP_WEIGHTS_INT4");
+            return nullptr;
+        }
+        if (!read_blob_i4(path, want, block, Q, clamp)) return nullptr;
+    } else if (!read_blob(path, want, P, clamp)) {
+        return nullptr;
+    }
 
     SnHipModel* m = new SnHipModel();
     m->vocab = vocab; m->D = dim; m->I = inner; m->R = rank; m->K = taps; m->L = layers;
@@ -843,7 +977,8 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     const float* p = P.data();
     bool ok = true;
     m->layers.resize(layers);
-    for (int l = 0; l < layers && ok; ++l) {
+    if (i4blob) ok = load_layers_i4(m, Q.data());
+    for (int l = 0; l < layers && ok && !i4blob; ++l) {
         Layer& A = m->layers[l];
         float* t;
         ok &= upload(m, t, p, D); A.ni_g = t; p += D;
@@ -862,7 +997,7 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         ok &= upload(m, t, p, D); A.delta = t; p += D;
         A.a_tanh = p[0]; A.b_gain = p[1]; p += 2;
     }
-    if (ok) {
+    if (ok && !i4blob) {
         m->eps = p[0]; m->p_floor = p[1]; p += 2;
         float* t;
         ok &= upload(m, t, p, D); m->no_g = t; p += D;
