@@ -36,10 +36,18 @@ typedef struct SnHipModel SnHipModel;
 #define SNHIP_WEIGHTS_INT4  1   /* V, U, W_z, W_c, W_s_eff and the LM head
                                    quantized at load with quant.c's symmetric
                                    group format; embedding lookup stays fp32  */
+#define SNHIP_WEIGHTS_F16   3   /* sn_load_h's values (sunnynet.c:455-579): the
+                                   same matrices rounded to fp16 (nearest even)
+                                   at load; this backend holds and multiplies
+                                   them as fp32 (no byte saving yet)          */
 
 /* sunnynet.h:22-23: B = 1, fp32 weights. */
 SnHipModel* snhip_load(const char* path, int vocab, int dim, int inner, int rank,
                        int taps, int layers, int group, int tied);
+
+/* sunnynet.h:25-28 (sn_load_h): B = 1, weight_format SNHIP_WEIGHTS_F16. */
+SnHipModel* snhip_load_h(const char* path, int vocab, int dim, int inner, int rank,
+                         int taps, int layers, int group, int tied);
 
 /* Same checks as snhip_load; max_batch sequences, weight_format SNHIP_WEIGHTS_*,
  * block = INT4 group size along the input dim (even, divides dim, inner, rank).

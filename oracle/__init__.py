@@ -275,6 +275,8 @@ def ref_lib(name: str):
     if name == "model":
         lib.sn_load.restype = V
         lib.sn_load.argtypes = [P, I, I, I, I, I, I, I, I]
+        lib.sn_load_h.restype = V
+        lib.sn_load_h.argtypes = [P, I, I, I, I, I, I, I, I]
         lib.sn_free.argtypes = [V]
         lib.sn_reset.argtypes = [V]
         lib.sn_step.argtypes = [V, I, V]
@@ -323,11 +325,11 @@ def ref_lib(name: str):
 class RefSnModel:
     """The reference's sn_load/sn_step handle (B=1), for pinning and timing."""
 
-    def __init__(self, path, vocab, dim, inner, rank, taps, layers, group=8, tied=1):
+    def __init__(self, path, vocab, dim, inner, rank, taps, layers, group=8, tied=1, half=False):
         self._lib = ref_lib("model")
         self.vocab = vocab
-        self._h = self._lib.sn_load(str(path).encode(), vocab, dim, inner, rank, taps,
-                                    layers, group, tied)
+        load = self._lib.sn_load_h if half else self._lib.sn_load
+        self._h = load(str(path).encode(), vocab, dim, inner, rank, taps, layers, group, tied)
         if not self._h:
             raise RuntimeError(f"reference sn_load rejected {path}")
         self._logits = np.empty(vocab, np.float32)

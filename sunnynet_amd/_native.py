@@ -66,6 +66,7 @@ _SIGS = {
     # include/snhip.h
     "snhip_load": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT]),
     "snhip_load_ex": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT, I32, I32, I32]),
+    "snhip_load_h": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT]),
     "snhip_free": (None, [V]),
     "snhip_reset": (None, [V]),
     "snhip_step": (None, [V, INT, V]),

@@ -22,6 +22,8 @@
 #include <tuple>
 #include <vector>
 
+#include <hip/hip_fp16.h>
+
 #include "common.h"
 #include "decode.h"
 #include "gemm.h"
@@ -65,6 +67,11 @@ constexpr int kLnPer = 16;
 // for every row in parallel and the scan only multiplies and adds
 // (k_gate_rows + k_scan_rows); above it k_core_scan fuses them.
 constexpr size_t kSplitScanChannels = 16384;
+
+__global__ void k_round_f16(float* __restrict__ x, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = __half2float(__float2half_rn(x[i]));
+}
 
 __global__ void k_embed(const int32_t* __restrict__ tok, const float* __restrict__ embed,
                         float* __restrict__ x, int D, int vocab) {
@@ -603,6 +610,7 @@ struct SnHipModel {
     unsigned long long* bbar = nullptr;   // barrier words
     unsigned* berr = nullptr;             // time-out flag
     unsigned batch_gen = 0;               // barriers of the launches since bbar was zeroed
+    bool half = false;                    // matrices rounded to fp16 at load (sn_load_h)
     int ready = 0;
 };
 
@@ -761,6 +769,11 @@ bool upload_mat(SnHipModel* m, Mat& M, const float* src, int in, int out, float*
         hipLaunchKernelGGL(k_permute_u, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr,
                            tmp_out, tmp_in, out / 2, in);
         rows = tmp_in;
+    }
+    if (m->half) {
+        // _cvtss_sh(x, 0) (sunnynet.c:517,570): round to the nearest fp16, ties to even
+        hipLaunchKernelGGL(k_round_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr,
+                           const_cast<float*>(rows), (long)n);
     }
     if (hipGetLastError() != hipSuccess) return false;
     if (m->wfmt == SNHIP_WEIGHTS_F32) {
@@ -945,10 +958,13 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
             set_last_error("INT4 block must divide dim, inner and rank");
             return nullptr;
         }
-    } else if (wfmt != SNHIP_WEIGHTS_F32) {
+    } else if (wfmt != SNHIP_WEIGHTS_F32 && wfmt != SNHIP_WEIGHTS_F16) {
         set_last_error("unknown weight format");
         return nullptr;
     }
+    // fp16 values (sn_load_h) are held as fp32: every kernel takes the fp32 path.
+    const bool half = wfmt == SNHIP_WEIGHTS_F16;
+    if (half) wfmt = SNHIP_WEIGHTS_F32;
     const int32_t want[9] = {vocab, dim, inner, rank, taps, layers, group, tied, 0};
     std::vector<float> P;
     std::vector<uint8_t> Q;                  // an INT4 blob, read whole
@@ -967,7 +983,7 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
     SnHipModel* m = new SnHipModel();
     m->vocab = vocab; m->D = dim; m->I = inner; m->R = rank; m->K = taps; m->L = layers;
     m->G = group; m->tied = tied; m->clamp = clamp; m->kh = taps > 1 ? taps - 1 : 0;
-    m->max_batch = max_batch; m->wfmt = wfmt; m->block = block;
+    m->max_batch = max_batch; m->wfmt = wfmt; m->block = block; m->half = half;
     const size_t D = dim, I = inner, R = rank, K = taps, V = vocab;
     const size_t big = std::max(std::max(D * R, R * 2 * D), std::max(D * I, std::max(D * D, D * V)));
     float* tmp_in = dalloc<float>(m, big);
@@ -1532,6 +1548,12 @@ SnHipModel* snhip_load(const char* path, int vocab, int dim, int inner, int rank
                        int layers, int group, int tied) {
     return load_model(path, vocab, dim, inner, rank, taps, layers, group, tied, 1,
                       SNHIP_WEIGHTS_F32, 32);
+}
+
+SnHipModel* snhip_load_h(const char* path, int vocab, int dim, int inner, int rank, int taps,
+                         int layers, int group, int tied) {
+    return load_model(path, vocab, dim, inner, rank, taps, layers, group, tied, 1,
+                      SNHIP_WEIGHTS_F16, 32);
 }
 
 SnHipModel* snhip_load_ex(const char* path, int vocab, int dim, int inner, int rank, int taps,

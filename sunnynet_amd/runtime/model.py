@@ -23,7 +23,7 @@ from .. import _native
 
 __all__ = ["HipModel", "SnModel", "model_available"]
 
-WEIGHT_FORMATS = {"fp32": 0, "int4": 1}
+WEIGHT_FORMATS = {"fp32": 0, "int4": 1, "fp16": 3}
 
 
 def model_available() -> bool:
@@ -37,8 +37,8 @@ class HipModel:
                  half=False, *, max_batch: int = 1, weights: str = "fp32", block: int = 32,
                  device=None):
         if half:
-            raise RuntimeError("fp16 weights are not provided by the HIP backend; "
-                               "use weights='int4' for reduced-precision weights")
+            # sn_load_h (runtime/model.py:100): the matrices rounded to fp16 at load
+            weights = "fp16"
         self._lib = _native.lib()
         self.device = torch.device(device or "cuda:0")
         self.vocab, self.dim, self.layers, self.taps = vocab, dim, layers, taps
