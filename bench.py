@@ -121,6 +121,55 @@ def bench_scan(steps: int, warmup: int, cpu: bool):
     }
     if cpu:
         res["cpu_baseline"] = cpu_scan_baseline(a, b, s0)
+    res["scan_bwd"] = bench_scan_bwd(da, db, d0, steps, warmup, cpu)
+    return res
+
+
+def bench_scan_bwd(dp_, dnu_, ds0_, steps, warmup, cpu):
+    """The gated scan's backward (scan_avx2.c:50-99) on the same workload:
+    read p, nu, the forward states and dout, write dp and dnu (6 x B*T*D*4
+    bytes per launch), timed per launch with HIP events on the kernel's
+    stream; the reference scan_bwd_f32 (single-threaded, as it ships) on the
+    same arrays beside it."""
+    B, T, D = dp_.shape
+    out, _ = runtime.scan(dp_, dnu_, ds0_, gated=True)
+    g = torch.Generator(device="cpu").manual_seed(2)
+    dout = torch.randn(B, T, D, generator=g).to(dp_.device)
+    for _ in range(warmup):
+        runtime.scan_bwd(dp_, dnu_, ds0_, out, dout)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dp_.device)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        runtime.scan_bwd(dp_, dnu_, ds0_, out, dout)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    avg_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1 in evs]))
+    nbytes = 6 * B * T * D * 4 + 2 * B * D * 4
+    gbs = nbytes / (avg_ms * 1e-3) / 1e9
+    log(f"[bench] scan_bwd: kernel avg {avg_ms*1e3:.1f} us, {gbs:.1f} GB/s")
+    res = {"kernel": "k_scan_bwd_buf", "kernel_avg_us": round(avg_ms * 1e3, 2),
+           "bytes_per_launch": nbytes,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    if cpu:
+        import oracle
+        if oracle.ref_available():
+            hp = [x.cpu().numpy() for x in (dp_, dnu_, ds0_, out, dout)]
+            o = [np.empty_like(hp[0]), np.empty_like(hp[0]), np.empty_like(hp[2])]
+            f = oracle._f
+            lib = oracle.ref_lib("scan")
+            t0 = time.perf_counter()
+            lib.scan_bwd_f32(f(hp[0]), f(hp[1]), f(hp[2]), f(hp[3]), f(hp[4]), f(o[0]), f(o[1]),
+                             f(o[2]), B, T, D)
+            sec = time.perf_counter() - t0
+            log(f"[bench] cpu reference scan_bwd_f32: {sec*1e3:.1f} ms, {nbytes/sec/1e9:.2f} GB/s")
+            res["cpu_baseline"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1,
+                                   "kind": "reference",
+                                   "sample": f"full workload B={B} D={D} T={T}, one run "
+                                             f"({sec*1e3:.0f} ms; scan_bwd_f32 is single-threaded)"}
     return res
 
 
@@ -400,6 +449,8 @@ def main(argv=None):
             "config": res["config"], "roofline": res["roofline"]}
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
+    if "scan_bwd" in res:
+        line["scan_bwd"] = res["scan_bwd"]
     if dec is not None:
         line["decode"] = dec
     print(json.dumps(line), flush=True)

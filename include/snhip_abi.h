@@ -95,6 +95,15 @@ snhip_status snhip_abi_recur_scan_dev(const float* a, const float* b,
                                       int32_t B, int32_t T, int32_t N,
                                       int32_t gated, void* stream);
 
+/* sunnynet/kernels/scan_avx2.c:50-99 (scan_bwd_f32), device pointers: the
+ * gradients of the gated scan s_t = p_t s_{t-1} + (1 - p_t) nu_t. Inputs p, nu,
+ * out (the forward states) and dout (B,T,N), s0 (B,N); outputs dp, dnu
+ * (B,T,N) and ds0 (B,N), bit-identical to the reference. Enqueued on `stream`. */
+snhip_status snhip_abi_scan_bwd_dev(const float* p, const float* nu, const float* s0,
+                                    const float* out, const float* dout, float* dp,
+                                    float* dnu, float* ds0, int32_t B, int32_t T,
+                                    int32_t N, void* stream);
+
 /* ----------------------------------------------- INT4 (group-wise) */
 /* Format of sunnynet/runtime/quant.c:34-87: W (rows, N) row-major; groups of
  * `block` inputs share scale = amax/7 (1 if amax == 0); byte k of a group

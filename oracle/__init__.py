@@ -68,6 +68,7 @@ def load():
     V, I, L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     lib.orc_recur_scan.argtypes = [V, V, V, V, V, I, I, I, I]
     lib.orc_recur_step.argtypes = [V, V, V, I, I, I]
+    lib.orc_scan_bwd.argtypes = [V, V, V, V, V, V, V, V, I, I, I]
     lib.orc_quant_i4.argtypes = [V, V, V, I, I, I]
     lib.orc_dequant_i4.argtypes = [V, V, V, I, I, I]
     lib.orc_sn_new.restype = V
@@ -105,6 +106,19 @@ def recur_scan(a, b, s0, gated: bool):
     send = np.empty_like(s0)
     lib.orc_recur_scan(_f(a), _f(b), _f(s0), _f(out), _f(send), B, T, N, int(bool(gated)))
     return out, send
+
+
+def scan_bwd(p, nu, s0, out, dout):
+    """scan_avx2.c:50-99: gradients of the gated scan s_t = p s + (1-p) nu.
+    p, nu, out (forward states), dout (B,T,N); s0 (B,N) -> (dp, dnu, ds0)."""
+    lib = load()
+    p, nu, out, dout = (np.ascontiguousarray(x, np.float32) for x in (p, nu, out, dout))
+    s0 = np.ascontiguousarray(s0, np.float32)
+    B, T, N = p.shape
+    dp, dnu = np.empty_like(p), np.empty_like(p)
+    ds0 = np.empty_like(s0)
+    lib.orc_scan_bwd(_f(p), _f(nu), _f(s0), _f(out), _f(dout), _f(dp), _f(dnu), _f(ds0), B, T, N)
+    return dp, dnu, ds0
 
 
 def recur_step(a, b, s, gated: bool):
@@ -310,6 +324,7 @@ def ref_lib(name: str):
         lib.sn_rk_vocab.restype = I
     elif name == "scan":
         lib.scan_f32.argtypes = [V, V, V, V, V, I, I, I]
+        lib.scan_bwd_f32.argtypes = [V, V, V, V, V, V, V, V, I, I, I]
     elif name == "abi":
         I32 = ctypes.c_int32
         lib.sn_abi_recur_scan.argtypes = [V, V, V, V, V, I32, I32, I32, I32]

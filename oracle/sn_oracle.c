@@ -41,6 +41,30 @@ void orc_recur_scan(const float* a, const float* b, const float* s0,
     }
 }
 
+/* scan_avx2.c:50-99. The 8-wide path and the scalar tail use the same
+ * operations in the same order (add, then sub and mul for each output, then
+ * mul), none fused, so one scalar loop restates both. */
+void orc_scan_bwd(const float* p, const float* nu, const float* s0, const float* out,
+                  const float* dout, float* dp, float* dnu, float* ds0, int B, int T, int N) {
+    #pragma omp parallel for schedule(static)
+    for (int bb = 0; bb < B; ++bb) {
+        const size_t rb = (size_t)bb * T * N;
+        for (int d = 0; d < N; ++d) {
+            float ds = 0.0f;
+            for (int t = T - 1; t >= 0; --t) {
+                const size_t off = rb + (size_t)t * N + d;
+                ds = dout[off] + ds;
+                const float pv = p[off];
+                const float sprev = t > 0 ? out[off - N] : s0[(size_t)bb * N + d];
+                dnu[off] = ds * (1.0f - pv);
+                dp[off] = ds * (sprev - nu[off]);
+                ds = ds * pv;
+            }
+            ds0[(size_t)bb * N + d] = ds;
+        }
+    }
+}
+
 /* recur.c:109-131, same lane split as the scan. */
 void orc_recur_step(const float* a, const float* b, float* s, int B, int N,
                     int gated) {

@@ -25,6 +25,12 @@ void orc_recur_scan(const float* a, const float* b, const float* s0,
 void orc_recur_step(const float* a, const float* b, float* s, int B, int N,
                     int gated);
 
+/* ---- gated-scan backward: sunnynet/kernels/scan_avx2.c:50-99 ----
+ * Reverse time per channel: ds += dout_t; dnu_t = ds (1 - p_t);
+ * dp_t = ds (s_{t-1} - nu_t) (s_{-1} = s0); ds *= p_t; ds0 = ds at the end. */
+void orc_scan_bwd(const float* p, const float* nu, const float* s0, const float* out,
+                  const float* dout, float* dp, float* dnu, float* ds0, int B, int T, int N);
+
 /* ---- group-wise INT4: sunnynet/runtime/quant.c:34-87 ---- */
 void orc_quant_i4(const float* x, uint8_t* q, float* scale, int rows, int N,
                   int block);

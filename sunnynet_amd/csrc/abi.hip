@@ -84,6 +84,14 @@ snhip_status snhip_abi_recur_scan_dev(const float* a, const float* b, const floa
     return launch_recur_scan(a, b, s0, out, send, B, T, N, gated ? 1 : 0, as_stream(stream));
 }
 
+snhip_status snhip_abi_scan_bwd_dev(const float* p, const float* nu, const float* s0,
+                                    const float* out, const float* dout, float* dp, float* dnu,
+                                    float* ds0, int32_t B, int32_t T, int32_t N, void* stream) {
+    if (dims_bad(p, B, N) || !nu || !s0 || !out || !dout || !dp || !dnu || !ds0 || T <= 0)
+        return SNHIP_E_INVAL;
+    return launch_scan_bwd(p, nu, s0, out, dout, dp, dnu, ds0, B, T, N, as_stream(stream));
+}
+
 snhip_status snhip_abi_recur_step(const float* a, const float* b, float* s, int32_t B,
                                   int32_t N, int32_t gated) {
     if (dims_bad(a, B, N) || b == nullptr || s == nullptr) return SNHIP_E_INVAL;

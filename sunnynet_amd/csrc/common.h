@@ -63,6 +63,9 @@ __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, 
 
 // Internal launchers shared across translation units.
 namespace snhip {
+snhip_status launch_scan_bwd(const float* p, const float* nu, const float* s0, const float* out,
+                             const float* dout, float* dp, float* dnu, float* ds0, int B, int T,
+                             int N, hipStream_t st);
 snhip_status launch_recur_scan(const float* a, const float* b, const float* s0,
                                float* out, float* send, int B, int T, int N,
                                int gated, hipStream_t st);

@@ -184,8 +184,8 @@ void k_recur_scan(const float* __restrict__ a, const float* __restrict__ b,
 // resources: the per-step row offset t*N*4 is a scalar (SGPR) operand, so the
 // active slot issues only its FMAs and stores (no per-access 64-bit address
 // arithmetic), and the prefetch registers hold data only, which leaves room
-// for deeper time chunks. Prefetches past T read as zero (hardware range
-// check) and are never used.
+// for deeper time chunks. Prefetches past T re-read step T - 1 (the scalar
+// row offset is not range-checked by the hardware) and are never used.
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // Cache policy of every scan load and store: non-temporal ("nt"), i.e.
@@ -263,12 +263,16 @@ void k_recur_scan_buf(const float* __restrict__ a, const float* __restrict__ b,
     // path). Separate arrays keep the two lifetimes disjoint for the allocator.
     float av[TC][CPL], bv[TC][CPL], bp[TC][CPL];
 
+    // Steps past T (the last tile's tail) load step T - 1 instead: the row
+    // offset is the scalar operand, which the buffer range check does not
+    // cover. Those values are never used.
     auto load_slot = [&](int tile) {
         const int t0 = tile * TILE + w * TC;
 #pragma unroll
         for (int k = 0; k < TC; ++k) {
-            IO::load(av[k], ra, voff, (t0 + k) * rowb);
-            IO::load(bv[k], rb, voff, (t0 + k) * rowb);
+            const int so = min(t0 + k, T - 1) * rowb;
+            IO::load(av[k], ra, voff, so);
+            IO::load(bv[k], rb, voff, so);
         }
     };
     auto prep = [&]() {
@@ -464,6 +468,168 @@ snhip_status launch_recur_step(const float* a, const float* b, float* s, int B, 
         hipLaunchKernelGGL((k_recur_step<true>), dim3(grid), dim3(256), 0, st, a, b, s, total, N, N & ~7);
     else
         hipLaunchKernelGGL((k_recur_step<false>), dim3(grid), dim3(256), 0, st, a, b, s, total, N, N & ~7);
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Backward of the gated scan s_t = p_t s_{t-1} + (1 - p_t) nu_t
+// (sunnynet/kernels/scan_avx2.c:50-99): per channel, in reverse time,
+//   ds += dout_t;  dnu_t = ds (1 - p_t);  dp_t = ds (s_{t-1} - nu_t);  ds *= p_t
+// with s_{-1} = s0, and ds0 = ds after t = 0. The reference's 8-wide path and
+// scalar tail use these unfused operations in this order, so the result is
+// bit-identical. Same slot pipeline as k_recur_scan_buf, walking time
+// backwards: wave w owns reversed steps [w TC, (w + 1) TC) of every tile of
+// W TC steps; while the active wave runs its TC dependent add/multiply pairs
+// the next wave prepares s_{t-1} - nu_t and 1 - p_t, off the carried chain.
+// HBM traffic per step: four reads (dout, p, nu, s_{t-1}), two writes.
+template <int CPL, int W, int TC>
+__global__ __launch_bounds__(64 * W)
+void k_scan_bwd_buf(const float* __restrict__ p, const float* __restrict__ nu,
+                    const float* __restrict__ s0, const float* __restrict__ out,
+                    const float* __restrict__ dout, float* __restrict__ dp,
+                    float* __restrict__ dnu, float* __restrict__ ds0, int T, int N) {
+    static_assert(W >= 2, "the hand-off pipeline needs at least two waves");
+    using IO = BufIO<CPL>;
+    __shared__ float carry[CPL * 64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wg_per_row = N / (64 * CPL);
+    const int bb = blockIdx.x / wg_per_row;
+    const int n0 = (blockIdx.x - bb * wg_per_row) * 64 * CPL;
+    const size_t row = (size_t)bb * T * N;
+    const uint32_t nbytes = (uint32_t)((size_t)T * N * 4);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + row, nbytes);
+    const __amdgpu_buffer_rsrc_t rn = make_rsrc(nu + row, nbytes);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + row, nbytes);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(dout + row, nbytes);
+    const __amdgpu_buffer_rsrc_t rgp = make_rsrc(dp + row, nbytes);
+    const __amdgpu_buffer_rsrc_t rgn = make_rsrc(dnu + row, nbytes);
+    const int voff = (n0 + lane * CPL) * 4;
+    const int rowb = N * 4;
+
+    constexpr int TILE = W * TC;
+    const int ntiles = (T + TILE - 1) / TILE;
+    // pv: p; gv: dout; dv: nu, then s_{t-1} - nu; qv: s_{t-1}, then 1 - p.
+    float pv[TC][CPL], gv[TC][CPL], dv[TC][CPL], qv[TC][CPL], sz[CPL];
+    ld<CPL>(sz, s0 + (size_t)bb * N + n0 + lane * CPL);
+
+    // Time step of reversed step k of this wave's slot in `tile`.
+    auto t_of = [&](int tile, int k) { return T - 1 - (tile * TILE + w * TC + k); };
+    // Steps before 0 (the last tile's tail) load step 0 (the scalar row offset
+    // is not range-checked); they are never used.
+    auto load_slot = [&](int tile) {
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const int t = max(t_of(tile, k), 0);
+            const int so = t * rowb, sp = max(t - 1, 0) * rowb;
+            IO::load(pv[k], rp, voff, so);
+            IO::load(gv[k], rd, voff, so);
+            IO::load(dv[k], rn, voff, so);
+            IO::load(qv[k], ro, voff, sp);
+        }
+    };
+    auto prep = [&](int tile) {
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const bool first = t_of(tile, k) == 0;           // s_{-1} is s0
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                dv[k][c] = sub_rn(first ? sz[c] : qv[k][c], dv[k][c]);
+                qv[k][c] = sub_rn(1.0f, pv[k][c]);
+            }
+        }
+    };
+    auto run_slot = [&](int tile) {
+        float ds[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) ds[c] = carry[c * 64 + lane];
+#pragma unroll
+        for (int k = 0; k < TC; ++k) {
+            const int t = t_of(tile, k);
+            if (t < 0) break;
+            float gn[CPL], gp[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                ds[c] = add_rn(gv[k][c], ds[c]);
+                gn[c] = mul_rn(ds[c], qv[k][c]);
+                gp[c] = mul_rn(ds[c], dv[k][c]);
+                ds[c] = mul_rn(ds[c], pv[k][c]);
+            }
+            IO::store(rgn, voff, t * rowb, gn);
+            IO::store(rgp, voff, t * rowb, gp);
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = ds[c];
+    };
+
+    if (w == 0)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) carry[c * 64 + lane] = 0.0f;
+    load_slot(0);
+    if (w == 0) prep(0);
+    __syncthreads();
+    for (int tile = 0; tile < ntiles; ++tile) {
+        for (int j = 0; j < W; ++j) {
+            if (w == j) {
+                run_slot(tile);
+                if (tile + 1 < ntiles) load_slot(tile + 1);
+            } else if (w == j + 1) {
+                prep(tile);
+            } else if (j == W - 1 && w == 0 && tile + 1 < ntiles) {
+                prep(tile + 1);
+            }
+            barrier_lds();
+        }
+    }
+    if (w == 0) {
+        float ds[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) ds[c] = carry[c * 64 + lane];
+        st<CPL>(ds0 + (size_t)bb * N + n0 + lane * CPL, ds);
+    }
+}
+
+// Any layout: one lane per channel, straight through time.
+__global__ void k_scan_bwd_gen(const float* __restrict__ p, const float* __restrict__ nu,
+                               const float* __restrict__ s0, const float* __restrict__ out,
+                               const float* __restrict__ dout, float* __restrict__ dp,
+                               float* __restrict__ dnu, float* __restrict__ ds0, int B, int T, int N) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)B * N) return;
+    const long bb = i / N;
+    const int n = (int)(i - bb * N);
+    const size_t rb = (size_t)bb * T * N + n;
+    float ds = 0.0f;
+    for (int t = T - 1; t >= 0; --t) {
+        const size_t off = rb + (size_t)t * N;
+        ds = add_rn(dout[off], ds);
+        const float pv = p[off];
+        const float sprev = t > 0 ? out[off - N] : s0[(size_t)bb * N + n];
+        dnu[off] = mul_rn(ds, sub_rn(1.0f, pv));
+        dp[off] = mul_rn(ds, sub_rn(sprev, nu[off]));
+        ds = mul_rn(ds, pv);
+    }
+    ds0[(size_t)bb * N + n] = ds;
+}
+
+snhip_status launch_scan_bwd(const float* p, const float* nu, const float* s0, const float* out,
+                             const float* dout, float* dp, float* dnu, float* ds0, int B, int T,
+                             int N, hipStream_t st) {
+    const bool al8 = aligned(p, 8) && aligned(nu, 8) && aligned(s0, 8) && aligned(out, 8) &&
+                     aligned(dout, 8) && aligned(dp, 8) && aligned(dnu, 8) && aligned(ds0, 8);
+    constexpr int C = 2, WW = 2, TT = 16;
+    const bool buf = N % (64 * C) == 0 && al8 && (long)T * N * 4 < (1L << 31) &&
+                     (long)B * N / 128 >= 128;
+    if (buf) {
+        const unsigned grid = (unsigned)((long)B * N / (64 * C));
+        hipLaunchKernelGGL((k_scan_bwd_buf<C, WW, TT>), dim3(grid), dim3(64 * WW), 0, st, p, nu, s0, out,
+                           dout, dp, dnu, ds0, T, N);
+    } else {
+        const long total = (long)B * N;
+        hipLaunchKernelGGL(k_scan_bwd_gen, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p, nu,
+                           s0, out, dout, dp, dnu, ds0, B, T, N);
+    }
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;
 }

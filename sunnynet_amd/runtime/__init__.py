@@ -15,7 +15,7 @@ import torch
 
 from .. import _native
 
-__all__ = ["FMA", "GATED", "load_runtime", "runtime_available", "scan", "step"]
+__all__ = ["FMA", "GATED", "GatedScan", "gated_scan", "load_runtime", "runtime_available", "scan", "scan_bwd", "step"]
 
 FMA = 0
 GATED = 1
@@ -56,6 +56,53 @@ def scan(a: torch.Tensor, b: torch.Tensor, s0: torch.Tensor, gated: bool = False
                                     out.data_ptr(), send.data_ptr(), B, T, N, g)
     _native.check(rc, "snhip_abi_recur_scan")
     return out, send
+
+
+def scan_bwd(p: torch.Tensor, nu: torch.Tensor, s0: torch.Tensor, out: torch.Tensor,
+             dout: torch.Tensor):
+    """Gradients of the gated scan s_t = p_t s_{t-1} + (1 - p_t) nu_t
+    (sunnynet/kernels/scan_avx2.c:50-99) on the device: p, nu, out (the
+    forward states), dout (B,T,N); s0 (B,N) -> (dp, dnu, ds0)."""
+    _check_f32(p, nu, s0, out, dout)
+    B, T, N = p.shape
+    if any(t.shape != p.shape for t in (nu, out, dout)) or s0.shape != (B, N):
+        raise ValueError("shape mismatch: p, nu, out, dout (B,T,N); s0 (B,N)")
+    if not all(t.is_cuda for t in (p, nu, s0, out, dout)):
+        raise ValueError("scan_bwd takes device tensors")
+    dp, dnu, ds0 = torch.empty_like(p), torch.empty_like(p), torch.empty_like(s0)
+    rc = _native.lib().snhip_abi_scan_bwd_dev(p.data_ptr(), nu.data_ptr(), s0.data_ptr(),
+                                              out.data_ptr(), dout.data_ptr(), dp.data_ptr(),
+                                              dnu.data_ptr(), ds0.data_ptr(), B, T, N,
+                                              _native.stream_handle(p.device))
+    _native.check(rc, "snhip_abi_scan_bwd_dev")
+    return dp, dnu, ds0
+
+
+class GatedScan(torch.autograd.Function):
+    """The gated scan under autograd: forward is the HIP scan, backward the
+    HIP scan_bwd (the seam the reference's kernels serve, core_auto.py:43-74).
+    Returns (out (B,T,N), send (B,N)); send is out's last step, so its
+    gradient joins dout there."""
+
+    @staticmethod
+    def forward(ctx, p, nu, s0):
+        p, nu, s0 = p.contiguous(), nu.contiguous(), s0.contiguous()
+        out, send = scan(p, nu, s0, gated=True)
+        ctx.save_for_backward(p, nu, s0, out)
+        return out, send
+
+    @staticmethod
+    def backward(ctx, dout, dsend):
+        p, nu, s0, out = ctx.saved_tensors
+        dout = torch.zeros_like(out) if dout is None else dout.contiguous().clone()
+        if dsend is not None:
+            dout[:, -1] += dsend
+        return scan_bwd(p, nu, s0, out, dout)
+
+
+def gated_scan(p: torch.Tensor, nu: torch.Tensor, s0: torch.Tensor):
+    """Differentiable gated scan (see GatedScan)."""
+    return GatedScan.apply(p, nu, s0)
 
 
 def step(a: torch.Tensor, b: torch.Tensor, s: torch.Tensor, gated: bool = False):

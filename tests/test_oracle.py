@@ -276,3 +276,22 @@ def test_weight_init_matches_reference_rng_order():
     Ws = a.layers[0].W_s
     assert torch.allclose(Ws @ Ws.T, 0.25 * torch.eye(Ws.shape[0]), atol=1e-5)   # rho/2
     assert abs(float(a.embed.std()) - 0.02) < 2e-3
+
+
+@pytest.mark.parametrize("B,T,N", [(2, 37, 21), (3, 64, 64)])
+def test_scan_bwd_bitexact_vs_reference(ref_built, B, T, N):
+    """orc_scan_bwd against the reference's scan_bwd_f32 (scan_avx2.c:50-99):
+    widths with and without the scalar tail, bit for bit."""
+    rng = np.random.default_rng(B * 1000 + N)
+    p = rng.uniform(0.3, 1.0, (B, T, N)).astype(np.float32)
+    nu = rng.standard_normal((B, T, N)).astype(np.float32)
+    s0 = rng.standard_normal((B, N)).astype(np.float32)
+    out, _ = oracle.recur_scan(p, nu, s0, gated=True)
+    dout = rng.standard_normal((B, T, N)).astype(np.float32)
+    got = oracle.scan_bwd(p, nu, s0, out, dout)
+    ref = [np.empty_like(p), np.empty_like(p), np.empty_like(s0)]
+    f = oracle._f
+    oracle.ref_lib("scan").scan_bwd_f32(f(p), f(nu), f(s0), f(out), f(dout), f(ref[0]), f(ref[1]),
+                                        f(ref[2]), B, T, N)
+    for a, b in zip(got, ref):
+        assert np.array_equal(a, b)
