@@ -1,6 +1,6 @@
 """Benchmark of the SunnyNet token loop on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|scan|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|scan|core|decode]
 
 Headline (``value``): the standalone gated prefill scan, B=16, D=2048
 channels, T=4096, fp32, inputs resident in HBM (``sunnynet_amd.workloads``).
@@ -9,6 +9,11 @@ write s: 3*B*T*D*4 bytes per step) over the K timed steps. ``roofline``
 times each launch with HIP events on the stream the kernel runs on;
 ``cpu_baseline`` times the reference C runtime's ``sn_recur_scan`` (built
 from the reference sources into oracle/_ref) on host cores, same inputs.
+
+``core`` (same JSON line): the fused block core (compete gate + decay gate +
+gated scan, core_avx2.c:34-149) forward and backward on the same B, T, D
+(q is (B,T,2D)), each launch timed with HIP events, HBM roofline of its
+algorithmic bytes, the reference core_fwd_f32 / core_bwd_f32 beside them.
 
 ``decode`` (same JSON line): SunnyNet-100M (L=12, D=1024, V=32000, seed-1
 random init), chunked prefill of a T=1024 random prompt, then 256 greedy
@@ -170,6 +175,80 @@ def bench_scan_bwd(dp_, dnu_, ds0_, steps, warmup, cpu):
                                    "kind": "reference",
                                    "sample": f"full workload B={B} D={D} T={T}, one run "
                                              f"({sec*1e3:.0f} ms; scan_bwd_f32 is single-threaded)"}
+    return res
+
+
+def _event_avg_ms(fn, steps, stream):
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([e0.elapsed_time(e1) for e0, e1 in evs]))
+
+
+def bench_core(steps, warmup, cpu, B=SCAN_B, T=SCAN_T, D=SCAN_D):
+    """The fused block core (core_avx2.c:34-149) on the scan's workload shape:
+    q (B,T,2D), D channels. Forward reads q and writes states, u, p (20 bytes
+    per channel-step); backward reads q, u, p, the previous states, dstate,
+    du_in and writes dq (36 bytes per channel-step). Each launch is timed with
+    HIP events on the kernel's stream; the reference core_fwd_f32 /
+    core_bwd_f32 on host cores beside them on a T/16 slice."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(9)
+    q = torch.randn(B, T, 2 * D, generator=g, device=dev) * 0.6
+    delta = 0.01 + 0.4 * torch.rand(D, generator=g, device=dev)
+    s0 = torch.randn(B, D, generator=g, device=dev) * 0.1
+    dstate = torch.randn(B, T, D, generator=g, device=dev)
+    du_in = torch.randn(B, T, D, generator=g, device=dev)
+    fwd = runtime.core_fwd(q, delta, s0)
+    for _ in range(warmup):
+        runtime.core_fwd(q, delta, s0)
+        runtime.core_bwd(q, delta, s0, *fwd, dstate, du_in)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    fms = _event_avg_ms(lambda: runtime.core_fwd(q, delta, s0), steps, stream)
+    bms = _event_avg_ms(lambda: runtime.core_bwd(q, delta, s0, *fwd, dstate, du_in), steps, stream)
+    n = B * T * D
+    fbytes, bbytes = 20 * n + 8 * B * D + 4 * D, 36 * n + 12 * B * D + 8 * D
+    fg, bg = fbytes / (fms * 1e-3) / 1e9, bbytes / (bms * 1e-3) / 1e9
+    log(f"[bench] core fwd: {fms*1e3:.1f} us, {fg:.1f} GB/s; bwd: {bms*1e3:.1f} us, {bg:.1f} GB/s")
+    res = {"workload": f"fused core B={B} D={D} T={T} fp32",
+           "fwd": {"kernel": "k_core_fwd_buf", "kernel_avg_us": round(fms * 1e3, 2), "bytes_per_launch": fbytes,
+                   "roofline": {"bound": "hbm", "achieved": round(fg, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(fg / HBM_PEAK_GBS, 4)}},
+           "bwd": {"kernel": "k_core_bwd_buf", "kernel_avg_us": round(bms * 1e3, 2), "bytes_per_launch": bbytes,
+                   "roofline": {"bound": "hbm", "achieved": round(bg, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(bg / HBM_PEAK_GBS, 4)}}}
+    if cpu:
+        import oracle
+        if oracle.ref_available():
+            Ts = T // 16
+            hq = q[:, :Ts].cpu().numpy().copy()
+            hd, hs = delta.cpu().numpy(), s0.cpu().numpy()
+            hds, hdu = dstate[:, :Ts].cpu().numpy().copy(), du_in[:, :Ts].cpu().numpy().copy()
+            st, u, p = (np.empty((B, Ts, D), np.float32) for _ in range(3))
+            dq, dd, ds0 = np.empty_like(hq), np.zeros(D, np.float32), np.empty_like(hs)
+            f = oracle._f
+            lib = oracle.ref_lib("core")
+            threads = min(16, physical_cores())
+            lib.sn_set_threads(threads)
+            t0 = time.perf_counter()
+            lib.core_fwd_f32(f(hq), f(hd), f(hs), f(st), f(u), f(p), B, Ts, D)
+            t1 = time.perf_counter()
+            lib.core_bwd_f32(f(hq), f(hd), f(hs), f(st), f(u), f(p), f(hds), f(hdu), f(dq), f(dd), f(ds0),
+                             B, Ts, D)
+            t2 = time.perf_counter()
+            ns = B * Ts * D
+            cf, cb = (20 * ns) / (t1 - t0) / 1e9, (36 * ns) / (t2 - t1) / 1e9
+            log(f"[bench] cpu reference core_fwd_f32 {cf:.2f} GB/s, core_bwd_f32 {cb:.2f} GB/s, {threads} threads")
+            smp = f"B={B} D={D} T={Ts} (a T/16 slice), one run each"
+            res["fwd"]["cpu_baseline"] = {"value": round(cf, 3), "unit": "GB/s", "cores": threads,
+                                          "kind": "reference", "sample": smp}
+            res["bwd"]["cpu_baseline"] = {"value": round(cb, 3), "unit": "GB/s", "cores": threads,
+                                          "kind": "reference", "sample": smp}
     return res
 
 
@@ -413,7 +492,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="all", choices=["all", "scan", "decode"])
+    ap.add_argument("--workload", default="all", choices=["all", "scan", "core", "decode"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the fixed launch sequence used for rocprofv3 --pmc and exit")
@@ -429,6 +508,13 @@ def main(argv=None):
         # The headline scan runs first, on a cold allocator and clean caches.
         res = bench_scan(args.steps, args.warmup, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
+    core = None
+    if args.workload in ("all", "core"):
+        core = bench_core(args.steps, args.warmup, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        if args.workload == "core":
+            print(json.dumps({"core": core}), flush=True)
+            return 0
     dec = None
     if args.workload in ("all", "decode"):
         dec = bench_decode(cpu=not args.no_cpu)
@@ -451,6 +537,8 @@ def main(argv=None):
         line["cpu_baseline"] = res["cpu_baseline"]
     if "scan_bwd" in res:
         line["scan_bwd"] = res["scan_bwd"]
+    if core is not None:
+        line["core"] = core
     if dec is not None:
         line["decode"] = dec
     print(json.dumps(line), flush=True)

@@ -104,6 +104,27 @@ snhip_status snhip_abi_scan_bwd_dev(const float* p, const float* nu, const float
                                     float* dnu, float* ds0, int32_t B, int32_t T,
                                     int32_t N, void* stream);
 
+/* sunnynet/kernels/core_avx2.c:34-73 (core_fwd_f32), device pointers: the
+ * fused compete gate + decay gate + gated scan of a block. q (B,T,2D) holds
+ * [u_raw | gate] per step, delta (D), s0 (B,D); outputs states, u, p (B,T,D).
+ * D must be a multiple of 8 (groups of 8 channels, as the reference's kernel
+ * assumes). Every operation is the reference's except expf (the device's,
+ * within 1 ulp). Enqueued on `stream`. */
+snhip_status snhip_abi_core_fwd_dev(const float* q, const float* delta, const float* s0,
+                                    float* states, float* u, float* p, int32_t B,
+                                    int32_t T, int32_t D, void* stream);
+/* sunnynet/kernels/core_avx2.c:78-149 (core_bwd_f32), device pointers: from
+ * the forward's inputs and outputs and the upstream gradients dstate, du_in
+ * (B,T,D), writes dq (B,T,2D) and ds0 (B,D), and ADDS the delta gradient into
+ * ddelta (D) as the reference does (its caller zeroes it). ddelta's terms are
+ * summed in a fixed order, so repeated calls give identical results.
+ * Enqueued on `stream` (allocates a B*D float workspace stream-ordered). */
+snhip_status snhip_abi_core_bwd_dev(const float* q, const float* delta, const float* s0,
+                                    const float* states, const float* u, const float* p,
+                                    const float* dstate, const float* du_in, float* dq,
+                                    float* ddelta, float* ds0, int32_t B, int32_t T,
+                                    int32_t D, void* stream);
+
 /* ----------------------------------------------- INT4 (group-wise) */
 /* Format of sunnynet/runtime/quant.c:34-87: W (rows, N) row-major; groups of
  * `block` inputs share scale = amax/7 (1 if amax == 0); byte k of a group

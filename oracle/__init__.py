@@ -69,6 +69,8 @@ def load():
     lib.orc_recur_scan.argtypes = [V, V, V, V, V, I, I, I, I]
     lib.orc_recur_step.argtypes = [V, V, V, I, I, I]
     lib.orc_scan_bwd.argtypes = [V, V, V, V, V, V, V, V, I, I, I]
+    lib.orc_core_fwd.argtypes = [V, V, V, V, V, V, I, I, I]
+    lib.orc_core_bwd.argtypes = [V, V, V, V, V, V, V, V, V, V, V, I, I, I]
     lib.orc_quant_i4.argtypes = [V, V, V, I, I, I]
     lib.orc_dequant_i4.argtypes = [V, V, V, I, I, I]
     lib.orc_sn_new.restype = V
@@ -119,6 +121,35 @@ def scan_bwd(p, nu, s0, out, dout):
     ds0 = np.empty_like(s0)
     lib.orc_scan_bwd(_f(p), _f(nu), _f(s0), _f(out), _f(dout), _f(dp), _f(dnu), _f(ds0), B, T, N)
     return dp, dnu, ds0
+
+
+def core_fwd(q, delta, s0):
+    """core_avx2.c:34-73: q (B,T,2D) [u_raw | gate], delta (D), s0 (B,D) ->
+    (states, u, p), each (B,T,D)."""
+    lib = load()
+    q = np.ascontiguousarray(q, np.float32)
+    delta = np.ascontiguousarray(delta, np.float32)
+    s0 = np.ascontiguousarray(s0, np.float32)
+    B, T, D2 = q.shape
+    D = D2 // 2
+    st, u, p = (np.empty((B, T, D), np.float32) for _ in range(3))
+    lib.orc_core_fwd(_f(q), _f(delta), _f(s0), _f(st), _f(u), _f(p), B, T, D)
+    return st, u, p
+
+
+def core_bwd(q, delta, s0, states, u, p, dstate, du_in):
+    """core_avx2.c:78-149 -> (dq (B,T,2D), ddelta (D), ds0 (B,D)); ddelta sums
+    the rows in order."""
+    lib = load()
+    arrs = [np.ascontiguousarray(x, np.float32) for x in (q, delta, s0, states, u, p, dstate, du_in)]
+    q = arrs[0]
+    B, T, D2 = q.shape
+    D = D2 // 2
+    dq = np.empty_like(q)
+    dd = np.zeros(D, np.float32)
+    ds0 = np.empty((B, D), np.float32)
+    lib.orc_core_bwd(*[_f(a) for a in arrs], _f(dq), _f(dd), _f(ds0), B, T, D)
+    return dq, dd, ds0
 
 
 def recur_step(a, b, s, gated: bool):
@@ -325,6 +356,10 @@ def ref_lib(name: str):
     elif name == "scan":
         lib.scan_f32.argtypes = [V, V, V, V, V, I, I, I]
         lib.scan_bwd_f32.argtypes = [V, V, V, V, V, V, V, V, I, I, I]
+    elif name == "core":
+        lib.core_fwd_f32.argtypes = [V, V, V, V, V, V, I, I, I]
+        lib.core_bwd_f32.argtypes = [V, V, V, V, V, V, V, V, V, V, V, I, I, I]
+        lib.sn_set_threads.argtypes = [I]
     elif name == "abi":
         I32 = ctypes.c_int32
         lib.sn_abi_recur_scan.argtypes = [V, V, V, V, V, I32, I32, I32, I32]

@@ -65,6 +65,90 @@ void orc_scan_bwd(const float* p, const float* nu, const float* s0, const float*
     }
 }
 
+/* core_avx2.c:34-73, lane by lane (lane i of a group reads e of lanes i+1,
+ * i+2 mod 8 where the reference permutes). */
+void orc_core_fwd(const float* q, const float* delta, const float* s0, float* states, float* uo,
+                  float* po, int B, int T, int D) {
+    #pragma omp parallel for schedule(static)
+    for (int b = 0; b < B; ++b) {
+        for (int d0 = 0; d0 < D; d0 += 8) {
+            float s[8], e[8];
+            for (int i = 0; i < 8; ++i) s[i] = s0[(size_t)b * D + d0 + i];
+            for (int t = 0; t < T; ++t) {
+                const size_t qo = ((size_t)b * T + t) * 2 * D + d0;
+                const size_t so = ((size_t)b * T + t) * D + d0;
+                for (int i = 0; i < 8; ++i) e[i] = expf(0.0f - q[qo + D + i]);
+                for (int i = 0; i < 8; ++i) {
+                    const float dl = delta[d0 + i];
+                    const float sig = 1.0f / (1.0f + e[i]);
+                    const float s1 = 1.0f / (1.0f + e[i] / e[(i + 1) & 7]);
+                    const float s2 = 1.0f / (1.0f + e[i] / e[(i + 2) & 7]);
+                    const float u = q[qo + i] * (s1 * s2);
+                    const float p = fmaf(dl, sig, 1.0f - dl);
+                    s[i] = fmaf(p, s[i], (1.0f - p) * u);
+                    states[so + i] = s[i];
+                    uo[so + i] = u;
+                    po[so + i] = p;
+                }
+            }
+        }
+    }
+}
+
+/* core_avx2.c:78-149, lane by lane in the reference's operation order. */
+void orc_core_bwd(const float* q, const float* delta, const float* s0, const float* states,
+                  const float* uo, const float* po, const float* dstate, const float* du_in,
+                  float* dq, float* ddelta, float* ds0, int B, int T, int D) {
+    float* acc = (float*)calloc((size_t)B * D, sizeof(float));
+    #pragma omp parallel for schedule(static)
+    for (int b = 0; b < B; ++b) {
+        for (int d0 = 0; d0 < D; d0 += 8) {
+            float ds[8] = {0}, dacc[8] = {0}, e[8], a1[8], a2[8];
+            for (int t = T - 1; t >= 0; --t) {
+                const size_t qo = ((size_t)b * T + t) * 2 * D + d0;
+                const size_t so = ((size_t)b * T + t) * D + d0;
+                float dp[8], du[8];
+                for (int i = 0; i < 8; ++i) {
+                    ds[i] = ds[i] + dstate[so + i];
+                    const float u = uo[so + i], p = po[so + i];
+                    const float sprev = t > 0 ? states[so + i - D] : s0[(size_t)b * D + d0 + i];
+                    dp[i] = ds[i] * (sprev - u);
+                    du[i] = fmaf(ds[i], 1.0f - p, du_in[so + i]);
+                    ds[i] = ds[i] * p;
+                }
+                for (int i = 0; i < 8; ++i) e[i] = expf(0.0f - q[qo + D + i]);
+                float sig[8], s1[8], s2[8];
+                for (int i = 0; i < 8; ++i) {
+                    sig[i] = 1.0f / (1.0f + e[i]);
+                    s1[i] = 1.0f / (1.0f + e[i] / e[(i + 1) & 7]);
+                    s2[i] = 1.0f / (1.0f + e[i] / e[(i + 2) & 7]);
+                    const float w = s1[i] * s2[i];
+                    const float dw = du[i] * q[qo + i];
+                    dq[qo + i] = du[i] * w;
+                    const float ds1 = dw * s2[i], ds2 = dw * s1[i];
+                    a1[i] = ds1 * (s1[i] * (1.0f - s1[i]));
+                    a2[i] = ds2 * (s2[i] * (1.0f - s2[i]));
+                }
+                for (int i = 0; i < 8; ++i) {
+                    float dg = a1[i] + a2[i];
+                    dg = dg - a1[(i + 7) & 7];
+                    dg = dg - a2[(i + 6) & 7];
+                    dg = fmaf(dp[i] * delta[d0 + i], sig[i] * (1.0f - sig[i]), dg);
+                    dacc[i] = fmaf(dp[i], sig[i] - 1.0f, dacc[i]);
+                    dq[qo + D + i] = dg;
+                }
+            }
+            for (int i = 0; i < 8; ++i) {
+                ds0[(size_t)b * D + d0 + i] = ds[i];
+                acc[(size_t)b * D + d0 + i] = dacc[i];
+            }
+        }
+    }
+    for (int b = 0; b < B; ++b)
+        for (int d = 0; d < D; ++d) ddelta[d] += acc[(size_t)b * D + d];
+    free(acc);
+}
+
 /* recur.c:109-131, same lane split as the scan. */
 void orc_recur_step(const float* a, const float* b, float* s, int B, int N,
                     int gated) {

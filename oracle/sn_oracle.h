@@ -31,6 +31,18 @@ void orc_recur_step(const float* a, const float* b, float* s, int B, int N,
 void orc_scan_bwd(const float* p, const float* nu, const float* s0, const float* out,
                   const float* dout, float* dp, float* dnu, float* ds0, int B, int T, int N);
 
+/* ---- fused compete + gate + scan, forward and backward:
+ * sunnynet/kernels/core_avx2.c:34-149. Groups of 8 channels; within a group,
+ * e = expf(-g), s1 = 1 / (1 + e_i / e_{i+1}), s2 = 1 / (1 + e_i / e_{i+2}),
+ * u = u_raw s1 s2, p = fma(delta, sigma, 1 - delta), s = fma(p, s, (1 - p) u).
+ * The backward accumulates ddelta += over b in order (the reference's result
+ * with one OpenMP thread). */
+void orc_core_fwd(const float* q, const float* delta, const float* s0, float* states, float* uo,
+                  float* po, int B, int T, int D);
+void orc_core_bwd(const float* q, const float* delta, const float* s0, const float* states,
+                  const float* uo, const float* po, const float* dstate, const float* du_in,
+                  float* dq, float* ddelta, float* ds0, int B, int T, int D);
+
 /* ---- group-wise INT4: sunnynet/runtime/quant.c:34-87 ---- */
 void orc_quant_i4(const float* x, uint8_t* q, float* scale, int rows, int N,
                   int block);

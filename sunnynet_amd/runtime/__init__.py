@@ -15,7 +15,8 @@ import torch
 
 from .. import _native
 
-__all__ = ["FMA", "GATED", "GatedScan", "gated_scan", "load_runtime", "runtime_available", "scan", "scan_bwd", "step"]
+__all__ = ["FMA", "GATED", "CoreFused", "GatedScan", "core_bwd", "core_forward", "core_fwd", "gated_scan",
+           "load_runtime", "runtime_available", "scan", "scan_bwd", "step"]
 
 FMA = 0
 GATED = 1
@@ -76,6 +77,75 @@ def scan_bwd(p: torch.Tensor, nu: torch.Tensor, s0: torch.Tensor, out: torch.Ten
                                               _native.stream_handle(p.device))
     _native.check(rc, "snhip_abi_scan_bwd_dev")
     return dp, dnu, ds0
+
+
+def core_fwd(q: torch.Tensor, delta: torch.Tensor, s0: torch.Tensor):
+    """The fused compete gate + decay gate + gated scan of a block
+    (sunnynet/kernels/core_avx2.c:34-73) on the device: q (B,T,2D) =
+    [u_raw | gate], delta (D), s0 (B,D) -> (states, u, p), each (B,T,D)."""
+    _check_f32(q, delta, s0)
+    if q.dim() != 3 or q.shape[2] % 2:
+        raise ValueError("q must be (B,T,2D)")
+    B, T, D2 = q.shape
+    D = D2 // 2
+    if delta.shape != (D,) or s0.shape != (B, D):
+        raise ValueError("shape mismatch: q (B,T,2D), delta (D), s0 (B,D)")
+    if D % 8:
+        raise ValueError("the compete gate works on groups of 8 channels: D % 8 must be 0")
+    if not all(t.is_cuda for t in (q, delta, s0)):
+        raise ValueError("core_fwd takes device tensors")
+    st, u, p = (torch.empty(B, T, D, device=q.device) for _ in range(3))
+    rc = _native.lib().snhip_abi_core_fwd_dev(q.data_ptr(), delta.data_ptr(), s0.data_ptr(), st.data_ptr(),
+                                              u.data_ptr(), p.data_ptr(), B, T, D,
+                                              _native.stream_handle(q.device))
+    _native.check(rc, "snhip_abi_core_fwd_dev")
+    return st, u, p
+
+
+def core_bwd(q, delta, s0, states, u, p, dstate, du_in):
+    """Backward of core_fwd (sunnynet/kernels/core_avx2.c:78-149) on the
+    device -> (dq (B,T,2D), ddelta (D), ds0 (B,D))."""
+    _check_f32(q, delta, s0, states, u, p, dstate, du_in)
+    B, T, D2 = q.shape
+    D = D2 // 2
+    if any(t.shape != (B, T, D) for t in (states, u, p, dstate, du_in)) or delta.shape != (D,) \
+            or s0.shape != (B, D) or D % 8:
+        raise ValueError("shape mismatch: q (B,T,2D); states, u, p, dstate, du_in (B,T,D); delta (D); s0 (B,D)")
+    if not all(t.is_cuda for t in (q, delta, s0, states, u, p, dstate, du_in)):
+        raise ValueError("core_bwd takes device tensors")
+    dq = torch.empty_like(q)
+    ddelta = torch.zeros(D, device=q.device)
+    ds0 = torch.empty_like(s0)
+    rc = _native.lib().snhip_abi_core_bwd_dev(q.data_ptr(), delta.data_ptr(), s0.data_ptr(), states.data_ptr(),
+                                              u.data_ptr(), p.data_ptr(), dstate.data_ptr(), du_in.data_ptr(),
+                                              dq.data_ptr(), ddelta.data_ptr(), ds0.data_ptr(), B, T, D,
+                                              _native.stream_handle(q.device))
+    _native.check(rc, "snhip_abi_core_bwd_dev")
+    return dq, ddelta, ds0
+
+
+class CoreFused(torch.autograd.Function):
+    """The reference's CoreAVX2 seam (sunnynet/kernels/core_auto.py:43-74) on
+    the HIP kernels: (q (B,T,2D), delta (D), s0 (B,D)) -> (u, states)."""
+
+    @staticmethod
+    def forward(ctx, q, delta, s0):
+        q, delta, s0 = q.contiguous().float(), delta.contiguous().float(), s0.contiguous().float()
+        st, u, p = core_fwd(q, delta, s0)
+        ctx.save_for_backward(q, delta, s0, st, u, p)
+        return u, st
+
+    @staticmethod
+    def backward(ctx, du, dstate):
+        q, delta, s0, st, u, p = ctx.saved_tensors
+        du = torch.zeros_like(u) if du is None else du.contiguous().float()
+        dstate = torch.zeros_like(st) if dstate is None else dstate.contiguous().float()
+        return core_bwd(q, delta, s0, st, u, p, dstate, du)
+
+
+def core_forward(q: torch.Tensor, delta: torch.Tensor, s0: torch.Tensor):
+    """(u, states) of the fused block core under autograd (core_auto.py:77-79)."""
+    return CoreFused.apply(q, delta, s0)
 
 
 class GatedScan(torch.autograd.Function):

@@ -10,6 +10,7 @@
 from __future__ import annotations
 
 import ctypes
+import os
 import tempfile
 
 import numpy as np
@@ -295,3 +296,85 @@ def test_scan_bwd_bitexact_vs_reference(ref_built, B, T, N):
                                         f(ref[2]), B, T, N)
     for a, b in zip(got, ref):
         assert np.array_equal(a, b)
+
+
+def _core_inputs(B, T, D, seed):
+    """The reference's own core test inputs (tests/test_architecture.py:714-719)."""
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((B, T, 2 * D)) * 0.6).astype(np.float32)
+    delta = (0.01 + 0.4 * rng.random(D)).astype(np.float32)
+    s0 = (rng.standard_normal((B, D)) * 0.1).astype(np.float32)
+    return rng, q, delta, s0
+
+
+def _ref_core(q, delta, s0, dstate=None, du_in=None):
+    lib = oracle.ref_lib("core")
+    f = oracle._f
+    B, T, D2 = q.shape
+    D = D2 // 2
+    st, u, p = (np.empty((B, T, D), np.float32) for _ in range(3))
+    lib.core_fwd_f32(f(q), f(delta), f(s0), f(st), f(u), f(p), B, T, D)
+    if dstate is None:
+        return st, u, p
+    dq = np.empty_like(q)
+    dd = np.zeros(D, np.float32)
+    ds0 = np.empty((B, D), np.float32)
+    lib.sn_set_threads(1)          # ddelta's per-row atomics then add in row order
+    try:
+        lib.core_bwd_f32(f(q), f(delta), f(s0), f(st), f(u), f(p), f(dstate), f(du_in), f(dq), f(dd),
+                         f(ds0), B, T, D)
+    finally:
+        lib.sn_set_threads(os.cpu_count() or 1)
+    return (st, u, p), (dq, dd, ds0)
+
+
+@pytest.mark.parametrize("B,T,D", [(2, 48, 32), (3, 37, 64), (5, 16, 8)])
+def test_core_fwd_bwd_bitexact_vs_reference(ref_built, B, T, D):
+    """orc_core_fwd / orc_core_bwd against the reference's core_fwd_f32 /
+    core_bwd_f32 (core_avx2.c:34-149), bit for bit (the reference run on one
+    OpenMP thread so that its ddelta sums the rows in order)."""
+    rng, q, delta, s0 = _core_inputs(B, T, D, 11 + B)
+    dstate = rng.standard_normal((B, T, D)).astype(np.float32)
+    du_in = rng.standard_normal((B, T, D)).astype(np.float32)
+    fwd, bwd = _ref_core(q, delta, s0, dstate, du_in)
+    got = oracle.core_fwd(q, delta, s0)
+    for a, b in zip(got, fwd):
+        assert np.array_equal(a, b)
+    gb = oracle.core_bwd(q, delta, s0, *got, dstate, du_in)
+    for a, b in zip(gb, bwd):
+        assert np.array_equal(a, b)
+
+
+def test_core_oracle_matches_float64_autograd():
+    """The closed form the kernel implements, in float64 torch: the compete
+    gate sigma(g_i - g_{i+1}) sigma(g_i - g_{i+2}) within groups of 8, p = 1 -
+    delta (1 - sigma(g)), the gated scan; gradients by autograd of
+    sum(states * dstate) + sum(u * du_in). The reference's own bars
+    (tests/test_architecture.py:738-740, 803-805): 1e-5 forward, 1e-4 backward."""
+    B, T, D, G = 2, 40, 32, 8
+    rng, q, delta, s0 = _core_inputs(B, T, D, 12)
+    st, u, p = oracle.core_fwd(q, delta, s0)
+    dstate = rng.standard_normal((B, T, D)).astype(np.float32)
+    du_in = rng.standard_normal((B, T, D)).astype(np.float32)
+    dq, dd, ds0 = oracle.core_bwd(q, delta, s0, st, u, p, dstate, du_in)
+    qt = torch.from_numpy(q).double().requires_grad_(True)
+    dt = torch.from_numpy(delta).double().requires_grad_(True)
+    s0t = torch.from_numpy(s0).double().requires_grad_(True)
+    ur, gt = qt[..., :D], qt[..., D:]
+    gg = gt.view(B, T, D // G, G)
+    w = torch.sigmoid(gg - torch.roll(gg, -1, dims=-1)) * torch.sigmoid(gg - torch.roll(gg, -2, dims=-1))
+    ut = ur * w.reshape(B, T, D)
+    pt = 1.0 - dt.view(1, 1, -1) * (1.0 - torch.sigmoid(gt))
+    s = s0t
+    sts = []
+    for t in range(T):
+        s = pt[:, t] * s + (1 - pt[:, t]) * ut[:, t]
+        sts.append(s)
+    stt = torch.stack(sts, 1)
+    assert float((torch.from_numpy(u).double() - ut).abs().max()) < 1e-5
+    assert float((torch.from_numpy(p).double() - pt).abs().max()) < 1e-5
+    assert float((torch.from_numpy(st).double() - stt).abs().max()) < 1e-5
+    ((stt * torch.from_numpy(dstate).double()).sum() + (ut * torch.from_numpy(du_in).double()).sum()).backward()
+    assert float(np.abs(dq - qt.grad.numpy()).max()) < 1e-4
+    assert float(np.abs(dd - dt.grad.numpy()).max()) < 1e-4
+    assert float(np.abs(ds0 - s0t.grad.numpy()).max()) < 1e-4
