@@ -472,7 +472,8 @@ def cpu_decode_baseline(path, cfg):
 def pmc_probe():
     """A short fixed sequence for `rocprofv3 --pmc` runs: 3 scans of the
     workload, then 3 plain device copies of one 537 MB input array (the copy
-    calibrates FETCH_SIZE / WRITE_SIZE against a known byte count)."""
+    calibrates FETCH_SIZE / WRITE_SIZE against a known byte count), then 3 each
+    of the scan backward, the core forward and the core backward."""
     dev = torch.device("cuda:0")
     a, b, s0 = scan_inputs(SCAN_B, SCAN_T, SCAN_D, gated=True)
     da, db, d0 = (torch.from_numpy(x).to(dev) for x in (a, b, s0))
@@ -484,6 +485,26 @@ def pmc_probe():
     torch.cuda.synchronize()
     log(f"[pmc] scan bytes/launch {scan_bytes(SCAN_B, SCAN_T, SCAN_D)}; copy bytes/launch "
         f"read {da.numel() * 4} write {da.numel() * 4}")
+    # Then 3 scan backwards, 3 core forwards and 3 core backwards on the same
+    # shape (each kernel is named in the trace).
+    out, _ = runtime.scan(da, db, d0, gated=True)
+    dout = torch.randn_like(da)
+    for _ in range(3):
+        runtime.scan_bwd(da, db, d0, out, dout)
+    del y, out, dout
+    B, T, D = SCAN_B, SCAN_T, SCAN_D
+    g = torch.Generator(device=dev).manual_seed(9)
+    q = torch.randn(B, T, 2 * D, generator=g, device=dev) * 0.6
+    delta = 0.01 + 0.4 * torch.rand(D, generator=g, device=dev)
+    s0 = torch.randn(B, D, generator=g, device=dev) * 0.1
+    for _ in range(3):
+        fwd = runtime.core_fwd(q, delta, s0)
+    dstate, du_in = torch.randn_like(fwd[0]), torch.randn_like(fwd[0])
+    for _ in range(3):
+        runtime.core_bwd(q, delta, s0, *fwd, dstate, du_in)
+    torch.cuda.synchronize()
+    log(f"[pmc] scan_bwd bytes/launch {6 * B * T * D * 4}; core fwd {20 * B * T * D}, "
+        f"core bwd {36 * B * T * D}")
     return 0
 
 

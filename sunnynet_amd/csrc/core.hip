@@ -430,8 +430,15 @@ __global__ void k_core_ddelta(const float* __restrict__ dacc, float* __restrict_
     ddelta[d] = add_rn(ddelta[d], r);
 }
 
-constexpr int kFW = 4, kFTC = 16;       // forward ring: waves, steps per slot
-constexpr int kBW = 4, kBTC = 8;        // backward ring
+// Ring shapes (waves per workgroup, steps per slot), from a sweep on the
+// B=16, T=4096, D=2048 workload (median of 3 interleaved rounds, us per
+// launch, forward / backward): W=4 TC=16 / W=4 TC=8: 479 / 842; W=4 TC=8 /
+// W=4 TC=4: 454 / 847; W=8 TC=4 / W=8 TC=2: 456 / 831; W=16 TC=4 / W=16
+// TC=2: 463 / 835; W=16 TC=2 / W=16 TC=1: 525 / 1733. Eight waves (two per
+// SIMD) with short slots keep the most loads in flight per CU; a
+// reciprocal-based variant of the divisions measured no faster.
+constexpr int kFW = 8, kFTC = 4;        // forward ring
+constexpr int kBW = 8, kBTC = 2;        // backward ring
 
 bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 

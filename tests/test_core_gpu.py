@@ -22,8 +22,8 @@ from sunnynet_amd import _native, runtime
 pytestmark = pytest.mark.gpu
 
 FWD_TOL, BWD_TOL = 1e-5, 1e-4
-SHAPES = [(2, 128, 128), (3, 192, 256), (1, 512, 384), (2, 96, 128), (2, 48, 32), (2, 37, 40),
-          (4, 100, 128)]
+SHAPES = [(2, 128, 128), (3, 192, 256), (1, 512, 384), (2, 96, 128), (2, 80, 128), (2, 48, 32),
+          (2, 37, 40), (4, 100, 128)]
 
 
 def _inputs(B, T, D, seed, gate_scale=0.6):
