@@ -152,15 +152,18 @@ def dequant_i4_np(codes: np.ndarray, scale: np.ndarray, N: int, block: int) -> n
     return (q * scale[:, :, None]).reshape(rows, N).astype(np.float32)
 
 
-def pack_rwkv7_blob(w: RwkvWeights, int4: bool = False) -> bytes:
-    """The v3 blob of `w` (fp32, or INT4 group 64 where allowed)."""
+def pack_rwkv7_blob(w: RwkvWeights, int4: bool = False, ranks=None) -> bytes:
+    """The v3 blob of `w` (fp32, or INT4 group 64 where allowed). `ranks`:
+    per-layer (Rw, Ra, Rv, Rg), default cfg.ranks for every layer; the header
+    holds the largest Rg (_export_rwkv7.py:73-79)."""
     cfg = w.cfg
     L, D, HS, NH, F, V = cfg.layers, cfg.dim, cfg.head_size, cfg.n_head, cfg.ff, cfg.vocab
-    parts = [struct.pack("<10i", RK_MAGIC, RK_VERSION, L, D, HS, NH, F, cfg.ranks[3], V,
+    ranks = [tuple(cfg.ranks)] * L if ranks is None else [tuple(r) for r in ranks]
+    parts = [struct.pack("<10i", RK_MAGIC, RK_VERSION, L, D, HS, NH, F, max(r[3] for r in ranks), V,
                          1 if int4 else 0),
              struct.pack("<f", cfg.eps)]
-    for _ in range(L):
-        parts.append(struct.pack("<4i", *cfg.ranks))
+    for r in ranks:
+        parts.append(struct.pack("<4i", *r))
 
     def vecs(a):
         parts.append(struct.pack("<i", 0))
