@@ -58,6 +58,10 @@ int snhip_rk_ready(const SnHipRwkv7* m);
 /* ---- extensions ---------------------------------------------------------- */
 snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream);
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m);
+/* Workgroups of the one-launch-per-step kernel that runs steps of a single
+ * sequence (0 when that path is off: SNHIP_RK_PERSIST=0, no cooperative
+ * launch, or a shape it does not take). No reference counterpart. */
+int32_t snhip_rk_persist_grid(const SnHipRwkv7* m);
 /* One step of sequences [0, B): tokens_dev (B) int32, logits_dev (B, vocab). */
 snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
                                      float* logits_dev);

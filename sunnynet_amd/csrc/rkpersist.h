@@ -1,0 +1,62 @@
+// RWKV-7 decode at one sequence as one cooperative launch per step
+// (rkpersist.hip): the shared types between the handle (rwkv.hip) and the
+// kernel.
+#pragma once
+
+#include "common.h"
+
+namespace snhip {
+
+// A weight matrix, row-major (M, K): fp32 w (block 0) or INT4 q + sc with
+// group `block` (32 or 64).
+struct RkPMat {
+    const float* w;
+    const uint8_t* q;
+    const float* sc;
+    int M, K, block;
+};
+
+struct RkPLayer {
+    RkPMat r, k, v, w1, a1, g1, v1, w2, a2, g2, v2, o, cmk, cmv;
+    const float *ln1w, *ln1b, *ln2w, *ln2b, *lerp, *w0, *a0, *v0, *kk, *ka, *rk, *lnxw, *lnxb, *cmk_lerp;
+};
+
+struct RkPArgs {
+    const RkPLayer* layers;   // device array of L entries
+    int L, D, F, NH, vocab;
+    float eps;
+    const float *embed, *en_w, *en_b, *on_w, *on_b;
+    RkPMat head;
+    float* S;                 // (L, NH, 64, 64)
+    float* shift;             // (L, 2, D)
+    float* vfirst;            // (D)
+    float* xch;               // per-layer exchange slabs, rkp_slab(D, F) floats each
+    float* logits;            // (vocab)
+    unsigned long long* keys; // (grid) argmax keys
+    int32_t* tok;             // the step's input token (and, greedy, the next one)
+    int32_t* tok_hist;
+    int32_t* counter;
+    int hist_cap, greedy;
+    unsigned long long* bar;  // kRkPBarWords words, zero at the first launch of a call
+    unsigned gen0;            // barriers passed by earlier launches of the call
+    unsigned* err;
+    unsigned spin_limit;
+};
+
+constexpr int kRkPMaxD = 1024, kRkPMaxF = 4096, kRkPRank = 256, kRkPBarWords = 512;
+
+// Floats of one layer's exchange slab: r, k, v, y, x after the time mix,
+// x after the channel mix (D each), the four LoRA middles (256 each), ck (F).
+__host__ __device__ inline size_t rkp_slab(int D, int F) { return (size_t)6 * D + 4 * kRkPRank + F; }
+
+// Grid barriers one launch passes: five per layer, one more before the
+// greedy token reduction.
+inline unsigned rkp_barriers(int L, bool greedy) { return 5u * (unsigned)L + (greedy ? 1u : 0u); }
+
+bool rkp_shape_ok(int D, int F, int HS, int NH, const int (*ranks)[4], int L);
+// Workgroups of the launch (a multiple of 8, one per CU), or 0 when the
+// device cannot run it.
+int rkp_grid(int NH);
+snhip_status launch_rk_persist(const RkPArgs& a, int G, hipStream_t st);
+
+}  // namespace snhip

@@ -33,6 +33,7 @@
 #include "common.h"
 #include "gemm.h"
 #include "gemv.h"
+#include "rkpersist.h"
 #include "snhip.h"
 #include "snhip_rwkv7.h"
 
@@ -430,6 +431,13 @@ struct SnHipRwkv7 {
     size_t gemm_work_floats = 0;
     unsigned* gemm_cnt = nullptr;      // skinny-GEMM tile counters (zero between launches)
     int gemm_ncnt = 0;
+    // One-sequence steps as one cooperative launch each (rkpersist.hip);
+    // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
+    int p_grid = 0;
+    snhip::RkPArgs p_args{};
+    unsigned long long* p_bar = nullptr;
+    unsigned* p_err = nullptr;
+    unsigned p_spin = 1u << 22;
     int ready = 0;
 };
 
@@ -532,6 +540,77 @@ bool take_mat(SnHipRwkv7* m, Cur& c, RMat& M, int in, int out, float* tmp0, floa
         return false;
     }
     return hipDeviceSynchronize() == hipSuccess;
+}
+
+RkPMat pmat(const RMat& M) { return RkPMat{M.w, M.q, M.sc, M.M, M.Kd, M.q ? M.block : 0}; }
+
+// The one-sequence persistent step (rkpersist.hip), when the device and the
+// shape allow it: its layer table, exchange slabs, barrier words and keys.
+void setup_rk_persist(SnHipRwkv7* m) {
+    if (const char* e = getenv("SNHIP_RK_PERSIST"))
+        if (e[0] == '0') return;
+    if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->p_spin = (unsigned)std::max(1, atoi(e));
+    std::vector<int> rk(4 * (size_t)m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const RkLayer& A = m->layers[l];
+        rk[4 * l] = A.Rw; rk[4 * l + 1] = A.Ra; rk[4 * l + 2] = A.Rv; rk[4 * l + 3] = A.Rg;
+    }
+    if (!rkp_shape_ok(m->D, m->F, m->HS, m->NH, reinterpret_cast<const int(*)[4]>(rk.data()), m->L)) return;
+    const int G = rkp_grid(m->NH);
+    if (G == 0) return;
+    std::vector<RkPLayer> tab(m->L);
+    for (int l = 0; l < m->L; ++l) {
+        const RkLayer& A = m->layers[l];
+        RkPLayer& P = tab[l];
+        P.r = pmat(A.r); P.k = pmat(A.k); P.v = pmat(A.v); P.w1 = pmat(A.w1); P.a1 = pmat(A.a1);
+        P.g1 = pmat(A.g1); P.v1 = pmat(A.v1); P.w2 = pmat(A.w2); P.a2 = pmat(A.a2); P.g2 = pmat(A.g2);
+        P.v2 = pmat(A.v2); P.o = pmat(A.o); P.cmk = pmat(A.cmk); P.cmv = pmat(A.cmv);
+        P.ln1w = A.ln1w; P.ln1b = A.ln1b; P.ln2w = A.ln2w; P.ln2b = A.ln2b; P.lerp = A.lerp; P.w0 = A.w0;
+        P.a0 = A.a0; P.v0 = A.v0; P.kk = A.kk; P.ka = A.ka; P.rk = A.rk; P.lnxw = A.lnxw; P.lnxb = A.lnxb;
+        P.cmk_lerp = A.cmk_lerp;
+    }
+    RkPLayer* dtab = ralloc<RkPLayer>(m, tab.size());
+    float* xch = ralloc<float>(m, (size_t)m->L * rkp_slab(m->D, m->F));
+    unsigned long long* keys = ralloc<unsigned long long>(m, G);
+    m->p_bar = ralloc<unsigned long long>(m, kRkPBarWords);
+    m->p_err = ralloc<unsigned>(m, 1);
+    if (!dtab || !xch || !keys || !m->p_bar || !m->p_err ||
+        hipMemcpy(dtab, tab.data(), tab.size() * sizeof(RkPLayer), hipMemcpyHostToDevice) != hipSuccess)
+        return;
+    RkPArgs& a = m->p_args;
+    a.layers = dtab; a.L = m->L; a.D = m->D; a.F = m->F; a.NH = m->NH; a.vocab = m->vocab; a.eps = m->eps;
+    a.embed = m->embed; a.en_w = m->en_w; a.en_b = m->en_b; a.on_w = m->on_w; a.on_b = m->on_b;
+    a.head = pmat(m->head);
+    a.S = m->S; a.shift = m->shift; a.vfirst = m->vfirst; a.xch = xch; a.keys = keys;
+    a.tok = m->tok; a.counter = m->counter;
+    a.bar = m->p_bar; a.err = m->p_err; a.spin_limit = m->p_spin;
+    m->p_grid = G;
+}
+
+// reps persistent steps of sequence 0; the call waits for them and reports a
+// barrier time-out as an error.
+snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps) {
+    RkPArgs a = m->p_args;
+    a.logits = logits_out;
+    a.greedy = greedy ? 1 : 0;
+    a.tok_hist = m->tok_hist;
+    a.hist_cap = m->hist_cap;
+    SNHIP_CHECK(hipMemsetAsync(m->p_bar, 0, kRkPBarWords * sizeof(unsigned long long), m->work));
+    SNHIP_CHECK(hipMemsetAsync(m->p_err, 0, sizeof(unsigned), m->work));
+    const unsigned per = rkp_barriers(m->L, greedy);
+    for (int i = 0; i < reps; ++i) {
+        a.gen0 = per * (unsigned)i;
+        const snhip_status rc = launch_rk_persist(a, m->p_grid, m->work);
+        if (rc != SNHIP_OK) return rc;
+    }
+    unsigned err = 0;
+    SNHIP_CHECK(hipMemcpyAsync(&err, m->p_err, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
+    SNHIP_CHECK(hipStreamSynchronize(m->work));
+    if (err) {
+        set_last_error("RWKV-7 persistent step: a grid barrier timed out");
+        return SNHIP_E_DEVICE;
+    }
+    return SNHIP_OK;
 }
 
 SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
@@ -682,6 +761,7 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
     }
     if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
     if (const char* e = getenv("SNHIP_GEMM_MIN_BATCH")) m->gemm_min_batch = std::max(1, atoi(e));
+    setup_rk_persist(m);
     m->ready = 1;
     return m;
 }
@@ -835,7 +915,10 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
 snhip_status run_steps(SnHipRwkv7* m, int B, float* logits_out, bool greedy, int reps) {
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
     SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
-    if (!m->use_graphs) {
+    if (B == 1 && m->p_grid > 0) {
+        const snhip_status rc = run_persist(m, logits_out, greedy, reps);
+        if (rc != SNHIP_OK) return rc;
+    } else if (!m->use_graphs) {
         for (int i = 0; i < reps; ++i) {
             const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
             if (rc != SNHIP_OK) return rc;
@@ -950,6 +1033,8 @@ snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream) {
 }
 
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m) { return m ? m->max_batch : 0; }
+
+int32_t snhip_rk_persist_grid(const SnHipRwkv7* m) { return m ? m->p_grid : 0; }
 
 snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
                                      float* logits_dev) {

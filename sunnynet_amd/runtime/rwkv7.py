@@ -48,6 +48,12 @@ class HipRwkv7:
         self._logits = (ctypes.c_float * self.vocab)()
         self._bind_stream()
 
+    @property
+    def persist_grid(self) -> int:
+        """Workgroups of the one-launch-per-step path for single-sequence steps
+        (0 when off)."""
+        return int(self._lib.snhip_rk_persist_grid(self._h))
+
     def _bind_stream(self):
         _native.check(self._lib.snhip_rk_set_stream(self._h, _native.stream_handle(self.device)),
                       "snhip_rk_set_stream")

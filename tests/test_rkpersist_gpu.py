@@ -1,0 +1,112 @@
+"""The one-launch-per-step RWKV-7 path for a single sequence (rkpersist.hip)
+against the oracle and against the per-kernel (graph) path.
+
+Bar as for every RWKV-7 decode path: logits within 2e-5 absolute of the C
+oracle (bit-identical to the reference's sn_rk_step on fp32 blobs), the same
+argmax on every step, states within the tolerances of tests/test_rwkv7_gpu.py.
+The per-kernel path (SNHIP_RK_PERSIST=0) is a second witness. Covers fp32,
+the INT4 blob as stored (group 64, the 32-input V_2 kept fp32) and INT4 group
+32 quantized at load, the 12-layer 65536-vocab configuration, and greedy
+decoding.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from sunnynet_amd.runtime.rwkv7 import HipRwkv7
+from sunnynet_amd.rwkv7 import RWKV_CFG4, RWKV_TINY, init_rwkv7, pack_rwkv7_blob
+from tests.test_rwkv7_gpu import TOL, dequant_weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    w = init_rwkv7(RWKV_TINY, 7)
+    d = tmp_path_factory.mktemp("rkp")
+    p32 = d / "tiny.bin"
+    p32.write_bytes(pack_rwkv7_blob(w))
+    p4 = d / "tiny_q4.bin"
+    p4.write_bytes(pack_rwkv7_blob(w, int4=True))
+    return w, p32, p4
+
+
+def _pair(path, monkeypatch, **kw):
+    hp = HipRwkv7(path, **kw)
+    monkeypatch.setenv("SNHIP_RK_PERSIST", "0")
+    hg = HipRwkv7(path, **kw)
+    monkeypatch.delenv("SNHIP_RK_PERSIST")
+    assert hp.persist_grid > 0 and hg.persist_grid == 0
+    return hp, hg
+
+
+@pytest.mark.parametrize("fmt", ["fp32", "int4_blob", "int4_g32"])
+def test_persist_matches_oracle_and_graph_path(gpu, tiny, monkeypatch, fmt):
+    w, p32, p4 = tiny
+    print(f"rwkv7 persistent B=1 tiny {fmt}", flush=True)
+    if fmt == "fp32":
+        hp, hg = _pair(p32, monkeypatch)
+        orc = oracle.RkOracle(p32.read_bytes())
+    elif fmt == "int4_blob":
+        hp, hg = _pair(p4, monkeypatch)
+        orc = oracle.RkOracle(p4.read_bytes())
+    else:
+        hp, hg = _pair(p32, monkeypatch, weights="int4", block=32)
+        orc = oracle.RkOracle(pack_rwkv7_blob(dequant_weights(w, 32)))
+    for t in np.random.default_rng(11).integers(0, RWKV_TINY.vocab, 24):
+        a = np.asarray(hp.step(int(t)), np.float32)
+        g = np.asarray(hg.step(int(t)), np.float32)
+        b = orc.step([t])[0]
+        assert np.abs(a - b).max() < TOL and np.abs(a - g).max() < TOL
+        assert a.argmax() == b.argmax() == g.argmax()
+    S, sh = hp.get_state(1)
+    So, sho = orc.get_state()
+    assert np.abs(S.cpu().numpy() - So).max() < 1e-4 and np.abs(sh.cpu().numpy() - sho).max() < 1e-5
+
+
+def test_persist_greedy_matches_oracle_chain(gpu, tiny):
+    w, p32, _ = tiny
+    n = 20
+    print(f"rwkv7 persistent greedy tiny n={n}", flush=True)
+    hm = HipRwkv7(p32)
+    assert hm.persist_grid > 0
+    orc = oracle.RkOracle(p32.read_bytes())
+    lg = torch.empty(1, RWKV_TINY.vocab, device="cuda")
+    start = np.array([42], np.int32)
+    out = hm.decode_greedy(torch.from_numpy(start).cuda(), n, logits=lg).cpu().numpy()
+    cur = start
+    for i in range(n):
+        ref = orc.step(cur)
+        nxt = ref.argmax(1).astype(np.int32)
+        assert np.array_equal(out[i], nxt), i
+        cur = nxt
+    assert np.abs(lg.cpu().numpy() - ref).max() < TOL
+    # A second call continues from the state the first one left.
+    out2 = hm.decode_greedy(torch.from_numpy(cur).cuda(), 4).cpu().numpy()
+    for i in range(4):
+        nxt = orc.step(cur).argmax(1).astype(np.int32)
+        assert np.array_equal(out2[i], nxt), i
+        cur = nxt
+
+
+def test_persist_cfg4_int4(gpu, tmp_path_factory, monkeypatch):
+    """12 layers, D=768, 12 heads, F=3072, vocab 65536, INT4 g32 at load."""
+    cfg = RWKV_CFG4
+    print("rwkv7 cfg4 persistent: generating weights", flush=True)
+    w = init_rwkv7(cfg, 2)
+    p = tmp_path_factory.mktemp("rkp4") / "cfg4.bin"
+    p.write_bytes(pack_rwkv7_blob(w))
+    orc = oracle.RkOracle(pack_rwkv7_blob(dequant_weights(w, 32)))
+    hp, hg = _pair(p, monkeypatch, weights="int4", block=32)
+    print("rwkv7 cfg4 persistent: stepping", flush=True)
+    for t in np.random.default_rng(5).integers(0, cfg.vocab, 4):
+        a = np.asarray(hp.step(int(t)), np.float32)
+        g = np.asarray(hg.step(int(t)), np.float32)
+        b = orc.step([t])[0]
+        print("worst |dlogit| persist", float(np.abs(a - b).max()), "graph", float(np.abs(g - b).max()),
+              flush=True)
+        assert np.abs(a - b).max() < TOL and np.abs(a - g).max() < TOL
+        assert a.argmax() == b.argmax() == g.argmax()
