@@ -632,7 +632,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             }
         };
         if (A.head.block == 0) head_rows(std::false_type{}, std::integral_constant<int, 4>{});
-        else head_rows(std::true_type{}, std::integral_constant<int, 8>{});
+        else head_rows(std::true_type{}, std::integral_constant<int, 16>{});
         if (lane == 0) kred[wv] = best;
         __syncthreads();
         if (tid == 0) {
