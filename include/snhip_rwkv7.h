@@ -60,7 +60,9 @@ snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream);
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m);
 /* Workgroups of the one-launch-per-step kernel that runs steps of a single
  * sequence (0 when that path is off: SNHIP_RK_PERSIST=0, no cooperative
- * launch, or a shape it does not take). No reference counterpart. */
+ * launch, or a shape it does not take). Calls that take it (B = 1) return
+ * once their steps have finished, so that a grid-barrier time-out is
+ * reported as SNHIP_E_DEVICE. No reference counterpart. */
 int32_t snhip_rk_persist_grid(const SnHipRwkv7* m);
 /* One step of sequences [0, B): tokens_dev (B) int32, logits_dev (B, vocab). */
 snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
