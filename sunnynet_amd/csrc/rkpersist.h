@@ -41,6 +41,7 @@ struct RkPArgs {
     unsigned gen0;            // barriers passed by earlier launches of the call
     unsigned* err;
     unsigned spin_limit;
+    unsigned stall;           // added to every wait target: tests force time-outs with it
 };
 
 constexpr int kRkPMaxD = 1024, kRkPMaxF = 4096, kRkPRank = 256, kRkPBarWords = 512;

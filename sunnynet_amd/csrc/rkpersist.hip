@@ -276,13 +276,14 @@ __device__ __forceinline__ void bar_arrive(u64* bar, unsigned& gen, int wg, int 
     }
 }
 
-__device__ __forceinline__ bool bar_wait(u64* bar, unsigned* err, unsigned limit, unsigned gen, int* slast,
-                                         int* sdead) {
+__device__ __forceinline__ bool bar_wait(u64* bar, unsigned* err, unsigned limit, unsigned stall, unsigned gen,
+                                         int* slast, int* sdead) {
     if (threadIdx.x == 0) {
         int dead = 0;
         if (!*slast) {
             unsigned n = 0;
-            while (__hip_atomic_load(bar + 32 * 9, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (u64)gen) {
+            while (__hip_atomic_load(bar + 32 * 9, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                   (u64)gen + stall) {
                 if (++n > limit) {
                     __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     dead = 1;
@@ -442,7 +443,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             pvf = __hip_atomic_load(A.vfirst + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         issued();
-        if (bar_wait(A.bar, A.err, A.spin_limit, gen, &slast, &sdead)) return;
+        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
         RKP_MARK(l * 6 + 1, 0);
 
         // ---- P2: head h = wg (rwkv7.c:143-189, 229-299)
@@ -530,7 +531,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         }
         RKP_MARK(l * 6 + 1, 1);
         bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, gen, &slast, &sdead)) return;
+        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
         RKP_MARK(l * 6 + 2, 0);
 
         // ---- P3: x_a = x + W_o y (:290-292)
@@ -546,7 +547,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         }
         RKP_MARK(l * 6 + 2, 1);
         bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, gen, &slast, &sdead)) return;
+        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
         RKP_MARK(l * 6 + 3, 0);
 
         // ---- P4: xn2 = LN_2(x_a); xk2 = xn2 + cmk_lerp (shift_1 - xn2); ck = relu(W_ck xk2)^2
@@ -584,7 +585,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         }
         RKP_MARK(l * 6 + 3, 1);
         bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, gen, &slast, &sdead)) return;
+        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
         RKP_MARK(l * 6 + 4, 0);
 
         // ---- P5: x_b = x_a + W_cv ck; shift_1 <- xn2 (:305-315)
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         }
         RKP_MARK(l * 6 + 4, 1);
         bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, gen, &slast, &sdead)) return;
+        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
     }
     RKP_MARK(64 * 6, 0);
 
@@ -644,7 +645,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     RKP_MARK(64 * 6, 1);
     if (!A.greedy) return;
     bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, gen, &slast, &sdead)) return;
+        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
     RKP_MARK(64 * 6 + 1, 0);
     if (wg == 0) {
         u64 b = 0ull;

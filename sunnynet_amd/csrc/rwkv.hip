@@ -550,6 +550,8 @@ void setup_rk_persist(SnHipRwkv7* m) {
     if (const char* e = getenv("SNHIP_RK_PERSIST"))
         if (e[0] == '0') return;
     if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->p_spin = (unsigned)std::max(1, atoi(e));
+    unsigned stall = 0;
+    if (const char* e = getenv("SNHIP_PERSIST_STALL")) stall = (unsigned)std::max(0, atoi(e));
     std::vector<int> rk(4 * (size_t)m->L);
     for (int l = 0; l < m->L; ++l) {
         const RkLayer& A = m->layers[l];
@@ -583,7 +585,7 @@ void setup_rk_persist(SnHipRwkv7* m) {
     a.head = pmat(m->head);
     a.S = m->S; a.shift = m->shift; a.vfirst = m->vfirst; a.xch = xch; a.keys = keys;
     a.tok = m->tok; a.counter = m->counter;
-    a.bar = m->p_bar; a.err = m->p_err; a.spin_limit = m->p_spin;
+    a.bar = m->p_bar; a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = stall;
     m->p_grid = G;
 }
 

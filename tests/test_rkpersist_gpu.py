@@ -110,3 +110,23 @@ def test_persist_cfg4_int4(gpu, tmp_path_factory, monkeypatch):
               flush=True)
         assert np.abs(a - b).max() < TOL and np.abs(a - g).max() < TOL
         assert a.argmax() == b.argmax() == g.argmax()
+
+
+def test_persist_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
+    """Every barrier wait is given a target the host raised out of reach: each
+    workgroup gives up after its poll limit and leaves the kernel, the call
+    reports an error, and a handle loaded normally afterwards is correct."""
+    w, p32, _ = tiny
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
+    hm = HipRwkv7(p32)
+    assert hm.persist_grid > 0
+    tok = torch.tensor([3], dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.step_batch(tok)
+    monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
+    h2 = HipRwkv7(p32)
+    orc = oracle.RkOracle(p32.read_bytes())
+    a = np.asarray(h2.step(3), np.float32)
+    assert np.abs(a - orc.step([3])[0]).max() < TOL
