@@ -86,8 +86,8 @@ def test_core_matches_float64_closed_form(gpu):
             sts.append(s)
         stt = torch.stack(sts, 1)
         ((stt * torch.from_numpy(dstate).double()).sum() + (ut * torch.from_numpy(du_in).double()).sum()).backward()
-        assert float((u.detach().cpu().double() - ut).abs().max()) < FWD_TOL
-        assert float((st.detach().cpu().double() - stt).abs().max()) < FWD_TOL
+        assert float((u.detach().cpu().double() - ut.detach()).abs().max()) < FWD_TOL
+        assert float((st.detach().cpu().double() - stt.detach()).abs().max()) < FWD_TOL
         assert float((qd.grad.cpu().double() - qt.grad).abs().max()) < BWD_TOL
         assert float((dd.grad.cpu().double() - dt.grad).abs().max()) < BWD_TOL
         assert float((sd.grad.cpu().double() - s0t.grad).abs().max()) < BWD_TOL
