@@ -184,3 +184,34 @@ def test_rwkv7_ragged_ranks_run_on_the_reference_runtime(tmp_path):
     orc = oracle.RkOracle(blob)
     for t in (3, 77, 400, 9):
         assert np.array_equal(ref.step(t), orc.step([t])[0])
+
+
+def test_reader_rejects_malformed_files(tmp_path):
+    """Wrong magic, an unsupported version, a misaligned tensor offset and
+    tensor data past the end of the file are refused, not read."""
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"GGUX" + struct.pack("<IQQ", 3, 0, 0))
+    with pytest.raises(ValueError, match="not a GGUF"):
+        GGUFFile(bad)
+    bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 9, 0, 0))
+    with pytest.raises(ValueError, match="version"):
+        GGUFFile(bad)
+    head = b"GGUF" + struct.pack("<IQQ", 3, 1, 0) + _s("t") + struct.pack("<IQIQ", 1, 8, 0, 4)
+    bad.write_bytes(head + b"\0" * ((-len(head)) % 32) + b"\0" * 64)
+    with pytest.raises(ValueError, match="not aligned"):
+        GGUFFile(bad)
+    head = b"GGUF" + struct.pack("<IQQ", 3, 1, 0) + _s("t") + struct.pack("<IQIQ", 1, 1000, 0, 0)
+    bad.write_bytes(head + b"\0" * ((-len(head)) % 32) + b"\0" * 64)
+    with pytest.raises(ValueError, match="past the end"):
+        GGUFFile(bad)
+
+
+def test_converter_cli_writes_the_blob(tmp_path):
+    from sunnynet_amd.gguf import main
+    w = init_rwkv7(RWKV_TINY, 8)
+    src = _rwkv_gguf(tmp_path, w, "cli.gguf")
+    dst = tmp_path / "cli.bin"
+    assert main([str(src), str(dst), "--f32"]) == 0
+    assert dst.read_bytes() == pack_rwkv7_blob(w)
+    assert main([str(src), str(dst)]) == 0
+    assert dst.read_bytes() == pack_rwkv7_blob(w, int4=True)
