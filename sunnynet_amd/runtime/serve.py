@@ -9,6 +9,9 @@ it unchanged. Each request's state is a pair of device tensors; the handle
 holds one of them at a time and swaps states in and out only when another
 request steps, so a single stream costs one step per token.
 
+``HipRwkvEngine`` does the same for RWKV-7 (the reference's C-runtime RWKV-7
+engine, ``serve.py:177-207``).
+
 ``BatchScheduler`` serves many requests on one ``max_batch`` handle. Every
 iteration each active request consumes one input token (the next prompt token
 while it is prefilling, as ``sn_prefill`` steps through a prompt,
@@ -30,7 +33,8 @@ import torch
 
 from .model import HipModel
 
-__all__ = ["HipEngine", "HipState", "BatchScheduler", "Request", "sample_logits"]
+__all__ = ["HipEngine", "HipState", "HipRwkvEngine", "HipRwkvState", "BatchScheduler", "Request",
+           "sample_logits"]
 
 
 def sample_logits(logits, temperature=1.0, top_p=1.0, top_k=0, rng=None) -> int:
@@ -126,6 +130,71 @@ class HipEngine:
             s, h = self.model.get_state(1)
             state.s.copy_(s)
             state.hist.copy_(h)
+
+
+class HipRwkvState:
+    """One request's RWKV-7 state on the device: S (1, L, H, 64, 64) and the
+    two token-shift vectors (1, L, 2, D)."""
+
+    def __init__(self, S: torch.Tensor, shift: torch.Tensor):
+        self.S, self.shift = S, shift
+
+
+class HipRwkvEngine:
+    """The reference's RWKV-7 engine over its C runtime (sunnynet/serve.py:
+    177-207, GGUFCEngine: one handle, step(token) then logits) on the HIP
+    backend, with each request's state kept on the device and swapped in when
+    another request steps, as HipEngine does."""
+
+    name = "rwkv7-hip"
+
+    def __init__(self, blob, vocab=None, *, tokenizer=None, eos=None, weights="stored", block=32,
+                 device=None):
+        from .rwkv7 import HipRwkv7
+        self.model = HipRwkv7(blob, vocab, weights=weights, block=block, device=device)
+        self.vocab = self.model.vocab
+        self.eos = eos
+        self.tk = tokenizer
+        self._live = None
+        self._tok = torch.empty(1, dtype=torch.int32, device=self.model.device)
+
+    def encode(self, text: str) -> list[int]:
+        if self.tk is None:
+            raise RuntimeError("no tokenizer given")
+        return list(self.tk.encode(text))
+
+    def decode(self, ids) -> str:
+        if self.tk is None:
+            raise RuntimeError("no tokenizer given")
+        return self.tk.decode([int(i) for i in ids])
+
+    def init_state(self) -> HipRwkvState:
+        m = self.model
+        return HipRwkvState(torch.zeros(1, m.layers, m.n_head, m.head_size, m.head_size, device=m.device),
+                            torch.zeros(1, m.layers, 2, m.dim, device=m.device))
+
+    def _swap_in(self, state: HipRwkvState):
+        if self._live is state:
+            return
+        if self._live is not None:
+            S, sh = self.model.get_state(1)
+            self._live.S.copy_(S)
+            self._live.shift.copy_(sh)
+        self.model.set_state(state.S, state.shift)
+        self._live = state
+
+    def step(self, token: int, state: HipRwkvState):
+        """-> (logits (V,) float32 numpy, state), the state updated lazily."""
+        self._swap_in(state)
+        self._tok.fill_(int(token))
+        logits = self.model.step_batch(self._tok)
+        return logits[0].float().cpu().numpy(), state
+
+    def sync_state(self, state: HipRwkvState):
+        if self._live is state:
+            S, sh = self.model.get_state(1)
+            state.S.copy_(S)
+            state.shift.copy_(sh)
 
 
 @dataclass

@@ -108,3 +108,28 @@ def test_engine_protocol_interleaved_requests(gpu, small):
     eng.sync_state(sb)
     so, ho = ob.get_state()
     assert np.abs(sb.s.cpu().numpy() - so).max() < 1e-5
+
+
+@pytest.mark.gpu
+def test_rwkv_engine_interleaved_requests(gpu, tmp_path):
+    """Two RWKV-7 requests stepped alternately through one HipRwkvEngine give
+    each request's solo logits (oracle, one handle per request)."""
+    from sunnynet_amd.runtime.serve import HipRwkvEngine
+    from sunnynet_amd.rwkv7 import RWKV_TINY, init_rwkv7, pack_rwkv7_blob
+    blob = pack_rwkv7_blob(init_rwkv7(RWKV_TINY, 9))
+    path = tmp_path / "rk.bin"
+    path.write_bytes(blob)
+    eng = HipRwkvEngine(path, RWKV_TINY.vocab)
+    oa, ob = oracle.RkOracle(blob), oracle.RkOracle(blob)
+    sa, sb = eng.init_state(), eng.init_state()
+    rng = np.random.default_rng(10)
+    ta = rng.integers(0, RWKV_TINY.vocab, 12)
+    tb = rng.integers(0, RWKV_TINY.vocab, 12)
+    for i in range(12):
+        la, sa = eng.step(int(ta[i]), sa)
+        lb, sb = eng.step(int(tb[i]), sb)
+        assert np.abs(la - oa.step([ta[i]])[0]).max() < TOL
+        assert np.abs(lb - ob.step([tb[i]])[0]).max() < TOL
+    eng.sync_state(sb)
+    S, sh = ob.get_state()
+    assert np.abs(sb.S.cpu().numpy() - S).max() < 1e-4 and np.abs(sb.shift.cpu().numpy() - sh).max() < 1e-5
