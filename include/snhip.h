@@ -72,7 +72,27 @@ void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits);
 int snhip_vocab(const SnHipModel* m);
 int snhip_ready(const SnHipModel* m);
 
+/* sunnynet.h:42-47. n <= 0 keeps the current setting. The decode products run
+ * on the GPU; the count sizes host-side work (blob preparation at load) and is
+ * the same setting as snhip_abi_set_threads / snhip_abi_get_threads.
+ * snhip_recommended_threads: physical cores ((physical id, core id) pairs of
+ * /proc/cpuinfo), the logical count if none are listed, 0 if unreadable. */
+void snhip_set_threads(int n);
+int snhip_get_threads(void);
+int snhip_recommended_threads(void);
+
 /* ---- extensions ---------------------------------------------------------- */
+/* snhip_prefill with a status: SNHIP_E_INVAL for out-of-range tokens or bad
+ * arguments, SNHIP_E_DEVICE for a HIP failure or a refused handle (below). */
+snhip_status snhip_prefill_host(SnHipModel* m, const int32_t* tokens, int32_t n, float* logits);
+
+/* Time-outs. Every wait of the persistent kernels is bounded; a call whose
+ * launch timed out returns SNHIP_E_DEVICE once its work has finished (calls
+ * that run a persistent kernel wait for it). A single-sequence call leaves the
+ * state as it was. A batched step may have written some layers' state: the
+ * handle then refuses every stepping call (SNHIP_E_DEVICE) until snhip_reset or
+ * snhip_set_state_dev gives it a valid state. */
+
 /* Stream for all later work of this handle (NULL = the null stream). */
 snhip_status snhip_set_stream(SnHipModel* m, void* stream);
 int32_t snhip_max_batch(const SnHipModel* m);
@@ -96,7 +116,8 @@ snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, i
 /* Greedy decoding on the device: feeds tokens_dev (B), then repeatedly takes
  * the first maximal logit as the next token, for n_steps steps. out_tokens_dev
  * (n_steps, B) receives the tokens chosen after each step; logits_dev (B,
- * vocab), if not NULL, the last step's logits. No host synchronization. */
+ * vocab), if not NULL, the last step's logits. No host synchronization, except
+ * that a call running a persistent kernel waits for it (Time-outs above). */
 snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                      int32_t n_steps, int32_t* out_tokens_dev,
                                      float* logits_dev);

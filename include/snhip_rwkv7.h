@@ -56,6 +56,11 @@ int snhip_rk_vocab(const SnHipRwkv7* m);
 int snhip_rk_ready(const SnHipRwkv7* m);
 
 /* ---- extensions ---------------------------------------------------------- */
+/* Time-outs: the single-sequence persistent step updates S and shift in place
+ * layer by layer; a call whose launch timed out returns SNHIP_E_DEVICE and the
+ * handle refuses every stepping call (SNHIP_E_DEVICE) until snhip_rk_reset or
+ * snhip_rk_set_state_dev. The void mirrors drop the status: use
+ * snhip_abi_rwkv7_step / snhip_abi_rwkv7_prefill to see it. */
 snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream);
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m);
 /* Workgroups of the one-launch-per-step kernel that runs steps of a single

@@ -74,8 +74,12 @@ _SIGS = {
     "snhip_reset": (None, [V]),
     "snhip_step": (None, [V, INT, V]),
     "snhip_prefill": (None, [V, V, INT, V]),
+    "snhip_prefill_host": (I32, [V, V, I32, V]),
     "snhip_vocab": (INT, [V]),
     "snhip_ready": (INT, [V]),
+    "snhip_set_threads": (None, [INT]),
+    "snhip_get_threads": (INT, []),
+    "snhip_recommended_threads": (INT, []),
     "snhip_set_stream": (I32, [V, V]),
     "snhip_max_batch": (I32, [V]),
     "snhip_persistent_grid": (I32, [V]),
@@ -164,6 +168,35 @@ def stream_handle(device=None) -> int:
 
 def ptr(t) -> int:
     return t.data_ptr()
+
+
+# Handles still open when the interpreter exits are closed by an atexit hook,
+# which runs before module teardown (torch and its HIP runtime are still up);
+# a handle's __del__ during finalization then finds nothing left to free.
+_open_handles = None
+
+
+def track(handle_owner) -> None:
+    """Register an object with a close() method to be closed at exit."""
+    global _open_handles
+    if _open_handles is None:
+        import atexit
+        import weakref
+        _open_handles = weakref.WeakSet()
+
+        def _close_all():
+            for h in list(_open_handles):
+                try:
+                    h.close()
+                except Exception:
+                    pass
+        atexit.register(_close_all)
+    _open_handles.add(handle_owner)
+
+
+def finalizing() -> bool:
+    import sys
+    return sys.is_finalizing()
 
 
 def declared_symbols() -> list:

@@ -1,8 +1,11 @@
 // Stable C ABI of the HIP backend (include/snhip_abi.h), mirroring
 // sunnynet/runtime/sn_abi.c:17-86: same argument validation, status codes
 // and version rules; the recurrence and INT4 primitives run on the GPU.
+#include <cstdio>
 #include <cstring>
+#include <set>
 #include <thread>
+#include <utility>
 
 #include "common.h"
 
@@ -68,6 +71,39 @@ snhip_status snhip_abi_set_threads(int32_t n) {
     return SNHIP_OK;
 }
 int32_t snhip_abi_get_threads(void) { return (int32_t)host_threads(); }
+
+// sunnynet.h:42-47. The reference sizes its OpenMP GEMVs with these; here the
+// products run on the GPU and the count sizes the host-side load preparation
+// (the same setting as snhip_abi_set_threads).
+void snhip_set_threads(int n) {
+    if (n > 0) g_threads = n;
+}
+int snhip_get_threads(void) { return host_threads(); }
+
+// Physical cores: distinct (physical id, core id) pairs of /proc/cpuinfo; the
+// logical count when the file lists none; 0 when it cannot be read.
+int snhip_recommended_threads(void) {
+    FILE* f = std::fopen("/proc/cpuinfo", "r");
+    if (!f) return 0;
+    std::set<std::pair<int, int>> cores;
+    char line[512];
+    int phys = -1, core = -1;
+    auto flush = [&]() {
+        if (core >= 0) cores.emplace(phys, core);
+        phys = core = -1;
+    };
+    while (std::fgets(line, sizeof line, f)) {
+        int v;
+        if (std::sscanf(line, "physical id : %d", &v) == 1) phys = v;
+        else if (std::sscanf(line, "core id : %d", &v) == 1) core = v;
+        else if (line[0] == '\n') flush();
+    }
+    flush();
+    std::fclose(f);
+    if (!cores.empty()) return (int)cores.size();
+    const unsigned n = std::thread::hardware_concurrency();
+    return (int)n;
+}
 
 snhip_status snhip_abi_recur_step_dev(const float* a, const float* b, float* s, int32_t B,
                                       int32_t N, int32_t gated, void* stream) {

@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "snhip_abi.h"
@@ -39,6 +40,15 @@ const std::string& last_error();
     } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Unsigned value of an environment variable (at least lo), or dflt if unset.
+// Read at call time, so a test may change it between calls of one handle.
+inline unsigned env_unsigned(const char* name, unsigned dflt, unsigned lo) {
+    const char* e = getenv(name);
+    if (!e) return dflt;
+    const long v = atol(e);
+    return v < (long)lo ? lo : (unsigned)v;
+}
 
 // Waits for this wave's outstanding LDS operations only (gfx9 s_waitcnt
 // encoding: vmcnt = 63, expcnt = 7, lgkmcnt = 0); global loads stay in flight.

@@ -601,7 +601,10 @@ struct SnHipModel {
     unsigned* perr = nullptr;             // time-out flag
     unsigned* h_err = nullptr;            // pinned copies of the time-out flags: [0] perr, [1] berr
     unsigned persist_spin = 1u << 22;     // poll limit (SNHIP_PERSIST_SPIN)
-    unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests)
+    unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests), read per call
+    // A batched persistent step timed out after some layers had written their
+    // state: every stepping call fails until snhip_reset or snhip_set_state_dev.
+    int poisoned = 0;
     // Persistent batched step (batch.hip) for batches of gemm_min_batch ..
     // batch_max sequences: grid size, 0 when the shape or device does not allow it.
     int batch_wg = 0;
@@ -1078,8 +1081,7 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         free_model(m);
         return nullptr;
     }
-    if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->persist_spin = (unsigned)std::max(1, atoi(e));
-    if (const char* e = getenv("SNHIP_PERSIST_STALL")) m->persist_stall = (unsigned)std::max(0, atoi(e));
+    m->persist_spin = env_unsigned("SNHIP_PERSIST_SPIN", m->persist_spin, 1);
     setup_persist(m);
     setup_batch(m);
     m->ready = 1;
@@ -1265,6 +1267,34 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
     return enqueue_head(m, B, m->x, logits_out, greedy, st);
 }
 
+// After a synchronization: did a persistent launch time out at a barrier? A
+// batched step that timed out may have written some layers' state: the handle
+// is then refused for stepping until its state is reset or set.
+snhip_status persist_status(SnHipModel* m) {
+    if (m->h_err && m->h_err[0]) {
+        m->h_err[0] = 0;
+        set_last_error("persistent decode: exchange wait timed out");
+        return SNHIP_E_DEVICE;
+    }
+    if (m->h_err && m->h_err[1]) {
+        m->h_err[1] = 0;
+        m->poisoned = 1;
+        set_last_error("batched persistent decode: barrier wait timed out");
+        return SNHIP_E_DEVICE;
+    }
+    return SNHIP_OK;
+}
+
+// Stepping calls refuse a handle whose state a timed-out step left part-written.
+snhip_status check_usable(const SnHipModel* m) {
+    if (m->poisoned) {
+        set_last_error("the sequence state was left part-stepped by a timed-out batched step; "
+                       "call snhip_reset or snhip_set_state_dev first");
+        return SNHIP_E_DEVICE;
+    }
+    return SNHIP_OK;
+}
+
 // Runs `reps` decode steps on the internal stream, ordered after the work
 // already queued on the caller's stream and before anything queued on it
 // later. The step's kernels are captured once per (B, logits, greedy) into a
@@ -1278,6 +1308,7 @@ snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int
         // are queued directly (a cooperative launch is not captured).
         if (batch) {
             // Barrier counters restart from zero for this call's launches.
+            m->persist_stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
             SNHIP_CHECK(hipMemsetAsync(m->berr, 0, sizeof(unsigned), m->work));
             SNHIP_CHECK(hipMemsetAsync(m->bbar, 0, kBatchBarWords * sizeof(unsigned long long), m->work));
             m->batch_gen = 0;
@@ -1286,8 +1317,14 @@ snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int
             const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
             if (rc != SNHIP_OK) return rc;
         }
-        if (batch)
+        if (batch) {
+            // The call returns once its launches have finished, so that a
+            // barrier time-out is reported by this call, not a later one.
             SNHIP_CHECK(hipMemcpyAsync(m->h_err + 1, m->berr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
+            SNHIP_CHECK(hipStreamSynchronize(m->work));
+            const snhip_status st = persist_status(m);
+            if (st != SNHIP_OK) return st;
+        }
     } else {
         const auto key = std::make_tuple(B, (const void*)logits_out, greedy ? 1 : 0);
         auto it = m->graphs.find(key);
@@ -1466,8 +1503,12 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
 // out_tok (n_steps) receives each step's argmax token, fed to the next step;
 // otherwise n_steps must be 1. logits (device), if not NULL, gets the last
 // step's logits.
+// The call returns once the launches have finished and reports an exchange
+// time-out as SNHIP_E_DEVICE (the handle's state is then unchanged: the kernel
+// writes it back only after its last step). *launch_failed is set when the
+// first cooperative launch could not be queued at all (nothing ran).
 snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_tok,
-                         float* logits) {
+                         float* logits, bool* launch_failed) {
     constexpr int kMaxStepsPerLaunch = 1 << 20;   // keeps exchange epochs far from wrapping
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
     SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
@@ -1482,7 +1523,7 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
     a.ring = m->pring; a.ex = m->pex; a.sx = m->psx; a.err = m->perr;
     a.greedy = greedy ? 1 : 0;
     a.spin_limit = m->persist_spin;
-    a.stall = m->persist_stall;
+    a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
     const int blk = m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0;
     for (int done = 0; done < n_steps;) {
         const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
@@ -1494,28 +1535,17 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
         a.logits = done + n == n_steps ? logits : nullptr;
         a.n_steps = n;
         const snhip_status rc = launch_decode_persist(a, m->persist_wg, blk, m->work);
-        if (rc != SNHIP_OK) return rc;
+        if (rc != SNHIP_OK) {
+            if (done == 0 && launch_failed) *launch_failed = true;
+            return rc;
+        }
         done += n;
     }
     SNHIP_CHECK(hipMemcpyAsync(m->h_err, m->perr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
     SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
     SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
-    return SNHIP_OK;
-}
-
-// After a synchronization: did a persistent launch time out at a barrier?
-snhip_status persist_status(SnHipModel* m) {
-    if (m->h_err && m->h_err[0]) {
-        m->h_err[0] = 0;
-        set_last_error("persistent decode: exchange wait timed out");
-        return SNHIP_E_DEVICE;
-    }
-    if (m->h_err && m->h_err[1]) {
-        m->h_err[1] = 0;
-        set_last_error("batched persistent decode: barrier wait timed out");
-        return SNHIP_E_DEVICE;
-    }
-    return SNHIP_OK;
+    SNHIP_CHECK(hipStreamSynchronize(m->work));
+    return persist_status(m);
 }
 
 // One step of sequence 0 (tokens already in m->tok): the persistent kernel
@@ -1523,8 +1553,9 @@ snhip_status persist_status(SnHipModel* m) {
 // turns the persistent path off for this handle and falls back.
 snhip_status step_one(SnHipModel* m, float* logits_out) {
     if (m->persist_wg) {
-        const snhip_status rc = run_persist(m, 1, false, nullptr, logits_out);
-        if (rc == SNHIP_OK) return rc;
+        bool launch_failed = false;
+        const snhip_status rc = run_persist(m, 1, false, nullptr, logits_out, &launch_failed);
+        if (!launch_failed) return rc;
         m->persist_wg = 0;
         (void)hipGetLastError();
     }
@@ -1565,8 +1596,10 @@ SnHipModel* snhip_load_ex(const char* path, int vocab, int dim, int inner, int r
 
 void snhip_free(SnHipModel* m) {
     if (!m) return;
-    if (m->stream) (void)hipStreamSynchronize(m->stream);
-    else (void)hipDeviceSynchronize();
+    // Only this handle's work is waited for: its internal stream and the
+    // caller's stream it was bound to (NULL = the null stream).
+    if (m->work) (void)hipStreamSynchronize(m->work);
+    (void)hipStreamSynchronize(m->stream);
     free_model(m);
 }
 
@@ -1577,6 +1610,7 @@ void snhip_reset(SnHipModel* m) {
     (void)hipMemsetAsync(m->hist, 0, B * m->L * (m->kh ? m->kh : 1) * m->D * sizeof(float),
                          m->stream);
     (void)hipStreamSynchronize(m->stream);
+    m->poisoned = 0;
 }
 
 int snhip_vocab(const SnHipModel* m) { return m ? m->vocab : 0; }
@@ -1595,6 +1629,7 @@ snhip_status snhip_set_stream(SnHipModel* m, void* stream) {
 snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                   float* logits_dev) {
     if (!m || !tokens_dev || !logits_dev || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     const snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
     if (rc != SNHIP_OK) return rc;
     return B == 1 ? step_one(m, logits_dev) : run_steps(m, B, logits_dev, false, 1);
@@ -1603,13 +1638,14 @@ snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int3
 snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits) {
     if (!m || !tokens || !logits || B <= 0 || B > m->max_batch) return SNHIP_E_INVAL;
     if (!tokens_ok(m, tokens, B)) return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     snhip_status rc = put_tokens(m, tokens, B, hipMemcpyHostToDevice);
     if (rc == SNHIP_OK) rc = B == 1 ? step_one(m, m->logits) : run_steps(m, B, m->logits, false, 1);
     if (rc != SNHIP_OK) return rc;
     SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)B * m->vocab * sizeof(float),
                                hipMemcpyDeviceToHost, m->stream));
     SNHIP_CHECK(hipStreamSynchronize(m->stream));
-    return persist_status(m);
+    return SNHIP_OK;
 }
 
 void snhip_step(SnHipModel* m, int token, float* logits) {
@@ -1618,29 +1654,43 @@ void snhip_step(SnHipModel* m, int token, float* logits) {
     (void)snhip_step_batch(m, &t, 1, logits);
 }
 
-void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits) {
-    if (!m || !tokens || n <= 0 || !logits) return;
-    if (!tokens_ok(m, tokens, n)) return;
+snhip_status snhip_prefill_host(SnHipModel* m, const int32_t* tokens, int32_t n, float* logits) {
+    if (!m || !tokens || n <= 0 || !logits) return SNHIP_E_INVAL;
+    if (!tokens_ok(m, tokens, n)) return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     int32_t* dt = nullptr;
-    if (hipMalloc(&dt, (size_t)n * sizeof(int32_t)) != hipSuccess) return;
-    bool ok = hipMemcpy(dt, tokens, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess;
-    if (ok && m->gemm_ok && m->D % 64 == 0) {
-        ok = run_prefill(m, dt, 1, n, m->logits) == SNHIP_OK;
+    SNHIP_CHECK(hipMalloc(&dt, (size_t)n * sizeof(int32_t)));
+    snhip_status rc = SNHIP_OK;
+    if (hipMemcpy(dt, tokens, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice) != hipSuccess) {
+        set_last_error("prefill: token copy failed");
+        rc = SNHIP_E_DEVICE;
+    } else if (m->gemm_ok && m->D % 64 == 0) {
+        rc = run_prefill(m, dt, 1, n, m->logits);
     } else {
-        for (int i = 0; i < n && ok; ++i)    // the reference's step loop (sunnynet.c:347-349)
-            ok = put_tokens(m, dt + i, 1, hipMemcpyDeviceToDevice) == SNHIP_OK &&
-                 run_steps(m, 1, m->logits, false, 1) == SNHIP_OK;
+        for (int i = 0; i < n && rc == SNHIP_OK; ++i) {   // the reference's step loop (sunnynet.c:347-349)
+            rc = put_tokens(m, dt + i, 1, hipMemcpyDeviceToDevice);
+            if (rc == SNHIP_OK) rc = run_steps(m, 1, m->logits, false, 1);
+        }
     }
-    if (ok)
-        (void)hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float),
-                             hipMemcpyDeviceToHost, m->stream);
+    if (rc == SNHIP_OK &&
+        hipMemcpyAsync(logits, m->logits, (size_t)m->vocab * sizeof(float), hipMemcpyDeviceToHost,
+                       m->stream) != hipSuccess) {
+        set_last_error("prefill: logits copy failed");
+        rc = SNHIP_E_DEVICE;
+    }
     (void)hipStreamSynchronize(m->stream);
     (void)hipFree(dt);
+    return rc;
+}
+
+void snhip_prefill(SnHipModel* m, const int* tokens, int n, float* logits) {
+    (void)snhip_prefill_host(m, tokens, n, logits);
 }
 
 snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                      int32_t T, float* logits_dev) {
     if (!m || !tokens_dev || B <= 0 || B > m->max_batch || T <= 0) return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     return run_prefill(m, tokens_dev, B, T, logits_dev);
 }
 
@@ -1649,10 +1699,13 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
                                      float* logits_dev) {
     if (!m || !tokens_dev || !out_tokens_dev || B <= 0 || B > m->max_batch || n_steps <= 0)
         return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     if (B == 1 && m->persist_wg) {
         snhip_status rc = put_tokens(m, tokens_dev, 1, hipMemcpyDeviceToDevice);
-        if (rc == SNHIP_OK) rc = run_persist(m, n_steps, true, out_tokens_dev, logits_dev);
-        if (rc == SNHIP_OK) return rc;
+        if (rc != SNHIP_OK) return rc;
+        bool launch_failed = false;
+        rc = run_persist(m, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
+        if (!launch_failed) return rc;
         m->persist_wg = 0;
         (void)hipGetLastError();
     }
@@ -1705,6 +1758,7 @@ snhip_status snhip_set_state_dev(SnHipModel* m, const float* s_dev, const float*
     if (m->kh)
         SNHIP_CHECK(hipMemcpyAsync(m->hist, hist_dev, (size_t)B * m->L * m->kh * m->D * sizeof(float),
                                    hipMemcpyDeviceToDevice, m->stream));
+    m->poisoned = 0;
     return SNHIP_OK;
 }
 

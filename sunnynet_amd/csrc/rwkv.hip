@@ -438,6 +438,9 @@ struct SnHipRwkv7 {
     unsigned long long* p_bar = nullptr;
     unsigned* p_err = nullptr;
     unsigned p_spin = 1u << 22;
+    // A persistent step timed out after some layers had written S and shift in
+    // place: every stepping call fails until snhip_rk_reset or set_state.
+    int poisoned = 0;
     int ready = 0;
 };
 
@@ -549,9 +552,7 @@ RkPMat pmat(const RMat& M) { return RkPMat{M.w, M.q, M.sc, M.M, M.Kd, M.q ? M.bl
 void setup_rk_persist(SnHipRwkv7* m) {
     if (const char* e = getenv("SNHIP_RK_PERSIST"))
         if (e[0] == '0') return;
-    if (const char* e = getenv("SNHIP_PERSIST_SPIN")) m->p_spin = (unsigned)std::max(1, atoi(e));
-    unsigned stall = 0;
-    if (const char* e = getenv("SNHIP_PERSIST_STALL")) stall = (unsigned)std::max(0, atoi(e));
+    m->p_spin = env_unsigned("SNHIP_PERSIST_SPIN", m->p_spin, 1);
     std::vector<int> rk(4 * (size_t)m->L);
     for (int l = 0; l < m->L; ++l) {
         const RkLayer& A = m->layers[l];
@@ -585,14 +586,17 @@ void setup_rk_persist(SnHipRwkv7* m) {
     a.head = pmat(m->head);
     a.S = m->S; a.shift = m->shift; a.vfirst = m->vfirst; a.xch = xch; a.keys = keys;
     a.tok = m->tok; a.counter = m->counter;
-    a.bar = m->p_bar; a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = stall;
+    a.bar = m->p_bar; a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = 0;
     m->p_grid = G;
 }
 
 // reps persistent steps of sequence 0; the call waits for them and reports a
-// barrier time-out as an error.
+// barrier time-out as an error. The kernel updates S and shift in place layer
+// by layer, so a time-out leaves them part-stepped: the handle is then refused
+// for stepping until its state is reset or set.
 snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps) {
     RkPArgs a = m->p_args;
+    a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
     a.logits = logits_out;
     a.greedy = greedy ? 1 : 0;
     a.tok_hist = m->tok_hist;
@@ -609,7 +613,17 @@ snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps
     SNHIP_CHECK(hipMemcpyAsync(&err, m->p_err, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
     SNHIP_CHECK(hipStreamSynchronize(m->work));
     if (err) {
+        m->poisoned = 1;
         set_last_error("RWKV-7 persistent step: a grid barrier timed out");
+        return SNHIP_E_DEVICE;
+    }
+    return SNHIP_OK;
+}
+
+snhip_status check_usable(const SnHipRwkv7* m) {
+    if (m->poisoned) {
+        set_last_error("the sequence state was left part-stepped by a timed-out step; "
+                       "call snhip_rk_reset or snhip_rk_set_state_dev first");
         return SNHIP_E_DEVICE;
     }
     return SNHIP_OK;
@@ -915,6 +929,7 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
 // reps steps on the internal stream, ordered after the caller's stream;
 // captured once per (B, logits, greedy) into a graph and replayed.
 snhip_status run_steps(SnHipRwkv7* m, int B, float* logits_out, bool greedy, int reps) {
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
     SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
     if (B == 1 && m->p_grid > 0) {
@@ -1003,8 +1018,9 @@ SnHipRwkv7* snhip_rk_load_ex(const char* path, int32_t max_batch, int32_t weight
 
 void snhip_rk_free(SnHipRwkv7* m) {
     if (!m) return;
-    if (m->stream) (void)hipStreamSynchronize(m->stream);
-    else (void)hipDeviceSynchronize();
+    // Only this handle's work is waited for (see snhip_free).
+    if (m->work) (void)hipStreamSynchronize(m->work);
+    (void)hipStreamSynchronize(m->stream);
     free_rk(m);
 }
 
@@ -1014,6 +1030,7 @@ void snhip_rk_reset(SnHipRwkv7* m) {
     (void)hipMemsetAsync(m->S, 0, B * m->L * m->NH * m->HS * m->HS * sizeof(float), m->stream);
     (void)hipMemsetAsync(m->shift, 0, B * m->L * 2 * m->D * sizeof(float), m->stream);
     (void)hipStreamSynchronize(m->stream);
+    m->poisoned = 0;
 }
 
 void snhip_rk_step(SnHipRwkv7* m, int token, float* logits) {
@@ -1095,6 +1112,7 @@ snhip_status snhip_rk_set_state_dev(SnHipRwkv7* m, const float* S_dev, const flo
                                hipMemcpyDeviceToDevice, m->stream));
     SNHIP_CHECK(hipMemcpyAsync(m->shift, shift_dev, (size_t)B * m->L * 2 * m->D * sizeof(float),
                                hipMemcpyDeviceToDevice, m->stream));
+    m->poisoned = 0;
     return SNHIP_OK;
 }
 

@@ -21,13 +21,38 @@ import torch
 
 from .. import _native
 
-__all__ = ["HipModel", "SnModel", "model_available"]
+__all__ = ["HipModel", "SnModel", "model_available", "set_threads", "get_threads",
+           "recommended_threads"]
 
 WEIGHT_FORMATS = {"fp32": 0, "int4": 1, "fp16": 3}
 
 
 def model_available() -> bool:
     return _native.available()
+
+
+def set_threads(n: int) -> int:
+    """sunnynet/runtime/model.py:69-73: sets the host thread count (n <= 0
+    keeps it) and returns the count in effect. The products run on the GPU;
+    the count sizes host-side load preparation."""
+    L = _native.lib()
+    L.snhip_set_threads(int(n))
+    return int(L.snhip_get_threads())
+
+
+def get_threads() -> int:
+    """sunnynet/runtime/model.py:76-77."""
+    return int(_native.lib().snhip_get_threads())
+
+
+def recommended_threads() -> int:
+    """sunnynet/runtime/model.py:80-89: physical cores; half the logical
+    count when the library cannot tell."""
+    n = int(_native.lib().snhip_recommended_threads())
+    if n <= 0:
+        import os
+        n = max(1, (os.cpu_count() or 2) // 2)
+    return n
 
 
 class HipModel:
@@ -52,8 +77,9 @@ class HipModel:
             raise RuntimeError(f"snhip_load failed: {path}: {_native.last_error()}")
         if not self._lib.snhip_ready(self._h):
             raise RuntimeError("snhip_load returned a handle that is not ready")
-        self._logits = (ctypes.c_float * vocab)()
+        self._logits = np.empty(vocab, np.float32)
         self._bind_stream()
+        _native.track(self)
 
     def _bind_stream(self):
         _native.check(self._lib.snhip_set_stream(self._h, _native.stream_handle(self.device)),
@@ -65,16 +91,20 @@ class HipModel:
         self._lib.snhip_reset(self._h)
 
     def step(self, token: int) -> list:
+        """One step of sequence 0 (sn_step); raises on an invalid token or a
+        device failure, which the reference's void call cannot report."""
+        t = np.array([int(token)], np.int32)
         self._bind_stream()
-        self._lib.snhip_step(self._h, int(token), ctypes.byref(self._logits))
-        return list(self._logits)
+        _native.check(self._lib.snhip_step_batch(self._h, t.ctypes.data, 1,
+                                                 self._logits.ctypes.data), "snhip_step")
+        return self._logits.tolist()
 
     def prefill(self, tokens) -> list:
-        toks = list(tokens)
+        toks = np.ascontiguousarray(np.asarray(list(tokens), np.int32))
         self._bind_stream()
-        buf = (ctypes.c_int * len(toks))(*toks)
-        self._lib.snhip_prefill(self._h, buf, len(toks), ctypes.byref(self._logits))
-        return list(self._logits)
+        _native.check(self._lib.snhip_prefill_host(self._h, toks.ctypes.data, toks.size,
+                                                   self._logits.ctypes.data), "snhip_prefill")
+        return self._logits.tolist()
 
     # -------------------------------------------------------- device surface
     def step_batch(self, tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -154,6 +184,10 @@ class HipModel:
             self._h = None
 
     def __del__(self):
+        # During interpreter teardown the HIP runtime may already be gone;
+        # the atexit hook has closed every open handle before that point.
+        if _native.finalizing():
+            return
         try:
             self.close()
         except Exception:

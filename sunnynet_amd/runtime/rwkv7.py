@@ -45,8 +45,9 @@ class HipRwkv7:
         if vocab is not None and int(vocab) != self.vocab:
             self.close()
             raise ValueError(f"vocab {vocab} does not match the blob's {self.vocab}")
-        self._logits = (ctypes.c_float * self.vocab)()
+        self._logits = np.empty(self.vocab, np.float32)
         self._bind_stream()
+        _native.track(self)
 
     @property
     def persist_grid(self) -> int:
@@ -64,24 +65,27 @@ class HipRwkv7:
         self._lib.snhip_rk_reset(self._h)
 
     def step(self, token: int) -> list:
-        self._bind_stream()
-        self._lib.snhip_rk_step(self._h, int(token), ctypes.byref(self._logits))
-        return np.frombuffer(self._logits, np.float32).tolist()
+        self.step_raw(token)
+        return self._logits.tolist()
 
     def step_raw(self, token: int) -> None:
-        """Advance the state; the logits stay in the handle's buffer."""
+        """Advance the state; the logits stay in the handle's buffer. Raises
+        on an invalid token or a device failure (a timed-out step leaves the
+        handle refusing steps until reset() or set_state())."""
         self._bind_stream()
-        self._lib.snhip_rk_step(self._h, int(token), ctypes.byref(self._logits))
+        _native.check(self._lib.snhip_abi_rwkv7_step(self._h, int(token), self._logits.ctypes.data),
+                      "snhip_rk_step")
 
     def logits(self) -> list:
-        return np.frombuffer(self._logits, np.float32).tolist()
+        return self._logits.tolist()
 
     def prefill(self, tokens) -> list:
-        toks = [int(t) for t in tokens]
+        toks = np.ascontiguousarray(np.asarray([int(t) for t in tokens], np.int32))
         self._bind_stream()
-        buf = (ctypes.c_int * len(toks))(*toks)
-        self._lib.snhip_rk_prefill(self._h, buf, len(toks), ctypes.byref(self._logits))
-        return np.frombuffer(self._logits, np.float32).tolist()
+        _native.check(self._lib.snhip_abi_rwkv7_prefill(self._h, toks.ctypes.data, toks.size,
+                                                        self._logits.ctypes.data),
+                      "snhip_rk_prefill")
+        return self._logits.tolist()
 
     # -------------------------------------------------------- device surface
     def step_batch(self, tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -131,6 +135,8 @@ class HipRwkv7:
             self._h = None
 
     def __del__(self):
+        if _native.finalizing():   # see HipModel.__del__
+            return
         try:
             self.close()
         except Exception:

@@ -100,3 +100,34 @@ def test_model_load_rejects_bad_blobs(tmp_path):
     L.snhip_reset(None)
     assert L.snhip_vocab(None) == 0 and L.snhip_ready(None) == 0
     assert L.snhip_step_batch(None, None, 1, None) == -1
+
+
+def test_thread_controls_mirror_sunnynet_h():
+    """sunnynet.h:42-47 / runtime/model.py:69-89: set_threads(n <= 0) keeps the
+    setting, a positive n takes effect and is what get_threads reports (the
+    same setting as the stable ABI's); recommended_threads is the number of
+    distinct (physical id, core id) pairs in /proc/cpuinfo."""
+    from sunnynet_amd.runtime import model as rt
+    L = _native.lib()
+    before = rt.get_threads()
+    assert before >= 1
+    assert rt.set_threads(0) == before
+    assert rt.set_threads(-3) == before
+    assert rt.set_threads(3) == 3 and L.snhip_abi_get_threads() == 3
+    assert L.snhip_abi_set_threads(5) == 0 and rt.get_threads() == 5
+    rt.set_threads(before)
+    pairs, phys, core = set(), -1, -1
+    with open("/proc/cpuinfo") as f:
+        for line in list(f) + ["\n"]:
+            k, _, v = line.partition(":")
+            if k.strip() == "physical id":
+                phys = int(v)
+            elif k.strip() == "core id":
+                core = int(v)
+            elif line == "\n":
+                if core >= 0:
+                    pairs.add((phys, core))
+                phys = core = -1
+    want = len(pairs) if pairs else __import__("os").cpu_count()
+    assert L.snhip_recommended_threads() == want
+    assert rt.recommended_threads() == want

@@ -117,25 +117,43 @@ def test_batched_kernel_is_deterministic(gpu, small):
 
 def test_batched_barrier_timeout_reports_error(gpu, small, monkeypatch):
     """Every barrier wait is given a target the host raised out of reach: each
-    workgroup gives up after its poll limit and leaves the kernel, the call
-    reports an error, and a handle loaded normally afterwards is correct."""
+    workgroup gives up after its poll limit and leaves the kernel, and the
+    call itself reports the error, on the device-tensor path as on the host
+    one. The state may be part-stepped, so the handle refuses further steps
+    until reset(); then it matches the oracle again."""
     w, buf, path = small
     B = 8
     monkeypatch.setenv("SNHIP_PERSIST", "0")
-    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
     monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
     hm = _model(path, SMALL, max_batch=B)
     assert hm.batch_grid > 0
     toks = np.arange(B, dtype=np.int32)
+    dt = torch.from_numpy(toks).to(gpu)
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    print("batched time-out: device path", flush=True)
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.step_batch(dt)
+    monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm.step_batch(dt)
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm.decode_greedy(dt, 2)
+    hm.reset()
+    orc = oracle.SnOracle(buf, batch=B)
+    a = hm.step_batch(dt).cpu().numpy()
+    assert np.abs(a - orc.step(toks)).max() < TOL
+    print("batched time-out: host path", flush=True)
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
     with pytest.raises(RuntimeError, match="timed out"):
         hm.step_batch_host(toks)
     monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    s, h = (torch.zeros(B, SMALL.layers, SMALL.dim, device=gpu),
+            torch.zeros(B, SMALL.layers, SMALL.taps - 1, SMALL.dim, device=gpu))
+    hm.set_state(s, h)     # a valid state also clears the refusal
+    a = hm.step_batch_host(toks)
+    assert np.abs(a - oracle.SnOracle(buf, batch=B).step(toks)).max() < TOL
     monkeypatch.delenv("SNHIP_PERSIST_SPIN")
     monkeypatch.delenv("SNHIP_PERSIST")
-    hm2 = _model(path, SMALL, max_batch=B)
-    orc = oracle.SnOracle(buf, batch=B)
-    a = hm2.step_batch_host(toks)
-    assert np.abs(a - orc.step(toks)).max() < TOL
 
 
 def test_batched_kernel_out_of_range_token_gives_nan_row(gpu, small):

@@ -163,17 +163,29 @@ def test_100m_fp32_and_int4(gpu, tmp_path_factory):
 
 def test_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
     """A barrier target the host raised out of reach: every workgroup gives up
-    after its poll limit and leaves the kernel, the call reports an error, and
-    the handle keeps working once the target is normal again."""
+    after its poll limit and leaves the kernel, and the call reports the error
+    (device-tensor step, greedy decoding and host step alike). The kernel
+    writes the state back only after its last step, so the same handle
+    continues from an untouched state once the target is normal again."""
     w, buf, path = tiny
-    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
     monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
     hm = _model(path, TINY)
+    assert hm.persistent_grid > 0
+    t = torch.tensor([3], dtype=torch.int32, device=gpu)
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    print("persistent time-out: device step, greedy, host step", flush=True)
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.step_batch(t)
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.decode_greedy(t, 4)
     with pytest.raises(RuntimeError, match="timed out"):
         hm.step_batch_host([3])
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.step(3)
     monkeypatch.delenv("SNHIP_PERSIST_STALL")
     monkeypatch.delenv("SNHIP_PERSIST_SPIN")
-    hm2 = _model(path, TINY)
     orc = oracle.SnOracle(buf)
-    a = hm2.step_batch_host([3])[0]
+    a = hm.step_batch(t).cpu().numpy()[0]
     assert np.abs(a - orc.step([3])[0]).max() < TOL
+    b = np.asarray(hm.step(5), np.float32)
+    assert np.abs(b - orc.step([5])[0]).max() < TOL

@@ -114,19 +114,36 @@ def test_persist_cfg4_int4(gpu, tmp_path_factory, monkeypatch):
 
 def test_persist_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
     """Every barrier wait is given a target the host raised out of reach: each
-    workgroup gives up after its poll limit and leaves the kernel, the call
-    reports an error, and a handle loaded normally afterwards is correct."""
+    workgroup gives up after its poll limit and leaves the kernel and the call
+    reports an error (device step and host step alike). The kernel writes S
+    and shift in place layer by layer, so the handle then refuses steps until
+    reset() or set_state(), after which it matches the oracle again."""
     w, p32, _ = tiny
-    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
     monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
     hm = HipRwkv7(p32)
     assert hm.persist_grid > 0
     tok = torch.tensor([3], dtype=torch.int32, device="cuda")
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    print("rwkv7 persistent time-out", flush=True)
     with pytest.raises(RuntimeError, match="timed out"):
         hm.step_batch(tok)
     monkeypatch.delenv("SNHIP_PERSIST_STALL")
-    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
-    h2 = HipRwkv7(p32)
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm.step(3)
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm.prefill([3, 4])
+    hm.reset()
     orc = oracle.RkOracle(p32.read_bytes())
-    a = np.asarray(h2.step(3), np.float32)
+    a = np.asarray(hm.step(3), np.float32)
     assert np.abs(a - orc.step([3])[0]).max() < TOL
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.step_raw(4)
+    monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    S = torch.zeros(1, RWKV_TINY.layers, RWKV_TINY.n_head, 64, 64, device="cuda")
+    sh = torch.zeros(1, RWKV_TINY.layers, 2, RWKV_TINY.dim, device="cuda")
+    hm.set_state(S, sh)
+    orc.reset()
+    a = np.asarray(hm.step(4), np.float32)
+    assert np.abs(a - orc.step([4])[0]).max() < TOL
+    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
