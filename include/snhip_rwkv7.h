@@ -82,6 +82,14 @@ snhip_status snhip_rk_get_state_dev(SnHipRwkv7* m, float* S_dev, float* shift_de
 snhip_status snhip_rk_set_state_dev(SnHipRwkv7* m, const float* S_dev, const float* shift_dev,
                                     int32_t B);
 
+/* expf and tanhf as the step computes them: restatements of the host C
+ * library's algorithms (glibc expf, fdlibm tanhf), so that they round as the
+ * reference's CPU runtime does. x, e, t hold n floats; _host computes on the
+ * CPU, _dev on the GPU (device pointers, enqueued on `stream`). For tests of
+ * the restatement against the host libm; no reference counterpart. */
+snhip_status snhip_refmath_host(const float* x, float* e, float* t, int32_t n);
+snhip_status snhip_refmath_dev(const float* x, float* e, float* t, int32_t n, void* stream);
+
 /* Stable-ABI mirror of sn_abi.h:88-100 (sn_abi_rwkv7_*): status codes of
  * snhip_abi.h; logits host memory of at least snhip_abi_rwkv7_vocab floats. */
 SnHipRwkv7* snhip_abi_rwkv7_load(const char* blob_path);

@@ -83,6 +83,7 @@ def load():
     lib.orc_sn_get_state.argtypes = [V, V, V]
     lib.orc_sn_set_state.argtypes = [V, V, V]
     lib.orc_sn_dbg_layer.argtypes = [V, I, ctypes.c_int32, I, V]
+    lib.orc_libm.argtypes = [V, V, V, L]
     lib.orc_rk_new.restype = V
     lib.orc_rk_new.argtypes = [V, L, I, I]
     for n in ("orc_rk_free", "orc_rk_reset"):
@@ -304,6 +305,15 @@ class RkOracle:
 
 
 # ------------------------------------------------------- the reference's own C
+def libm(x):
+    """(expf(x), tanhf(x)) from the host C library, elementwise."""
+    x = np.ascontiguousarray(x, np.float32)
+    e = np.empty_like(x)
+    t = np.empty_like(x)
+    load().orc_libm(_f(x), _f(e), _f(t), x.size)
+    return e, t
+
+
 def ref_available() -> bool:
     return (REF_DIR / "libref_model.so").exists()
 

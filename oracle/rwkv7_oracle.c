@@ -59,6 +59,14 @@ static void rk_gemv(float* y, const float* x, const OrcMat* M) {
 
 static float sgnf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+void orc_libm(const float* x, float* e, float* t, int64_t n) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        e[i] = expf(x[i]);
+        t[i] = tanhf(x[i]);
+    }
+}
+
 static void rk_layernorm(float* y, const float* x, const float* g,
                          const float* c, int n, float eps) {
     float sum = 0.0f;

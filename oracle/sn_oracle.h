@@ -76,6 +76,10 @@ void orc_sn_dbg_layer(OrcSn* m, int b, int32_t token, int layer, float* dbg);
 typedef struct OrcRk OrcRk;
 /* block: INT4 group size used by tag-1 matrices in the blob (the reference
  * hard-codes 64, rwkv7.c:35). */
+/* The host C library's expf and tanhf over n inputs: what the reference's
+ * runtime computes (its transcendentals are libm's). */
+void orc_libm(const float* x, float* e, float* t, int64_t n);
+
 OrcRk* orc_rk_new(const void* blob, int64_t nbytes, int batch, int block);
 void orc_rk_free(OrcRk* m);
 void orc_rk_reset(OrcRk* m);

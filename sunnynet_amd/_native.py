@@ -112,6 +112,8 @@ _SIGS = {
     "snhip_abi_rwkv7_reset": (I32, [V]),
     "snhip_abi_rwkv7_free": (None, [V]),
     "snhip_abi_rwkv7_vocab": (I32, [V]),
+    "snhip_refmath_host": (I32, [V, V, V, I32]),
+    "snhip_refmath_dev": (I32, [V, V, V, I32, V]),
 }
 
 

@@ -15,12 +15,14 @@
 //   logits = W_head LN_out(x)
 //
 // One step is a short sequence of kernels on the handle's stream (captured
-// into a HIP graph and replayed); every kernel processes all B sequences.
-// Matrix-vector products use the shared GEMV (gemv.hip) below 8 sequences
-// and the MFMA GEMM (gemm.hip) from 8 on; everything between them is fused
-// per sequence (token-shift mixes) or per head (k_rk_heads: decay, mixes,
-// normalized kk, the 64 x 64 state update and read-out, group norm, bonus,
-// gate), keeping each head's state tile in registers for one pass over HBM.
+// into a HIP graph and replayed); every kernel processes all B sequences and
+// follows the reference's rounding order (rkseq.hip): row LayerNorms with the
+// token-shift mixes, matrix products as sequential fmaf chains on the matrix
+// cores (with the LoRA tanh / sigmoid, relu^2 and residual epilogues), and one
+// kernel per head for the decay, mixes, normalized kk, the 64 x 64 state
+// update and read-out, group norm, bonus and gate. A step therefore gives the
+// reference's logits bit for bit on the same weights. Single-sequence steps
+// may instead run as one cooperative launch (rkpersist.hip).
 // Weights live row-major (out, in), fp32 or INT4.
 #include <cstdio>
 #include <cstdlib>
@@ -31,9 +33,9 @@
 #include <vector>
 
 #include "common.h"
-#include "gemm.h"
 #include "gemv.h"
 #include "rkpersist.h"
+#include "rkseq.h"
 #include "snhip.h"
 #include "snhip_rwkv7.h"
 
@@ -47,282 +49,7 @@ constexpr float kR2 = 0.6065306597126334f;   // 1/sqrt(e), rwkv7.c:38
 constexpr float kEpsGroup = 6.4e-4f;          // rwkv7.c:39
 constexpr int kHS = 64;                        // head size this backend runs
 constexpr int kMaxRank = 256;                  // rwkv7.c: LoRA scratch of 256
-constexpr int kLnPer = 16;                     // LayerNorm values per thread (dim <= 4096)
-
-__device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x)); }
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[w] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-// Two-pass LayerNorm over n <= 4096 values (rwkv7.c:127-140 form), element
-// k * 256 + tid in xv[k], PER per thread.
-template <int PER>
-__device__ __forceinline__ void ln_stats(const float (&xv)[PER], int n, float eps, float* red,
-                                         float& mean, float& rstd) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < PER; ++k)
-        if (k * 256 + (int)threadIdx.x < n) sum += xv[k];
-    mean = block_sum256(sum, red) / (float)n;
-    float vs = 0.0f;
-#pragma unroll
-    for (int k = 0; k < PER; ++k)
-        if (k * 256 + (int)threadIdx.x < n) {
-            const float d = xv[k] - mean;
-            vs += d * d;
-        }
-    rstd = 1.0f / sqrtf(block_sum256(vs, red) / (float)n + eps);
-}
-
-// Element index of slot k of this thread, clamped so every load is valid
-// (slots past n are loaded but never used).
-__device__ __forceinline__ int ln_idx(int k, int n) { return min(k * 256 + (int)threadIdx.x, n - 1); }
-
-// x[b] = LN_0(E[tok[b]]) (rwkv7.c:351-352); NaN rows for out-of-range ids.
-template <int PER>
-__global__ __launch_bounds__(256) void k_rk_embed(const int32_t* __restrict__ tok,
-                                                  const float* __restrict__ embed,
-                                                  const float* __restrict__ g,
-                                                  const float* __restrict__ c, float* __restrict__ x,
-                                                  int D, int vocab, float eps) {
-    __shared__ float red[4];
-    const int b = blockIdx.x;
-    const int t = tok[b];
-    const bool ok = t >= 0 && t < vocab;
-    const float* er = embed + (size_t)(ok ? t : 0) * D;
-    float xv[PER], gv[PER], cv[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = ln_idx(k, D);
-        xv[k] = ok ? er[i] : __builtin_nanf("");
-        gv[k] = g[i];
-        cv[k] = c[i];
-    }
-    float mean, rstd;
-    ln_stats<PER>(xv, D, eps, red, mean, rstd);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        if (i < D) x[(size_t)b * D + i] = (xv[k] - mean) * rstd * gv[k] + cv[k];
-    }
-}
-
-// y[b] = LN(x[b]) (the output norm, rwkv7.c:358).
-template <int PER>
-__global__ __launch_bounds__(256) void k_rk_ln(const float* __restrict__ x, const float* __restrict__ g,
-                                               const float* __restrict__ c, float* __restrict__ y,
-                                               int D, float eps) {
-    __shared__ float red[4];
-    const int b = blockIdx.x;
-    float xv[PER], gv[PER], cv[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = ln_idx(k, D);
-        xv[k] = x[(size_t)b * D + i];
-        gv[k] = g[i];
-        cv[k] = c[i];
-    }
-    float mean, rstd;
-    ln_stats<PER>(xv, D, eps, red, mean, rstd);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        if (i < D) y[(size_t)b * D + i] = (xv[k] - mean) * rstd * gv[k] + cv[k];
-    }
-}
-
-// Time-mix inputs (rwkv7.c:213-227): xn = LN_1(x); d = shift_0 - xn;
-// X6[b][s] = xn + lerp[s] d for s = r, w, k, v, a, g; shift_0 <- xn.
-template <int PER>
-__global__ __launch_bounds__(256) void k_rk_mix1(const float* __restrict__ x,
-                                                 const float* __restrict__ g,
-                                                 const float* __restrict__ c,
-                                                 const float* __restrict__ lerp,
-                                                 float* __restrict__ shift, size_t shift_bstride,
-                                                 float* __restrict__ X6, int D, float eps) {
-    __shared__ float red[4];
-    const int b = blockIdx.x;
-    float* sh = shift + (size_t)b * shift_bstride;
-    float xv[PER], gv[PER], cv[PER], sv[PER], lv[6][PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = ln_idx(k, D);
-        xv[k] = x[(size_t)b * D + i];
-        gv[k] = g[i];
-        cv[k] = c[i];
-        sv[k] = sh[i];
-#pragma unroll
-        for (int s6 = 0; s6 < 6; ++s6) lv[s6][k] = lerp[(size_t)s6 * D + i];
-    }
-    float mean, rstd;
-    ln_stats<PER>(xv, D, eps, red, mean, rstd);
-    float* o = X6 + (size_t)b * 6 * D;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        if (i >= D) continue;
-        const float xn = (xv[k] - mean) * rstd * gv[k] + cv[k];
-        const float d = sv[k] - xn;
-#pragma unroll
-        for (int s6 = 0; s6 < 6; ++s6) o[(size_t)s6 * D + i] = xn + lv[s6][k] * d;
-        sh[i] = xn;
-    }
-}
-
-// Channel-mix input (rwkv7.c:303-305,315): xn2 = LN_2(x);
-// xk2 = xn2 + cmk_lerp (shift_1 - xn2); shift_1 <- xn2.
-template <int PER>
-__global__ __launch_bounds__(256) void k_rk_mix2(const float* __restrict__ x,
-                                                 const float* __restrict__ g,
-                                                 const float* __restrict__ c,
-                                                 const float* __restrict__ lerp,
-                                                 float* __restrict__ shift1, size_t shift_bstride,
-                                                 float* __restrict__ xk2, int D, float eps) {
-    __shared__ float red[4];
-    const int b = blockIdx.x;
-    float* sh = shift1 + (size_t)b * shift_bstride;
-    float xv[PER], gv[PER], cv[PER], sv[PER], lv[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = ln_idx(k, D);
-        xv[k] = x[(size_t)b * D + i];
-        gv[k] = g[i];
-        cv[k] = c[i];
-        sv[k] = sh[i];
-        lv[k] = lerp[i];
-    }
-    float mean, rstd;
-    ln_stats<PER>(xv, D, eps, red, mean, rstd);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = k * 256 + threadIdx.x;
-        if (i >= D) continue;
-        const float xn = (xv[k] - mean) * rstd * gv[k] + cv[k];
-        xk2[(size_t)b * D + i] = xn + lv[k] * (sv[k] - xn);
-        sh[i] = xn;
-    }
-}
-
-// Per-thread slot count of the row kernels for a row of D values.
-int rk_per(int D) {
-    const int p = (D + 255) / 256;
-    return p <= 1 ? 1 : p <= 2 ? 2 : p <= 3 ? 3 : p <= 4 ? 4 : p <= 8 ? 8 : 16;
-}
-
-// Launches K<PER> for the row length's slot count.
-#define SNHIP_RK_ROWS(K, D, grid, st, ...)                                                    \
-    do {                                                                                      \
-        switch (rk_per(D)) {                                                                  \
-        case 1: hipLaunchKernelGGL(K<1>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
-        case 2: hipLaunchKernelGGL(K<2>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
-        case 3: hipLaunchKernelGGL(K<3>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
-        case 4: hipLaunchKernelGGL(K<4>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
-        case 8: hipLaunchKernelGGL(K<8>, grid, dim3(256), 0, st, __VA_ARGS__); break;          \
-        default: hipLaunchKernelGGL(K<16>, grid, dim3(256), 0, st, __VA_ARGS__); break;        \
-        }                                                                                     \
-    } while (0)
-
-// LoRA middle activations (rwkv7.c:235,256): lw = tanh(lw), lg = sig(lg).
-__global__ void k_rk_lora_act(float* __restrict__ lw, int Rw, float* __restrict__ lg, int Rg,
-                              int ld) {
-    const int b = blockIdx.x;
-    for (int i = threadIdx.x; i < Rw; i += blockDim.x) lw[(size_t)b * ld + i] = tanhf(lw[(size_t)b * ld + i]);
-    for (int i = threadIdx.x; i < Rg; i += blockDim.x) lg[(size_t)b * ld + i] = sgm(lg[(size_t)b * ld + i]);
-}
-
-struct HeadArgs {
-    const float *r, *k, *v, *dw, *da, *dv, *g;   // (B, D) each
-    float* vfirst;                                // (B, D)
-    const float *w0, *a0, *v0, *kk_w, *ka_w, *rk_w, *lnx_w, *lnx_b;
-    float* S;            // layer base; sequence b at S + b * s_bstride, head h at + h * HS*HS
-    size_t s_bstride;
-    float* y;            // (B, D)
-    int D, first;
-};
-
-// One head of one sequence per workgroup (rwkv7.c:143-189 and :236-299).
-// Channel work by the first wave; the 64 x 64 state by all 256 threads,
-// thread t owning row i = t / 4, columns 16 (t % 4) .. 16 (t % 4) + 15.
-__global__ __launch_bounds__(256) void k_rk_heads(HeadArgs A) {
-    __shared__ float w_[kHS], k_[kHS], v_[kHS], a_[kHS], kn_[kHS], r_[kHS], y_[kHS];
-    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-    const size_t row = (size_t)b * A.D;
-    if (t < kHS) {
-        const int c = h * kHS + t;
-        const float ww = expf(-sgm(A.dw[row + c] + A.w0[c]) * kR2);          // :236-237
-        float vv = A.v[row + c];
-        if (A.first) {
-            A.vfirst[row + c] = vv;                                            // :240
-        } else {
-            const float mix = sgm(A.dv[row + c] + A.v0[c]);                    // :244-246
-            vv = vv + (A.vfirst[row + c] - vv) * mix;
-        }
-        const float av = sgm(A.da[row + c] + A.a0[c]);                        // :251-252
-        const float kv = A.k[row + c];
-        const float kkv = kv * A.kk_w[c];                                      // :259
-        const float k2 = kv + kv * (av - 1.0f) * A.ka_w[c];                   // :260
-        // |kk| of the head, floored at 1e-12 (:158-162)
-        float nrm = sqrtf(wave_sum(kkv * kkv));
-        if (!(nrm > 1e-12f)) nrm = 1e-12f;
-        const float inv = 1.0f / nrm;
-        w_[t] = ww; k_[t] = k2; v_[t] = vv; a_[t] = av; kn_[t] = kkv * inv; r_[t] = A.r[row + c];
-    }
-    __syncthreads();
-    const int i = t >> 2, j0 = (t & 3) * 16;
-    float* Sr = A.S + (size_t)b * A.s_bstride + (size_t)h * kHS * kHS + (size_t)i * kHS + j0;
-    float s[16];
-#pragma unroll
-    for (int q = 0; q < 16; q += 4) {
-        const float4 v4 = *reinterpret_cast<const float4*>(Sr + q);
-        s[q] = v4.x; s[q + 1] = v4.y; s[q + 2] = v4.z; s[q + 3] = v4.w;
-    }
-    float pv = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
-    pv += __shfl_xor(pv, 1, 64);
-    pv += __shfl_xor(pv, 2, 64);
-    const float vi = v_[i];
-    float yacc = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int j = j0 + q;
-        const float kka = kn_[j] * a_[j];
-        const float vk = vi * k_[j];
-        const float ns = fmaf(s[q], w_[j], vk - pv * kka);                    // :180-181
-        s[q] = ns;
-        yacc = fmaf(ns, r_[j], yacc);
-    }
-#pragma unroll
-    for (int q = 0; q < 16; q += 4)
-        *reinterpret_cast<float4*>(Sr + q) = make_float4(s[q], s[q + 1], s[q + 2], s[q + 3]);
-    yacc += __shfl_xor(yacc, 1, 64);
-    yacc += __shfl_xor(yacc, 2, 64);
-    if ((t & 3) == 0) y_[i] = yacc;
-    __syncthreads();
-    if (t < kHS) {
-        // group norm, bonus and gate (:266-288)
-        const int c = h * kHS + t;
-        const float yy = y_[t];
-        const float mean = wave_sum(yy) / (float)kHS;
-        const float d = yy - mean;
-        const float rstd = 1.0f / sqrtf(wave_sum(d * d) / (float)kHS + kEpsGroup);
-        const float dot = wave_sum(r_[t] * k_[t] * A.rk_w[c]);
-        const float n = (yy - mean) * rstd * A.lnx_w[c] + A.lnx_b[c];
-        A.y[row + c] = (n + dot * v_[t]) * A.g[row + c];
-    }
-}
+constexpr int kMaxDim = 4096;                  // row kernels hold one row in LDS
 
 // (in, out) row-major -> (out, in) row-major, 32x32 tiles through LDS.
 __global__ void k_rk_transpose(const float* __restrict__ src, float* __restrict__ dst, int in, int out) {
@@ -426,11 +153,6 @@ struct SnHipRwkv7 {
     hipEvent_t ev_in = nullptr, ev_out = nullptr;
     std::map<std::tuple<int, const void*, int>, hipGraphExec_t> graphs;
     bool use_graphs = true;
-    int gemm_min_batch = 8;
-    float* gemm_work = nullptr;
-    size_t gemm_work_floats = 0;
-    unsigned* gemm_cnt = nullptr;      // skinny-GEMM tile counters (zero between launches)
-    int gemm_ncnt = 0;
     // One-sequence steps as one cooperative launch each (rkpersist.hip);
     // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
     int p_grid = 0;
@@ -653,7 +375,7 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
     memcpy(h, buf.data(), sizeof h);
     if (h[0] != kRkMagic || h[1] != kRkVersion) { set_last_error("bad RWKV-7 blob header (magic/version)"); return nullptr; }
     const int L = h[2], D = h[3], HS = h[4], NH = h[5], F = h[6], V = h[8];
-    if (L <= 0 || D <= 0 || HS != kHS || NH * HS != D || F <= 0 || V <= 0 || D > kLnPer * 256 ||
+    if (L <= 0 || D <= 0 || HS != kHS || NH * HS != D || F <= 0 || V <= 0 || D > kMaxDim ||
         D % 32 || F % 4) {
         set_last_error("unsupported RWKV-7 shape (head size must be 64, dim <= 4096)");
         return nullptr;
@@ -756,14 +478,9 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
     m->best = ralloc<unsigned long long>(m, B * 4096);
     m->counter = ralloc<int32_t>(m, 1);
     m->done = ralloc<int32_t>(m, 1);
-    m->gemm_work_floats = (size_t)16 << 20;
-    m->gemm_work = ralloc<float>(m, m->gemm_work_floats);
-    m->gemm_ncnt = 4096;
-    m->gemm_cnt = ralloc<unsigned>(m, m->gemm_ncnt);
     if (!m->S || !m->shift || !m->x || !m->X6 || !m->r || !m->k || !m->v || !m->lo || !m->dw ||
         !m->da || !m->dv || !m->g || !m->y || !m->vfirst || !m->xk2 || !m->ck || !m->nrm ||
-        !m->logits || !m->tok || !m->best || !m->counter || !m->done || !m->gemm_work ||
-        !m->gemm_cnt || hipMemset(m->gemm_cnt, 0, m->gemm_ncnt * sizeof(unsigned)) != hipSuccess ||
+        !m->logits || !m->tok || !m->best || !m->counter || !m->done ||
         hipMemset(m->S, 0, B * L * NH * HS * HS * sizeof(float)) != hipSuccess ||
         hipMemset(m->shift, 0, B * L * 2 * D * sizeof(float)) != hipSuccess ||
         hipMemset(m->counter, 0, sizeof(int32_t)) != hipSuccess ||
@@ -776,43 +493,27 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
         return nullptr;
     }
     if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
-    if (const char* e = getenv("SNHIP_GEMM_MIN_BATCH")) m->gemm_min_batch = std::max(1, atoi(e));
     setup_rk_persist(m);
     m->ready = 1;
     return m;
 }
 
-// Matrix products of one dependency level: GEMV jobs grouped by weight
-// format (up to kGemvMaxJobs per launch); from gemm_min_batch sequences on,
-// the MFMA GEMM for every product whose contraction is a multiple of 32.
+// Matrix products of one dependency level, grouped by weight format into
+// launches of up to kRkqMaxJobs jobs.
 struct MMList {
-    SnHipRwkv7* m;
     int B;
-    GemvJob jobs[8];
-    int blk[8];
+    RkqJob jobs[kRkqMaxJobs];
+    int blk[kRkqMaxJobs];
     int n = 0;
 
-    // xact (GEMV path only): activation applied to X as it is staged.
-    snhip_status add(const RMat& W, const float* X, int ldx, float* Y, int ldy, int epi,
-                     int xact = ACT_NONE) {
-        if (B >= m->gemm_min_batch && W.Kd % 32 == 0) {
-            GemmArgs g{};
-            g.X = X; g.ldx = ldx;
-            g.w = W.w; g.q = W.q; g.sc = W.sc; g.block = W.q ? W.block : 0;
-            g.M = B; g.N = W.M; g.K = W.Kd;
-            g.Y = Y; g.ldy = ldy;
-            g.epi = epi == EPI_ADD ? GEPI_ADD : epi == EPI_RELU2 ? GEPI_RELU2 : GEPI_STORE;
-            GemmWork gw;
-            gw.part = m->gemm_work; gw.part_floats = m->gemm_work_floats;
-            gw.cnt = m->gemm_cnt; gw.ncnt = m->gemm_ncnt;
-            return launch_gemm(g, gw, m->work);
-        }
-        GemvJob j{};
+    snhip_status add(const RMat& W, const float* X, int ldx, float* Y, int ldy, int epi) {
+        if (n == kRkqMaxJobs) return SNHIP_E_INVAL;
+        RkqJob j{};
+        j.X = X; j.ldx = ldx;
         j.w = W.w; j.q = W.q; j.sc = W.sc;
-        j.M = W.M; j.Kd = W.Kd; j.B = B;
-        j.X = X; j.ldx = ldx; j.Y = Y; j.ldy = ldy;
+        j.M = W.M; j.Kd = W.Kd;
+        j.Y = Y; j.ldy = ldy;
         j.epi = epi;
-        j.xact = xact;
         jobs[n] = j;
         blk[n] = W.q ? W.block : 0;
         ++n;
@@ -820,14 +521,15 @@ struct MMList {
     }
 
     snhip_status flush(hipStream_t st) {
-        bool used[8] = {false};
+        bool used[kRkqMaxJobs] = {false};
         for (int i = 0; i < n; ++i) {
             if (used[i]) continue;
-            GemvJob batch[kGemvMaxJobs];
+            RkqJob batch[kRkqMaxJobs];
             int nb = 0;
-            for (int j = i; j < n && nb < kGemvMaxJobs; ++j)
+            for (int j = i; j < n; ++j)
                 if (!used[j] && blk[j] == blk[i]) { batch[nb++] = jobs[j]; used[j] = true; }
-            SNHIP_CHECK(launch_gemv(batch, nb, blk[i], st));
+            const snhip_status rc = launch_rkq_mm(batch, nb, B, blk[i], st);
+            if (rc != SNHIP_OK) return rc;
         }
         n = 0;
         return SNHIP_OK;
@@ -842,15 +544,19 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
     float* la = m->lo + kMaxRank;
     float* lv = m->lo + 2 * kMaxRank;
     float* lg = m->lo + 3 * kMaxRank;
-    SNHIP_RK_ROWS(k_rk_embed, D, dim3(B), st, m->tok, m->embed, m->en_w, m->en_b, m->x, D, m->vocab,
-                  m->eps);
-    MMList mm{m, B};
     snhip_status rc;
+    RkqLnArgs ln{};
+    ln.D = D; ln.vocab = m->vocab; ln.eps = m->eps; ln.shift_bstride = sh_bstride;
+    ln.mode = RKQ_LN_EMBED;
+    ln.tok = m->tok; ln.embed = m->embed; ln.g = m->en_w; ln.c = m->en_b; ln.out = m->x;
+    if ((rc = launch_rkq_ln(ln, B, st)) != SNHIP_OK) return rc;
+    MMList mm{B};
     for (int l = 0; l < L; ++l) {
         const RkLayer& A = m->layers[l];
         float* sh = m->shift + (size_t)l * 2 * D;
-        SNHIP_RK_ROWS(k_rk_mix1, D, dim3(B), st, m->x, A.ln1w, A.ln1b, A.lerp, sh, sh_bstride, m->X6, D,
-                      m->eps);
+        ln.mode = RKQ_LN_MIX1;
+        ln.x = m->x; ln.g = A.ln1w; ln.c = A.ln1b; ln.lerp = A.lerp; ln.shift = sh; ln.out = m->X6;
+        if ((rc = launch_rkq_ln(ln, B, st)) != SNHIP_OK) return rc;
         const float* xr = m->X6;
         const float* xw = m->X6 + D;
         const float* xk = m->X6 + 2 * D;
@@ -858,27 +564,20 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         const float* xa = m->X6 + 4 * D;
         const float* xg = m->X6 + 5 * D;
         const int ld6 = 6 * D;
-        if ((rc = mm.add(A.r, xr, ld6, m->r, D, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.k, xk, ld6, m->k, D, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.v, xv, ld6, m->v, D, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.w1, xw, ld6, lw, ldl, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.a1, xa, ld6, la, ldl, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.g1, xg, ld6, lg, ldl, EPI_STORE)) != SNHIP_OK) return rc;
-        if (l > 0 && (rc = mm.add(A.v1, xv, ld6, lv, ldl, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.r, xr, ld6, m->r, D, RKQ_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.k, xk, ld6, m->k, D, RKQ_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.v, xv, ld6, m->v, D, RKQ_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.w1, xw, ld6, lw, ldl, RKQ_TANH)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.a1, xa, ld6, la, ldl, RKQ_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.g1, xg, ld6, lg, ldl, RKQ_SIGMOID)) != SNHIP_OK) return rc;
+        if (l > 0 && (rc = mm.add(A.v1, xv, ld6, lv, ldl, RKQ_STORE)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        // tanh / sigmoid of the LoRA middles: in the GEMV's input staging below
-        // gemm_min_batch sequences, else one small kernel.
-        const bool gemv = B < m->gemm_min_batch;
-        if (!gemv)
-            hipLaunchKernelGGL(k_rk_lora_act, dim3(B), dim3(256), 0, st, lw, A.Rw, lg, A.Rg, ldl);
-        if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, EPI_STORE, gemv ? ACT_TANH : ACT_NONE)) != SNHIP_OK)
-            return rc;
-        if ((rc = mm.add(A.a2, la, ldl, m->da, D, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.g2, lg, ldl, m->g, D, EPI_STORE, gemv ? ACT_SIGMOID : ACT_NONE)) != SNHIP_OK)
-            return rc;
-        if (l > 0 && (rc = mm.add(A.v2, lv, ldl, m->dv, D, EPI_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, RKQ_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.a2, la, ldl, m->da, D, RKQ_STORE)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.g2, lg, ldl, m->g, D, RKQ_STORE)) != SNHIP_OK) return rc;
+        if (l > 0 && (rc = mm.add(A.v2, lv, ldl, m->dv, D, RKQ_STORE)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        HeadArgs H{};
+        RkqHeadArgs H{};
         H.r = m->r; H.k = m->k; H.v = m->v; H.dw = m->dw; H.da = m->da; H.dv = m->dv; H.g = m->g;
         H.vfirst = m->vfirst;
         H.w0 = A.w0; H.a0 = A.a0; H.v0 = A.v0; H.kk_w = A.kk; H.ka_w = A.ka; H.rk_w = A.rk;
@@ -886,41 +585,30 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         H.S = m->S + (size_t)l * NH * HS * HS;
         H.s_bstride = s_bstride;
         H.y = m->y;
-        H.D = D;
+        H.D = D; H.NH = NH;
         H.first = l == 0;
-        hipLaunchKernelGGL(k_rk_heads, dim3(NH, B), dim3(256), 0, st, H);
-        if ((rc = mm.add(A.o, m->y, D, m->x, D, EPI_ADD)) != SNHIP_OK) return rc;
+        if ((rc = launch_rkq_heads(H, B, st)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.o, m->y, D, m->x, D, RKQ_ADD)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        SNHIP_RK_ROWS(k_rk_mix2, D, dim3(B), st, m->x, A.ln2w, A.ln2b, A.cmk_lerp, sh + D, sh_bstride,
-                      m->xk2, D, m->eps);
-        if ((rc = mm.add(A.cmk, m->xk2, D, m->ck, F, EPI_RELU2)) != SNHIP_OK) return rc;
+        ln.mode = RKQ_LN_MIX2;
+        ln.x = m->x; ln.g = A.ln2w; ln.c = A.ln2b; ln.lerp = A.cmk_lerp; ln.shift = sh + D; ln.out = m->xk2;
+        if ((rc = launch_rkq_ln(ln, B, st)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.cmk, m->xk2, D, m->ck, F, RKQ_RELU2)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.cmv, m->ck, F, m->x, D, EPI_ADD)) != SNHIP_OK) return rc;
+        if ((rc = mm.add(A.cmv, m->ck, F, m->x, D, RKQ_ADD)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
     }
-    SNHIP_RK_ROWS(k_rk_ln, D, dim3(B), st, m->x, m->on_w, m->on_b, m->nrm, D, m->eps);
-    const RMat& Hm = m->head;
-    if (B >= m->gemm_min_batch) {
-        if ((rc = mm.add(Hm, m->nrm, D, logits_out, m->vocab, EPI_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        if (greedy) {
-            const int nblk = 64;
-            hipLaunchKernelGGL(k_rk_argmax_partial, dim3(nblk, B), dim3(256), 0, st, logits_out,
-                               m->vocab, m->best);
-            hipLaunchKernelGGL(k_rk_finalize, dim3(B), dim3(256), 0, st, m->best, nblk, B, m->tok,
-                               m->tok_hist, m->counter, m->done, m->hist_cap);
-        }
-    } else {
-        GemvJob j{};
-        j.w = Hm.w; j.q = Hm.q; j.sc = Hm.sc;
-        j.M = Hm.M; j.Kd = Hm.Kd; j.B = B;
-        j.X = m->nrm; j.ldx = D; j.Y = logits_out; j.ldy = m->vocab;
-        j.epi = greedy ? EPI_ARGMAX : EPI_STORE;
-        j.best = m->best;
-        SNHIP_CHECK(launch_gemv(&j, 1, Hm.q ? Hm.block : 0, st));
-        if (greedy)
-            hipLaunchKernelGGL(k_rk_finalize, dim3(B), dim3(256), 0, st, m->best, j.nblk, B, m->tok,
-                               m->tok_hist, m->counter, m->done, m->hist_cap);
+    ln.mode = RKQ_LN_PLAIN;
+    ln.x = m->x; ln.g = m->on_w; ln.c = m->on_b; ln.out = m->nrm;
+    if ((rc = launch_rkq_ln(ln, B, st)) != SNHIP_OK) return rc;
+    if ((rc = mm.add(m->head, m->nrm, D, logits_out, m->vocab, RKQ_STORE)) != SNHIP_OK) return rc;
+    if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+    if (greedy) {
+        const int nblk = 64;
+        hipLaunchKernelGGL(k_rk_argmax_partial, dim3(nblk, B), dim3(256), 0, st, logits_out,
+                           m->vocab, m->best);
+        hipLaunchKernelGGL(k_rk_finalize, dim3(B), dim3(256), 0, st, m->best, nblk, B, m->tok,
+                           m->tok_hist, m->counter, m->done, m->hist_cap);
     }
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;

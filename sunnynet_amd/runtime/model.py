@@ -184,12 +184,12 @@ class HipModel:
             self._h = None
 
     def __del__(self):
-        # During interpreter teardown the HIP runtime may already be gone;
-        # the atexit hook has closed every open handle before that point.
-        if _native.finalizing():
-            return
+        # During interpreter teardown the HIP runtime may already be gone
+        # (and this module's globals with it); the atexit hook has closed
+        # every open handle before that point.
         try:
-            self.close()
+            if not _native.finalizing():
+                self.close()
         except Exception:
             pass
 

@@ -135,9 +135,11 @@ class HipRwkv7:
             self._h = None
 
     def __del__(self):
-        if _native.finalizing():   # see HipModel.__del__
-            return
+        # During interpreter teardown the HIP runtime may already be gone
+        # (and this module's globals with it); the atexit hook has closed
+        # every open handle before that point.
         try:
-            self.close()
+            if not _native.finalizing():
+                self.close()
         except Exception:
             pass

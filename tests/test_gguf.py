@@ -215,3 +215,31 @@ def test_converter_cli_writes_the_blob(tmp_path):
     assert dst.read_bytes() == pack_rwkv7_blob(w)
     assert main([str(src), str(dst)]) == 0
     assert dst.read_bytes() == pack_rwkv7_blob(w, int4=True)
+
+
+@pytest.mark.gpu
+def test_rwkv7_gguf_ragged_ranks_on_the_gpu_handle(gpu, tmp_path):
+    """A GGUF file converted with ragged per-layer LoRA ranks, loaded by the
+    HIP handle (snhip_rk_load): every step's logits equal the oracle's (the
+    per-kernel step at B=2 follows the reference's rounding order)."""
+    import torch
+
+    from sunnynet_amd.runtime.rwkv7 import HipRwkv7
+    w = init_rwkv7(RWKV_TINY, 6)
+    rng = np.random.default_rng(7)
+    D = w.cfg.dim
+    for k, r in (("w", 32), ("g", 16)):
+        w.layers[1][k + "1"] = (rng.standard_normal((r, D)) / np.sqrt(D)).astype(np.float32)
+        w.layers[1][k + "2"] = (rng.standard_normal((D, r)) * 0.5 / np.sqrt(r)).astype(np.float32)
+    path = _rwkv_gguf(tmp_path, w, "rag.gguf")
+    for int4 in (False, True):
+        blob = gguf_to_rwkv7_blob(path, int4=int4)
+        bp = tmp_path / f"rag{int(int4)}.bin"
+        bp.write_bytes(blob)
+        hm = HipRwkv7(bp, max_batch=2)
+        orc = oracle.RkOracle(blob, batch=2)
+        for t in ((3, 77), (400, 9), (12, 500)):
+            tt = np.array(t, np.int32)
+            a = hm.step_batch(torch.from_numpy(tt).to(gpu)).cpu().numpy()
+            assert np.array_equal(a, orc.step(tt)), (int4, t)
+        hm.close()
