@@ -125,6 +125,21 @@ snhip_status snhip_abi_core_bwd_dev(const float* q, const float* delta, const fl
                                     float* ddelta, float* ds0, int32_t B, int32_t T,
                                     int32_t D, void* stream);
 
+/* snhip_abi_core_bwd_dev without any device allocation: same arguments,
+ * kernels and results (bit for bit). No counterpart in the reference; for
+ * callers that cannot allocate (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc). The (B, D) ddelta
+ * partials live in a fixed per-GPU scratch array of 2^20 floats (4 MiB, held
+ * until the process ends): B * D above 1048576 returns SNHIP_E_INVAL with an
+ * error text. Calls that overlap on one GPU share that array and race; serialize
+ * them (one stream, or events). The first call on a device resolves the array's
+ * address there. */
+snhip_status snhip_abi_core_bwd_dev_noalloc(const float* q, const float* delta, const float* s0,
+                                            const float* states, const float* u, const float* p,
+                                            const float* dstate, const float* du_in, float* dq,
+                                            float* ddelta, float* ds0, int32_t B, int32_t T,
+                                            int32_t D, void* stream);
+
 /* ----------------------------------------------- INT4 (group-wise) */
 /* Format of sunnynet/runtime/quant.c:34-87: W (rows, N) row-major; groups of
  * `block` inputs share scale = amax/7 (1 if amax == 0); byte k of a group

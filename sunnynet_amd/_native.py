@@ -63,6 +63,7 @@ _SIGS = {
     "snhip_abi_scan_bwd_dev": (I32, [V, V, V, V, V, V, V, V, I32, I32, I32, V]),
     "snhip_abi_core_fwd_dev": (I32, [V, V, V, V, V, V, I32, I32, I32, V]),
     "snhip_abi_core_bwd_dev": (I32, [V, V, V, V, V, V, V, V, V, V, V, I32, I32, I32, V]),
+    "snhip_abi_core_bwd_dev_noalloc": (I32, [V, V, V, V, V, V, V, V, V, V, V, I32, I32, I32, V]),
     "snhip_abi_quant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
     "snhip_abi_dequant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
     "snhip_abi_linear_dev": (I32, [V, V, V, I32, I32, I32, V]),

@@ -148,6 +148,18 @@ snhip_status snhip_abi_core_bwd_dev(const float* q, const float* delta, const fl
                            as_stream(stream));
 }
 
+snhip_status snhip_abi_core_bwd_dev_noalloc(const float* q, const float* delta, const float* s0,
+                                            const float* states, const float* u, const float* p,
+                                            const float* dstate, const float* du_in, float* dq,
+                                            float* ddelta, float* ds0, int32_t B, int32_t T,
+                                            int32_t D, void* stream) {
+    if (!q || !delta || !s0 || !states || !u || !p || !dstate || !du_in || !dq || !ddelta || !ds0 ||
+        B <= 0 || T <= 0 || D <= 0 || D % 8 != 0)
+        return SNHIP_E_INVAL;
+    return launch_core_bwd_noalloc(q, delta, s0, states, u, p, dstate, du_in, dq, ddelta, ds0, B, T, D,
+                                   as_stream(stream));
+}
+
 snhip_status snhip_abi_recur_step(const float* a, const float* b, float* s, int32_t B,
                                   int32_t N, int32_t gated) {
     if (dims_bad(a, B, N) || b == nullptr || s == nullptr) return SNHIP_E_INVAL;

@@ -81,6 +81,10 @@ snhip_status launch_core_fwd(const float* q, const float* delta, const float* s0
 snhip_status launch_core_bwd(const float* q, const float* delta, const float* s0, const float* states,
                              const float* uo, const float* po, const float* dstate, const float* du_in,
                              float* dq, float* ddelta, float* ds0, int B, int T, int D, hipStream_t st);
+snhip_status launch_core_bwd_noalloc(const float* q, const float* delta, const float* s0,
+                                     const float* states, const float* uo, const float* po,
+                                     const float* dstate, const float* du_in, float* dq, float* ddelta,
+                                     float* ds0, int B, int T, int D, hipStream_t st);
 snhip_status launch_recur_scan(const float* a, const float* b, const float* s0,
                                float* out, float* send, int B, int T, int N,
                                int gated, hipStream_t st);

@@ -30,6 +30,9 @@
 // needs D % 128 == 0 and T % (W TC) == 0 (the reference's block pads T to its
 // scan chunk before it calls the kernel); any other shape takes a one lane per
 // channel kernel.
+#include <mutex>
+#include <string>
+
 #include "bufio.h"
 
 namespace snhip {
@@ -467,12 +470,13 @@ snhip_status launch_core_fwd(const float* q, const float* delta, const float* s0
     return SNHIP_OK;
 }
 
-snhip_status launch_core_bwd(const float* q, const float* delta, const float* s0, const float* states,
-                             const float* uo, const float* po, const float* dstate, const float* du_in,
-                             float* dq, float* ddelta, float* ds0, int B, int T, int D, hipStream_t st) {
-    // Per-row sums of ddelta's terms, reduced over rows in order afterwards.
-    float* acc = nullptr;
-    SNHIP_CHECK(hipMallocAsync(reinterpret_cast<void**>(&acc), (size_t)B * D * sizeof(float), st));
+namespace {
+// Backward kernels plus the in-order row reduction of ddelta, with the (B, D)
+// per-row partials in `acc` (every element is written before it is read).
+snhip_status core_bwd_ws(const float* q, const float* delta, const float* s0, const float* states,
+                         const float* uo, const float* po, const float* dstate, const float* du_in,
+                         float* dq, float* ddelta, float* ds0, int B, int T, int D, float* acc,
+                         hipStream_t st) {
     if (fast_ok(B, T, D, kBW * kBTC, {q, states, uo, po, dstate, du_in, dq})) {
         const unsigned grid = (unsigned)((long)B * D / 128);
         hipLaunchKernelGGL((k_core_bwd_buf<kBW, kBTC>), dim3(grid), dim3(64 * kBW), 0, st, q, delta, s0,
@@ -482,16 +486,69 @@ snhip_status launch_core_bwd(const float* q, const float* delta, const float* s0
         hipLaunchKernelGGL(k_core_bwd_gen, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, q, delta,
                            s0, states, uo, po, dstate, du_in, dq, acc, ds0, B, T, D);
     }
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess) {
-        hipLaunchKernelGGL(k_core_ddelta, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, acc, ddelta,
-                           B, D);
-        e = hipGetLastError();
+    SNHIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(k_core_ddelta, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, acc, ddelta, B, D);
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
+
+// Scratch of the allocation-free backward: the (B, D) ddelta partials of
+// calls with B * D <= kCoreBwdScratchFloats (4 MiB per GPU, held for the life
+// of the process). Host code uses the per-device address from
+// hipGetSymbolAddress, never the array's name.
+constexpr size_t kCoreBwdScratchFloats = (size_t)1 << 20;
+static __device__ __align__(256) float scratch[kCoreBwdScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+
+// This device's address of `scratch`, resolved once per device with it current.
+snhip_status scratch_ptr(float** out) {
+    int dev = 0;
+    SNHIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_last_error("device index beyond the scratch table");
+        return SNHIP_E_UNSUPPORTED;
     }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        SNHIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch[dev];
+    return SNHIP_OK;
+}
+}  // namespace
+
+snhip_status launch_core_bwd(const float* q, const float* delta, const float* s0, const float* states,
+                             const float* uo, const float* po, const float* dstate, const float* du_in,
+                             float* dq, float* ddelta, float* ds0, int B, int T, int D, hipStream_t st) {
+    // Per-row sums of ddelta's terms, reduced over rows in order afterwards.
+    float* acc = nullptr;
+    SNHIP_CHECK(hipMallocAsync(reinterpret_cast<void**>(&acc), (size_t)B * D * sizeof(float), st));
+    const snhip_status rc = core_bwd_ws(q, delta, s0, states, uo, po, dstate, du_in, dq, ddelta, ds0,
+                                        B, T, D, acc, st);
     const hipError_t f = hipFreeAsync(acc, st);
-    SNHIP_CHECK(e);
+    if (rc != SNHIP_OK) return rc;
     SNHIP_CHECK(f);
     return SNHIP_OK;
+}
+
+snhip_status launch_core_bwd_noalloc(const float* q, const float* delta, const float* s0,
+                                     const float* states, const float* uo, const float* po,
+                                     const float* dstate, const float* du_in, float* dq, float* ddelta,
+                                     float* ds0, int B, int T, int D, hipStream_t st) {
+    if ((size_t)B * (size_t)D > kCoreBwdScratchFloats) {
+        set_last_error("core backward without allocation: B * D = " + std::to_string((long long)B * D) +
+                       " exceeds the scratch of " + std::to_string(kCoreBwdScratchFloats) + " floats");
+        return SNHIP_E_INVAL;
+    }
+    float* acc = nullptr;
+    const snhip_status rc = scratch_ptr(&acc);
+    if (rc != SNHIP_OK) return rc;
+    return core_bwd_ws(q, delta, s0, states, uo, po, dstate, du_in, dq, ddelta, ds0, B, T, D, acc, st);
 }
 
 }  // namespace snhip
