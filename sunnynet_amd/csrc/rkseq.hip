@@ -41,27 +41,24 @@ __device__ __forceinline__ float hsum8(const float* v) {
 }
 
 // ------------------------------------------------------------------ rows
-// Sequential fp32 sum of n4 float4 in LDS (element order), by one lane. Rows
-// whose length is a multiple of 64 take blocks of 64 values with the next
-// block's reads in flight while the current block is added; only the chain
-// of dependent adds is exposed.
+// Sequential fp32 sum of n4 float4 in LDS (element order), by one lane.
+// Rows whose length is a multiple of 64 run through a window of 16 float4:
+// slot i is added, then refilled with the same slot of the next block, so
+// the reads stay one block (64 dependent adds) ahead with no register copies
+// and only the chain of dependent adds is exposed.
 __device__ __forceinline__ float seq_sum(const float4* v, int n4) {
     float s = 0.0f;
     if (n4 % 16 == 0) {
-        float4 cur[16], nxt[16];
+        float4 w[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) cur[i] = v[i];
+        for (int i = 0; i < 16; ++i) w[i] = v[i];
         for (int base = 0; base < n4; base += 16) {
-            if (base + 16 < n4) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) nxt[i] = v[base + 16 + i];
-            }
+            const int nb = min(base + 16, n4 - 16);   // the next block (the last block again at the end)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                s = s + cur[i].x; s = s + cur[i].y; s = s + cur[i].z; s = s + cur[i].w;
+                s = s + w[i].x; s = s + w[i].y; s = s + w[i].z; s = s + w[i].w;
+                w[i] = v[nb + i];
             }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) cur[i] = nxt[i];
         }
         return s;
     }
@@ -229,7 +226,7 @@ __device__ __forceinline__ void step4(const float4 (&x4)[S], float w0, float w1,
 
 // Inputs per chunk staged in LDS at once (X rows; INT4 codes in registers).
 constexpr int kRkqKC = 768;
-constexpr int kRkqU = 64;                  // inputs per pipeline unit (two producer halves of 32)
+constexpr int kRkqU = 64;                  // INT4: inputs per pipeline unit (two producer halves of 32)
 constexpr int kRkqNP = 2;                  // producer waves of an INT4 workgroup
 
 // This workgroup's job (uniform selects: no dynamic index into the arguments).
@@ -333,129 +330,187 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
     for (int s = 0; s < S; ++s) rkq_finish(J, A.B, 0, seq0 + 4 * s, out, acc[s]);
 }
 
-// INT4 weights: a workgroup of 1 + NC waves (one per SIMD) per 64 rows x
-// 4 NC sequences. Wave 0 (producer) holds the rows' codes and scales of the
-// chunk in registers and dequantizes one unit of 32 inputs per step into a
-// three-slot LDS ring ([k/4][row] float4, conflict-free). Consumer wave c runs
-// the k-ordered MFMA chains of sequences 4c .. 4c+3. Step t ends with one
-// workgroup barrier: the producer writes unit t; a consumer reads unit t-1
-// into registers (alternating between two register sets) and multiplies unit
-// t-2 from the other set, so its MFMA chain never waits on LDS or on VALU work
-// of its own. Every weight is dequantized once per workgroup.
-template <int BLK, int NC>
+// INT4 weights: a workgroup of kRkqNP producer waves and NC consumer waves
+// per 64 rows x 4 S NC sequences.
+//
+// Producer wave h dequantizes half h (32 inputs) of every 64-input unit of
+// the rows: at step t it converts unit t from codes and scales it loaded
+// kRkqPF units earlier into slot t % 3 of an LDS ring ([block][row] float4,
+// conflict-free). Consumer c multiplies unit t - 2 at step t, S independent
+// k-ordered MFMA chains of 4 sequences each sharing the weight operand. Its
+// weight window runs kRkqWD blocks of 4 inputs ahead of the MFMAs and
+// crosses into unit t - 1 (complete since the previous step), and its X
+// operands come from global memory one unit ahead, so the chains wait on
+// neither LDS nor global memory. One workgroup barrier per step, waiting on
+// LDS only; every weight is dequantized once per workgroup.
+constexpr int kRkqPF = 4;     // producer code prefetch, units
+constexpr int kRkqWD = 8;     // consumer weight window, blocks of 4 inputs (a half unit)
+
+template <int BLK, int NC, int S>
 __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArgs A) {
-    constexpr int U4 = kRkqU / 4;
-    __shared__ float4 xs4[NC][4][kRkqKC / 4];          // consumer c's X rows
-    __shared__ float4 wring[2][U4][64];                // dequantized units
-    __shared__ uint4 cq[kRkqKC / 32][64];              // producer: codes, [16-byte slot][row]
-    __shared__ float cs[kRkqKC / BLK][64];             // producer: scales, [group][row]
+    constexpr int U4 = kRkqU / 4;                      // blocks per unit
+    constexpr int NQ = BLK / 32;                       // code uint4 per half unit
+    static_assert(U4 % kRkqWD == 0 && kRkqWD == U4 / 2, "the weight window is a half unit");
+    __shared__ float4 wring[3][U4][64];
     RkqJob J;
     int u0;
     rkq_job(A, J, u0);
     const int ot = u0 / A.seq_tiles, st = u0 % A.seq_tiles;
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r4 = l & 3;
+    // wave index in a scalar register: every branch on the role is uniform
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, r4 = l & 3;
     const int out = ot * 64 + l;
     const int orow = out < J.M ? out : J.M - 1;
-    const int cw_ = wv - kRkqNP;                      // consumer index (< 0: producer)
-    const int seqw = st * 4 * NC + 4 * cw_;            // consumer's first sequence
-    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < J.Kd; k0 += kRkqKC) {
-        const int kc = min(kRkqKC, J.Kd - k0);
-        const int nu = (kc + kRkqU - 1) / kRkqU;
+    const int Kd = J.Kd;
+    const int nu = (Kd + kRkqU - 1) / kRkqU;            // the last unit is half when Kd % 64 == 32
+    const bool half_last = (Kd % kRkqU) != 0;
+    // Steps (one barrier each) for both roles: units 0 .. nu - 1 are written
+    // at steps 0 .. nu - 1 and multiplied at steps 2 .. nu + 1; the count is
+    // rounded up to the producer's prefetch depth (idle steps at the end).
+    const int nsteps = (nu + 2 + kRkqPF - 1) / kRkqPF * kRkqPF;
+    if (wv < kRkqNP) {
+        // ---- producer: half h of every unit
+        const int h = wv;
+        const uint8_t* qrow = J.q + (size_t)orow * (size_t)(Kd / 2);
+        const float* srow = J.sc + (size_t)orow * (size_t)(Kd / BLK);
+        uint4 qw[kRkqPF][NQ];
+        float sw[kRkqPF];
+        // Branch-free loads: a unit past the end reads the last half again
+        // (never converted), so no wait depends on control flow.
+        auto load = [&](int u, uint4 (&q)[NQ], float& s) {
+            const int k = min(u * kRkqU + 32 * h, Kd - 32);
+            if (BLK == 32) {
+                q[0] = *reinterpret_cast<const uint4*>(qrow + k / 2);
+                s = srow[k / 32];
+            } else {
+                const int g = k / 64;
+#pragma unroll
+                for (int i = 0; i < NQ; ++i) q[i] = *reinterpret_cast<const uint4*>(qrow + g * 32 + 16 * i);
+                s = srow[g];
+            }
+        };
+#pragma unroll
+        for (int p = 0; p < kRkqPF; ++p) load(p, qw[p], sw[p]);
+        // Groups of kRkqPF steps: a group first issues the loads of the next
+        // group's units, then converts its own (loaded one group earlier), so
+        // every wait on codes covers loads a whole group old.
+        for (int t0 = 0; t0 < nsteps; t0 += kRkqPF) {
+            uint4 qn[kRkqPF][NQ];
+            float sn[kRkqPF];
+#pragma unroll
+            for (int p = 0; p < kRkqPF; ++p) load(t0 + kRkqPF + p, qn[p], sn[p]);
+#pragma unroll
+            for (int p = 0; p < kRkqPF; ++p) {
+                const int t = t0 + p;
+                // Converted unconditionally: past the last unit (or the
+                // missing half of a half unit) this writes leftovers to slot
+                // t % 3, which the consumers do not read at or after step t.
+                const float scg = sw[p], m8 = -8.0f * scg;
+                // Block i of the half: inputs 4i .. 4i+3. BLK 64: nibble h of
+                // bytes 4i .. 4i+3; BLK 32: low nibbles of word i for i < 4,
+                // high nibbles of word i - 4 after.
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint4 v = BLK == 32 ? qw[p][0] : qw[p][(i >> 2) % NQ];
+                    const int wi = i & 3;
+                    const uint32_t word = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
+                    const bool hi = BLK == 32 ? i >= 4 : h == 1;
+                    uint32_t nib = (hi ? (word >> 4) : word) & 0x0F0F0F0Fu;
+                    // Opaque to the compiler, so that each byte converts with
+                    // one v_cvt_f32_ubyteN (no field extraction).
+                    asm volatile("" : "+v"(nib));
+                    float4 w;
+                    w.x = fmaf((float)(nib & 0xFFu), scg, m8);
+                    w.y = fmaf((float)((nib >> 8) & 0xFFu), scg, m8);
+                    w.z = fmaf((float)((nib >> 16) & 0xFFu), scg, m8);
+                    w.w = fmaf((float)(nib >> 24), scg, m8);
+                    wring[t % 3][8 * h + i][l] = w;
+                }
+                __syncthreads();
+                // keep each step's conversion after its barrier
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int p = 0; p < kRkqPF; ++p) {
+#pragma unroll
+                for (int i = 0; i < NQ; ++i) qw[p][i] = qn[p][i];
+                sw[p] = sn[p];
+            }
+        }
+        return;
+    }
+    // ---- consumer c: sequences seqb + 4 s + (0..3), lane row r4 of each chain.
+    // Rows past the batch read the last sequence's X (their outputs are not
+    // stored), and loads past the end re-read the last block, so every load
+    // is unconditional and no wait depends on control flow.
+    const int c = wv - kRkqNP;
+    const int seqb = st * (4 * S * NC) + c * (4 * S);
+    const float* xr[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        xr[s] = J.X + (size_t)min(seqb + 4 * s + r4, A.B - 1) * (size_t)J.ldx;
+    float4 xw[S][U4];   // block i of the unit in multiplication; refilled with the next unit's
+    float4 ww[kRkqWD];  // weight blocks, slot = block % kRkqWD
+    v4f acc[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < U4; ++i) xw[s][i] = *reinterpret_cast<const float4*>(xr[s] + min(4 * i, Kd - 4));
+    }
+    // Steps 0 and 1: the producers write units 0 and 1; the window takes
+    // unit 0's first half once it is complete.
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRkqWD; ++j) ww[j] = wring[0][j][l];
+    __syncthreads();
+    // One full unit: block i's MFMAs, then its refills (weight block
+    // i + kRkqWD, from the next unit's slot for the last half; X block i of
+    // the next unit). Straight-line, so the window stays in place.
+    auto full_unit = [&](int slot, int nslot, int knext) {
+#pragma unroll
+        for (int i = 0; i < U4; ++i) {
+            const float4 wc = ww[i % kRkqWD];
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].x, wc.x, acc[s], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].y, wc.y, acc[s], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].z, wc.z, acc[s], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].w, wc.w, acc[s], 0, 0, 0);
+            ww[i % kRkqWD] = i + kRkqWD < U4 ? wring[slot][i + kRkqWD][l] : wring[nslot][i + kRkqWD - U4][l];
+            const int kx = min(knext + 4 * i, Kd - 4);
+#pragma unroll
+            for (int s = 0; s < S; ++s) xw[s][i] = *reinterpret_cast<const float4*>(xr[s] + kx);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Steps 2 .. nu: units 0 .. nu - 2, each followed by another.
+    for (int u = 0; u < nu - 1; ++u) {
+        full_unit(u % 3, (u + 1) % 3, (u + 1) * kRkqU);
         __syncthreads();
-        if (cw_ >= 0) {
-            // Consumer: stage its 4 X rows of the chunk (zero rows past the batch).
-            const int nq = kc / 4;
-            for (int idx = l; idx < 4 * nq; idx += 64) {
-                const int row = idx / nq, q = idx - row * nq;
-                const int sq = seqw + row;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (sq < A.B) v = *reinterpret_cast<const float4*>(J.X + (size_t)sq * J.ldx + k0 + 4 * q);
-                xs4[cw_][row][q] = v;
-            }
-            __syncthreads();
-            const float4* xl = xs4[cw_][r4];
-            for (int t = 0; t < nu + 1; ++t) {
-                if (t >= 1) {
-                    const int u = t - 1;
-                    const int n4 = min(U4, (kc - u * kRkqU) / 4);   // a last unit may be half
-                    float4 w[U4], x[U4];
-                    if (n4 == U4) {
+    }
+    // Step nu + 1: the last unit (its refills read in-bounds leftovers).
+    const int ul = nu - 1;
+    if (!half_last) {
+        full_unit(ul % 3, (ul + 1) % 3, Kd);
+    } else {
 #pragma unroll
-                        for (int i = 0; i < U4; ++i) {
-                            w[i] = wring[u & 1][i][l];
-                            x[i] = xl[u * U4 + i];
-                        }
+        for (int i = 0; i < U4 / 2; ++i) {
+            const float4 wc = ww[i % kRkqWD];
 #pragma unroll
-                        for (int i = 0; i < U4; ++i) {
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(x[i].x, w[i].x, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(x[i].y, w[i].y, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(x[i].z, w[i].z, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(x[i].w, w[i].w, acc, 0, 0, 0);
-                        }
-                    } else {
-                        for (int i = 0; i < n4; ++i) {
-                            const float4 wi = wring[u & 1][i][l], xi = xl[u * U4 + i];
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(xi.x, wi.x, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(xi.y, wi.y, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(xi.z, wi.z, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_4x4x1f32(xi.w, wi.w, acc, 0, 0, 0);
-                        }
-                    }
-                }
-                __syncthreads();
-            }
-        } else {
-            // Producer: stage row orow's codes and scales of the chunk in LDS
-            // (every load in flight at once; the lane reads back only its own),
-            // then dequantize unit t at step t from there.
-            const int ng = kc / BLK;
-            const uint4* qr = reinterpret_cast<const uint4*>(J.q + (size_t)orow * (J.Kd / 2) + k0 / 2);
-            const float* sr = J.sc + (size_t)orow * (J.Kd / BLK) + k0 / BLK;
-            // (both producers stage every slot; each reads back its own lane's)
-            for (int i = 0; i < kc / 32; ++i) cq[i][l] = qr[i];
-            for (int g = 0; g < ng; ++g) cs[g][l] = sr[g];
-            __syncthreads();
-            // Unit t: inputs 64 t .. 64 t + 63 of the chunk, from the 16-byte
-            // code slots 4 t .. 4 t + 3 (element e of a group is byte
-            // e % (BLK/2), low nibble for e < BLK/2).
-            for (int t = 0; t < nu + 1; ++t) {
-                if (t < nu) {
-                    if (t * kRkqU + 32 * wv < kc) {            // this producer's 32-input half
-                        const int h = wv;
-                        const int k = t * kRkqU + 32 * h;
-                        const int g = k / BLK;
-                        const float scg = cs[g][l], m8 = -8.0f * scg;
-                        uint32_t cw[BLK / 8];
-#pragma unroll
-                        for (int i = 0; i < BLK / 32; ++i) {
-                            const uint4 v = cq[g * (BLK / 32) + i][l];
-                            cw[4 * i] = v.x; cw[4 * i + 1] = v.y; cw[4 * i + 2] = v.z; cw[4 * i + 3] = v.w;
-                        }
-                        const int e0 = k % BLK;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const int e = e0 + 4 * i;
-                            const int by = e % (BLK / 2);
-                            const uint32_t word = cw[by / 4];
-                            uint32_t nib = (e >= BLK / 2 ? (word >> 4) : word) & 0x0F0F0F0Fu;
-                            // Opaque to the compiler, so that each byte converts
-                            // with one v_cvt_f32_ubyteN (no field extraction).
-                            asm volatile("" : "+v"(nib));
-                            float4 w;
-                            w.x = fmaf((float)(nib & 0xFFu), scg, m8);
-                            w.y = fmaf((float)((nib >> 8) & 0xFFu), scg, m8);
-                            w.z = fmaf((float)((nib >> 16) & 0xFFu), scg, m8);
-                            w.w = fmaf((float)(nib >> 24), scg, m8);
-                            wring[t & 1][8 * h + i][l] = w;
-                        }
-                    }
-                }
-                __syncthreads();
+            for (int s = 0; s < S; ++s) {
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].x, wc.x, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].y, wc.y, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].z, wc.z, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].w, wc.w, acc[s], 0, 0, 0);
             }
         }
     }
-    if (cw_ >= 0) rkq_finish(J, A.B, BLK, seqw, out, acc);
+    __syncthreads();
+    for (int t = nu + 2; t < nsteps; ++t) __syncthreads();
+#pragma unroll
+    for (int s = 0; s < S; ++s) rkq_finish(J, A.B, BLK, seqb + 4 * s, out, acc[s]);
 }
 
 // ---------------------------------------------------------------- heads
@@ -590,7 +645,10 @@ snhip_status launch_rkq_heads(const RkqHeadArgs& a, int B, hipStream_t st) {
     return SNHIP_OK;
 }
 
-snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStream_t st) {
+// nc, s: INT4 consumer waves per workgroup and chains per consumer (0: chosen
+// here); fp32: s groups of 4 sequences per wave.
+snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int nc, int s,
+                               hipStream_t st) {
     if (n <= 0 || n > kRkqMaxJobs || B <= 0 || (block != 0 && block != 32 && block != 64))
         return SNHIP_E_INVAL;
     RkqMMArgs a{};
@@ -605,18 +663,26 @@ snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStrea
         a.tiles_out[i] = (J.M + 63) / 64;
         tiles1 += a.tiles_out[i];
     }
-    // fp32: groups of 4 sequences per wave (S); INT4: consumer waves per
-    // workgroup (NC), 4 sequences each.
     int per;   // sequences per workgroup
     int S = 1, NC = 1;
     if (block == 0) {
         const long waves1 = (long)tiles1 * ((B + 3) / 4);
-        S = (B > 8 && waves1 / 4 >= 1024) ? 4 : (B > 4 && waves1 / 2 >= 1024) ? 2 : 1;
+        S = s ? s : (B > 8 && waves1 / 4 >= 1024) ? 4 : (B > 4 && waves1 / 2 >= 1024) ? 2 : 1;
+        if (S != 1 && S != 2 && S != 4) return SNHIP_E_INVAL;
         per = 4 * S;
     } else {
-        // One wave per SIMD: two producers and one or two consumers.
-        NC = B <= 4 ? 1 : 2;
-        per = 4 * NC;
+        // Measured on MI355X (K = 768 / 3072 products, B = 1 / 8 / 64): one
+        // consumer of one chain is fastest while the grid of such workgroups
+        // stays within ~1024 (up to 3 reside per CU); larger grids (the
+        // vocabulary head) share the dequantized units among more chains.
+        const long wg11 = (long)tiles1 * ((B + 3) / 4);
+        const int nc0 = wg11 <= 1024 ? 1 : 2;
+        const int s0 = wg11 <= 1024 || B < 16 ? 1 : 2;
+        NC = nc ? nc : nc0;
+        S = s ? s : s0;
+        if (!((NC == 1 || NC == 2 || NC == 4) && (S == 1 || S == 2)) || (NC == 4 && S == 2))
+            return SNHIP_E_INVAL;
+        per = 4 * NC * S;
     }
     a.n = n;
     a.B = B;
@@ -629,22 +695,34 @@ snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStrea
     a.start[n] = total;
     for (int i = n + 1; i <= kRkqMaxJobs; ++i) a.start[i] = total;
 #define SNHIP_RKQ_F32(S_) hipLaunchKernelGGL((k_rkq_mm_f32<S_>), dim3(total), dim3(64), 0, st, a)
-#define SNHIP_RKQ_Q4(B_, N_) hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
+#define SNHIP_RKQ_Q4(B_, N_, S_) \
+    hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_, S_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
+#define SNHIP_RKQ_Q4B(B_)                                 \
+    do {                                                  \
+        if (NC == 1 && S == 1) SNHIP_RKQ_Q4(B_, 1, 1);   \
+        else if (NC == 2 && S == 1) SNHIP_RKQ_Q4(B_, 2, 1); \
+        else if (NC == 4) SNHIP_RKQ_Q4(B_, 4, 1);        \
+        else if (NC == 1) SNHIP_RKQ_Q4(B_, 1, 2);        \
+        else SNHIP_RKQ_Q4(B_, 2, 2);                     \
+    } while (0)
     if (block == 0) {
         if (S == 1) SNHIP_RKQ_F32(1);
         else if (S == 2) SNHIP_RKQ_F32(2);
         else SNHIP_RKQ_F32(4);
     } else if (block == 32) {
-        if (NC == 1) SNHIP_RKQ_Q4(32, 1);
-        else SNHIP_RKQ_Q4(32, 2);
+        SNHIP_RKQ_Q4B(32);
     } else {
-        if (NC == 1) SNHIP_RKQ_Q4(64, 1);
-        else SNHIP_RKQ_Q4(64, 2);
+        SNHIP_RKQ_Q4B(64);
     }
 #undef SNHIP_RKQ_F32
 #undef SNHIP_RKQ_Q4
+#undef SNHIP_RKQ_Q4B
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;
+}
+
+snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStream_t st) {
+    return launch_rkq_mm_cfg(jobs, n, B, block, 0, 0, st);
 }
 
 }  // namespace snhip
