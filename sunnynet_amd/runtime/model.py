@@ -11,18 +11,24 @@ group ``block`` (INT4 quantized at load in the reference's quant.c format),
 ``step_batch`` / ``decode_greedy`` on torch device tensors without host
 round trips, and ``get_state`` / ``set_state`` in the torch ``SunnyState``
 layout (s (B,L,D), hist (B,L,K-1,D), newest entry first).
+
+``HipSunnyNet`` puts the torch backend's step contract on a handle:
+``init_state(B)`` and ``forward_step(idx_t, state) -> (logits, SunnyState)``
+(sunnynet/model.py:82-87, 113-124), so a sequence can move between the torch
+path and this one mid-stream.
 """
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 
 import numpy as np
 import torch
 
 from .. import _native
 
-__all__ = ["HipModel", "SnModel", "model_available", "set_threads", "get_threads",
-           "recommended_threads"]
+__all__ = ["HipModel", "SnModel", "HipSunnyNet", "SunnyState", "model_available",
+           "set_threads", "get_threads", "recommended_threads"]
 
 WEIGHT_FORMATS = {"fp32": 0, "int4": 1, "fp16": 3}
 
@@ -196,3 +202,55 @@ class HipModel:
 
 # The reference's name, for drop-in use with the same constructor arguments.
 SnModel = HipModel
+
+
+@dataclass
+class SunnyState:
+    """The torch backend's recurrent state (sunnynet/layers.py:21-30): per
+    layer rolling state ``s`` (B, L, D) and causal-conv history ``hist``
+    (B, L, K-1, D), newest entry first."""
+
+    s: torch.Tensor
+    hist: torch.Tensor
+
+    def to(self, device=None, dtype=None):
+        return SunnyState(self.s.to(device=device, dtype=dtype),
+                          self.hist.to(device=device, dtype=dtype))
+
+
+class HipSunnyNet:
+    """``SunnyNet``'s single-step surface over a ``HipModel``.
+
+    ``forward_step(idx_t, state)`` (sunnynet/model.py:113-124) loads ``state``
+    into sequences [0, B) of the handle, steps them on ``idx_t`` and returns
+    the logits (B, V) with a new ``SunnyState`` (fresh tensors, fp32, on the
+    handle's device), as the torch path returns new tensors. Any float dtype
+    or device is accepted for ``state``; the handle computes in fp32.
+    """
+
+    def __init__(self, handle: HipModel):
+        self.handle = handle
+
+    @property
+    def device(self):
+        return self.handle.device
+
+    def init_state(self, batch: int, device=None, dtype=torch.float32) -> SunnyState:
+        """model.py:82-87: zero state for ``batch`` sequences."""
+        h = self.handle
+        dev = device if device is not None else h.device
+        return SunnyState(torch.zeros(batch, h.layers, h.dim, device=dev, dtype=dtype),
+                          torch.zeros(batch, h.layers, h.kh, h.dim, device=dev, dtype=dtype))
+
+    @torch.no_grad()
+    def forward_step(self, idx_t: torch.Tensor, state: SunnyState):
+        h = self.handle
+        B = int(idx_t.shape[0])
+        if B > h.max_batch:
+            raise ValueError(f"batch {B} exceeds the handle's max_batch {h.max_batch}")
+        if state.s.shape[0] != B or state.hist.shape[0] != B:
+            raise ValueError("state batch does not match idx_t")
+        h.set_state(state.s, state.hist)
+        logits = h.step_batch(idx_t.to(device=h.device, dtype=torch.int32))
+        s, hist = h.get_state(B)
+        return logits, SunnyState(s, hist)

@@ -266,9 +266,10 @@ def test_torch_ref_step_equals_forward_fp64():
     assert float((torch.cat([o1, o2], 1) - full).abs().max()) < 1e-10
 
 
-def test_weight_init_matches_reference_rng_order():
-    """Same seed -> same weights; a different construction order would change
-    the QR draws of every layer (pinned further by tests/golden)."""
+def test_weight_init_is_deterministic_and_orthogonal():
+    """Same seed -> same weights, orthogonal rows scaled by rho (rho/2 for
+    W_s), embedding std 0.02. The values themselves are pinned against the
+    reference's SunnyNet(cfg) in test_weights_golden.py."""
     a = init_sunnynet(TINY, 0)
     b = init_sunnynet(TINY, 0)
     assert torch.equal(a.layers[1].W_s, b.layers[1].W_s)
