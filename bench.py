@@ -19,11 +19,21 @@ algorithmic bytes, the reference core_fwd_f32 / core_bwd_f32 beside them.
 random init), chunked prefill of a T=1024 random prompt, then 256 greedy
 steps on the device at B=1 and B=64, fp32; and the same shape with INT4 g32
 weights (matmuls ~ N(0, 0.02)) after a T=2048 prefill at B=1, 8, 32. Each
-entry gives tokens/s, us/step and the HBM roofline of the step's weight
-bytes; ``cpu_baseline`` there is the reference ``sn_step`` on host cores.
+case gives tokens/s, us/step and a ``roofline`` of the step (HBM bytes for
+the weight-streaming cases; fp32 MFMA flops for fp32 B=64 and INT4 B=32).
+CPU legs: the reference ``sn_step`` (fp32 B=1), the fp32 torch
+``forward_step`` restatement at B=64 (the reference has no batched C step),
+and the reference ``sn_gemv_i4`` over one step's INT4 matrices.
+``decode.small``: SunnyNet small (seed 0), prefill 256 then 64 greedy steps
+at B=1, with the reference ``sn_prefill`` / ``sn_step`` beside it.
 ``decode.rwkv7``: the RWKV-7 configuration (12 layers, D=768, vocab 65536,
 INT4 g32), 512-token prompt, 128 greedy steps at B=1 and B=64, with the
-reference ``sn_rk_step`` timed on its INT4 blob.
+reference ``sn_rk_step`` timed on its INT4 blob. Every CPU leg states the
+host's sockets, physical cores and logical CPUs.
+
+Modes that run a fixed sequence and exit: ``--pmc-probe [scan|decode]`` (for
+``rocprofv3 --pmc`` counter runs) and ``--profile b1|batch|rwkv|small`` (for
+``rocprofv3 --kernel-trace`` summaries of the decode paths).
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -75,6 +85,23 @@ def physical_cores() -> int:
     except OSError:
         n = 0
     return n or (os.cpu_count() or 1)
+
+
+def host_cpu() -> dict:
+    """The host's CPU counts (lscpu's sockets / cores / logical CPUs), read
+    from /proc/cpuinfo, for every CPU baseline."""
+    sockets, model = set(), ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("physical id"):
+                    sockets.add(line.split(":")[1].strip())
+                elif line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return {"sockets": len(sockets) or 1, "physical_cores": physical_cores(),
+            "logical_cpus": os.cpu_count() or 1, "model": model}
 
 
 def bench_scan(steps: int, warmup: int, cpu: bool):
@@ -245,9 +272,9 @@ def bench_core(steps, warmup, cpu, B=SCAN_B, T=SCAN_T, D=SCAN_D):
             cf, cb = (20 * ns) / (t1 - t0) / 1e9, (36 * ns) / (t2 - t1) / 1e9
             log(f"[bench] cpu reference core_fwd_f32 {cf:.2f} GB/s, core_bwd_f32 {cb:.2f} GB/s, {threads} threads")
             smp = f"B={B} D={D} T={Ts} (a T/16 slice), one run each"
-            res["fwd"]["cpu_baseline"] = {"value": round(cf, 3), "unit": "GB/s", "cores": threads,
+            res["fwd"]["cpu_baseline"] = {"value": round(cf, 3), "unit": "GB/s", "cores": threads, "host": host_cpu(),
                                           "kind": "reference", "sample": smp}
-            res["bwd"]["cpu_baseline"] = {"value": round(cb, 3), "unit": "GB/s", "cores": threads,
+            res["bwd"]["cpu_baseline"] = {"value": round(cb, 3), "unit": "GB/s", "cores": threads, "host": host_cpu(),
                                           "kind": "reference", "sample": smp}
     return res
 
@@ -279,7 +306,7 @@ def cpu_scan_baseline(a, b, s0):
     med = float(np.median(times))
     gbs = scan_bytes(B, T, D) / med / 1e9
     log(f"[bench] cpu {kind} sn_recur_scan: {med*1e3:.1f} ms, {gbs:.2f} GB/s, {threads} threads")
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "host": host_cpu(), "kind": kind,
             "sample": f"full workload B={B} D={D} T={T}, median of {len(times)} runs "
                       f"({med*1e3:.1f} ms each)"}
 
@@ -291,6 +318,38 @@ def decode_bytes(cfg, int4: bool, block: int = 32) -> int:
     return int(n * 4) if not int4 else int(n // 2 + (n // block) * 4)
 
 
+def decode_step_bytes(cfg, int4: bool, B: int) -> int:
+    """Algorithmic HBM bytes of one decode step: the weights, the per-layer
+    vectors (norm gains and centres, conv taps, delta; 4 B each) and per
+    sequence the embedding row, the state and history read and written, and
+    the logits written."""
+    D, I, K, L, V = cfg.dim, cfg.inner, cfg.taps, cfg.layers, cfg.vocab_size
+    small = (L * (2 * D + 2 * I + K * D + D) + 2 * D) * 4
+    per_seq = D * 4 + 2 * L * K * D * 4 + V * 4
+    return decode_bytes(cfg, int4) + small + B * per_seq
+
+
+FP32_MFMA_TFLOPS = 157.3
+
+
+def decode_roofline(cfg, fmt: str, B: int, us_per_step: float, kernel: str) -> dict:
+    """Roofline of a decode step from its measured time: HBM for the
+    weight-streaming cases, fp32 MFMA (2 flops per weight per sequence) for
+    fp32 B >= 64 and INT4 B >= 32, where the products are dense contractions."""
+    nbytes = decode_step_bytes(cfg, fmt == "int4", B)
+    flops = 2 * matmul_params(cfg) * B
+    sec = us_per_step * 1e-6
+    if (fmt == "fp32" and B >= 64) or (fmt == "int4" and B >= 32):
+        ach = flops / sec / 1e12
+        return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / FP32_MFMA_TFLOPS, 4), "traffic": None,
+                "kernel": kernel, "flops_per_step": flops, "bytes_per_step": nbytes}
+    ach = nbytes / sec / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+            "bytes_per_step": nbytes, "flops_per_step": flops}
+
+
 def _time_ms(fn):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -298,6 +357,91 @@ def _time_ms(fn):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1)
+
+
+def _write_blob(tmp, name, buf):
+    path = os.path.join(tmp, name)
+    with open(path, "wb") as f:
+        f.write(buf)
+    return path
+
+
+def bench_decode_small(cpu: bool):
+    """SunnyNet small (4 layers, D=256, I=384, R=128, V=4096, seed 0): a
+    256-token random prompt through the chunked prefill, then 64 greedy steps
+    on the device, B=1, fp32. Launch- and latency-bound: its 9.96 MB of weights
+    stay in the caches. The reference ``sn_prefill`` + ``sn_step`` on the same
+    blob beside it."""
+    import tempfile
+
+    from sunnynet_amd.blob import pack_sunny_blob
+    from sunnynet_amd.config import SMALL
+    from sunnynet_amd.runtime.model import HipModel
+    from sunnynet_amd.weights import init_sunnynet
+    cfg = SMALL
+    dev = torch.device("cuda:0")
+    tmp = tempfile.mkdtemp(prefix="snhip_bench_small_")
+    path = _write_blob(tmp, "small.bin", pack_sunny_blob(init_sunnynet(cfg, 0)))
+    prompt = torch.from_numpy(np.random.default_rng(256).integers(0, cfg.vocab_size, (1, 256))
+                              .astype(np.int32)).to(dev)
+    hm = HipModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers)
+    tok = hm.prefill_batch(prompt).argmax(1).int()       # warm: prefill path and step graph
+    hm.decode_greedy(tok, 8)
+    hm.reset()
+    torch.cuda.synchronize()
+    lg = None
+
+    def pre():
+        nonlocal lg
+        lg = hm.prefill_batch(prompt)
+    pms = _time_ms(pre)
+    tok = lg.argmax(1).int()
+    n = 64
+    ms = _time_ms(lambda: hm.decode_greedy(tok, n)) / n
+    grid = hm.persistent_grid
+    hm.close()
+    us = ms * 1e3
+    case = {"workload": "SunnyNet small B=1 fp32: prefill 256 then 64 greedy steps",
+            "prefill_ms": round(pms, 3), "us_per_step": round(us, 2), "tok_s": round(1e3 / ms, 1),
+            "roofline": decode_roofline(cfg, "fp32", 1, us, "k_decode_persist<0>" if grid else
+                                        "per-kernel step")}
+    case["roofline"]["bound"] = "latency"
+    case["roofline"]["note"] = ("launch- and latency-bound: the step's 9.96 MB of weights stay in "
+                                "L2/MALL; frac is against the HBM peak")
+    log(f"[bench] decode small B=1: {case['us_per_step']} us/step, {case['tok_s']} tok/s, "
+        f"prefill 256 {pms:.2f} ms")
+    if cpu:
+        case["cpu_baseline"] = cpu_decode_small_baseline(path, cfg, prompt.cpu().numpy()[0])
+    return case
+
+
+def cpu_decode_small_baseline(path, cfg, prompt):
+    """The reference sn_prefill over the 256-token prompt, then 64 greedy
+    sn_step calls, on host cores (the reference's OpenMP GEMVs)."""
+    import oracle
+    threads = min(16, physical_cores())
+    if not oracle.ref_available():
+        return {"value": None, "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(),
+                "kind": "reference", "sample": "reference build absent"}
+    oracle.ref_lib("model").sn_set_threads(threads)
+    m = oracle.RefSnModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers)
+    t0 = time.perf_counter()
+    lg = m.prefill(prompt.tolist())
+    pre = time.perf_counter() - t0
+    times = []
+    for _ in range(64):
+        t = int(np.argmax(lg))
+        t0 = time.perf_counter()
+        lg = m.step(t)
+        times.append(time.perf_counter() - t0)
+    m.close()
+    med = float(np.median(times))
+    log(f"[bench] cpu reference sn_step small: {med*1e3:.3f} ms/token, prefill {pre*1e3:.1f} ms, "
+        f"{threads} threads")
+    return {"value": round(1.0 / med, 1), "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(),
+            "kind": "reference", "ms_per_token": round(med * 1e3, 4), "prefill_ms": round(pre * 1e3, 2),
+            "sample": "the whole workload: sn_prefill of the 256-token prompt, then the median of "
+                      "64 greedy sn_step calls"}
 
 
 def bench_decode(cpu: bool):
@@ -311,18 +455,13 @@ def bench_decode(cpu: bool):
     tmp = tempfile.mkdtemp(prefix="snhip_bench_")
     log("[bench] SunnyNet-100M weights (seed 1)")
     w = init_sunnynet(cfg, 1)
-    p32 = os.path.join(tmp, "m100_fp32.bin")
-    with open(p32, "wb") as f:
-        f.write(pack_sunny_blob(w))
+    p32 = _write_blob(tmp, "m100_fp32.bin", pack_sunny_blob(w))
     w4 = gaussian_matmuls(init_sunnynet(cfg, 1), seed=3)
-    p4 = os.path.join(tmp, "m100_gauss.bin")
-    with open(p4, "wb") as f:
-        f.write(pack_sunny_blob(w4))
+    p4 = _write_blob(tmp, "m100_gauss.bin", pack_sunny_blob(w4))
     out = {"model": "SunnyNet-100M L=12 D=1024 I=1536 R=512 V=32000",
            "steps": 256, "cases": []}
     g = torch.Generator(device="cpu").manual_seed(123)
     for fmt, path, T, batches in (("fp32", p32, 1024, (1, 64)), ("int4", p4, 2048, (1, 8, 32))):
-        nbytes = decode_bytes(cfg, fmt == "int4")
         for B in batches:
             hm = HipModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
                           max_batch=B, weights=fmt, block=32)
@@ -341,19 +480,109 @@ def bench_decode(cpu: bool):
             torch.cuda.synchronize()
             n = out["steps"]
             ms = _time_ms(lambda: hm.decode_greedy(tok, n)) / n
+            kernel = (f"k_decode_persist<{32 if fmt == 'int4' else 0}> (the whole step)"
+                      if B == 1 and hm.persistent_grid else
+                      "k_decode_batch (layers) + head GEMM + greedy argmax" if hm.batch_grid else
+                      "per-kernel step")
             hm.close()
+            us = ms * 1e3
             case = {"weights": fmt, "B": B, "prefill_T": T, "prefill_ms": round(pms, 2),
-                    "prefill_tok_s": round(B * T / pms * 1e3, 1), "us_per_step": round(ms * 1e3, 2),
-                    "tok_s": round(B / ms * 1e3, 1), "weight_bytes_per_step": nbytes,
-                    "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
-                    "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                    "prefill_tok_s": round(B * T / pms * 1e3, 1), "us_per_step": round(us, 2),
+                    "tok_s": round(B / ms * 1e3, 1),
+                    "roofline": decode_roofline(cfg, fmt, B, us, kernel)}
             log(f"[bench] decode {fmt} B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s, "
-                f"prefill T={T} {pms:.1f} ms")
+                f"prefill T={T} {pms:.1f} ms, {case['roofline']['frac']:.4f} of {case['roofline']['bound']}")
             out["cases"].append(case)
     if cpu:
         out["cpu_baseline"] = cpu_decode_baseline(p32, cfg)
+        out["cpu_baseline_b64"] = cpu_decode_b64_baseline(w)
+        out["cpu_baseline_int4_gemv"] = cpu_gemv_i4_baseline(w4)
+    out["small"] = bench_decode_small(cpu)
     out["rwkv7"] = bench_rwkv7(cpu)
     return out
+
+
+def cpu_decode_b64_baseline(w):
+    """B=64 on host cores: the reference C runtime steps one sequence per
+    handle, so the batched figure is the fp32 torch restatement of
+    ``forward_step`` (the oracle, same operation sequence as the reference's
+    torch path) at B=64 with one torch thread per physical core."""
+    from oracle.torch_ref import TorchSunny
+    threads = min(16, physical_cores())
+    old = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        tr = TorchSunny(w, torch.float32)
+        st = tr.init_state(64)
+        idx = torch.from_numpy(np.random.default_rng(64).integers(0, w.cfg.vocab_size, 64))
+        with torch.no_grad():
+            _, st = tr.forward_step(idx, st)
+            times = []
+            deadline = time.perf_counter() + 15.0
+            while len(times) < 8 and time.perf_counter() < deadline:
+                t0 = time.perf_counter()
+                _, st = tr.forward_step(idx, st)
+                times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(old)
+    med = float(np.median(times))
+    log(f"[bench] cpu port forward_step B=64 fp32: {med*1e3:.1f} ms/step, {threads} threads")
+    return {"value": round(64 / med, 1), "unit": "tok/s (B=64)", "cores": threads, "host": host_cpu(),
+            "kind": "port", "ms_per_step": round(med * 1e3, 2),
+            "sample": f"SunnyNet-100M fp32, torch forward_step restatement at B=64, one warm-up "
+                      f"step then the median of {len(times)} steps"}
+
+
+def cpu_gemv_i4_baseline(w4):
+    """The reference's INT4 GEMV ``sn_gemv_i4`` (W4A8, group 32,
+    quant.c:89-154, OpenMP over rows) over one decode step's matrices: per
+    layer V, U, W_z, W_c, W_eff, then the head, quantized with the reference's
+    ``sn_quant_i4``. There is no INT4 SunnyNet step in the reference, so this
+    times the products alone."""
+    import ctypes
+
+    import oracle
+    from sunnynet_amd.blob import layer_matrices
+    threads = min(16, physical_cores())
+    if not oracle.ref_available():
+        return {"value": None, "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(),
+                "kind": "reference", "sample": "reference build absent"}
+    oracle.ref_lib("model").sn_set_threads(threads)
+    q4 = oracle.ref_lib("quant")
+    mats = []
+    for l in range(w4.cfg.layers):
+        M = layer_matrices(w4, l)
+        mats += [M.V, M.U, M.W_z, M.W_c, M.W_s_eff]
+    mats.append(np.ascontiguousarray(w4.embed.numpy(), np.float32))
+    packed = []
+    for W in mats:
+        W = np.ascontiguousarray(W, np.float32)
+        out, inn = W.shape
+        q = np.empty((out, inn // 2), np.uint8)
+        sc = np.empty((out, inn // 32), np.float32)
+        q4.sn_quant_i4(W.ctypes.data, q.ctypes.data, sc.ctypes.data, out, inn, 32)
+        x = np.random.default_rng(out + inn).standard_normal(inn).astype(np.float32)
+        y = np.empty(out, np.float32)
+        packed.append((q, sc, x, y, inn, out))
+
+    def step():
+        for q, sc, x, y, inn, out in packed:
+            q4.sn_gemv_i4(y.ctypes.data, x.ctypes.data, q.ctypes.data, sc.ctypes.data, inn, out, 32)
+    step()
+    times = []
+    deadline = time.perf_counter() + 10.0
+    while len(times) < 32 and time.perf_counter() < deadline:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nbytes = sum(q.nbytes + sc.nbytes for q, sc, *_ in packed)
+    log(f"[bench] cpu reference sn_gemv_i4 step products: {med*1e3:.2f} ms, {threads} threads")
+    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1, products only)", "cores": threads,
+            "host": host_cpu(), "kind": "reference", "ms_per_step": round(med * 1e3, 3),
+            "gbs": round(nbytes / med / 1e9, 2),
+            "sample": f"SunnyNet-100M INT4 g32 weights: the 61 products of one step (12 x V, U, W_z, "
+                      f"W_c, W_eff and the head) through sn_gemv_i4, median of {len(times)} steps"}
 
 
 def bench_rwkv7(cpu: bool):
@@ -389,12 +618,18 @@ def bench_rwkv7(cpu: bool):
         torch.cuda.synchronize()
         steps = out["steps"]
         ms = _time_ms(lambda: hm.decode_greedy(tok, steps)) / steps
+        kernel = ("k_rk_persist (the whole step)" if hm.persist_grid and B == 1 else
+                  "per-kernel step: k_rkq_ln, k_rkq_mm_q4, k_rkq_heads")
         hm.close()
         nb = wbytes + B * sbytes
+        ach = nb / (ms * 1e-3) / 1e9
         case = {"weights": "int4-g32", "B": B, "us_per_step": round(ms * 1e3, 2),
-                "tok_s": round(B / ms * 1e3, 1), "bytes_per_step": nb,
-                "hbm_gbs": round(nb / (ms * 1e-3) / 1e9, 2),
-                "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                "tok_s": round(B / ms * 1e3, 1),
+                "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                             "kernel": kernel, "bytes_per_step": nb,
+                             "note": "weights, plus the 64x64 head states read and written per "
+                                     "sequence"}}
         log(f"[bench] rwkv7 B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s")
         out["cases"].append(case)
     if cpu:
@@ -410,7 +645,7 @@ def cpu_rwkv7_baseline(w, tmp):
     from sunnynet_amd.rwkv7 import pack_rwkv7_blob
     threads = min(16, physical_cores())
     if not oracle.ref_available():
-        return {"value": None, "unit": "tok/s (B=1)", "cores": threads, "kind": "reference",
+        return {"value": None, "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(), "kind": "reference",
                 "sample": "reference build absent"}
     oracle.ref_lib("model").sn_set_threads(threads)     # process-wide OpenMP thread count
     p4 = os.path.join(tmp, "rk_q4.bin")
@@ -427,7 +662,7 @@ def cpu_rwkv7_baseline(w, tmp):
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     log(f"[bench] cpu reference sn_rk_step int4: {med*1e3:.2f} ms/token, {threads} threads")
-    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": threads, "kind": "reference",
+    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(), "kind": "reference",
             "ms_per_token": round(med * 1e3, 3),
             "sample": f"RWKV-7 same shape, INT4 group-64 blob (W4A8), 4 warm-up steps then median "
                       f"of {len(times)} single steps"}
@@ -463,10 +698,9 @@ def cpu_decode_baseline(path, cfg):
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     log(f"[bench] cpu {kind} sn_step 100M fp32: {med*1e3:.2f} ms/token, {threads} threads")
-    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": threads, "kind": kind,
+    return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(), "kind": kind,
             "ms_per_token": round(med * 1e3, 3),
-            "sample": f"SunnyNet-100M fp32, 16-token prefill then median of {len(times)} single steps; "
-                      "B=64 on this runtime is 64 sequential handles (64x the B=1 time)"}
+            "sample": f"SunnyNet-100M fp32, 16-token prefill then median of {len(times)} single steps"}
 
 
 def pmc_probe():
@@ -508,6 +742,125 @@ def pmc_probe():
     return 0
 
 
+def _m100_blobs(tmp):
+    from sunnynet_amd.blob import pack_sunny_blob
+    from sunnynet_amd.weights import gaussian_matmuls, init_sunnynet
+    w = init_sunnynet(SUNNY_100M, 1)
+    return {"fp32": _write_blob(tmp, "m100_fp32.bin", pack_sunny_blob(w)),
+            "int4": _write_blob(tmp, "m100_int4.bin", pack_sunny_blob(gaussian_matmuls(w, seed=3)))}
+
+
+def profile_sequence(which: str) -> int:
+    """Fixed launch sequences for rocprofv3 kernel-trace summaries:
+
+    b1: SunnyNet-100M (seed 1; INT4 g32 on N(0, 0.02) matmuls), a chunked
+        prefill of 1024 random ids, then 256 greedy steps at B=1, fp32 then INT4.
+    batch: 64 greedy steps from random tokens at fp32 B=64, INT4 B=8, INT4 B=32.
+    rwkv: RWKV-7 (12 layers, D=768, vocab 65536, seed-2 weights, INT4 g32 at
+        load), 8 warm-up then 64 greedy steps at B=1 and at B=64.
+    small: SunnyNet small (seed 0), prefill of 256 random ids, 64 greedy steps.
+    """
+    import tempfile
+
+    from sunnynet_amd.runtime.model import HipModel
+    dev = torch.device("cuda:0")
+    tmp = tempfile.mkdtemp(prefix="snhip_prof_")
+    g = torch.Generator(device="cpu").manual_seed(5)
+    if which == "rwkv":
+        from sunnynet_amd.runtime.rwkv7 import HipRwkv7
+        from sunnynet_amd.rwkv7 import RWKV_CFG4, init_rwkv7, pack_rwkv7_blob
+        cfg = RWKV_CFG4
+        path = _write_blob(tmp, "rk.bin", pack_rwkv7_blob(init_rwkv7(cfg, 2)))
+        for B in (1, 64):
+            hm = HipRwkv7(path, weights="int4", block=32, max_batch=B)
+            tok = torch.randint(0, cfg.vocab, (B,), generator=g, dtype=torch.int32).to(dev)
+            hm.decode_greedy(tok, 8)
+            hm.decode_greedy(tok, 64)
+            torch.cuda.synchronize()
+            log(f"[profile] rwkv7 int4 B={B}: 64 greedy steps (persistent grid {hm.persist_grid})")
+            hm.close()
+        return 0
+    if which == "small":
+        from sunnynet_amd.blob import pack_sunny_blob
+        from sunnynet_amd.config import SMALL
+        from sunnynet_amd.weights import init_sunnynet
+        cfg = SMALL
+        path = _write_blob(tmp, "small.bin", pack_sunny_blob(init_sunnynet(cfg, 0)))
+        hm = HipModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers)
+        ids = torch.randint(0, cfg.vocab_size, (1, 256), generator=g, dtype=torch.int32).to(dev)
+        tok = hm.prefill_batch(ids).argmax(1).int()
+        hm.decode_greedy(tok, 64)
+        torch.cuda.synchronize()
+        hm.close()
+        log("[profile] small fp32 B=1: prefill 256, 64 greedy steps")
+        return 0
+    cfg = SUNNY_100M
+    paths = _m100_blobs(tmp)
+    cases = [("fp32", 1), ("int4", 1)] if which == "b1" else [("fp32", 64), ("int4", 8), ("int4", 32)]
+    for fmt, B in cases:
+        hm = HipModel(paths[fmt], cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
+                      max_batch=B, weights=fmt, block=32)
+        if B == 1:
+            ids = torch.randint(0, cfg.vocab_size, (1, 1024), generator=g, dtype=torch.int32).to(dev)
+            tok = hm.prefill_batch(ids).argmax(1).int()
+            n = 256
+        else:
+            tok = torch.randint(0, cfg.vocab_size, (B,), generator=g, dtype=torch.int32).to(dev)
+            n = 64
+        hm.decode_greedy(tok, n)
+        torch.cuda.synchronize()
+        hm.close()
+        log(f"[profile] {fmt} B={B}: {n} greedy steps")
+    return 0
+
+
+def pmc_probe_decode() -> int:
+    """A short fixed sequence for `rocprofv3 --pmc` runs on the decode
+    kernels: 3 plain device copies of a 512 MiB array (calibrating
+    FETCH_SIZE / WRITE_SIZE against a known byte count), then SunnyNet-100M
+    INT4 g32 B=1 (one k_decode_persist launch of 16 greedy steps, twice),
+    fp32 B=64 (4 greedy steps, one k_decode_batch launch each) and RWKV-7
+    INT4 B=1 (one k_rk_persist launch of 16 steps, twice)."""
+    import tempfile
+
+    from sunnynet_amd.runtime.model import HipModel
+    from sunnynet_amd.runtime.rwkv7 import HipRwkv7
+    from sunnynet_amd.rwkv7 import RWKV_CFG4, init_rwkv7, pack_rwkv7_blob
+    dev = torch.device("cuda:0")
+    x = torch.randn(128 << 20, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log(f"[pmc] copy bytes/launch read {x.numel() * 4} write {x.numel() * 4}")
+    del x, y
+    cfg = SUNNY_100M
+    tmp = tempfile.mkdtemp(prefix="snhip_pmc_")
+    paths = _m100_blobs(tmp)
+    g = torch.Generator(device="cpu").manual_seed(11)
+    for fmt, B, n in (("int4", 1, 16), ("fp32", 64, 4)):
+        hm = HipModel(paths[fmt], cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
+                      max_batch=B, weights=fmt, block=32)
+        tok = torch.randint(0, cfg.vocab_size, (B,), generator=g, dtype=torch.int32).to(dev)
+        for _ in range(2):
+            hm.decode_greedy(tok, n)
+        torch.cuda.synchronize()
+        log(f"[pmc] SunnyNet-100M {fmt} B={B}: 2 x {n} greedy steps; algorithmic bytes/step "
+            f"{decode_step_bytes(cfg, fmt == 'int4', B)}")
+        hm.close()
+    rc = RWKV_CFG4
+    path = _write_blob(tmp, "rk.bin", pack_rwkv7_blob(init_rwkv7(rc, 2)))
+    hm = HipRwkv7(path, weights="int4", block=32, max_batch=1)
+    tok = torch.randint(0, rc.vocab, (1,), generator=g, dtype=torch.int32).to(dev)
+    for _ in range(2):
+        hm.decode_greedy(tok, 16)
+    torch.cuda.synchronize()
+    n = rc.matmul_params()
+    log(f"[pmc] RWKV-7 int4 B=1: 2 x 16 greedy steps; weight bytes/step {n // 2 + (n // 32) * 4}")
+    hm.close()
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -515,11 +868,17 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="all", choices=["all", "scan", "core", "decode"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--pmc-probe", action="store_true",
+    ap.add_argument("--pmc-probe", nargs="?", const="scan", choices=["scan", "decode"],
                     help="run the fixed launch sequence used for rocprofv3 --pmc and exit")
+    ap.add_argument("--profile", choices=["b1", "batch", "rwkv", "small"],
+                    help="run a fixed decode launch sequence for rocprofv3 --kernel-trace and exit")
     args = ap.parse_args(argv)
-    if args.pmc_probe:
+    if args.pmc_probe == "scan":
         return pmc_probe()
+    if args.pmc_probe == "decode":
+        return pmc_probe_decode()
+    if args.profile:
+        return profile_sequence(args.profile)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one GPU only: this build has no multi-GPU path "
             "(each channel / sequence shards with no communication; see DESIGN.md).")

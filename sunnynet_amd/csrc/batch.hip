@@ -696,7 +696,7 @@ snhip_status launch_decode_batch(const BatchArgs& a, int G, int blk, hipStream_t
     }
     BatchArgs args = a;
     void* kargs[] = {&args};
-    SNHIP_CHECK(hipLaunchCooperativeKernel(k, dim3(G), dim3(NT), kargs, 0, st));
+    SNHIP_CHECK(launch_persistent(k, dim3(G), dim3(NT), kargs, st));
     return SNHIP_OK;
 }
 

@@ -50,6 +50,16 @@ inline unsigned env_unsigned(const char* name, unsigned dflt, unsigned lo) {
     return v < (long)lo ? lo : (unsigned)v;
 }
 
+// Launches a grid-synchronizing persistent kernel whose grid is sized to
+// co-reside: cooperatively (the runtime checks residency), or, with
+// SNHIP_COOP=0, as an ordinary launch of the same grid (for tools that do not
+// handle cooperative launches; every grid-wide wait in these kernels is
+// bounded, so a grid that did not co-reside ends in a reported time-out).
+inline hipError_t launch_persistent(const void* k, dim3 grid, dim3 block, void** args, hipStream_t st) {
+    if (env_unsigned("SNHIP_COOP", 1, 0) == 0) return hipLaunchKernel(k, grid, block, args, 0, st);
+    return hipLaunchCooperativeKernel(k, grid, block, args, 0, st);
+}
+
 // Waits for this wave's outstanding LDS operations only (gfx9 s_waitcnt
 // encoding: vmcnt = 63, expcnt = 7, lgkmcnt = 0); global loads stay in flight.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }

@@ -103,7 +103,7 @@ snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipSt
     }
     PersistArgs args = a;
     void* kargs[] = {&args};
-    SNHIP_CHECK(hipLaunchCooperativeKernel(kernel_for(blk), dim3(nwg), dim3(threads_for(blk)), kargs, 0, st));
+    SNHIP_CHECK(launch_persistent(kernel_for(blk), dim3(nwg), dim3(threads_for(blk)), kargs, st));
     return SNHIP_OK;
 }
 

@@ -707,8 +707,7 @@ snhip_status launch_rk_persist(const RkPArgs& a, int G, hipStream_t st) {
     }
     RkPArgs args = a;
     void* kargs[] = {&args};
-    SNHIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_rk_persist), dim3(G), dim3(NT),
-                                           kargs, 0, st));
+    SNHIP_CHECK(launch_persistent(reinterpret_cast<const void*>(k_rk_persist), dim3(G), dim3(NT), kargs, st));
     return SNHIP_OK;
 }
 

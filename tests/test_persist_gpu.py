@@ -189,3 +189,25 @@ def test_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
     assert np.abs(a - orc.step([3])[0]).max() < TOL
     b = np.asarray(hm.step(5), np.float32)
     assert np.abs(b - orc.step([5])[0]).max() < TOL
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_ordinary_launch_equals_cooperative(gpu, small, monkeypatch, B):
+    """SNHIP_COOP=0 launches the same co-resident grid without the
+    cooperative flag (for tools that do not handle cooperative launches):
+    the B=1 persistent kernel and the batched one give the same tokens and
+    logits, bit for bit."""
+    w, buf, path = small
+    print(f"cooperative vs ordinary launch, B={B}", flush=True)
+    start = torch.arange(3, 3 + B, dtype=torch.int32, device=gpu)
+    res = []
+    for coop in ("1", "0"):
+        monkeypatch.setenv("SNHIP_COOP", coop)
+        hm = _model(path, SMALL, max_batch=B)
+        assert (hm.persistent_grid if B == 1 else hm.batch_grid) > 0
+        lg = torch.empty(B, SMALL.vocab_size, device=gpu)
+        toks = hm.decode_greedy(start, 12, logits=lg)
+        res.append((toks.cpu(), lg.cpu()))
+        hm.close()
+    assert torch.equal(res[0][0], res[1][0])
+    assert torch.equal(res[0][1], res[1][1])
