@@ -311,14 +311,16 @@ def cpu_scan_baseline(a, b, s0):
                       f"({med*1e3:.1f} ms each)"}
 
 
-def decode_bytes(cfg, int4: bool, block: int = 32) -> int:
+def decode_bytes(cfg, fmt: str, block: int = 32) -> int:
     """Weight bytes one decode step must read: every matmul and the head
-    (fp32: 4 B per weight; INT4: 0.5 B + one fp32 scale per group)."""
+    (fp32: 4 B per weight; fp16: 2 B; INT4: 0.5 B + one fp32 scale per group)."""
     n = matmul_params(cfg)
-    return int(n * 4) if not int4 else int(n // 2 + (n // block) * 4)
+    if fmt == "int4":
+        return int(n // 2 + (n // block) * 4)
+    return int(n * (2 if fmt == "fp16" else 4))
 
 
-def decode_step_bytes(cfg, int4: bool, B: int) -> int:
+def decode_step_bytes(cfg, fmt: str, B: int) -> int:
     """Algorithmic HBM bytes of one decode step: the weights, the per-layer
     vectors (norm gains and centres, conv taps, delta; 4 B each) and per
     sequence the embedding row, the state and history read and written, and
@@ -326,7 +328,7 @@ def decode_step_bytes(cfg, int4: bool, B: int) -> int:
     D, I, K, L, V = cfg.dim, cfg.inner, cfg.taps, cfg.layers, cfg.vocab_size
     small = (L * (2 * D + 2 * I + K * D + D) + 2 * D) * 4
     per_seq = D * 4 + 2 * L * K * D * 4 + V * 4
-    return decode_bytes(cfg, int4) + small + B * per_seq
+    return decode_bytes(cfg, fmt) + small + B * per_seq
 
 
 FP32_MFMA_TFLOPS = 157.3
@@ -336,7 +338,7 @@ def decode_roofline(cfg, fmt: str, B: int, us_per_step: float, kernel: str) -> d
     """Roofline of a decode step from its measured time: HBM for the
     weight-streaming cases, fp32 MFMA (2 flops per weight per sequence) for
     fp32 B >= 64 and INT4 B >= 32, where the products are dense contractions."""
-    nbytes = decode_step_bytes(cfg, fmt == "int4", B)
+    nbytes = decode_step_bytes(cfg, fmt, B)
     flops = 2 * matmul_params(cfg) * B
     sec = us_per_step * 1e-6
     if (fmt == "fp32" and B >= 64) or (fmt == "int4" and B >= 32):
@@ -461,7 +463,8 @@ def bench_decode(cpu: bool):
     out = {"model": "SunnyNet-100M L=12 D=1024 I=1536 R=512 V=32000",
            "steps": 256, "cases": []}
     g = torch.Generator(device="cpu").manual_seed(123)
-    for fmt, path, T, batches in (("fp32", p32, 1024, (1, 64)), ("int4", p4, 2048, (1, 8, 32))):
+    for fmt, path, T, batches in (("fp32", p32, 1024, (1, 64)), ("fp16", p32, 1024, (1,)),
+                                  ("int4", p4, 2048, (1, 8, 32))):
         for B in batches:
             hm = HipModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
                           max_batch=B, weights=fmt, block=32)
@@ -480,7 +483,7 @@ def bench_decode(cpu: bool):
             torch.cuda.synchronize()
             n = out["steps"]
             ms = _time_ms(lambda: hm.decode_greedy(tok, n)) / n
-            kernel = (f"k_decode_persist<{32 if fmt == 'int4' else 0}> (the whole step)"
+            kernel = (f"k_decode_persist<{ {'int4': 32, 'fp16': 16}.get(fmt, 0)}> (the whole step)"
                       if B == 1 and hm.persistent_grid else
                       "k_decode_batch (layers) + head GEMM + greedy argmax" if hm.batch_grid else
                       "per-kernel step")
@@ -495,6 +498,7 @@ def bench_decode(cpu: bool):
             out["cases"].append(case)
     if cpu:
         out["cpu_baseline"] = cpu_decode_baseline(p32, cfg)
+        out["cpu_baseline_f16"] = cpu_decode_baseline(p32, cfg, half=True)
         out["cpu_baseline_b64"] = cpu_decode_b64_baseline(w)
         out["cpu_baseline_int4_gemv"] = cpu_gemv_i4_baseline(w4)
     out["small"] = bench_decode_small(cpu)
@@ -668,20 +672,25 @@ def cpu_rwkv7_baseline(w, tmp):
                       f"of {len(times)} single steps"}
 
 
-def cpu_decode_baseline(path, cfg):
+def cpu_decode_baseline(path, cfg, half: bool = False):
     """The reference sn_step on the fp32 blob (B = 1, host cores), after a
-    16-token prefill by stepping; bounded to a few seconds."""
+    16-token prefill by stepping; bounded to a few seconds. half: the
+    reference's sn_load_h handle (matrices held as fp16, sunnynet.c:455-579)."""
     import oracle
     threads = min(16, physical_cores())
     if oracle.ref_available():
         lib = oracle.ref_lib("model")
         lib.sn_set_threads(threads)
-        m = oracle.RefSnModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers)
+        m = oracle.RefSnModel(path, cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
+                              half=half)
         kind = "reference"
     else:
         m = None
         kind = "port"
     if m is None:
+        if half:
+            return {"value": None, "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(),
+                    "kind": "reference", "sample": "reference build absent"}
         blob = np.fromfile(path, np.uint8)
         orc = oracle.SnOracle(blob)
         os.environ["OMP_NUM_THREADS"] = str(threads)
@@ -696,11 +705,15 @@ def cpu_decode_baseline(path, cfg):
         t0 = time.perf_counter()
         step(len(times) + 100)
         times.append(time.perf_counter() - t0)
+    if m is not None:
+        m.close()
     med = float(np.median(times))
-    log(f"[bench] cpu {kind} sn_step 100M fp32: {med*1e3:.2f} ms/token, {threads} threads")
+    log(f"[bench] cpu {kind} sn_step 100M {'fp16 (sn_load_h)' if half else 'fp32'}: {med*1e3:.2f} ms/token, "
+        f"{threads} threads")
     return {"value": round(1.0 / med, 2), "unit": "tok/s (B=1)", "cores": threads, "host": host_cpu(), "kind": kind,
             "ms_per_token": round(med * 1e3, 3),
-            "sample": f"SunnyNet-100M fp32, 16-token prefill then median of {len(times)} single steps"}
+            "sample": f"SunnyNet-100M {'fp16 weights (sn_load_h)' if half else 'fp32'}, 16-token prefill "
+                      f"then median of {len(times)} single steps"}
 
 
 def pmc_probe():
@@ -846,7 +859,7 @@ def pmc_probe_decode() -> int:
             hm.decode_greedy(tok, n)
         torch.cuda.synchronize()
         log(f"[pmc] SunnyNet-100M {fmt} B={B}: 2 x {n} greedy steps; algorithmic bytes/step "
-            f"{decode_step_bytes(cfg, fmt == 'int4', B)}")
+            f"{decode_step_bytes(cfg, fmt, B)}")
         hm.close()
     rc = RWKV_CFG4
     path = _write_blob(tmp, "rk.bin", pack_rwkv7_blob(init_rwkv7(rc, 2)))

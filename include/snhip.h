@@ -38,8 +38,9 @@ typedef struct SnHipModel SnHipModel;
                                    group format; embedding lookup stays fp32  */
 #define SNHIP_WEIGHTS_F16   3   /* sn_load_h's values (sunnynet.c:455-579): the
                                    same matrices rounded to fp16 (nearest even)
-                                   at load; this backend holds and multiplies
-                                   them as fp32 (no byte saving yet)          */
+                                   at load; the single-sequence persistent step
+                                   reads them as fp16 (half the bytes), the
+                                   other paths from an fp32 copy of the values */
 
 /* sunnynet.h:22-23: B = 1, fp32 weights. */
 SnHipModel* snhip_load(const char* path, int vocab, int dim, int inner, int rank,

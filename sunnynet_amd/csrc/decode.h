@@ -25,6 +25,7 @@ struct PMat {
     const uint8_t* q;
     const float* sc;
     int M;
+    const uint16_t* h;      // fp16 copy of w (the fp16 format), else null
 };
 
 struct PLayer {

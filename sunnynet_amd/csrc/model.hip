@@ -303,6 +303,7 @@ struct Mat {
     float* w = nullptr;
     uint8_t* q = nullptr;
     float* sc = nullptr;
+    uint16_t* h = nullptr;    // fp16 bits of w (the fp16 format; read by the B=1 persistent kernel)
 };
 
 struct Layer {
@@ -796,7 +797,42 @@ bool upload_new(SnHipModel* m, Mat& M, const float* src, int in, int out, float*
     return store_ok(m, S) && upload_mat(m, M, src, in, out, tmp_in, tmp_out, S, 0, perm_u);
 }
 
-PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M}; }
+PMat pmat(const Mat& W) { return PMat{W.w, W.q, W.sc, W.M, W.h}; }
+
+__global__ void k_f32_to_f16(const float* __restrict__ x, uint16_t* __restrict__ h, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = __builtin_bit_cast(uint16_t, (_Float16)x[i]);
+}
+
+// fp16 storage of rows x in values of w (already rounded to fp16 values, so
+// the conversion is exact) into M.h.
+bool make_f16(SnHipModel* m, Mat& M, const float* w, size_t rows, size_t in) {
+    const long n = (long)(rows * in);
+    M.h = dalloc<uint16_t>(m, (size_t)n);
+    if (!M.h) return false;
+    hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr, w, M.h, n);
+    return hipGetLastError() == hipSuccess;
+}
+
+// The fp16 format: the five matrices and the head held as fp16 for the
+// single-sequence persistent step (half the bytes it streams, as sn_load_h
+// holds them, sunnynet.c:455-579); the other paths multiply the same values
+// from the fp32 copy.
+bool make_f16_copies(SnHipModel* m) {
+    for (Layer& A : m->layers) {
+        // V and W_eff share one storage: V's rows, then W_eff's
+        if (!make_f16(m, A.V, A.V.w, (size_t)A.V.M + A.Ws.M, A.V.Kd) ||
+            !make_f16(m, A.U, A.U.w, A.U.M, A.U.Kd) || !make_f16(m, A.Wz, A.Wz.w, A.Wz.M, A.Wz.Kd) ||
+            !make_f16(m, A.Wc, A.Wc.w, A.Wc.M, A.Wc.Kd))
+            return false;
+    }
+    return make_f16(m, m->head, m->head.w, m->head.M, m->head.Kd) && hipDeviceSynchronize() == hipSuccess;
+}
+
+// Weight-format code of the B=1 persistent kernel: 0 fp32, 16 fp16, else the INT4 group.
+int persist_blk(const SnHipModel* m) {
+    return m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : (m->half && m->head.h ? 16 : 0);
+}
 
 // The device layer table of the persistent kernels (built once).
 bool layer_table(SnHipModel* m) {
@@ -845,7 +881,7 @@ void setup_persist(SnHipModel* m) {
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return;
-    const int occ = persist_occupancy(m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0);
+    const int occ = persist_occupancy(persist_blk(m));
     if (occ < 1) return;
     int cap = std::min(m->D / 4, ncu);
     if (const char* e = getenv("SNHIP_PERSIST_WG")) cap = atoi(e);
@@ -1082,6 +1118,11 @@ SnHipModel* load_model(const char* path, int vocab, int dim, int inner, int rank
         return nullptr;
     }
     m->persist_spin = env_unsigned("SNHIP_PERSIST_SPIN", m->persist_spin, 1);
+    if (m->half && m->wfmt == SNHIP_WEIGHTS_F32 && !make_f16_copies(m)) {
+        set_last_error("fp16 weight copies: device allocation or conversion failed");
+        free_model(m);
+        return nullptr;
+    }
     setup_persist(m);
     setup_batch(m);
     m->ready = 1;
@@ -1524,7 +1565,7 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
     a.greedy = greedy ? 1 : 0;
     a.spin_limit = m->persist_spin;
     a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
-    const int blk = m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0;
+    const int blk = persist_blk(m);
     for (int done = 0; done < n_steps;) {
         const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
         // Epochs restart at 1 in every launch: clear the words of the last one.

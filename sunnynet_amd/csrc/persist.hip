@@ -75,10 +75,12 @@ extern "C" int snhip_persist_clk(unsigned long long* out) {
 #endif
 
 namespace {
-// fp32 rows stream more bytes per phase: 8 waves per workgroup measured
-// faster for them, 16 for INT4.
-int threads_for(int blk) { return blk == 0 ? 512 : 1024; }
-const void* kernel_for(int blk) { return blk == 0 ? nt512::kernel_for(0) : nt1024::kernel_for(blk); }
+// fp32 and fp16 rows stream more bytes per phase: 8 waves per workgroup
+// measured faster for fp32, 16 for INT4.
+int threads_for(int blk) { return blk == 0 || blk == 16 ? 512 : 1024; }
+const void* kernel_for(int blk) {
+    return blk == 0 || blk == 16 ? nt512::kernel_for(blk) : nt1024::kernel_for(blk);
+}
 }  // namespace
 
 int persist_occupancy(int blk) {

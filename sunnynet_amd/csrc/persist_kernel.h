@@ -36,6 +36,19 @@ __device__ __forceinline__ uint4 ldgq(const uint8_t* p) {
     const u32x4v v = *(g_u32x4*)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) const u32x2v g_u32x2;
+// Four fp16 weights (8 bytes) and their exact fp32 values.
+__device__ __forceinline__ uint2 ldgh4(const uint16_t* p) {
+    const u32x2v v = *(g_u32x2*)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float4 h4f(uint2 h) {
+    return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)),
+                       (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)),
+                       (float)__builtin_bit_cast(_Float16, (uint16_t)(h.y & 0xFFFFu)),
+                       (float)__builtin_bit_cast(_Float16, (uint16_t)(h.y >> 16)));
+}
 typedef __attribute__((address_space(3))) float l_f32;
 typedef __attribute__((address_space(3))) const f32x4v l_f32x4;
 __device__ __forceinline__ float4 lds4(const l_f32* p) {
@@ -201,6 +214,7 @@ static_assert(sizeof(Geo) == 64, "Geo is read as four 16-byte words");
 
 struct Job {
     const float* w;
+    const uint16_t* h;
     const uint8_t* q;
     const float* sc;
     const l_f32* x;
@@ -212,20 +226,25 @@ __device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, in
 
 __device__ __forceinline__ int job_row(const Geo& g, int j) { return j < g.n1 ? g.r0 + j * g.s0 : g.r1 + (j - g.n1); }
 
+// Weight formats of the template argument BLK: 0 fp32, 16 fp16 (both rows of
+// K contiguous values), 32 / 64 INT4 groups.
+constexpr bool is_i4(int blk) { return blk == 32 || blk == 64; }
+
 template <int BLK>
 struct Pool {
-    static constexpr int QW = BLK ? BLK / 32 : 1;    // uint4 per INT4 group
-    static constexpr int MU = 2;                     // INT4 units per batch
-    float4 wf[BLK ? 1 : CAPF];
-    uint4 wq[BLK ? MU : 1][QW];
-    float wsc[BLK ? MU : 1];
+    static constexpr int QW = is_i4(BLK) ? BLK / 32 : 1;    // uint4 per INT4 group
+    static constexpr int MU = 2;                            // INT4 units per batch
+    float4 wf[BLK == 0 ? CAPF : 1];
+    uint2 wh[BLK == 16 ? CAPF : 1];
+    uint4 wq[is_i4(BLK) ? MU : 1][QW];
+    float wsc[is_i4(BLK) ? MU : 1];
 };
 
 // The lane's slice of the job's input vector: fp32 nothing (read per item);
 // INT4 the quads of its group (low and high halves), zero past the row.
 template <int BLK>
 struct XCache {
-    float4 q[BLK ? BLK / 4 : 1];
+    float4 q[is_i4(BLK) ? BLK / 4 : 1];
 };
 
 template <int BLK>
@@ -241,7 +260,7 @@ __device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, in
     g.xsel = hi ? 1 : 0;
     g.pad = 0;
     const int nw = g.cnt > g.wl ? (g.cnt - g.wl + g.nwp - 1) / g.nwp : 0;   // the wave's rows
-    if constexpr (BLK == 0) {
+    if constexpr (!is_i4(BLK)) {
         g.nk4 = (K + 255) >> 8;
         g.ng = 0; g.lseg = 6; g.rpp = 1;
         g.nb = (nw * g.nk4 + CAPF - 1) / CAPF;
@@ -262,7 +281,7 @@ __device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, in
 template <int BLK>
 __device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int lane) {
     const Geo& g = J.g;
-    if constexpr (BLK == 0) {
+    if constexpr (!is_i4(BLK)) {
 #pragma unroll
         for (int s = 0; s < CAPF; ++s) {
             const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
@@ -270,7 +289,9 @@ __device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int
             const int k = i * 256 + lane * 4;
             const bool ok = jl < g.cnt && k < g.K;
             const int row = job_row(g, g.base + jl);
-            P.wf[s] = ldg4(J.w + (ok ? (size_t)(uint32_t)(row * g.K + k) : 0));
+            const size_t off = ok ? (size_t)(uint32_t)(row * g.K + k) : 0;
+            if constexpr (BLK == 16) P.wh[s] = ldgh4(J.h + off);
+            else P.wf[s] = ldg4(J.w + off);
         }
     } else {
         constexpr int MU = Pool<BLK>::MU;
@@ -291,7 +312,7 @@ __device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int
 
 template <int BLK>
 __device__ __forceinline__ void xcache_load(const Job& J, XCache<BLK>& X, int lane) {
-    if constexpr (BLK != 0) {
+    if constexpr (is_i4(BLK)) {
         const Geo& g = J.g;
         const int lg = min(lane & ((1 << g.lseg) - 1), g.ng - 1);
 #pragma unroll
@@ -301,8 +322,8 @@ __device__ __forceinline__ void xcache_load(const Job& J, XCache<BLK>& X, int la
 
 // epi(j, row, value, writer): `writer` is true on exactly one lane per row.
 // Every slot's loads are valid addresses; only rows of the job reach epi.
-template <class Epi>
-__device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<0>& P, int lane, float& pacc,
+template <int BLK, class Epi>
+__device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<BLK>& P, int lane, float& pacc,
                                             Epi&& epi) {
     const Geo& g = J.g;
     float4 xs[CAPF];
@@ -316,7 +337,7 @@ __device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<0>& 
         const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
         const int jl = g.wl + g.nwp * mr;
         if (i * 256 + lane * 4 < g.K) {
-            const float4 w4 = P.wf[s];
+            const float4 w4 = BLK == 16 ? h4f(P.wh[s]) : P.wf[s];
             pacc = pacc + (fmaf(w4.x, xs[s].x, w4.y * xs[s].y) + fmaf(w4.z, xs[s].z, w4.w * xs[s].w));
         }
         if (i == g.nk4 - 1) {
@@ -397,7 +418,7 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
 template <int BLK, class Epi>
 __device__ __forceinline__ void compute(const Job& J, int b, const Pool<BLK>& P, const XCache<BLK>& X, int lane,
                                         float& pacc, Epi&& epi) {
-    if constexpr (BLK == 0) compute_f32(J, b, P, lane, pacc, epi);
+    if constexpr (!is_i4(BLK)) compute_f32<BLK>(J, b, P, lane, pacc, epi);
     else compute_i4<BLK>(J, b, P, X, lane, epi);
 }
 
@@ -449,7 +470,7 @@ __device__ __forceinline__ void prefetch_job(const Job& J, Pool<BLK>& p0, int la
 // (q ng + g) * 4 (consecutive lanes, consecutive 16 bytes).
 template <int BLK>
 __device__ __forceinline__ int sidx(int i, int K) {
-    if constexpr (BLK == 0) return i;
+    if constexpr (!is_i4(BLK)) return i;
     else return ((((i % BLK) >> 2) * (K / BLK) + i / BLK) << 2) + (i & 3);
 }
 
@@ -536,7 +557,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
             const PLayer* Ly = lt + (p >> 2);
             W = t == 0 ? Ly->VW : t == 1 ? Ly->U : t == 2 ? Ly->Wz : Ly->Wc;
         }
-        J.w = W.w; J.q = W.q; J.sc = W.sc;
+        J.w = W.w; J.h = W.h; J.q = W.q; J.sc = W.sc;
         return J;
     };
 
@@ -773,6 +794,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
 
 const void* kernel_for(int blk) {
     return blk == 0 ? (const void*)k_decode_persist<0>
+         : blk == 16 ? (const void*)k_decode_persist<16>
          : blk == 32 ? (const void*)k_decode_persist<32>
                      : (const void*)k_decode_persist<64>;
 }

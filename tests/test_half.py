@@ -70,3 +70,39 @@ def test_half_weights_match_rounded_oracle(gpu, tmp_path, B):
         b = orc.step(toks)
         assert np.abs(a - b).max() < TOL
         assert np.array_equal(a.argmax(1), b.argmax(1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg_name", ["small", "100m"])
+def test_half_storage_step_equals_fp32_step_on_rounded_weights(gpu, tmp_path, cfg_name):
+    """The fp16 format stores the matrices as fp16 for the single-sequence
+    persistent step (half the bytes streamed) and converts them in registers:
+    its greedy chain and logits equal, bit for bit, the fp32 persistent step
+    on a blob holding the same fp16-rounded values (same kernel geometry,
+    same values multiplied)."""
+    import torch
+    from sunnynet_amd.config import SUNNY_100M
+    from sunnynet_amd.runtime.model import HipModel
+    cfg = {"small": SMALL, "100m": SUNNY_100M}[cfg_name]
+    w = init_sunnynet(cfg, 0 if cfg is SMALL else 1)
+    p32 = tmp_path / "f32.bin"
+    p32.write_bytes(pack_sunny_blob(w))
+    prd = tmp_path / "rounded.bin"
+    prd.write_bytes(half_blob(w))
+    dims = (cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers)
+    print(f"fp16 storage vs fp32 on rounded weights: {cfg_name}", flush=True)
+    hh = HipModel(p32, *dims, half=True)
+    hr = HipModel(prd, *dims)
+    assert hh.persistent_grid > 0 and hr.persistent_grid > 0
+    start = torch.tensor([7], dtype=torch.int32, device=gpu)
+    lh = torch.empty(1, cfg.vocab_size, device=gpu)
+    lr = torch.empty(1, cfg.vocab_size, device=gpu)
+    th = hh.decode_greedy(start, 24, logits=lh)
+    tr = hr.decode_greedy(start, 24, logits=lr)
+    assert torch.equal(th, tr)
+    assert torch.equal(lh, lr)
+    # and the one-step surface: host logits of a fresh pair of handles
+    hh.reset(); hr.reset()
+    for t in (5, 900, 31):
+        assert hh.step(t) == hr.step(t)
+    hh.close(); hr.close()
