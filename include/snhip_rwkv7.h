@@ -51,6 +51,13 @@ void snhip_rk_reset(SnHipRwkv7* m);
 /* rwkv7.h:21-22: sequence 0; logits host, length vocab. */
 void snhip_rk_step(SnHipRwkv7* m, int token, float* logits);
 void snhip_rk_prefill(SnHipRwkv7* m, const int* tokens, int n, float* logits);
+/* rwkv7.h:24-25 (sn_rk_dbg, rwkv7.c:366-374): sequence 0 steps `token`
+ * through layers 0..layer (their state advances, later layers are untouched)
+ * on the per-kernel step, which repeats the reference's rounding, and out
+ * (host, 9 * dim floats) receives that layer's xn, r, k, v, a, g, ww, y and
+ * output x, each (dim,), in the reference's order and bit for bit.
+ * SNHIP_E_INVAL for a bad token or layer. */
+snhip_status snhip_rk_dbg(SnHipRwkv7* m, int token, int layer, float* out);
 /* rwkv7.h:27-28 */
 int snhip_rk_vocab(const SnHipRwkv7* m);
 int snhip_rk_ready(const SnHipRwkv7* m);

@@ -363,6 +363,7 @@ def ref_lib(name: str):
         lib.sn_rk_prefill.argtypes = [V, V, I, V]
         lib.sn_rk_vocab.argtypes = [V]
         lib.sn_rk_vocab.restype = I
+        lib.sn_rk_dbg.argtypes = [V, I, I, V]
     elif name == "scan":
         lib.scan_f32.argtypes = [V, V, V, V, V, I, I, I]
         lib.scan_bwd_f32.argtypes = [V, V, V, V, V, V, V, V, I, I, I]
@@ -440,6 +441,11 @@ class RefRk:
     def step(self, token: int) -> np.ndarray:
         self._lib.sn_rk_step(self._h, int(token), _f(self._logits))
         return self._logits.copy()
+
+    def dbg(self, token: int, layer: int, dim: int) -> np.ndarray:
+        out = np.empty(9 * dim, np.float32)
+        self._lib.sn_rk_dbg(self._h, int(token), int(layer), _f(out))
+        return out.reshape(9, dim)
 
     def close(self):
         if getattr(self, "_h", None):

@@ -99,6 +99,7 @@ _SIGS = {
     "snhip_rk_step": (None, [V, INT, V]),
     "snhip_rk_prefill": (None, [V, V, INT, V]),
     "snhip_rk_vocab": (INT, [V]),
+    "snhip_rk_dbg": (I32, [V, INT, INT, V]),
     "snhip_rk_ready": (INT, [V]),
     "snhip_rk_set_stream": (I32, [V, V]),
     "snhip_rk_max_batch": (I32, [V]),

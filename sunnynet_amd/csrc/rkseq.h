@@ -75,6 +75,7 @@ struct RkqHeadArgs {
     size_t s_bstride;
     float* y;            // (B, D)
     int D, NH, first;
+    float* dbg;          // if set: sequence 0's k, v, a, ww at dbg + 2D, 3D, 4D, 6D (rwkv7.c:308-319)
 };
 snhip_status launch_rkq_heads(const RkqHeadArgs& a, int B, hipStream_t st);
 

@@ -547,6 +547,12 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
     const float av = refmath::sigmoid(da + a0);
     const float kkv = kv * kkw;
     const float k2 = kv + kv * (av - 1.0f) * kaw;
+    if (A.dbg && b == 0) {
+        A.dbg[(size_t)2 * A.D + c] = k2;
+        A.dbg[(size_t)3 * A.D + c] = vv;
+        A.dbg[(size_t)4 * A.D + c] = av;
+        A.dbg[(size_t)6 * A.D + c] = ww;
+    }
     w_[t] = ww; k_[t] = k2; v_[t] = vv; a_[t] = av; kn_[t] = kkv; r_[t] = rv;
     dt_[t] = rv * k2 * rkw;
     __syncthreads();

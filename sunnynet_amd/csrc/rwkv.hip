@@ -536,7 +536,10 @@ struct MMList {
     }
 };
 
-snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, hipStream_t st) {
+// dbg (device, 9 D floats): run layers 0..dbg_layer only and leave sequence
+// 0's intermediates of that layer there in the reference's order (rwkv7.c:308-319).
+snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, hipStream_t st,
+                          int dbg_layer = -1, float* dbg = nullptr) {
     const int D = m->D, F = m->F, NH = m->NH, L = m->L, HS = m->HS;
     const size_t s_bstride = (size_t)L * NH * HS * HS, sh_bstride = (size_t)L * 2 * D;
     const int ldl = 4 * kMaxRank;
@@ -551,8 +554,10 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
     ln.tok = m->tok; ln.embed = m->embed; ln.g = m->en_w; ln.c = m->en_b; ln.out = m->x;
     if ((rc = launch_rkq_ln(ln, B, st)) != SNHIP_OK) return rc;
     MMList mm{B};
-    for (int l = 0; l < L; ++l) {
+    const int nl = dbg ? dbg_layer + 1 : L;
+    for (int l = 0; l < nl; ++l) {
         const RkLayer& A = m->layers[l];
+        float* dl = dbg && l == dbg_layer ? dbg : nullptr;
         float* sh = m->shift + (size_t)l * 2 * D;
         ln.mode = RKQ_LN_MIX1;
         ln.x = m->x; ln.g = A.ln1w; ln.c = A.ln1b; ln.lerp = A.lerp; ln.shift = sh; ln.out = m->X6;
@@ -587,6 +592,7 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         H.y = m->y;
         H.D = D; H.NH = NH;
         H.first = l == 0;
+        H.dbg = dl;
         if ((rc = launch_rkq_heads(H, B, st)) != SNHIP_OK) return rc;
         if ((rc = mm.add(A.o, m->y, D, m->x, D, RKQ_ADD)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
@@ -597,6 +603,16 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
         if ((rc = mm.add(A.cmv, m->ck, F, m->x, D, RKQ_ADD)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        if (dl) {
+            // xn (the LayerNorm output, kept as shift_0), r, g, y and the layer's x
+            const size_t n = (size_t)D * sizeof(float);
+            SNHIP_CHECK(hipMemcpyAsync(dl, sh, n, hipMemcpyDeviceToDevice, st));
+            SNHIP_CHECK(hipMemcpyAsync(dl + D, m->r, n, hipMemcpyDeviceToDevice, st));
+            SNHIP_CHECK(hipMemcpyAsync(dl + 5 * D, m->g, n, hipMemcpyDeviceToDevice, st));
+            SNHIP_CHECK(hipMemcpyAsync(dl + 7 * D, m->y, n, hipMemcpyDeviceToDevice, st));
+            SNHIP_CHECK(hipMemcpyAsync(dl + 8 * D, m->x, n, hipMemcpyDeviceToDevice, st));
+            return SNHIP_OK;
+        }
     }
     ln.mode = RKQ_LN_PLAIN;
     ln.x = m->x; ln.g = m->on_w; ln.c = m->on_b; ln.out = m->nrm;
@@ -728,6 +744,27 @@ void snhip_rk_step(SnHipRwkv7* m, int token, float* logits) {
 
 void snhip_rk_prefill(SnHipRwkv7* m, const int* tokens, int n, float* logits) {
     (void)prefill_host(m, tokens, n, logits);
+}
+
+snhip_status snhip_rk_dbg(SnHipRwkv7* m, int token, int layer, float* out) {
+    if (!m || !out || layer < 0 || layer >= m->L || token < 0 || token >= m->vocab) return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
+    const size_t n = (size_t)9 * m->D;
+    float* d = ralloc<float>(m, n);
+    if (!d) return SNHIP_E_NOMEM;
+    const int32_t t = token;
+    snhip_status rc = SNHIP_OK;
+    if (hipMemcpyAsync(m->tok, &t, sizeof(int32_t), hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+        hipEventRecord(m->ev_in, m->stream) != hipSuccess || hipStreamWaitEvent(m->work, m->ev_in, 0) != hipSuccess)
+        rc = SNHIP_E_DEVICE;
+    if (rc == SNHIP_OK) rc = enqueue_step(m, 1, m->logits, false, m->work, layer, d);
+    if (rc == SNHIP_OK && (hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, m->work) != hipSuccess ||
+                           hipStreamSynchronize(m->work) != hipSuccess))
+        rc = SNHIP_E_DEVICE;
+    (void)hipStreamSynchronize(m->work);
+    for (auto it = m->allocs.begin(); it != m->allocs.end(); ++it)
+        if (*it == d) { (void)hipFree(d); m->allocs.erase(it); break; }
+    return rc;
 }
 
 int snhip_rk_vocab(const SnHipRwkv7* m) { return m ? m->vocab : 0; }

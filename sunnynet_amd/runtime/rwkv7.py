@@ -79,6 +79,16 @@ class HipRwkv7:
     def logits(self) -> list:
         return self._logits.tolist()
 
+    def dbg(self, token: int, layer: int) -> np.ndarray:
+        """rwkv7_c.py:98-101 / sn_rk_dbg: steps sequence 0 through layers
+        0..layer and returns that layer's intermediates (9, dim): xn, r, k, v,
+        a, g, ww, y and the layer's output x."""
+        out = np.empty(9 * self.dim, np.float32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_rk_dbg(self._h, int(token), int(layer), out.ctypes.data),
+                      "snhip_rk_dbg")
+        return out.reshape(9, self.dim)
+
     def prefill(self, tokens) -> list:
         toks = np.ascontiguousarray(np.asarray([int(t) for t in tokens], np.int32))
         self._bind_stream()

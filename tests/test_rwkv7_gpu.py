@@ -307,3 +307,31 @@ def test_loader_rejects_truncated_and_malformed_blobs(gpu, tiny, tmp_path):
         h = L.snhip_rk_load(str(src).encode())
         assert h
         L.snhip_rk_free(h)
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_dbg_equals_reference_sn_rk_dbg(gpu, tiny, monkeypatch, ref_built, layer):
+    """snhip_rk_dbg mirrors sn_rk_dbg (rwkv7.c:366-374): after the same steps
+    on both handles, the nine intermediates of the layer (xn, r, k, v, a, g,
+    ww, y, x) equal the reference's own dump bit for bit, and both handles
+    keep stepping identically afterwards (the dump advanced the same
+    layers' state)."""
+    w, p32 = tiny[0], tiny[1]
+    monkeypatch.setenv("SNHIP_RK_PERSIST", "0")      # the exact per-kernel step before the dump
+    hm = HipRwkv7(p32, RWKV_TINY.vocab)
+    ref = oracle.RefRk(p32, RWKV_TINY.vocab)
+    for t in (5, 77, 300):
+        assert np.array_equal(np.asarray(hm.step(t), np.float32), ref.step(t))
+    print(f"rwkv7 dbg layer {layer}", flush=True)
+    a = hm.dbg(41, layer)
+    b = ref.dbg(41, layer, RWKV_TINY.dim)
+    for i, name in enumerate(("xn", "r", "k", "v", "a", "g", "ww", "y", "x")):
+        assert np.array_equal(a[i], b[i]), name
+    for t in (9, 200):
+        assert np.array_equal(np.asarray(hm.step(t), np.float32), ref.step(t))
+    with pytest.raises(RuntimeError):
+        hm.dbg(RWKV_TINY.vocab, 0)
+    with pytest.raises(RuntimeError):
+        hm.dbg(1, RWKV_TINY.layers)
+    hm.close()
+    ref.close()
