@@ -38,7 +38,8 @@ constexpr int kRkqMaxJobs = 8;
 // Jobs share the weight format: block 0 = fp32, 32 or 64 = INT4 group.
 snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStream_t st);
 // The same with the INT4 workgroup shape given: nc consumer waves of s chains
-// of 4 sequences (nc in {1, 2, 4}, s in {1, 2}, not 4 x 2); 0 = chosen by B.
+// of 4 sequences (nc in {1, 2, 4}, s in {1, 2}, not 4 x 2), or s = 16: one
+// 16x16x1 chain of 16 sequences per consumer; 0 = chosen by B and the grid.
 snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int nc, int s,
                                hipStream_t st);
 

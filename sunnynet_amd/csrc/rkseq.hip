@@ -29,6 +29,7 @@ namespace snhip {
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr float kR2 = 0.6065306597126334f;   // 1/sqrt(e), rwkv7.c:38
 constexpr float kEpsGroup = 6.4e-4f;          // rwkv7.c:39
@@ -276,6 +277,26 @@ __device__ __forceinline__ void rkq_finish(const RkqJob& J, int B, int blk, int 
     }
 }
 
+// One output (sequence sq, column out) of a chain sum v: the scalar tail
+// past the last multiple of 8 as in rkq_finish, then the epilogue.
+__device__ __forceinline__ void rkq_finish1(const RkqJob& J, int B, int blk, int sq, int out, float v) {
+    if (out >= J.M || sq >= B) return;
+    if (out >= (J.M & ~7)) {
+        const float* x = J.X + (size_t)sq * J.ldx;
+        float a2 = 0.0f;
+        for (int k = 0; k < J.Kd; ++k) a2 = a2 + x[k] * dequant_at(J, out, k, blk);
+        v = a2;
+    }
+    float* y = J.Y + (size_t)sq * J.ldy + out;
+    switch (J.epi) {
+    case RKQ_ADD: *y = *y + v; break;
+    case RKQ_RELU2: { const float r = v > 0.0f ? v : 0.0f; *y = r * r; break; }
+    case RKQ_TANH: *y = refmath::tanhf(v); break;
+    case RKQ_SIGMOID: *y = refmath::sigmoid(v); break;
+    default: *y = v; break;
+    }
+}
+
 // fp32 weights: one wave per 64 rows x S groups of 4 sequences; X of the
 // chunk in LDS, the lane's weight row read 32 inputs ahead.
 template <int S>
@@ -346,6 +367,82 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 constexpr int kRkqPF = 4;     // producer code prefetch, units
 constexpr int kRkqWD = 8;     // consumer weight window, blocks of 4 inputs (a half unit)
 
+// Producer wave h (0 or 1) of an INT4 product workgroup: converts half h of
+// every 64-input unit of rows orow.. into slot t % 3 of the LDS ring at
+// step t, one workgroup barrier per step, nsteps steps in all.
+template <int BLK>
+__device__ __forceinline__ void rkq_produce(const RkqJob& J, int h, int l, int orow, int nu, int nsteps,
+                                            float4 (*wring)[kRkqU / 4][64]) {
+    const int Kd = J.Kd;
+    constexpr int NQ = BLK / 32;
+    const uint8_t* qrow = J.q + (size_t)orow * (size_t)(Kd / 2);
+    const float* srow = J.sc + (size_t)orow * (size_t)(Kd / BLK);
+    uint4 qw[kRkqPF][NQ];
+    float sw[kRkqPF];
+    // Branch-free loads: a unit past the end reads the last half again
+    // (never converted), so no wait depends on control flow.
+    auto load = [&](int u, uint4 (&q)[NQ], float& s) {
+        const int k = min(u * kRkqU + 32 * h, Kd - 32);
+        if (BLK == 32) {
+            q[0] = *reinterpret_cast<const uint4*>(qrow + k / 2);
+            s = srow[k / 32];
+        } else {
+            const int g = k / 64;
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) q[i] = *reinterpret_cast<const uint4*>(qrow + g * 32 + 16 * i);
+            s = srow[g];
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < kRkqPF; ++p) load(p, qw[p], sw[p]);
+    // Groups of kRkqPF steps: a group first issues the loads of the next
+    // group's units, then converts its own (loaded one group earlier), so
+    // every wait on codes covers loads a whole group old.
+    for (int t0 = 0; t0 < nsteps; t0 += kRkqPF) {
+        uint4 qn[kRkqPF][NQ];
+        float sn[kRkqPF];
+#pragma unroll
+        for (int p = 0; p < kRkqPF; ++p) load(t0 + kRkqPF + p, qn[p], sn[p]);
+#pragma unroll
+        for (int p = 0; p < kRkqPF; ++p) {
+            const int t = t0 + p;
+            // Converted unconditionally: past the last unit (or the
+            // missing half of a half unit) this writes leftovers to slot
+            // t % 3, which the consumers do not read at or after step t.
+            const float scg = sw[p], m8 = -8.0f * scg;
+            // Block i of the half: inputs 4i .. 4i+3. BLK 64: nibble h of
+            // bytes 4i .. 4i+3; BLK 32: low nibbles of word i for i < 4,
+            // high nibbles of word i - 4 after.
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint4 v = BLK == 32 ? qw[p][0] : qw[p][(i >> 2) % NQ];
+                const int wi = i & 3;
+                const uint32_t word = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
+                const bool hi = BLK == 32 ? i >= 4 : h == 1;
+                uint32_t nib = (hi ? (word >> 4) : word) & 0x0F0F0F0Fu;
+                // Opaque to the compiler, so that each byte converts with
+                // one v_cvt_f32_ubyteN (no field extraction).
+                asm volatile("" : "+v"(nib));
+                float4 w;
+                w.x = fmaf((float)(nib & 0xFFu), scg, m8);
+                w.y = fmaf((float)((nib >> 8) & 0xFFu), scg, m8);
+                w.z = fmaf((float)((nib >> 16) & 0xFFu), scg, m8);
+                w.w = fmaf((float)(nib >> 24), scg, m8);
+                wring[t % 3][8 * h + i][l] = w;
+            }
+            __syncthreads();
+            // keep each step's conversion after its barrier
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int p = 0; p < kRkqPF; ++p) {
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) qw[p][i] = qn[p][i];
+            sw[p] = sn[p];
+        }
+    }
+}
+
 template <int BLK, int NC, int S>
 __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArgs A) {
     constexpr int U4 = kRkqU / 4;                      // blocks per unit
@@ -368,74 +465,7 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
     // rounded up to the producer's prefetch depth (idle steps at the end).
     const int nsteps = (nu + 2 + kRkqPF - 1) / kRkqPF * kRkqPF;
     if (wv < kRkqNP) {
-        // ---- producer: half h of every unit
-        const int h = wv;
-        const uint8_t* qrow = J.q + (size_t)orow * (size_t)(Kd / 2);
-        const float* srow = J.sc + (size_t)orow * (size_t)(Kd / BLK);
-        uint4 qw[kRkqPF][NQ];
-        float sw[kRkqPF];
-        // Branch-free loads: a unit past the end reads the last half again
-        // (never converted), so no wait depends on control flow.
-        auto load = [&](int u, uint4 (&q)[NQ], float& s) {
-            const int k = min(u * kRkqU + 32 * h, Kd - 32);
-            if (BLK == 32) {
-                q[0] = *reinterpret_cast<const uint4*>(qrow + k / 2);
-                s = srow[k / 32];
-            } else {
-                const int g = k / 64;
-#pragma unroll
-                for (int i = 0; i < NQ; ++i) q[i] = *reinterpret_cast<const uint4*>(qrow + g * 32 + 16 * i);
-                s = srow[g];
-            }
-        };
-#pragma unroll
-        for (int p = 0; p < kRkqPF; ++p) load(p, qw[p], sw[p]);
-        // Groups of kRkqPF steps: a group first issues the loads of the next
-        // group's units, then converts its own (loaded one group earlier), so
-        // every wait on codes covers loads a whole group old.
-        for (int t0 = 0; t0 < nsteps; t0 += kRkqPF) {
-            uint4 qn[kRkqPF][NQ];
-            float sn[kRkqPF];
-#pragma unroll
-            for (int p = 0; p < kRkqPF; ++p) load(t0 + kRkqPF + p, qn[p], sn[p]);
-#pragma unroll
-            for (int p = 0; p < kRkqPF; ++p) {
-                const int t = t0 + p;
-                // Converted unconditionally: past the last unit (or the
-                // missing half of a half unit) this writes leftovers to slot
-                // t % 3, which the consumers do not read at or after step t.
-                const float scg = sw[p], m8 = -8.0f * scg;
-                // Block i of the half: inputs 4i .. 4i+3. BLK 64: nibble h of
-                // bytes 4i .. 4i+3; BLK 32: low nibbles of word i for i < 4,
-                // high nibbles of word i - 4 after.
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint4 v = BLK == 32 ? qw[p][0] : qw[p][(i >> 2) % NQ];
-                    const int wi = i & 3;
-                    const uint32_t word = wi == 0 ? v.x : wi == 1 ? v.y : wi == 2 ? v.z : v.w;
-                    const bool hi = BLK == 32 ? i >= 4 : h == 1;
-                    uint32_t nib = (hi ? (word >> 4) : word) & 0x0F0F0F0Fu;
-                    // Opaque to the compiler, so that each byte converts with
-                    // one v_cvt_f32_ubyteN (no field extraction).
-                    asm volatile("" : "+v"(nib));
-                    float4 w;
-                    w.x = fmaf((float)(nib & 0xFFu), scg, m8);
-                    w.y = fmaf((float)((nib >> 8) & 0xFFu), scg, m8);
-                    w.z = fmaf((float)((nib >> 16) & 0xFFu), scg, m8);
-                    w.w = fmaf((float)(nib >> 24), scg, m8);
-                    wring[t % 3][8 * h + i][l] = w;
-                }
-                __syncthreads();
-                // keep each step's conversion after its barrier
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
-            for (int p = 0; p < kRkqPF; ++p) {
-#pragma unroll
-                for (int i = 0; i < NQ; ++i) qw[p][i] = qn[p][i];
-                sw[p] = sn[p];
-            }
-        }
+        rkq_produce<BLK>(J, wv, l, orow, nu, nsteps, wring);
         return;
     }
     // ---- consumer c: sequences seqb + 4 s + (0..3), lane row r4 of each chain.
@@ -511,6 +541,86 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
     for (int t = nu + 2; t < nsteps; ++t) __syncthreads();
 #pragma unroll
     for (int s = 0; s < S; ++s) rkq_finish(J, A.B, BLK, seqb + 4 * s, out, acc[s]);
+}
+
+// INT4 weights, wide form: as k_rkq_mm_q4, but each consumer wave runs one
+// chain of v_mfma_f32_16x16x1_4b_f32 over 16 sequences. That instruction also
+// holds one product per output per instruction and rounds once (checked on
+// gfx950: a chain of them in k order equals the sequential fmaf chain), and
+// one chain of it keeps a SIMD's matrix pipe busy (a dependent one issues
+// every ~32.5 cycles, independent ones every ~32), so a wave covers 16
+// sequences x 64 rows with one accumulator. Lane l supplies weight row
+// out0 + l (B, block l / 16, column l % 16) and the input of sequence l % 16
+// (A, the same rows in every block); it then holds, in register 4 b + r,
+// sequence 4 (l / 16) + r of row out0 + 16 b + l % 16.
+template <int BLK, int NC>
+__global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4w(const RkqMMArgs A) {
+    constexpr int U4 = kRkqU / 4;
+    __shared__ float4 wring[3][U4][64];
+    RkqJob J;
+    int u0;
+    rkq_job(A, J, u0);
+    const int ot = u0 / A.seq_tiles, st = u0 % A.seq_tiles;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+    const int out = ot * 64 + l;
+    const int orow = out < J.M ? out : J.M - 1;
+    const int Kd = J.Kd;
+    const int nu = (Kd + kRkqU - 1) / kRkqU;
+    const bool half_last = (Kd % kRkqU) != 0;
+    const int nsteps = (nu + 2 + kRkqPF - 1) / kRkqPF * kRkqPF;
+    if (wv < kRkqNP) {
+        rkq_produce<BLK>(J, wv, l, orow, nu, nsteps, wring);
+        return;
+    }
+    const int c = wv - kRkqNP;
+    const int seqb = st * (16 * NC) + 16 * c;
+    const float* xr = J.X + (size_t)min(seqb + (l & 15), A.B - 1) * (size_t)J.ldx;
+    float4 xw[U4];
+    float4 ww[kRkqWD];
+    v16f acc = {};
+#pragma unroll
+    for (int i = 0; i < U4; ++i) xw[i] = *reinterpret_cast<const float4*>(xr + min(4 * i, Kd - 4));
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRkqWD; ++j) ww[j] = wring[0][j][l];
+    __syncthreads();
+    auto full_unit = [&](int slot, int nslot, int knext) {
+#pragma unroll
+        for (int i = 0; i < U4; ++i) {
+            const float4 wc = ww[i % kRkqWD];
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].x, wc.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].y, wc.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].z, wc.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].w, wc.w, acc, 0, 0, 0);
+            ww[i % kRkqWD] = i + kRkqWD < U4 ? wring[slot][i + kRkqWD][l] : wring[nslot][i + kRkqWD - U4][l];
+            xw[i] = *reinterpret_cast<const float4*>(xr + min(knext + 4 * i, Kd - 4));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    for (int u = 0; u < nu - 1; ++u) {
+        full_unit(u % 3, (u + 1) % 3, (u + 1) * kRkqU);
+        __syncthreads();
+    }
+    const int ul = nu - 1;
+    if (!half_last) {
+        full_unit(ul % 3, (ul + 1) % 3, Kd);
+    } else {
+#pragma unroll
+        for (int i = 0; i < U4 / 2; ++i) {
+            const float4 wc = ww[i % kRkqWD];
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].x, wc.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].y, wc.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].z, wc.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(xw[i].w, wc.w, acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    for (int t = nu + 2; t < nsteps; ++t) __syncthreads();
+    const int sq0 = seqb + 4 * (l >> 4), col = ot * 64 + (l & 15);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rkq_finish1(J, A.B, BLK, sq0 + r, col + 16 * b, acc[4 * b + r]);
 }
 
 // ---------------------------------------------------------------- heads
@@ -681,14 +791,29 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
         // consumer of one chain is fastest while the grid of such workgroups
         // stays within ~1024 (up to 3 reside per CU); larger grids (the
         // vocabulary head) share the dequantized units among more chains.
+        // S = 16 selects the wide kernel (one 16x16x1 chain of 16 sequences
+        // per consumer), used from B = 8 once the one-chain grid exceeds 256
+        // workgroups (SNHIP_RKQ_WIDE_GRID): the products are then bound by
+        // matrix-core throughput, not chain latency. NC then keeps the grid at
+        // >= ~512 workgroups. Measured on the RWKV-7 step (B = 64): head
+        // 376 -> 112 us, channel-mix key 26 -> 21 us.
         const long wg11 = (long)tiles1 * ((B + 3) / 4);
-        const int nc0 = wg11 <= 1024 ? 1 : 2;
-        const int s0 = wg11 <= 1024 || B < 16 ? 1 : 2;
+        int nc0 = wg11 <= 1024 ? 1 : 2, s0 = wg11 <= 1024 || B < 16 ? 1 : 2;
+        // Not for launches with a tanh / sigmoid epilogue (a wide lane finishes
+        // 16 outputs, not 4) or with a short K (fill-bound).
+        bool wide_ok = true;
+        for (int i = 0; i < n; ++i)
+            wide_ok = wide_ok && jobs[i].Kd >= 256 && jobs[i].epi != RKQ_TANH && jobs[i].epi != RKQ_SIGMOID;
+        if (wide_ok && B >= 8 && wg11 > (long)env_unsigned("SNHIP_RKQ_WIDE_GRID", 256, 0)) {
+            s0 = 16;
+            nc0 = std::min(4, (B + 15) / 16);
+            while (nc0 > 1 && (long)tiles1 * ((B + 16 * nc0 - 1) / (16 * nc0)) < 512) nc0 /= 2;
+        }
         NC = nc ? nc : nc0;
         S = s ? s : s0;
-        if (!((NC == 1 || NC == 2 || NC == 4) && (S == 1 || S == 2)) || (NC == 4 && S == 2))
+        if (!((NC == 1 || NC == 2 || NC == 4) && (S == 1 || S == 2 || S == 16)) || (NC == 4 && S == 2))
             return SNHIP_E_INVAL;
-        per = 4 * NC * S;
+        per = (S == 16 ? 16 : 4 * S) * NC;
     }
     a.n = n;
     a.B = B;
@@ -703,9 +828,15 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
 #define SNHIP_RKQ_F32(S_) hipLaunchKernelGGL((k_rkq_mm_f32<S_>), dim3(total), dim3(64), 0, st, a)
 #define SNHIP_RKQ_Q4(B_, N_, S_) \
     hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_, S_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
+#define SNHIP_RKQ_Q4W(B_, N_) \
+    hipLaunchKernelGGL((k_rkq_mm_q4w<B_, N_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
 #define SNHIP_RKQ_Q4B(B_)                                 \
     do {                                                  \
-        if (NC == 1 && S == 1) SNHIP_RKQ_Q4(B_, 1, 1);   \
+        if (S == 16) {                                    \
+            if (NC == 1) SNHIP_RKQ_Q4W(B_, 1);            \
+            else if (NC == 2) SNHIP_RKQ_Q4W(B_, 2);       \
+            else SNHIP_RKQ_Q4W(B_, 4);                    \
+        } else if (NC == 1 && S == 1) SNHIP_RKQ_Q4(B_, 1, 1); \
         else if (NC == 2 && S == 1) SNHIP_RKQ_Q4(B_, 2, 1); \
         else if (NC == 4) SNHIP_RKQ_Q4(B_, 4, 1);        \
         else if (NC == 1) SNHIP_RKQ_Q4(B_, 1, 2);        \
@@ -723,6 +854,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
 #undef SNHIP_RKQ_F32
 #undef SNHIP_RKQ_Q4
 #undef SNHIP_RKQ_Q4B
+#undef SNHIP_RKQ_Q4W
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;
 }
