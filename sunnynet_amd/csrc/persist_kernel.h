@@ -15,6 +15,7 @@ constexpr int CAPF = 4;                      // fp32: float4 per lane in one bat
 constexpr int KPT = (kPersistMaxGrid + NT - 1) / NT;   // argmax keys per thread
 constexpr int KT = kPersistTaps;             // conv taps
 constexpr int KH = KT - 1;                   // history entries
+constexpr int kStagePad = 2;                 // INT4 staged layout: pad groups per quad row
 
 typedef unsigned long long u64;
 
@@ -103,6 +104,10 @@ __device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x));
 // every phase so per-lane addresses are formed inside the phase instead of
 // being hoisted out of the step loop (hundreds would stay live and spill).
 __device__ __forceinline__ int opq(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ uint32_t opqu(uint32_t v) {
     asm volatile("" : "+v"(v));
     return v;
 }
@@ -208,7 +213,7 @@ struct Geo {
     int ng, lseg, rpp;       // INT4: groups per row, log2 lanes per row, rows per unit
     int nk4;                 // fp32: float4 items per row
     int xsel;                // multiplies x1 (1) or x0 (0)
-    int pad;
+    int nwu;                 // INT4: units of this wave
 };
 static_assert(sizeof(Geo) == 64, "Geo is read as four 16-byte words");
 
@@ -258,7 +263,7 @@ __device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, in
     g.base = hi ? n1 : 0;
     g.cnt = two ? (hi ? n - n1 : n1) : n;
     g.xsel = hi ? 1 : 0;
-    g.pad = 0;
+    g.nwu = 0;
     const int nw = g.cnt > g.wl ? (g.cnt - g.wl + g.nwp - 1) / g.nwp : 0;   // the wave's rows
     if constexpr (!is_i4(BLK)) {
         g.nk4 = (K + 255) >> 8;
@@ -270,10 +275,24 @@ __device__ __forceinline__ Geo make_geo(int K, int n1, int n, int r0, int s0, in
         g.lseg = g.ng <= 1 ? 0 : 32 - __clz(g.ng - 1);
         g.rpp = 64 >> g.lseg;
         const int nu = (g.cnt + g.rpp - 1) / g.rpp;
-        const int nwu = nu > g.wl ? (nu - g.wl + g.nwp - 1) / g.nwp : 0;
-        g.nb = (nwu + Pool<BLK>::MU - 1) / Pool<BLK>::MU;
+        g.nwu = nu > g.wl ? (nu - g.wl + g.nwp - 1) / g.nwp : 0;
+        g.nb = (g.nwu + Pool<BLK>::MU - 1) / Pool<BLK>::MU;
     }
     return g;
+}
+
+// fp32: item m = b CAPF + s of a wave's list is float4 i of its row mr (one
+// division per batch; the slots step through the list).
+__device__ __forceinline__ void first_item(const Geo& g, int b, int& mr, int& i) {
+    const int m = b * CAPF;
+    mr = m / g.nk4;
+    i = m - mr * g.nk4;
+}
+__device__ __forceinline__ void next_item(const Geo& g, int& mr, int& i) {
+    if (++i == g.nk4) {
+        i = 0;
+        ++mr;
+    }
 }
 
 // Batch b of J into P. Straight-line: every slot issues its loads (empty ones
@@ -282,9 +301,11 @@ template <int BLK>
 __device__ __forceinline__ void pool_load(const Job& J, int b, Pool<BLK>& P, int lane) {
     const Geo& g = J.g;
     if constexpr (!is_i4(BLK)) {
+        int mr, i;
+        first_item(g, b, mr, i);
 #pragma unroll
         for (int s = 0; s < CAPF; ++s) {
-            const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
+            if (s > 0) next_item(g, mr, i);
             const int jl = g.wl + g.nwp * mr;
             const int k = i * 256 + lane * 4;
             const bool ok = jl < g.cnt && k < g.K;
@@ -316,7 +337,7 @@ __device__ __forceinline__ void xcache_load(const Job& J, XCache<BLK>& X, int la
         const Geo& g = J.g;
         const int lg = min(lane & ((1 << g.lseg) - 1), g.ng - 1);
 #pragma unroll
-        for (int q = 0; q < BLK / 4; ++q) X.q[q] = lds4(J.x + 4 * (q * g.ng + lg));
+        for (int q = 0; q < BLK / 4; ++q) X.q[q] = lds4(J.x + 4 * (q * (g.ng + kStagePad) + lg));
     }
 }
 
@@ -327,14 +348,20 @@ __device__ __forceinline__ void compute_f32(const Job& J, int b, const Pool<BLK>
                                             Epi&& epi) {
     const Geo& g = J.g;
     float4 xs[CAPF];
+    int mr0, i0;
+    first_item(g, b, mr0, i0);
+    {
+        int mr = mr0, i = i0;
 #pragma unroll
-    for (int s = 0; s < CAPF; ++s) {
-        const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
-        xs[s] = lds4(J.x + min(i * 256 + lane * 4, g.K - 4));
+        for (int s = 0; s < CAPF; ++s) {
+            if (s > 0) next_item(g, mr, i);
+            xs[s] = lds4(J.x + min(i * 256 + lane * 4, g.K - 4));
+        }
     }
+    int mr = mr0, i = i0;
 #pragma unroll
     for (int s = 0; s < CAPF; ++s) {
-        const int m = b * CAPF + s, mr = m / g.nk4, i = m - mr * g.nk4;
+        if (s > 0) next_item(g, mr, i);
         const int jl = g.wl + g.nwp * mr;
         if (i * 256 + lane * 4 < g.K) {
             const float4 w4 = BLK == 16 ? h4f(P.wh[s]) : P.wf[s];
@@ -358,9 +385,7 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
     const int lrow = lane >> g.lseg, lg = lane & (seg - 1);
     const bool lane_ok = lg < g.ng;
     // Units of this batch that hold rows (the rest are skipped, uniformly).
-    const int nu = (g.cnt + g.rpp - 1) >> (6 - g.lseg);
-    const int u0 = g.wl + g.nwp * b * MU;
-    const int nvu = u0 < nu ? min(MU, (nu - u0 + g.nwp - 1) / g.nwp) : 0;
+    const int nvu = min(MU, g.nwu - b * MU);
     float acc[MU];
 #pragma unroll
     for (int s = 0; s < MU; ++s) {
@@ -378,8 +403,10 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
             const int wi = w & 3;
             const uint32_t word = wi == 0 ? qq.x : wi == 1 ? qq.y : wi == 2 ? qq.z : qq.w;
             // Byte 4w + e holds element 4w + e (low nibble) and 4w + e + BLK/2
-            // (high nibble).
-            const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+            // (high nibble). The nibble words are opaque to the optimizer, so
+            // each code converts with one v_cvt_f32_ubyte<e> (known-bits
+            // folding would otherwise emit a bit-field extract first).
+            const uint32_t lo = opqu(word & 0x0F0F0F0Fu), hi = opqu((word >> 4) & 0x0F0F0F0Fu);
             const float4 xl = X.q[w], xh = X.q[w + NW];
             a[0] = fmaf(fmaf((float)(lo & 0xFFu), sc, m8), xl.x, a[0]);
             a[1] = fmaf(fmaf((float)((lo >> 8) & 0xFFu), sc, m8), xl.y, a[1]);
@@ -394,10 +421,12 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
     }
     if (seg >= 16) {
 #pragma unroll
-        for (int s = 0; s < MU; ++s) acc[s] = row_sum(acc[s]);
+        for (int s = 0; s < MU; ++s)
+            if (s < nvu) acc[s] = row_sum(acc[s]);
         if (seg > 16) {
 #pragma unroll
             for (int s = 0; s < MU; ++s) {
+                if (s >= nvu) continue;
                 const float r0 = lane_val(acc[s], 0), r1 = lane_val(acc[s], 16);
                 const float r2 = lane_val(acc[s], 32), r3 = lane_val(acc[s], 48);
                 acc[s] = seg == 64 ? (r0 + r1) + (r2 + r3) : (lane < 32 ? r0 + r1 : r2 + r3);
@@ -406,12 +435,13 @@ __device__ __forceinline__ void compute_i4(const Job& J, int b, const Pool<BLK>&
     } else {
         for (int o = seg >> 1; o > 0; o >>= 1)
 #pragma unroll
-            for (int s = 0; s < MU; ++s) acc[s] += __shfl_xor(acc[s], o, 64);
+            for (int s = 0; s < MU; ++s)
+                if (s < nvu) acc[s] += __shfl_xor(acc[s], o, 64);
     }
 #pragma unroll
     for (int s = 0; s < MU; ++s) {
         const int jl = (g.wl + g.nwp * (b * MU + s)) * g.rpp + lrow;
-        if (jl < g.cnt) epi(g.base + jl, job_row(g, g.base + jl), acc[s], lg == 0);
+        if (s < nvu && jl < g.cnt) epi(g.base + jl, job_row(g, g.base + jl), acc[s], lg == 0);
     }
 }
 
@@ -423,10 +453,15 @@ __device__ __forceinline__ void compute(const Job& J, int b, const Pool<BLK>& P,
 }
 
 // Runs every batch of J (batch 0 is already in p0): batches alternate between
-// the pools, and each is issued before the previous one is multiplied. The
-// loads of a batch past the last read element 0 of the matrix (unused), so
-// every path of the loop issues the same loads and the wait counts stay
-// exact. A wave with no rows does nothing.
+// two pools, and each is issued before the previous one is multiplied. INT4
+// keeps p0 read-only and streams the later batches through two pools local
+// to the job, so no path leaves p0 different (a pool rewritten on one path
+// costs register copies, and a wait for their loads, where the paths join:
+// 188.6 -> 184.0 us per 100M step); fp32 rotates p0 and p1 (the local pools
+// measured 224.4 -> 236.3 us there). The loads of a batch past the last read
+// element 0 of the matrix (unused), so every path of the loop issues the
+// same loads and the wait counts stay exact. A wave with no rows does
+// nothing.
 #ifdef SNHIP_PERSIST_PROF
 __device__ unsigned long long g_jprof[64 * 4];
 #define JPROF(i) do { if (probe && lane == 0) g_jprof[(i) * 16 + wv] = wall_clock64(); } while (0)
@@ -451,11 +486,23 @@ __device__ __forceinline__ void run_job(const Job& J, Pool<BLK>& p0, Pool<BLK>& 
         JPROF(3);
         return;
     }
-    for (int b = 0; b < nb; b += 2) {
-        pool_load<BLK>(J, b + 1, p1, lane);
-        compute<BLK>(J, b, p0, X, lane, pacc, epi);
-        pool_load<BLK>(J, b + 2, p0, lane);
-        if (b + 1 < nb) compute<BLK>(J, b + 1, p1, X, lane, pacc, epi);
+    if constexpr (is_i4(BLK)) {
+        Pool<BLK> q0, q1;
+        pool_load<BLK>(J, 1, q1, lane);
+        compute<BLK>(J, 0, p0, X, lane, pacc, epi);
+        for (int b = 1; b < nb; b += 2) {
+            pool_load<BLK>(J, b + 1, q0, lane);
+            compute<BLK>(J, b, q1, X, lane, pacc, epi);
+            pool_load<BLK>(J, b + 2, q1, lane);
+            if (b + 1 < nb) compute<BLK>(J, b + 1, q0, X, lane, pacc, epi);
+        }
+    } else {
+        for (int b = 0; b < nb; b += 2) {
+            pool_load<BLK>(J, b + 1, p1, lane);
+            compute<BLK>(J, b, p0, X, lane, pacc, epi);
+            pool_load<BLK>(J, b + 2, p0, lane);
+            if (b + 1 < nb) compute<BLK>(J, b + 1, p1, X, lane, pacc, epi);
+        }
     }
 }
 
@@ -467,11 +514,13 @@ __device__ __forceinline__ void prefetch_job(const Job& J, Pool<BLK>& p0, int la
 
 // Index of element i of a K-long vector in the staged LDS layout: fp32 plain;
 // INT4 quad-major, so lane g of a row reads its group's quads q at
-// (q ng + g) * 4 (consecutive lanes, consecutive 16 bytes).
+// (q (ng + 2) + g) * 4 (consecutive lanes, consecutive 16 bytes). The stride
+// of ng + 2 groups puts the 64 floats a wave stages (8 quads of 2 groups)
+// on 64 different banks; with a stride of ng they shared 8.
 template <int BLK>
 __device__ __forceinline__ int sidx(int i, int K) {
     if constexpr (!is_i4(BLK)) return i;
-    else return ((((i % BLK) >> 2) * (K / BLK) + i / BLK) << 2) + (i & 3);
+    else return ((((i % BLK) >> 2) * (K / BLK + kStagePad) + i / BLK) << 2) + (i & 3);
 }
 
 #ifdef SNHIP_PERSIST_PROF
@@ -490,8 +539,10 @@ __device__ unsigned long long g_clk[4];
 // the head H; per-phase differences are uniform branches on the phase type.
 template <int BLK>
 __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
-    __shared__ __align__(16) float xin[kMaxK];    // input vector of the current products
-    __shared__ __align__(16) float xs2[kMaxD];    // old state s (W_eff's input in phase A)
+    // input vector of the current products, and the old state s (W_eff's
+    // input in phase A), in the staged layout (INT4: K + kStagePad BLK floats)
+    __shared__ __align__(16) float xin[kMaxK + kStagePad * 64];
+    __shared__ __align__(16) float xs2[kMaxD + kStagePad * 64];
     __shared__ float xres[kMaxD];                 // x of the layer (residual)
     __shared__ float res[kMaxK + kMaxD];          // products of the current phase, by job row
     __shared__ float sown[kMaxD];                 // s' of the owned channels
@@ -561,7 +612,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
         return J;
     };
 
-    Pool<BLK> p0, p1;
+    Pool<BLK> p0, p1;   // p1: fp32 jobs of more than one batch
     prefetch_job<BLK>(job(0), p0, lane);
 
     unsigned ep = 0;                  // epoch of the last exchange produced
@@ -642,7 +693,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
                 for (int k = 0; k < PD; ++k) dl[k] = ldg(Ly->delta + min(c0 + k * NT + tid, D - 1));
             }
             PROF(p * 8 + 0);
-            if (!agree(ll_spin(w, addr, want, pc))) return;
+            const bool polled = ll_spin(w, addr, want, pc);
             PROF(p * 8 + 1);
             float xv[PK];
 #pragma unroll
@@ -650,6 +701,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
                 const bool in = k * NT + tid < n0 && (t != 0 || k < PD);
                 xv[k] = !in ? 0.0f : (plain0 && !tok_ok) ? __builtin_nanf("") : ll_f(w[k]);
             }
+            if (!agree(polled)) return;
             float mean = 0.0f, rstd = 0.0f;
             if (ln) ln_stats(xv, n0, a.eps, red, mean, rstd);
             PROF(p * 8 + 2);
