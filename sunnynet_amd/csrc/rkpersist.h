@@ -30,29 +30,26 @@ struct RkPArgs {
     float* S;                 // (L, NH, 64, 64)
     float* shift;             // (L, 2, D)
     float* vfirst;            // (D)
-    float* xch;               // per-layer exchange slabs, rkp_slab(D, F) floats each
+    unsigned long long* xch;  // per-layer exchange slabs, rkp_slab(D, F) words each
     float* logits;            // (vocab)
-    unsigned long long* keys; // (grid) argmax keys
+    unsigned long long* keys; // (2 grid) exchange words of the argmax keys
     int32_t* tok;             // the step's input token (and, greedy, the next one)
     int32_t* tok_hist;
     int32_t* counter;
     int hist_cap, greedy;
-    unsigned long long* bar;  // kRkPBarWords words, zero at the first launch of a call
-    unsigned gen0;            // barriers passed by earlier launches of the call
+    unsigned epoch;           // this launch's epoch (> 0; every launch of the handle a new one)
     unsigned* err;
     unsigned spin_limit;
     unsigned stall;           // added to every wait target: tests force time-outs with it
 };
 
-constexpr int kRkPMaxD = 1024, kRkPMaxF = 4096, kRkPRank = 256, kRkPBarWords = 512;
+constexpr int kRkPMaxD = 1024, kRkPMaxF = 4096, kRkPRank = 256, kRkPMaxGrid = 1024;
 
-// Floats of one layer's exchange slab: r, k, v, y, x after the time mix,
-// x after the channel mix (D each), the four LoRA middles (256 each), ck (F).
+// Exchange words of one layer's slab (one 64-bit word per value: the epoch
+// of the launch that wrote it above the value's bits): r, k, v, y, x after
+// the time mix, x after the channel mix (D each), the four LoRA middles (256
+// each), ck (F).
 __host__ __device__ inline size_t rkp_slab(int D, int F) { return (size_t)6 * D + 4 * kRkPRank + F; }
-
-// Grid barriers one launch passes: five per layer, one more before the
-// greedy token reduction.
-inline unsigned rkp_barriers(int L, bool greedy) { return 5u * (unsigned)L + (greedy ? 1u : 0u); }
 
 bool rkp_shape_ok(int D, int F, int HS, int NH, const int (*ranks)[4], int L);
 // Workgroups of the launch (a multiple of 8, one per CU), or 0 when the

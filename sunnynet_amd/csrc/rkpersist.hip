@@ -6,8 +6,7 @@
 // separate kernels (even replayed from a graph) each costs about 4.6 us of
 // launch and drain on gfx950 whatever its size, about 100 of them per step.
 // Here one launch runs the whole step: one 512-thread workgroup per CU, the
-// products' rows spread over every wave of the grid, and a grid barrier
-// between the phases that depend on a whole vector. Five phases per layer:
+// products' rows spread over every wave of the grid. Five phases per layer:
 //
 //   P1  LN_1 + token-shift mixes (every workgroup, into LDS), then the rows of
 //       W_r, W_k, W_v and the LoRA down-projections W_1, A_1, G_1, V_1;
@@ -20,13 +19,18 @@
 //   P5  rows of W_cv, x_b = x_a + W_cv ck.
 //
 // then LN_out and the head rows with a per-workgroup argmax key, and workgroup
-// 0 reduces the keys to the greedy token. Every vector a phase produces has
-// its own slot in a per-layer slab and is written once per launch with
-// agent-scope stores, so after the barrier (each wave's stores complete
-// before it arrives) plain loads read it from any XCD; the kernel boundary
-// orders one step's writes before the next step's reads. The recurrent state
-// (S, the two shift vectors, v_first) is read and written only by the
-// workgroup that owns it.
+// 0 reduces the keys to the greedy token.
+//
+// Exchange without grid barriers. Every value a phase produces has its own
+// word in a per-layer slab: the launch's epoch in the high half, the value's
+// bits in the low half, written once per launch with one agent-scope store.
+// A phase's readers poll the words they need until each carries the epoch,
+// so a phase waits for exactly its inputs, in one store-to-load round trip
+// across XCDs. The kernel boundary orders one step's writes before the next
+// step's reads. The recurrent state (S, v_first) is read and written only by
+// the workgroup that owns it; the shift vectors, read by every workgroup in
+// P1 / P4 and rewritten by workgroup 0, are rewritten only once workgroup 0
+// has seen outputs of every workgroup that follow those reads.
 #include <type_traits>
 
 #include "gemv.h"
@@ -39,6 +43,7 @@ constexpr int NT = 512, NW = NT / 64, HS = 64;
 constexpr float kR2 = 0.6065306597126334f;   // 1/sqrt(e), rwkv7.c:38
 constexpr float kEpsGroup = 6.4e-4f;          // rwkv7.c:39
 constexpr int kPer = kRkPMaxD / NT;           // LayerNorm values per thread
+constexpr int kPerF = kRkPMaxF / NT;          // channel-mix key values per thread
 typedef unsigned long long u64;
 
 template <class T>
@@ -52,10 +57,28 @@ __device__ __forceinline__ void st_ag(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane sums through DPP moves (VALU, no LDS round trips): within
+// aligned groups of 2, 4, 8 and 16 lanes (quad permutations, then the half
+// row and row mirrors, each pairing every lane with one whose partial covers
+// the other half of its group), and over the wave (the four row sums read
+// from lanes 0, 16, 32, 48). Every lane of a group gets its group's sum.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float grp_sum(float v, int n) {
+    if (n >= 2) v += dppf<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    if (n >= 4) v += dppf<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    if (n >= 8) v += dppf<0x141>(v);   // row_half_mirror
+    if (n >= 16) v += dppf<0x140>(v);  // row_mirror
     return v;
+}
+__device__ __forceinline__ float lane_val(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wsum(float v) {
+    v = grp_sum(v, 16);
+    return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
 }
 
 __device__ __forceinline__ float bsum(float v, float* red) {
@@ -203,6 +226,63 @@ __device__ void row_dotn(const RkPMat& W, int row0, int stride, int end, const f
     }
 }
 
+// NR rows of W (row0 + k stride, clamped to the matrix) with NU units per
+// lane each, loaded before the vector they multiply has arrived: a phase
+// issues them ahead of its exchange wait, so the weights' memory latency
+// overlaps the wait instead of following it.
+template <bool Q, int NU, int NR>
+struct PreRows {
+    Unit u[NR][NU];
+};
+
+template <bool Q, int NU, int NR>
+__device__ __forceinline__ void pre_load(PreRows<Q, NU, NR>& R, const RkPMat& W, int row0, int stride, int lane) {
+    const int nu = W.K >> 4;
+#pragma unroll
+    for (int k = 0; k < NR; ++k)
+#pragma unroll
+        for (int j = 0; j < NU; ++j)
+            unit_load<Q>(R.u[k][j], W, min(row0 + k * stride, W.M - 1), min(lane + 64 * j, nu - 1));
+}
+
+// out[k] = (row k of R) . X over the wave, in row_dot's order.
+template <bool Q, int NU, int NR>
+__device__ __forceinline__ void pre_dot(const PreRows<Q, NU, NR>& R, const RkPMat& W, const float* X, int lane,
+                                        float (&out)[NR]) {
+    const int nu = W.K >> 4;
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = min(lane + 64 * j, nu - 1);
+            const float v = unit_dot<Q>(R.u[k][j], W, u, X, 0.0f);
+            acc += lane + 64 * j < nu ? v : 0.0f;
+        }
+        out[k] = wsum(acc);
+    }
+}
+
+// f(format, units per lane) for the instantiation that fits W: INT4 or fp32,
+// NU = 1, 2 or 4 units of 16 values per lane (K <= 4096; K <= 1024 when
+// ONE, the matrices whose input is a model-width vector).
+template <bool ONE = false, class Fn>
+__device__ __forceinline__ bool with_format(const RkPMat& W, Fn&& f) {
+    if constexpr (ONE) {
+        if (W.block != 0) return f(std::true_type{}, std::integral_constant<int, 1>{});
+        return f(std::false_type{}, std::integral_constant<int, 1>{});
+    }
+    const int n = ((W.K >> 4) + 63) >> 6;
+    if (W.block != 0) {
+        if (n <= 1) return f(std::true_type{}, std::integral_constant<int, 1>{});
+        if (n == 2) return f(std::true_type{}, std::integral_constant<int, 2>{});
+        return f(std::true_type{}, std::integral_constant<int, 4>{});
+    }
+    if (n <= 1) return f(std::false_type{}, std::integral_constant<int, 1>{});
+    if (n == 2) return f(std::false_type{}, std::integral_constant<int, 2>{});
+    return f(std::false_type{}, std::integral_constant<int, 4>{});
+}
+
 // Two rows of two matrices with K <= 1024 at once (both loads first).
 template <bool QA, bool QB>
 __device__ __forceinline__ void pair_t(const RkPMat& WA, int rA, const float* XA, const RkPMat& WB, int rB,
@@ -248,57 +328,80 @@ __device__ void small_rows(const RkPMat& W, int r0, int n, const float* X, float
             acc = unit_dot<true>(U, W, u, X, 0.0f);
         }
         acc = i < n ? acc : 0.0f;
-        for (int o = nu >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        acc = grp_sum(acc, nu);
         if (i < n && u == 0) out[i] = acc;
     }
 }
 
-// Grid barrier in two halves (two levels: eight group counters, then one top
-// counter and a flag). Arrival waits for this wave's stores (and loads: the
-// wait count covers both), so loads that do not depend on the barrier are
-// issued between arrival and the wait. The wait is true when it timed out
-// and the launch is abandoned.
-__device__ __forceinline__ void bar_arrive(u64* bar, unsigned& gen, int wg, int G, int* slast) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    ++gen;
-    if (threadIdx.x == 0) {
-        u64* grp = bar + 32 * (1 + (wg & 7));
-        const int ng = G >> 3;
-        int last = 0;
-        const u64 old = __hip_atomic_fetch_add(grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == (u64)gen * ng - 1) {
-            const u64 o2 = __hip_atomic_fetch_add(bar, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = o2 == (u64)gen * 8 - 1;
+// ---- exchange words: the epoch of the launch that wrote the value in the
+// high half, the value's bits in the low half, stored and loaded as one
+// single-copy-atomic word at agent scope. A reader polls a word until it
+// carries its launch's epoch, so data and readiness travel in one round trip
+// and no grid barrier is needed.
+__device__ __forceinline__ void ex_put_bits(u64* p, uint32_t bits, unsigned ep) {
+    __hip_atomic_store(p, ((u64)ep << 32) | (u64)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ex_put(u64* p, float v, unsigned ep) { ex_put_bits(p, __float_as_uint(v), ep); }
+__device__ __forceinline__ u64 ex_get(const u64* p) {
+    return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool ex_ok(u64 w, unsigned ep) { return (uint32_t)(w >> 32) == ep; }
+__device__ __forceinline__ float ex_f(u64 w) { return __uint_as_float((uint32_t)w); }
+
+struct PollCtl {
+    unsigned* err;
+    unsigned limit;
+    unsigned want;   // the launch's epoch (plus the test stall)
+};
+
+// Re-polls the words of w still short of the epoch (word k from src[k];
+// words a thread does not take start out ready) until all carry it. False on
+// a time-out (the thread then sets the error word) or when another
+// workgroup reported one.
+template <int W>
+__device__ __forceinline__ bool ex_spin(u64 (&w)[W], const u64* const (&src)[W], const PollCtl& pc) {
+    unsigned spins = 0;
+    while (true) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < W; ++k) all = all && ex_ok(w[k], pc.want);
+        if (all) return true;
+        if ((++spins & 255) == 0) {
+            if (__hip_atomic_load(pc.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+            if (spins > pc.limit) {
+                __hip_atomic_store(pc.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
         }
-        if (last) __hip_atomic_store(bar + 32 * 9, (u64)gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *slast = last;
+#pragma unroll
+        for (int k = 0; k < W; ++k)
+            if (!ex_ok(w[k], pc.want)) w[k] = ex_get(src[k]);
     }
 }
 
-__device__ __forceinline__ bool bar_wait(u64* bar, unsigned* err, unsigned limit, unsigned stall, unsigned gen,
-                                         int* slast, int* sdead) {
-    if (threadIdx.x == 0) {
-        int dead = 0;
-        if (!*slast) {
-            unsigned n = 0;
-            while (__hip_atomic_load(bar + 32 * 9, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                   (u64)gen + stall) {
-                if (++n > limit) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    dead = 1;
-                    break;
-                }
-                if ((n & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                    dead = 1;
-                    break;
-                }
-            }
-        }
-        *sdead = dead;
+// Words [0, n) of src into dst (LDS), word i by thread i mod NT; W words per
+// thread at most (n <= W NT). The workgroup's barrier between the polls and
+// the writes: every wave is done with what dst held before (the caller's
+// agree() then orders the writes before any read).
+template <int W>
+__device__ __forceinline__ bool poll_vec(const u64* src, int n, float* dst, const PollCtl& pc) {
+    const int tid = threadIdx.x;
+    u64 w[W];
+    const u64* at[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+        const int i = k * NT + tid;
+        at[k] = src + min(i, n - 1);
+        w[k] = i < n ? ex_get(at[k]) : ((u64)pc.want << 32);
     }
+    const bool ok = ex_spin(w, at, pc);
     __syncthreads();
-    return *sdead != 0;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+        const int i = k * NT + tid;
+        if (i < n) dst[i] = ex_f(w[k]);
+    }
+    return ok;
 }
 
 // Keeps loads issued so far where they are (the optimizer would sink them to
@@ -345,14 +448,27 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     __shared__ float hv[12][HS];              // per-channel values of the owned head
     __shared__ float red[NW];
     __shared__ u64 kred[NW];
-    __shared__ int sdead, slast;
-    __shared__ RkPLayer Ls;
+    __shared__ int sdead;
+    __shared__ RkPLayer Ls2[2];                  // layer tables of layers l (l & 1) and l + 1
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wg = blockIdx.x, G = gridDim.x;
     const int D = A.D, F = A.F, L = A.L, NH = A.NH;
     const size_t slab = rkp_slab(D, F);
-    unsigned gen = A.gen0;
+    const unsigned ep = A.epoch;
+    const PollCtl pc{A.err, A.spin_limit, A.epoch + A.stall};
+    if (tid == 0) sdead = 0;
+    if (tid < (int)(sizeof(RkPLayer) / 4))
+        reinterpret_cast<int*>(&Ls2[0])[tid] = reinterpret_cast<const int*>(A.layers)[tid];
+    __syncthreads();
+    // Leaves the kernel (in every thread of the workgroup) when any thread's
+    // poll failed.
+    auto agree = [&](bool ok) -> bool {
+        if (!ok) sdead = 1;
+        __syncthreads();
+        return sdead == 0;
+    };
+    float vfo = 0.0f;   // head owners, thread c < 64: v_first of channel c (layer 0's v)
 
     // x = LN_0(E[tok]) (rwkv7.c:351-352); NaN for an out-of-range id.
     {
@@ -365,47 +481,50 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     }
 
     for (int l = 0; l < L; ++l) {
-        if (tid < (int)(sizeof(RkPLayer) / 4))
-            reinterpret_cast<int*>(&Ls)[tid] = reinterpret_cast<const int*>(A.layers + l)[tid];
-        float* sl = A.xch + (size_t)l * slab;
-        float *s_r = sl, *s_k = sl + D, *s_v = sl + 2 * D, *s_y = sl + 3 * D, *s_xa = sl + 4 * D,
-              *s_xb = sl + 5 * D, *s_lw = sl + 6 * D, *s_la = s_lw + kRkPRank, *s_lg = s_la + kRkPRank,
-              *s_lv = s_lg + kRkPRank, *s_ck = s_lv + kRkPRank;
+        u64* sl = A.xch + (size_t)l * slab;
+        u64 *s_r = sl, *s_k = sl + D, *s_v = sl + 2 * D, *s_y = sl + 3 * D, *s_xa = sl + 4 * D,
+            *s_xb = sl + 5 * D, *s_lw = sl + 6 * D, *s_la = s_lw + kRkPRank, *s_lg = s_la + kRkPRank,
+            *s_lv = s_lg + kRkPRank, *s_ck = s_lv + kRkPRank;
         float* sh0 = A.shift + (size_t)l * 2 * D;
         float* sh1 = sh0 + D;
-        if (l > 0) {
-            const float* xb = A.xch + (size_t)(l - 1) * slab + 5 * D;
-            for (int i = tid; i < D; i += NT) xs[i] = xb[i];
-        }
-        __syncthreads();
-        const RkPLayer& P = Ls;
 
         // ---- P1: xn = LN_1(x); X6 = xn + lerp (shift_0 - xn); r k v, LoRA down
-        RKP_MARK(l * 6 + 0, 0);
         {
-            float shv[kPer], lrp[6][kPer];      // loaded before the LayerNorm
-#pragma unroll
-            for (int k = 0; k < kPer; ++k) {
-                const int ic = min(k * NT + tid, D - 1);
-                shv[k] = sh0[ic];
-#pragma unroll
-                for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = P.lerp[(size_t)s6 * D + ic];
+            // x_b of the layer before (every wave is past its last use of xs
+            // and of the other layer-table slot once the poll's barrier is)
+            if (l > 0) {
+                const bool ok = poll_vec<kPer>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
+                if (!agree(ok)) return;
             }
-            layer_norm(xs, xn, P.ln1w, P.ln1b, D, A.eps, red);
+            const RkPLayer& P = Ls2[l & 1];
+            // the next layer's table into the other slot
+            if (l + 1 < L && tid < (int)(sizeof(RkPLayer) / 4))
+                reinterpret_cast<int*>(&Ls2[(l + 1) & 1])[tid] = reinterpret_cast<const int*>(A.layers + l + 1)[tid];
+            __syncthreads();
+            RKP_MARK(l * 6 + 0, 0);
+            {
+                float shv[kPer], lrp[6][kPer];      // loaded before the LayerNorm
 #pragma unroll
-            for (int k = 0; k < kPer; ++k) {
-                const int i = k * NT + tid;
-                if (i < D) {
-                    const float d = shv[k] - xn[i];
+                for (int k = 0; k < kPer; ++k) {
+                    const int ic = min(k * NT + tid, D - 1);
+                    shv[k] = sh0[ic];
 #pragma unroll
-                    for (int s6 = 0; s6 < 6; ++s6) buf[s6 * D + i] = xn[i] + lrp[s6][k] * d;
+                    for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = P.lerp[(size_t)s6 * D + ic];
+                }
+                layer_norm(xs, xn, P.ln1w, P.ln1b, D, A.eps, red);
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) {
+                    const int i = k * NT + tid;
+                    if (i < D) {
+                        const float d = shv[k] - xn[i];
+#pragma unroll
+                        for (int s6 = 0; s6 < 6; ++s6) buf[s6 * D + i] = xn[i] + lrp[s6][k] * d;
+                    }
                 }
             }
-        }
-        __syncthreads();
-        {
+            __syncthreads();
             const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
-            float* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
+            u64* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
             const int nseg = l > 0 ? 7 : 6;
             int total = 0;
             for (int s = 0; s < nseg; ++s) total += p1_mat(P, s).M;
@@ -419,77 +538,84 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 float dA, dB;
                 row_pair(p1_mat(P, sA), rA, buf + xoff[sA], p1_mat(P, sB), rB, buf + xoff[sB], lane, dA, dB);
                 if (lane == 0) {
-                    st_ag(outs[sA] + rA, dA);
-                    if (row + NW < hi) st_ag(outs[sB] + rB, dB);
+                    ex_put(outs[sA] + rA, dA, ep);
+                    if (row + NW < hi) ex_put(outs[sB] + rB, dB, ep);
                 }
             }
         }
+        const RkPLayer& P = Ls2[l & 1];
         RKP_MARK(l * 6 + 0, 1);
-        // Head owners load their state rows and channel parameters while the
-        // barrier completes (none depends on it).
-        f4 pS0 = {0, 0, 0, 0}, pS1 = {0, 0, 0, 0};
-        float pw0 = 0, pv0 = 0, pa0 = 0, pkk = 0, pka = 0, prk = 0, plw = 0, plb = 0, pvf = 0;
-        bar_arrive(A.bar, gen, wg, G, &slast);
-        if (wg < NH) {
-            const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
-                                           (tid & 7) * 8);
-            pS0 = Sp[0];
-            pS1 = Sp[1];
-            const int c = wg * HS + (tid & 63);
-            pw0 = glb(P.w0)[c]; pv0 = glb(P.v0)[c]; pa0 = glb(P.a0)[c]; pkk = glb(P.kk)[c];
-            pka = glb(P.ka)[c]; prk = glb(P.rk)[c]; plw = glb(P.lnxw)[c]; plb = glb(P.lnxb)[c];
-            // v_first is rewritten by this workgroup in layer 0 of every launch:
-            // read it past the caches.
-            pvf = __hip_atomic_load(A.vfirst + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        issued();
-        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
-        RKP_MARK(l * 6 + 1, 0);
 
         // ---- P2: head h = wg (rwkv7.c:143-189, 229-299)
-        if (wg == 0)
-            for (int i = tid; i < D; i += NT) sh0[i] = xn[i];        // shift_0 <- xn (:229)
+        if (wg >= NH) RKP_MARK(l * 6 + 1, 0);
         if (wg < NH) {
             const int h = wg, c0 = h * HS;
+            // State rows and channel parameters first (no exchange orders
+            // them), then the LoRA middles and r, k, v of the head's channels.
+            const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
+                                           (tid & 7) * 8);
+            const f4 pS0 = Sp[0], pS1 = Sp[1];
+            const int cc = c0 + (tid & 63);
+            const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
+            const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
             const int Rw = P.w1.M, Ra = P.a1.M, Rg = P.g1.M, Rv = P.v1.M;
             float* in_w = buf;                  // tanh(lw)
             float* in_a = buf + kRkPRank;       // la
             float* in_g = buf + 2 * kRkPRank;   // sig(lg)
             float* in_v = buf + 3 * kRkPRank;   // lv
-            for (int i = tid; i < kRkPRank; i += NT) {
-                if (i < Rw) in_w[i] = tanhf(s_lw[i]);
-                if (i < Ra) in_a[i] = s_la[i];
-                if (i < Rg) in_g[i] = sgm(s_lg[i]);
-                if (l > 0 && i < Rv) in_v[i] = s_lv[i];
+            float* r_ = hv[9];
+            float* kx = hv[11];                 // k of the channel (before k2)
+            float* vx = hv[3];                  // v (dv goes to hv[10] below)
+            {
+                const int i = min(tid, kRkPRank - 1), c = c0 + (tid & 63);
+                const bool lora = tid < kRkPRank, chan = tid < HS;
+                const u64* at[7] = {s_lw + i, s_la + i, s_lg + i, s_lv + i, s_r + c, s_k + c, s_v + c};
+                const bool use[7] = {lora && i < Rw, lora && i < Ra, lora && i < Rg, lora && l > 0 && i < Rv,
+                                     chan, chan, chan};
+                u64 w[7];
+#pragma unroll
+                for (int k = 0; k < 7; ++k) w[k] = use[k] ? ex_get(at[k]) : ((u64)pc.want << 32);
+                const bool ok = ex_spin(w, at, pc);
+                __syncthreads();   // every wave is done with X6 in buf
+                if (use[0]) in_w[i] = tanhf(ex_f(w[0]));
+                if (use[1]) in_a[i] = ex_f(w[1]);
+                if (use[2]) in_g[i] = sgm(ex_f(w[2]));
+                if (use[3]) in_v[i] = ex_f(w[3]);
+                if (chan) {
+                    r_[tid] = ex_f(w[4]);
+                    kx[tid] = ex_f(w[5]);
+                    vx[tid] = ex_f(w[6]);
+                }
+                if (!agree(ok)) return;
             }
-            __syncthreads();
+            RKP_MARK(l * 6 + 1, 0);
             small_rows(P.w2, c0, HS, in_w, hv[0], wv, lane);     // dw
             small_rows(P.a2, c0, HS, in_a, hv[1], wv, lane);     // da
             small_rows(P.g2, c0, HS, in_g, hv[2], wv, lane);     // g
-            if (l > 0) small_rows(P.v2, c0, HS, in_v, hv[3], wv, lane);   // dv
+            if (l > 0) small_rows(P.v2, c0, HS, in_v, hv[10], wv, lane);   // dv
             __syncthreads();
             float* w_ = hv[4]; float* k_ = hv[5]; float* v_ = hv[6]; float* a_ = hv[7];
-            float* kn_ = hv[8]; float* r_ = hv[9]; float* y_ = hv[10];
+            float* kn_ = hv[8]; float* y_ = hv[10];
             if (tid < HS) {
                 const int c = c0 + tid;
                 const float ww = expf(-sgm(hv[0][tid] + pw0) * kR2);            // :236-237
-                float vv = s_v[c];
+                float vv = vx[tid];
                 if (l == 0) {
-                    st_ag(A.vfirst + c, vv);                                     // :240
+                    vfo = vv;
+                    A.vfirst[c] = vv;                                            // :240
                 } else {
-                    const float mix = sgm(hv[3][tid] + pv0);                     // :244-246
-                    vv = vv + (pvf - vv) * mix;
+                    const float mix = sgm(hv[10][tid] + pv0);                    // :244-246
+                    vv = vv + (vfo - vv) * mix;
                 }
                 const float av = sgm(hv[1][tid] + pa0);                         // :251-252
-                const float kv = s_k[c];
+                const float kv = kx[tid];
                 const float kkv = kv * pkk;                                      // :259
                 const float k2 = kv + kv * (av - 1.0f) * pka;                   // :260
                 float nrm = sqrtf(wsum(kkv * kkv));                              // :158-162
                 if (!(nrm > 1e-12f)) nrm = 1e-12f;
                 w_[tid] = ww; k_[tid] = k2; v_[tid] = vv; a_[tid] = av; kn_[tid] = kkv * (1.0f / nrm);
-                r_[tid] = s_r[c];
             }
-            __syncthreads();
+            __syncthreads();   // (y_ reuses dv's row: dv was read above)
             // S = S diag(w) - (S kk^)(kk^ a)^T + v k^T; y = S r. Thread t owns
             // row i = t / 8, columns 8 (t % 8) .. 8 (t % 8) + 7.
             const int i = tid >> 3, j0 = (tid & 7) * 8;
@@ -498,9 +624,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             float pv = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
-            pv += __shfl_xor(pv, 1, 64);
-            pv += __shfl_xor(pv, 2, 64);
-            pv += __shfl_xor(pv, 4, 64);
+            pv = grp_sum(pv, 8);
             const float vi = v_[i];
             float yacc = 0.0f;
 #pragma unroll
@@ -512,9 +636,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             }
             *reinterpret_cast<float4*>(Sr) = make_float4(s[0], s[1], s[2], s[3]);
             *reinterpret_cast<float4*>(Sr + 4) = make_float4(s[4], s[5], s[6], s[7]);
-            yacc += __shfl_xor(yacc, 1, 64);
-            yacc += __shfl_xor(yacc, 2, 64);
-            yacc += __shfl_xor(yacc, 4, 64);
+            yacc = grp_sum(yacc, 8);
             if ((tid & 7) == 0) y_[i] = yacc;
             __syncthreads();
             if (tid < HS) {
@@ -526,102 +648,132 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 const float rstd = 1.0f / sqrtf(wsum(d * d) / (float)HS + kEpsGroup);
                 const float dot = wsum(r_[tid] * k_[tid] * prk);
                 const float n = d * rstd * plw + plb;
-                st_ag(s_y + c, (n + dot * v_[tid]) * hv[2][tid]);
+                ex_put(s_y + c, (n + dot * v_[tid]) * hv[2][tid], ep);
             }
         }
         RKP_MARK(l * 6 + 1, 1);
-        bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
-        RKP_MARK(l * 6 + 2, 0);
 
         // ---- P3: x_a = x + W_o y (:290-292)
-        for (int i = tid; i < D; i += NT) buf[i] = s_y[i];
-        __syncthreads();
         {
             int lo, hi;
             share(D, wg, G, lo, hi);
-            for (int row = lo + wv; row < hi; row += NW) {
-                const float d = row_dot(P.o, row, buf, lane);
-                if (lane == 0) st_ag(s_xa + row, xs[row] + d);
-            }
+            const bool ok = with_format<true>(P.o, [&](auto q, auto nu) -> bool {
+                constexpr bool Q = decltype(q)::value;
+                constexpr int NU = decltype(nu)::value;
+                PreRows<Q, NU, 1> pr;
+                pre_load(pr, P.o, lo + wv, NW, lane);
+                issued();
+                if (!agree(poll_vec<kPer>(s_y, D, buf, pc))) return false;
+                RKP_MARK(l * 6 + 2, 0);
+                // shift_0 <- xn (:229). Every workgroup has read shift_0 by
+                // now: the owners have all of r, k, v and the LoRA middles,
+                // and every workgroup has rows among them (at most as many
+                // workgroups as those rows).
+                if (wg == 0)
+                    for (int i = tid; i < D; i += NT) sh0[i] = xn[i];
+                for (int row = lo + wv; row < hi; row += NW) {
+                    float d[1];
+                    if (row == lo + wv) pre_dot(pr, P.o, buf, lane, d);
+                    else d[0] = row_dot(P.o, row, buf, lane);
+                    if (lane == 0) ex_put(s_xa + row, xs[row] + d[0], ep);
+                }
+                return true;
+            });
+            if (!ok) return;
         }
         RKP_MARK(l * 6 + 2, 1);
-        bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
-        RKP_MARK(l * 6 + 3, 0);
 
         // ---- P4: xn2 = LN_2(x_a); xk2 = xn2 + cmk_lerp (shift_1 - xn2); ck = relu(W_ck xk2)^2
-        for (int i = tid; i < D; i += NT) xs[i] = s_xa[i];
-        __syncthreads();
-        {
-            float shv[kPer], lrp[kPer];
-#pragma unroll
-            for (int k = 0; k < kPer; ++k) {
-                const int ic = min(k * NT + tid, D - 1);
-                shv[k] = sh1[ic];
-                lrp[k] = P.cmk_lerp[ic];
-            }
-            layer_norm(xs, xn2, P.ln2w, P.ln2b, D, A.eps, red);
-#pragma unroll
-            for (int k = 0; k < kPer; ++k) {
-                const int i = k * NT + tid;
-                if (i < D) buf[i] = xn2[i] + lrp[k] * (shv[k] - xn2[i]);
-            }
-        }
-        __syncthreads();
         {
             int lo, hi;
             share(F, wg, G, lo, hi);
-            for (int row = lo + wv; row < hi; row += 2 * NW) {
-                const int rowB = min(row + NW, hi - 1);
-                float dA, dB;
-                row_pair(P.cmk, row, buf, P.cmk, rowB, buf, lane, dA, dB);
-                const float tA = dA > 0.0f ? dA : 0.0f, tB = dB > 0.0f ? dB : 0.0f;
-                if (lane == 0) {
-                    st_ag(s_ck + row, tA * tA);
-                    if (row + NW < hi) st_ag(s_ck + rowB, tB * tB);
+            const bool ok = with_format<true>(P.cmk, [&](auto q, auto nu) -> bool {
+                constexpr bool Q = decltype(q)::value;
+                constexpr int NU = decltype(nu)::value;
+                PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
+                pre_load(pr, P.cmk, lo + wv, NW, lane);
+                float shv[kPer], lrp[kPer];
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) {
+                    const int ic = min(k * NT + tid, D - 1);
+                    shv[k] = sh1[ic];
+                    lrp[k] = P.cmk_lerp[ic];
                 }
-            }
+                issued();
+                if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
+                RKP_MARK(l * 6 + 3, 0);
+                layer_norm(xs, xn2, P.ln2w, P.ln2b, D, A.eps, red);
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) {
+                    const int i = k * NT + tid;
+                    if (i < D) buf[i] = xn2[i] + lrp[k] * (shv[k] - xn2[i]);
+                }
+                __syncthreads();
+                for (int row = lo + wv; row < hi; row += 2 * NW) {
+                    const int rowB = min(row + NW, hi - 1);
+                    float d[2];
+                    if (row == lo + wv) pre_dot(pr, P.cmk, buf, lane, d);
+                    else row_pair(P.cmk, row, buf, P.cmk, rowB, buf, lane, d[0], d[1]);
+                    const float tA = d[0] > 0.0f ? d[0] : 0.0f, tB = d[1] > 0.0f ? d[1] : 0.0f;
+                    if (lane == 0) {
+                        ex_put(s_ck + row, tA * tA, ep);
+                        if (row + NW < hi) ex_put(s_ck + rowB, tB * tB, ep);
+                    }
+                }
+                return true;
+            });
+            if (!ok) return;
         }
         RKP_MARK(l * 6 + 3, 1);
-        bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
-        RKP_MARK(l * 6 + 4, 0);
 
         // ---- P5: x_b = x_a + W_cv ck; shift_1 <- xn2 (:305-315)
-        if (wg == 0)
-            for (int i = tid; i < D; i += NT) sh1[i] = xn2[i];
-        for (int i = tid; i < F; i += NT) buf[i] = s_ck[i];
-        __syncthreads();
         {
             int lo, hi;
             share(D, wg, G, lo, hi);
-            for (int row = lo + wv; row < hi; row += NW) {
-                const float d = row_dot(P.cmv, row, buf, lane);
-                if (lane == 0) st_ag(s_xb + row, xs[row] + d);
-            }
+            const bool ok = with_format(P.cmv, [&](auto q, auto nu) -> bool {
+                constexpr bool Q = decltype(q)::value;
+                constexpr int NU = decltype(nu)::value;
+                PreRows<Q, NU, 1> pr;
+                pre_load(pr, P.cmv, lo + wv, NW, lane);
+                issued();
+                if (!agree(poll_vec<kPerF>(s_ck, F, buf, pc))) return false;
+                RKP_MARK(l * 6 + 4, 0);
+                // Every workgroup has read shift_1 by now: each has rows of
+                // ck (at most F workgroups).
+                if (wg == 0)
+                    for (int i = tid; i < D; i += NT) sh1[i] = xn2[i];
+                for (int row = lo + wv; row < hi; row += NW) {
+                    float d[1];
+                    if (row == lo + wv) pre_dot(pr, P.cmv, buf, lane, d);
+                    else d[0] = row_dot(P.cmv, row, buf, lane);
+                    if (lane == 0) ex_put(s_xb + row, xs[row] + d[0], ep);
+                }
+                return true;
+            });
+            if (!ok) return;
         }
         RKP_MARK(l * 6 + 4, 1);
-        bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
     }
     RKP_MARK(64 * 6, 0);
 
-    // ---- head: logits = W_head LN_out(x) (:358-359), argmax keys
+    // ---- head: logits = W_head LN_out(x) (:358-359), argmax keys. Passes of
+    // N rows per wave alternate between two register sets: the next pass is
+    // issued before the current one is multiplied, and the first before x
+    // arrives.
     {
-        const float* xb = A.xch + (size_t)(L - 1) * slab + 5 * D;
-        for (int i = tid; i < D; i += NT) xs[i] = xb[i];
-        __syncthreads();
-        layer_norm(xs, buf, A.on_w, A.on_b, D, A.eps, red);
         int lo, hi;
         share(A.vocab, wg, G, lo, hi);
         u64 best = 0ull;
-        auto head_rows = [&](auto q, auto nrows) {
+        auto head_rows = [&](auto q, auto nrows) -> bool {
             constexpr bool Q = decltype(q)::value;
             constexpr int N = decltype(nrows)::value;
-            for (int row = lo + wv; row < hi; row += N * NW) {
-                float d[N];
-                row_dotn<Q, N>(A.head, row, NW, hi, buf, lane, d);
+            constexpr int STEP = N * NW;
+            PreRows<Q, 1, N> ra, rb;
+            pre_load(ra, A.head, lo + wv, NW, lane);
+            issued();
+            if (!agree(poll_vec<kPer>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
+            layer_norm(xs, buf, A.on_w, A.on_b, D, A.eps, red);
+            auto finish = [&](const float (&d)[N], int row) {
 #pragma unroll
                 for (int k = 0; k < N; ++k) {
                     const int rk = row + k * NW;
@@ -630,26 +782,56 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                         best = max(best, argmax_key(d[k], rk));
                     }
                 }
+            };
+            for (int row = lo + wv; row < hi; row += 2 * STEP) {
+                pre_load(rb, A.head, row + STEP, NW, lane);
+                {
+                    float d[N];
+                    pre_dot(ra, A.head, buf, lane, d);
+                    finish(d, row);
+                }
+                pre_load(ra, A.head, row + 2 * STEP, NW, lane);
+                if (row + STEP < hi) {
+                    float d[N];
+                    pre_dot(rb, A.head, buf, lane, d);
+                    finish(d, row + STEP);
+                }
             }
+            return true;
         };
-        if (A.head.block == 0) head_rows(std::false_type{}, std::integral_constant<int, 4>{});
-        else head_rows(std::true_type{}, std::integral_constant<int, 16>{});
+        const bool ok = A.head.block == 0 ? head_rows(std::false_type{}, std::integral_constant<int, 2>{})
+                                          : head_rows(std::true_type{}, std::integral_constant<int, 16>{});
+        if (!ok) return;
         if (lane == 0) kred[wv] = best;
         __syncthreads();
-        if (tid == 0) {
+        if (tid < 2) {
             u64 b = kred[0];
             for (int w = 1; w < NW; ++w) b = max(b, kred[w]);
-            __hip_atomic_store(A.keys + wg, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ex_put_bits(A.keys + 2 * wg + tid, tid == 0 ? (uint32_t)(b >> 32) : (uint32_t)b, ep);
         }
     }
     RKP_MARK(64 * 6, 1);
-    if (!A.greedy) return;
-    bar_arrive(A.bar, gen, wg, G, &slast);
-        if (bar_wait(A.bar, A.err, A.spin_limit, A.stall, gen, &slast, &sdead)) return;
+    if (!A.greedy || wg != 0) return;
+    // ---- workgroup 0 reduces the keys to the greedy token
     RKP_MARK(64 * 6 + 1, 0);
-    if (wg == 0) {
+    {
+        constexpr int KW = 2 * kRkPMaxGrid / NT;
+        u64 w[KW];
+        const u64* at[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) {
+            const int i = k * NT + tid;
+            at[k] = A.keys + min(i, 2 * G - 1);
+            w[k] = i < 2 * G ? ex_get(at[k]) : ((u64)pc.want << 32);
+        }
+        if (!agree(ex_spin(w, at, pc))) return;
+        // word 2 j + 1 of a pair sits in the next lane (NT is even)
         u64 b = 0ull;
-        for (int i = tid; i < G; i += NT) b = max(b, A.keys[i]);
+#pragma unroll
+        for (int k = 0; k < KW; ++k) {
+            const uint32_t hi = (uint32_t)w[k], lo = (uint32_t)__shfl_down((int)(uint32_t)w[k], 1, 64);
+            if (k * NT + tid < 2 * G && (tid & 1) == 0) b = max(b, ((u64)hi << 32) | lo);
+        }
         for (int o = 32; o > 0; o >>= 1) {
             const u64 v = __shfl_xor(b, o, 64);
             b = max(b, v);
@@ -658,7 +840,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         __syncthreads();
         if (tid == 0) {
             u64 m = kred[0];
-            for (int w = 1; w < NW; ++w) m = max(m, kred[w]);
+            for (int w2 = 1; w2 < NW; ++w2) m = max(m, kred[w2]);
             const int32_t tk = (int32_t)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull));
             const int step = *A.counter;
             *A.tok = tk;
@@ -701,7 +883,7 @@ int rkp_grid(int NH) {
 }
 
 snhip_status launch_rk_persist(const RkPArgs& a, int G, hipStream_t st) {
-    if (G < 8 || G % 8 || G < a.NH) {
+    if (G < 8 || G % 8 || G < a.NH || G > kRkPMaxGrid) {
         set_last_error("RWKV-7 persistent step: bad grid");
         return SNHIP_E_INVAL;
     }

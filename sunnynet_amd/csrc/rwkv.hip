@@ -157,7 +157,9 @@ struct SnHipRwkv7 {
     // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
     int p_grid = 0;
     snhip::RkPArgs p_args{};
-    unsigned long long* p_bar = nullptr;
+    unsigned p_epoch = 0;                 // epoch of the last persistent launch
+    unsigned long long* p_words = nullptr;   // exchange slabs and key words (zeroed: epoch 0)
+    size_t p_nwords = 0;
     unsigned* p_err = nullptr;
     unsigned p_spin = 1u << 22;
     // A persistent step timed out after some layers had written S and shift in
@@ -270,7 +272,11 @@ bool take_mat(SnHipRwkv7* m, Cur& c, RMat& M, int in, int out, float* tmp0, floa
 RkPMat pmat(const RMat& M) { return RkPMat{M.w, M.q, M.sc, M.M, M.Kd, M.q ? M.block : 0}; }
 
 // The one-sequence persistent step (rkpersist.hip), when the device and the
-// shape allow it: its layer table, exchange slabs, barrier words and keys.
+// shape allow it: its layer table, exchange slabs and key words. The grid is
+// at most one workgroup per CU, and at most the rows of the first product
+// (r, k, v and the LoRA middles) and of the channel-mix key, so that every
+// workgroup produces rows of both: the kernel relies on that to know when
+// every workgroup has read the shift vectors it then overwrites.
 void setup_rk_persist(SnHipRwkv7* m) {
     if (const char* e = getenv("SNHIP_RK_PERSIST"))
         if (e[0] == '0') return;
@@ -281,8 +287,11 @@ void setup_rk_persist(SnHipRwkv7* m) {
         rk[4 * l] = A.Rw; rk[4 * l + 1] = A.Ra; rk[4 * l + 2] = A.Rv; rk[4 * l + 3] = A.Rg;
     }
     if (!rkp_shape_ok(m->D, m->F, m->HS, m->NH, reinterpret_cast<const int(*)[4]>(rk.data()), m->L)) return;
-    const int G = rkp_grid(m->NH);
-    if (G == 0) return;
+    int G = rkp_grid(m->NH);
+    int p1rows = 1 << 30;
+    for (int l = 0; l < m->L; ++l) p1rows = std::min(p1rows, 3 * m->D + rk[4 * l] + rk[4 * l + 1] + rk[4 * l + 3]);
+    G = std::min(G, std::min(p1rows, m->F)) / 8 * 8;
+    if (G < 8 || G < m->NH) return;
     std::vector<RkPLayer> tab(m->L);
     for (int l = 0; l < m->L; ++l) {
         const RkLayer& A = m->layers[l];
@@ -295,25 +304,27 @@ void setup_rk_persist(SnHipRwkv7* m) {
         P.cmk_lerp = A.cmk_lerp;
     }
     RkPLayer* dtab = ralloc<RkPLayer>(m, tab.size());
-    float* xch = ralloc<float>(m, (size_t)m->L * rkp_slab(m->D, m->F));
-    unsigned long long* keys = ralloc<unsigned long long>(m, G);
-    m->p_bar = ralloc<unsigned long long>(m, kRkPBarWords);
+    m->p_nwords = (size_t)m->L * rkp_slab(m->D, m->F) + 2 * (size_t)G;
+    m->p_words = ralloc<unsigned long long>(m, m->p_nwords);
     m->p_err = ralloc<unsigned>(m, 1);
-    if (!dtab || !xch || !keys || !m->p_bar || !m->p_err ||
-        hipMemcpy(dtab, tab.data(), tab.size() * sizeof(RkPLayer), hipMemcpyHostToDevice) != hipSuccess)
+    if (!dtab || !m->p_words || !m->p_err ||
+        hipMemcpy(dtab, tab.data(), tab.size() * sizeof(RkPLayer), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(m->p_words, 0, m->p_nwords * sizeof(unsigned long long)) != hipSuccess)
         return;
+    unsigned long long* xch = m->p_words;
+    unsigned long long* keys = xch + (size_t)m->L * rkp_slab(m->D, m->F);
     RkPArgs& a = m->p_args;
     a.layers = dtab; a.L = m->L; a.D = m->D; a.F = m->F; a.NH = m->NH; a.vocab = m->vocab; a.eps = m->eps;
     a.embed = m->embed; a.en_w = m->en_w; a.en_b = m->en_b; a.on_w = m->on_w; a.on_b = m->on_b;
     a.head = pmat(m->head);
     a.S = m->S; a.shift = m->shift; a.vfirst = m->vfirst; a.xch = xch; a.keys = keys;
     a.tok = m->tok; a.counter = m->counter;
-    a.bar = m->p_bar; a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = 0;
+    a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = 0;
     m->p_grid = G;
 }
 
-// reps persistent steps of sequence 0; the call waits for them and reports a
-// barrier time-out as an error. The kernel updates S and shift in place layer
+// reps persistent steps of sequence 0, each launch with a new epoch; the call
+// waits for them and reports a time-out of an exchange wait as an error. The kernel updates S and shift in place layer
 // by layer, so a time-out leaves them part-stepped: the handle is then refused
 // for stepping until its state is reset or set.
 snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps) {
@@ -323,11 +334,14 @@ snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps
     a.greedy = greedy ? 1 : 0;
     a.tok_hist = m->tok_hist;
     a.hist_cap = m->hist_cap;
-    SNHIP_CHECK(hipMemsetAsync(m->p_bar, 0, kRkPBarWords * sizeof(unsigned long long), m->work));
     SNHIP_CHECK(hipMemsetAsync(m->p_err, 0, sizeof(unsigned), m->work));
-    const unsigned per = rkp_barriers(m->L, greedy);
     for (int i = 0; i < reps; ++i) {
-        a.gen0 = per * (unsigned)i;
+        if (m->p_epoch == 0xFFFFFFFFu) {
+            // epochs start over from clean words
+            SNHIP_CHECK(hipMemsetAsync(m->p_words, 0, m->p_nwords * sizeof(unsigned long long), m->work));
+            m->p_epoch = 0;
+        }
+        a.epoch = ++m->p_epoch;
         const snhip_status rc = launch_rk_persist(a, m->p_grid, m->work);
         if (rc != SNHIP_OK) return rc;
     }
@@ -336,7 +350,7 @@ snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps
     SNHIP_CHECK(hipStreamSynchronize(m->work));
     if (err) {
         m->poisoned = 1;
-        set_last_error("RWKV-7 persistent step: a grid barrier timed out");
+        set_last_error("RWKV-7 persistent step: an exchange wait timed out");
         return SNHIP_E_DEVICE;
     }
     return SNHIP_OK;
