@@ -502,14 +502,53 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 reinterpret_cast<int*>(&Ls2[(l + 1) & 1])[tid] = reinterpret_cast<const int*>(A.layers + l + 1)[tid];
             __syncthreads();
             RKP_MARK(l * 6 + 0, 0);
-            {
+            // The workgroup's rows (r, k, v, then the LoRA down-projections,
+            // with V_1 from layer 1 on), from the segment sizes read at once.
+            const int nseg = l > 0 ? 7 : 6;
+            int M[7];
+#pragma unroll
+            for (int sg = 0; sg < 7; ++sg) M[sg] = sg < nseg ? p1_mat(P, sg).M : 0;
+            int total = 0;
+#pragma unroll
+            for (int sg = 0; sg < 7; ++sg) total += M[sg];
+            int lo, hi;
+            share(total, wg, G, lo, hi);
+            auto locate = [&](int row, int& sg, int& r) {
+                sg = 0;
+                r = row;
+#pragma unroll
+                for (int q = 0; q < 6; ++q)
+                    if (sg == q && r >= M[q]) {
+                        r -= M[q];
+                        sg = q + 1;
+                    }
+            };
+            bool uni = true;
+#pragma unroll
+            for (int sg = 1; sg < 7; ++sg) uni = uni && (sg >= nseg || (p1_mat(P, sg).block == 0) == (P.r.block == 0));
+            const float* lerp = P.lerp;
+            auto body = [&](auto q, bool pre) {
+                constexpr bool Q = decltype(q)::value;
+                const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
+                u64* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
                 float shv[kPer], lrp[6][kPer];      // loaded before the LayerNorm
 #pragma unroll
                 for (int k = 0; k < kPer; ++k) {
                     const int ic = min(k * NT + tid, D - 1);
                     shv[k] = sh0[ic];
 #pragma unroll
-                    for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = P.lerp[(size_t)s6 * D + ic];
+                    for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = lerp[(size_t)s6 * D + ic];
+                }
+                // the wave's first two rows, issued after x arrived and
+                // before the LayerNorm, which they overlap
+                const int row0 = lo + wv;
+                int sA0, rA0, sB0, rB0;
+                locate(min(row0, total - 1), sA0, rA0);
+                locate(min(row0 + NW, hi - 1) < 0 ? 0 : min(row0 + NW, hi - 1), sB0, rB0);
+                Unit UA, UB;
+                if (pre && row0 < hi) {
+                    unit_load<Q>(UA, p1_mat(P, sA0), rA0, min(lane, (p1_mat(P, sA0).K >> 4) - 1));
+                    unit_load<Q>(UB, p1_mat(P, sB0), rB0, min(lane, (p1_mat(P, sB0).K >> 4) - 1));
                 }
                 layer_norm(xs, xn, P.ln1w, P.ln1b, D, A.eps, red);
 #pragma unroll
@@ -521,27 +560,34 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                         for (int s6 = 0; s6 < 6; ++s6) buf[s6 * D + i] = xn[i] + lrp[s6][k] * d;
                     }
                 }
-            }
-            __syncthreads();
-            const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
-            u64* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
-            const int nseg = l > 0 ? 7 : 6;
-            int total = 0;
-            for (int s = 0; s < nseg; ++s) total += p1_mat(P, s).M;
-            int lo, hi;
-            share(total, wg, G, lo, hi);
-            for (int row = lo + wv; row < hi; row += 2 * NW) {
-                const int rowB = min(row + NW, hi - 1);
-                int sA = 0, rA = row, sB = 0, rB = rowB;
-                while (rA >= p1_mat(P, sA).M) rA -= p1_mat(P, sA++).M;
-                while (rB >= p1_mat(P, sB).M) rB -= p1_mat(P, sB++).M;
-                float dA, dB;
-                row_pair(p1_mat(P, sA), rA, buf + xoff[sA], p1_mat(P, sB), rB, buf + xoff[sB], lane, dA, dB);
-                if (lane == 0) {
-                    ex_put(outs[sA] + rA, dA, ep);
-                    if (row + NW < hi) ex_put(outs[sB] + rB, dB, ep);
+                __syncthreads();
+                for (int row = row0; row < hi; row += 2 * NW) {
+                    const int rowB = min(row + NW, hi - 1);
+                    int sA, rA, sB, rB;
+                    locate(row, sA, rA);
+                    locate(rowB, sB, rB);
+                    float dA, dB;
+                    if (pre && row == row0) {
+                        const RkPMat& WA = p1_mat(P, sA);
+                        const RkPMat& WB = p1_mat(P, sB);
+                        const int nA = WA.K >> 4, nB = WB.K >> 4;
+                        const float a = unit_dot<Q>(UA, WA, min(lane, nA - 1), buf + xoff[sA], 0.0f);
+                        const float b = unit_dot<Q>(UB, WB, min(lane, nB - 1), buf + xoff[sB], 0.0f);
+                        dA = wsum(lane < nA ? a : 0.0f);
+                        dB = wsum(lane < nB ? b : 0.0f);
+                    } else {
+                        row_pair(p1_mat(P, sA), rA, buf + xoff[sA], p1_mat(P, sB), rB, buf + xoff[sB], lane, dA,
+                                 dB);
+                    }
+                    if (lane == 0) {
+                        ex_put(outs[sA] + rA, dA, ep);
+                        if (row + NW < hi) ex_put(outs[sB] + rB, dB, ep);
+                    }
                 }
-            }
+            };
+            if (!uni) body(std::false_type{}, false);
+            else if (P.r.block != 0) body(std::true_type{}, true);
+            else body(std::false_type{}, true);
         }
         const RkPLayer& P = Ls2[l & 1];
         RKP_MARK(l * 6 + 0, 1);
@@ -550,14 +596,6 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         if (wg >= NH) RKP_MARK(l * 6 + 1, 0);
         if (wg < NH) {
             const int h = wg, c0 = h * HS;
-            // State rows and channel parameters first (no exchange orders
-            // them), then the LoRA middles and r, k, v of the head's channels.
-            const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
-                                           (tid & 7) * 8);
-            const f4 pS0 = Sp[0], pS1 = Sp[1];
-            const int cc = c0 + (tid & 63);
-            const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
-            const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
             const int Rw = P.w1.M, Ra = P.a1.M, Rg = P.g1.M, Rv = P.v1.M;
             float* in_w = buf;                  // tanh(lw)
             float* in_a = buf + kRkPRank;       // la
@@ -589,6 +627,15 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 if (!agree(ok)) return;
             }
             RKP_MARK(l * 6 + 1, 0);
+            // State rows and channel parameters, issued once the inputs are
+            // in (loads ahead of the wait would hold its first check back);
+            // the up-projections overlap them.
+            const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
+                                           (tid & 7) * 8);
+            const f4 pS0 = Sp[0], pS1 = Sp[1];
+            const int cc = c0 + (tid & 63);
+            const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
+            const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
             small_rows(P.w2, c0, HS, in_w, hv[0], wv, lane);     // dw
             small_rows(P.a2, c0, HS, in_a, hv[1], wv, lane);     // da
             small_rows(P.g2, c0, HS, in_g, hv[2], wv, lane);     // g
@@ -690,8 +737,11 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             const bool ok = with_format<true>(P.cmk, [&](auto q, auto nu) -> bool {
                 constexpr bool Q = decltype(q)::value;
                 constexpr int NU = decltype(nu)::value;
-                PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
-                pre_load(pr, P.cmk, lo + wv, NW, lane);
+                // x_a first; then the mix inputs and the wave's first two
+                // rows, which the LayerNorm overlaps (loads issued before the
+                // wait would hold the wait's first check back)
+                if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
+                RKP_MARK(l * 6 + 3, 0);
                 float shv[kPer], lrp[kPer];
 #pragma unroll
                 for (int k = 0; k < kPer; ++k) {
@@ -699,9 +749,9 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     shv[k] = sh1[ic];
                     lrp[k] = P.cmk_lerp[ic];
                 }
+                PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
+                pre_load(pr, P.cmk, lo + wv, NW, lane);
                 issued();
-                if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
-                RKP_MARK(l * 6 + 3, 0);
                 layer_norm(xs, xn2, P.ln2w, P.ln2b, D, A.eps, red);
 #pragma unroll
                 for (int k = 0; k < kPer; ++k) {
