@@ -3,8 +3,7 @@
 // snhip_decode_greedy_dev from 8 sequences up).
 //
 // The math is the decode step of sunnynet/runtime/sunnynet.c:212-334 for each
-// sequence. Per layer the grid walks through five phases, each ended by a grid
-// barrier:
+// sequence. Per layer the grid walks through five phases:
 //
 //   P0  at = LN_in(x) + conv(history) per sequence row; history shifted
 //   P1  v = V at and sfb = W_eff s (V's rows then W_eff's, one storage)
@@ -19,24 +18,34 @@
 // v_mfma_f32_16x16x4f32 number j multiplies component j of both, so a chunk's
 // 16 MFMAs cover its 64 k once; the waves' tiles are summed through LDS in wave
 // order. A workgroup takes tiles wg, wg + G, ...; the weights of its first tile
-// in the next product are loaded before it enters the barrier (they depend on
-// nothing the barrier orders), and those of its next tile while it multiplies
-// the current one.
+// in the next product are loaded once its tiles of the current one are done
+// (they depend on nothing the waits order), and those of its next tile while
+// it multiplies the current one.
 //
-// Coherence without cache fences. Every phase writes its outputs to a buffer
-// that no other phase of the launch writes (per-layer slabs of at, v, sfb, u,
-// z, s', x), with agent-coherent (sc1) stores, and each wave waits for its
-// stores before the barrier's arrival. A workgroup's XCD therefore never holds
-// a line of a buffer it reads after a barrier from earlier in the launch, and
-// plain cached loads return the new values; the kernel boundary orders launch
-// against launch. The old state s is read in P1/P2 and overwritten only in P4,
-// after its last reader in the launch.
+// Dataflow instead of grid barriers. Every row of P0 and every tile of P1-P4
+// has a flag word per layer; once the writer's stores (agent-coherent, sc1)
+// have completed, its thread 0 stores the launch's epoch there (agent scope),
+// and a tile waits only for the flags of what it reads:
 //
-// Barrier: workgroups arrive on one of 8 group counters (wg mod 8); the last
-// of a group adds to the top counter, the last there publishes the barrier's
-// generation in a flag word that everyone else polls. Counters are zeroed
-// before every launch; every poll is bounded (time-out -> error word -> every
-// workgroup leaves at its next barrier).
+//   P0 row b       the x' tiles of b's row block (layer l - 1)
+//   P1 V tile      the 16 rows of at of its row block (W_eff tiles: nothing;
+//                  s is the previous step's)
+//   P2 tile        the V tiles of its row block (all of v)
+//   P3 tile        the P2 tiles of its row block (all of u)
+//   P4 tile        the P3 tiles (all of z) and the W_eff tiles of its row
+//                  block: after those every reader of the old s rows it
+//                  overwrites is done (P2's readers precede P3)
+//
+// and the final LayerNorm of row b the last layer's x' tiles of its block.
+// Every wait is on an earlier phase (or layer), so with every workgroup
+// resident the launch always drains. Every phase writes its outputs to a
+// buffer no other phase of the launch writes (per-layer slabs of at, v, sfb,
+// u, z, s', x), and every reader of a row waits for all of the row's writers,
+// so no XCD holds a line of it from earlier in the launch and plain cached
+// loads return the new values; the kernel boundary orders launch against
+// launch. Flags are zeroed with the handle and epochs grow by one per launch;
+// every poll is bounded (time-out -> error word -> every workgroup leaves at
+// its next wait).
 #include "decode.h"
 
 namespace snhip {
@@ -234,54 +243,48 @@ __device__ __forceinline__ void row_stats(const float (&xv)[PERM], int n, float 
 // optimizer would otherwise sink a prefetch past the barrier wait to its use).
 __device__ __forceinline__ void issued() { asm volatile("" ::: "memory"); }
 
-// Grid barrier in two halves. Arrival: every wave's stores have completed,
-// then thread 0 counts the workgroup in (the last of a group adds to the top
-// counter, the last there publishes the generation in a flag word). Between
-// the halves the workgroup issues loads that depend on nothing the barrier
-// orders (the next product's weights), so their latency overlaps the wait.
-// (Measured: polling the 8 group counters directly instead of one flag word
-// is slower; the pollers contend with the arriving atomics.)
-__device__ __forceinline__ void bar_arrive(u64* bar, int G, unsigned& gen, int wg, bool& last) {
+// The writer's half: every wave's stores have completed, then thread 0
+// publishes the epoch in flag f.
+__device__ __forceinline__ void publish(unsigned* f, unsigned ep) {
     __builtin_amdgcn_s_waitcnt(0);          // this wave's stores have completed
     __syncthreads();
-    ++gen;
-    last = false;
-    if (threadIdx.x == 0) {
-        u64* top = bar;
-        u64* grp = bar + 32 * (1 + (wg & 7));   // 256 bytes apart
-        u64* flag = bar + 32 * 9;
-        const int ng = G >> 3;
-        const u64 old = __hip_atomic_fetch_add(grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == (u64)gen * ng - 1) {
-            const u64 o2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = o2 == (u64)gen * 8 - 1;
-        }
-        if (last) __hip_atomic_store(flag, (u64)gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(f, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The writer's half for every tile this workgroup took in a product (tiles
+// wg, wg + G, ... < T): one wait for all of their stores, then one flag each.
+__device__ __forceinline__ void publish_tiles(unsigned* f, int wg, int G, int T, int mb, int N, unsigned ep) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int t = wg + (int)threadIdx.x * G;
+    if (t < T) {
+        const Tile tl = tile_of(t, mb, N);
+        __hip_atomic_store(f + (size_t)(tl.m0 >> 4) * N + (tl.n0 >> 4), ep, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// Wait half: true if the launch is abandoned (a wait timed out).
-__device__ __forceinline__ bool bar_wait(u64* bar, unsigned* err, unsigned limit, unsigned stall, unsigned gen,
-                                         bool last, int* sdead) {
-    if (threadIdx.x == 0) {
-        u64* flag = bar + 32 * 9;
-        int dead = 0;
-        if (!last) {
-            unsigned n = 0;
-            while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (u64)gen + stall) {
-                if (++n > limit) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    dead = 1;
-                    break;
-                }
-                if ((n & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                    dead = 1;
-                    break;
-                }
+// The reader's half: until each of the n flags f[0 .. n) holds `want`; true
+// if the launch is abandoned (a wait timed out, here or in another
+// workgroup).
+__device__ __forceinline__ bool await(const unsigned* f, int n, unsigned want, unsigned* err, unsigned limit,
+                                      int* sdead) {
+    int dead = 0;
+    for (int i = threadIdx.x; i < n && !dead; i += NT) {
+        unsigned k = 0;
+        while (__hip_atomic_load(const_cast<unsigned*>(f + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
+            if (++k > limit) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                dead = 1;
+                break;
+            }
+            if ((k & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                dead = 1;
+                break;
             }
         }
-        *sdead = dead;
     }
+    if (dead) *sdead = 1;
     __syncthreads();
     return *sdead != 0;
 }
@@ -328,8 +331,7 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
     const int mb = (B + 15) / 16;
     const size_t sbs = (size_t)L * D;                    // state row stride
     const size_t hbs = (size_t)L * a.kh * D;             // history row stride
-    unsigned gen = a.gen0;
-    bool last = false;
+    const unsigned ep = a.epoch, want = a.epoch + a.stall;
     // Layer 0's input row b: the embedding row of token b (NaN for an id
     // outside the vocabulary, as k_embed writes), later layers' the residual.
     auto in_row = [&](int l, int b, bool& ok) -> const float* {
@@ -342,6 +344,7 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
         return a.embed + (size_t)(ok ? t : 0) * D;
     };
 
+    if (tid == 0) sdead = 0;
     for (int i = tid; i < L * (int)sizeof(PLayer) / 4; i += NT)
         reinterpret_cast<unsigned*>(ltab)[i] = reinterpret_cast<const unsigned*>(a.layers)[i];
     __syncthreads();
@@ -350,6 +353,21 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
     // Weight tiles and tiles of each product: (weight rows / 16) x mb.
     const int N1 = (R + D) / 16, N2 = (2 * D) / 16, N3 = I / 16, N4 = D / 16;
     const int T1 = N1 * mb, T2 = N2 * mb, T3 = N3 * mb, T4 = N4 * mb;
+    // Flags of layer l, phase ph: P0 one per row, P1-P4 one per tile, by
+    // (row block, weight tile).
+    const size_t nfl = batch_flag_words(1, B, D, I, R);
+    auto fl = [&](int l, int ph) -> unsigned* {
+        unsigned* f = a.flags + (size_t)l * nfl;
+        if (ph == 0) return f;
+        f += B;
+        if (ph == 1) return f;
+        f += (size_t)mb * N1;
+        if (ph == 2) return f;
+        f += (size_t)mb * N2;
+        if (ph == 3) return f;
+        return f + (size_t)mb * N3;
+    };
+    auto wait = [&](const unsigned* f, int n) { return await(f, n, want, a.err, a.spin_limit, &sdead); };
 
     WF<BLK> wa[NCM];
     if (wg < T1) load_w<BLK, NCD, FULL>(wa, mat(ltab[0].VW, R + D, D), tile_of(wg, mb, N1).n0, wv, lane);
@@ -369,6 +387,7 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
         BPROF(5 * l, 0);
         for (int b = wg; b < B; b += G) {
             fresh();
+            if (l > 0 && wait(fl(l - 1, 4) + (size_t)(b >> 4) * N4, N4)) return;
             bool xok;
             const float* xr = in_row(l, b, xok);
             const gptr<float> ng = glb(uni(P->ni_g));
@@ -403,21 +422,25 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
                 for (int t = kTaps - 2; t >= 1; --t) hb[(size_t)t * D + i] = h[t - 1][k];
                 hb[i] = raw;
             }
+            publish(fl(l, 0) + b, ep);
         }
         BPROF(5 * l, 2);
         BPROF(5 * l, 3);
-        bar_arrive(a.bar, G, gen, wg, last);
-        if (bar_wait(a.bar, a.err, a.spin_limit, a.stall, gen, last, &sdead)) return;
 
         // ---- P1: v = V at (rows 0..R) and sfb = W_eff s_old (rows R..R+D)
         {
             const Mat W = mat(P->VW, R + D, D);
             BPROF(5 * l + 1, 0);
+            int done_m = -1;                        // row block whose inputs are in
             for (int t = wg; t < T1; t += G) {
                 fresh();
                 const Tile tl = tile_of(t, mb, N1);
                 XF x[NCM];
                 const bool vrow = tl.n0 < R;            // V rows read at, W_eff rows s
+                if (vrow && tl.m0 != done_m) {         // (a row block waited for once)
+                    if (wait(fl(l, 0) + tl.m0, min(16, B - tl.m0))) return;
+                    done_m = tl.m0;
+                }
                 load_x<NCD, FULL>(x, vrow ? atl : s_l, vrow ? (long)D : (long)sbs, tl.m0, B, D, wv, lane);
                 if (t == wg) BPROF_LOADED(5 * l + 1, 1);
                 f4 acc[4] = {};
@@ -435,11 +458,10 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
             }
         }
         BPROF(5 * l + 1, 3);
-        bar_arrive(a.bar, G, gen, wg, last);
+        publish_tiles(fl(l, 1), wg, G, T1, mb, N1, ep);
         fresh();
         if (wg < T2) load_w<BLK, NCR, FULL>(wa, mat(P->U, 2 * D, R), tile_of(wg, mb, N2).n0, wv, lane);
         issued();
-        if (bar_wait(a.bar, a.err, a.spin_limit, a.stall, gen, last, &sdead)) return;
 
         // ---- P2: q = U v for channel group n0 / 16 (rows 0-7 values, 8-15
         // gates), competitive + decay gate, s' (sunnynet.c:248-266)
@@ -447,6 +469,7 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
             const Mat W = mat(P->U, 2 * D, R);
             const gptr<float> delta = glb(uni(P->delta));
             BPROF(5 * l + 2, 0);
+            int done_m = -1;                        // row block whose inputs are in
             for (int t = wg; t < T2; t += G) {
                 fresh();
                 const Tile tl = tile_of(t, mb, N2);
@@ -455,6 +478,10 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
                 const bool eon = tid < 128 && em < B;
                 const float e_dl = delta[ei];
                 const float e_s = s_l[(size_t)min(em, B - 1) * sbs + ei];
+                if (tl.m0 != done_m) {
+                    if (wait(fl(l, 1) + (size_t)(tl.m0 >> 4) * N1, R / 16)) return;
+                    done_m = tl.m0;
+                }
                 XF x[NCM];
                 load_x<NCR, FULL>(x, vl, R, tl.m0, B, R, wv, lane);
                 if (t == wg) BPROF_LOADED(5 * l + 2, 1);
@@ -476,11 +503,10 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
             }
         }
         BPROF(5 * l + 2, 3);
-        bar_arrive(a.bar, G, gen, wg, last);
+        publish_tiles(fl(l, 2), wg, G, T2, mb, N2, ep);
         fresh();
         if (wg < T3) load_w<BLK, NCD, FULL>(wa, mat(P->Wz, I, D), tile_of(wg, mb, N3).n0, wv, lane);
         issued();
-        if (bar_wait(a.bar, a.err, a.spin_limit, a.stall, gen, last, &sdead)) return;
 
         // ---- P3: z = wedge(W_z u) (sunnynet.c:268-271)
         // (the LN_mid gains of P4 are loaded here and staged in LDS before
@@ -500,9 +526,14 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
             const Mat W = mat(P->Wz, I, D);
             const float at = uni(P->a_tanh);
             BPROF(5 * l + 3, 0);
+            int done_m = -1;                        // row block whose inputs are in
             for (int t = wg; t < T3; t += G) {
                 fresh();
                 const Tile tl = tile_of(t, mb, N3);
+                if (tl.m0 != done_m) {
+                    if (wait(fl(l, 2) + (size_t)(tl.m0 >> 4) * N2, N2)) return;
+                    done_m = tl.m0;
+                }
                 XF x[NCM];
                 load_x<NCD, FULL>(x, ul, D, tl.m0, B, D, wv, lane);
                 if (t == wg) BPROF_LOADED(5 * l + 3, 1);
@@ -525,11 +556,10 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
                 gc[kBatchMaxK + k * NT + tid] = gcv[1][k];
             }
         BPROF(5 * l + 3, 3);
-        bar_arrive(a.bar, G, gen, wg, last);
+        publish_tiles(fl(l, 3), wg, G, T3, mb, N3, ep);
         fresh();
         if (wg < T4) load_w<BLK, NCI, FULL>(wa, mat(P->Wc, D, I), tile_of(wg, mb, N4).n0, wv, lane);
         issued();
-        if (bar_wait(a.bar, a.err, a.spin_limit, a.stall, gen, last, &sdead)) return;
 
         // ---- P4: x' = W_c LN_mid(z) + b s' + sfb + x (sunnynet.c:273-276)
         {
@@ -537,9 +567,16 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
             const float bg = uni(P->b_gain);
             const int nch = I / CH;
             BPROF(5 * l + 4, 0);
+            int done_m = -1;                        // row block whose inputs are in
             for (int t = wg; t < T4; t += G) {
                 fresh();
                 const Tile tl = tile_of(t, mb, N4);
+                if (tl.m0 != done_m) {
+                    if (wait(fl(l, 3) + (size_t)(tl.m0 >> 4) * N3, N3) ||
+                        wait(fl(l, 1) + (size_t)(tl.m0 >> 4) * N1 + R / 16, D / 16))
+                        return;
+                    done_m = tl.m0;
+                }
                 const int em = tl.m0 + ((tid & 255) >> 4), en = tl.n0 + (tid & 15);
                 const bool eon = tid < 256 && em < B;
                 const size_t eo = (size_t)min(em, B - 1) * D + en;
@@ -610,12 +647,11 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
             }
         }
         BPROF(5 * l + 4, 3);
-        bar_arrive(a.bar, G, gen, wg, last);
+        publish_tiles(fl(l, 4), wg, G, T4, mb, N4, ep);
         fresh();
         if (l + 1 < L && wg < T1)
             load_w<BLK, NCD, FULL>(wa, mat(ltab[l + 1].VW, R + D, D), tile_of(wg, mb, N1).n0, wv, lane);
         issued();
-        if (bar_wait(a.bar, a.err, a.spin_limit, a.stall, gen, last, &sdead)) return;
     }
 
     // ---- final LayerNorm of every row (sunnynet.c:330-332): the head's input
@@ -623,6 +659,7 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
     const float* xl = a.xs + (size_t)(L - 1) * B * D;
     for (int b = wg; b < B; b += G) {
         fresh();
+        if (wait(fl(L - 1, 4) + (size_t)(b >> 4) * N4, N4)) return;
         float xv[PERM], gv[PERM], cv[PERM];
 #pragma unroll
         for (int k = 0; k < PERM; ++k) {

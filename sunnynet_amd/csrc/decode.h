@@ -78,7 +78,6 @@ snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipSt
 // its XCD earlier in the launch.
 constexpr int kBatchMaxK = 1536;       // deepest product: 8 waves x 3 chunks of 64
 constexpr int kBatchMaxRow = 2048;     // longest LayerNorm row: 512 threads x 4
-constexpr int kBatchBarWords = 512;    // barrier words (zeroed before each launch)
 
 struct BatchArgs {
     const PLayer* layers;   // device array of L layers
@@ -98,12 +97,20 @@ struct BatchArgs {
     float* s;               // (B, L, D) state: old in, new out
     float* hist;            // (B, L, kh, D) conv history, newest first
     float* nrm;             // (B, D) LN_out of the last residual (the head's input)
-    unsigned long long* bar;  // kBatchBarWords barrier words, zero before the first launch of a call
-    unsigned gen0;          // barriers completed by the earlier launches since they were zeroed
-    unsigned* err;          // set on a barrier time-out
-    unsigned spin_limit;    // polls before a barrier wait gives up
-    unsigned stall;         // added to every awaited generation: > 0 only to test the time-out path
+    unsigned* flags;        // batch_flag_words(L, B, ...) dataflow flags, zeroed once
+    unsigned epoch;         // this launch's epoch (> 0, one more per launch)
+    unsigned* err;          // set on a wait's time-out
+    unsigned spin_limit;    // polls before a wait gives up
+    unsigned stall;         // added to every awaited epoch: > 0 only to test the time-out path
 };
+
+// Flag words of the batched kernel for L layers at B rows: per layer one per
+// row (P0) and one per 16 x 16 tile of P1-P4.
+__host__ __device__ inline size_t batch_flag_words(int L, int B, int D, int I, int R) {
+    const size_t mb = (size_t)(B + 15) / 16;
+    return (size_t)L * ((size_t)B + mb * ((size_t)(R + D) / 16 + (size_t)(2 * D) / 16 + (size_t)I / 16 +
+                                          (size_t)D / 16));
+}
 
 // Shapes the batched kernel handles: products no deeper than kBatchMaxK in
 // whole chunks of 64, LayerNorm rows up to kBatchMaxRow, four conv taps.

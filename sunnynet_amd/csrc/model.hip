@@ -611,9 +611,10 @@ struct SnHipModel {
     int batch_wg = 0;
     int batch_max = 64;
     float* bbuf = nullptr;                // per-layer slabs: xs, at, v, sfb, u, z, sn
-    unsigned long long* bbar = nullptr;   // barrier words
+    unsigned* bflags = nullptr;           // dataflow flags (zeroed once)
+    size_t bflag_words = 0;
     unsigned* berr = nullptr;             // time-out flag
-    unsigned batch_gen = 0;               // barriers of the launches since bbar was zeroed
+    unsigned batch_epoch = 0;             // epoch of the last batched launch
     bool half = false;                    // matrices rounded to fp16 at load (sn_load_h)
     int ready = 0;
 };
@@ -912,10 +913,12 @@ void setup_batch(SnHipModel* m) {
     const size_t B = (size_t)std::min(m->max_batch, m->batch_max);
     const size_t per = (size_t)m->L * (5 * (size_t)m->D + m->R + m->I);
     m->bbuf = dalloc<float>(m, B * per);
-    m->bbar = dalloc<unsigned long long>(m, kBatchBarWords);
+    m->bflag_words = batch_flag_words(m->L, (int)B, m->D, m->I, m->R);
+    m->bflags = dalloc<unsigned>(m, m->bflag_words);
     m->berr = dalloc<unsigned>(m, 1);
-    if (!m->bbuf || !m->bbar || !m->berr || !layer_table(m) || !host_err(m) ||
-        hipMemset(m->berr, 0, sizeof(unsigned)) != hipSuccess)
+    if (!m->bbuf || !m->bflags || !m->berr || !layer_table(m) || !host_err(m) ||
+        hipMemset(m->berr, 0, sizeof(unsigned)) != hipSuccess ||
+        hipMemset(m->bflags, 0, m->bflag_words * sizeof(unsigned)) != hipSuccess)
         return;
     m->batch_wg = G;
 }
@@ -1236,9 +1239,13 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
         a.z = p; p += LB * I;
         a.sn = p;
         a.s = m->s; a.hist = m->hist; a.nrm = m->nrm;
-        a.bar = m->bbar; a.err = m->berr; a.spin_limit = m->persist_spin; a.stall = m->persist_stall;
-        a.gen0 = m->batch_gen;
-        m->batch_gen += 5 * (unsigned)L;
+        a.flags = m->bflags; a.err = m->berr; a.spin_limit = m->persist_spin; a.stall = m->persist_stall;
+        if (m->batch_epoch == 0xFFFFFFFFu) {
+            // epochs start over from clean flags
+            SNHIP_CHECK(hipMemsetAsync(m->bflags, 0, m->bflag_words * sizeof(unsigned), st));
+            m->batch_epoch = 0;
+        }
+        a.epoch = ++m->batch_epoch;
         const snhip_status rc = launch_decode_batch(a, m->batch_wg, m->wfmt == SNHIP_WEIGHTS_INT4 ? m->block : 0, st);
         if (rc != SNHIP_OK) return rc;
         return enqueue_head(m, B, nullptr, logits_out, greedy, st, true);
@@ -1320,7 +1327,7 @@ snhip_status persist_status(SnHipModel* m) {
     if (m->h_err && m->h_err[1]) {
         m->h_err[1] = 0;
         m->poisoned = 1;
-        set_last_error("batched persistent decode: barrier wait timed out");
+        set_last_error("batched persistent decode: a dataflow wait timed out");
         return SNHIP_E_DEVICE;
     }
     return SNHIP_OK;
@@ -1348,11 +1355,8 @@ snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int
         // The batched persistent step is a handful of launches per step: they
         // are queued directly (a cooperative launch is not captured).
         if (batch) {
-            // Barrier counters restart from zero for this call's launches.
             m->persist_stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
             SNHIP_CHECK(hipMemsetAsync(m->berr, 0, sizeof(unsigned), m->work));
-            SNHIP_CHECK(hipMemsetAsync(m->bbar, 0, kBatchBarWords * sizeof(unsigned long long), m->work));
-            m->batch_gen = 0;
         }
         for (int i = 0; i < reps; ++i) {
             const snhip_status rc = enqueue_step(m, B, logits_out, greedy, m->work);
