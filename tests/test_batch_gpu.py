@@ -1,6 +1,6 @@
 """The persistent batched step (every layer of a step of 8..64 sequences in one
-cooperative launch, grid barriers between the phases) against the oracle and
-the per-kernel step path.
+cooperative launch, each tile waiting on the flags of the tiles it reads)
+against the oracle and the per-kernel step path.
 
 Bar as for every decode path: logits within 2e-5 absolute of the C oracle
 (bit-identical to the reference's sn_step), greedy tokens equal to the
@@ -116,7 +116,7 @@ def test_batched_kernel_is_deterministic(gpu, small):
 
 
 def test_batched_barrier_timeout_reports_error(gpu, small, monkeypatch):
-    """Every barrier wait is given a target the host raised out of reach: each
+    """Every dataflow wait is given a target the host raised out of reach: each
     workgroup gives up after its poll limit and leaves the kernel, and the
     call itself reports the error, on the device-tensor path as on the host
     one. The state may be part-stepped, so the handle refuses further steps

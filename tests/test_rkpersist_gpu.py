@@ -113,7 +113,7 @@ def test_persist_cfg4_int4(gpu, tmp_path_factory, monkeypatch):
 
 
 def test_persist_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
-    """Every barrier wait is given a target the host raised out of reach: each
+    """Every exchange wait is given a target the host raised out of reach: each
     workgroup gives up after its poll limit and leaves the kernel and the call
     reports an error (device step and host step alike). The kernel writes S
     and shift in place layer by layer, so the handle then refuses steps until
