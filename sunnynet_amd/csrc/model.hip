@@ -869,8 +869,11 @@ bool host_err(SnHipModel* m) {
 // Enables the persistent single-sequence decode when the shape fits it and the
 // device supports cooperative launches (SNHIP_PERSIST=0 turns it off;
 // SNHIP_PERSIST_WG caps the grid size). The grid is the largest size the
-// kernel accepts for the shape (persist_grid_ok) up to one workgroup per
-// four channels and per CU (measured fastest at dim 1024: 256 workgroups).
+// kernel accepts for the shape (persist_grid_ok) up to one workgroup per CU
+// and per four channels (fp32 / fp16 rows) or eight (INT4 rows): measured
+// fastest at dim 1024, 256 workgroups for fp32 (225.2 us/step against 250.4
+// at 128) and 128 for INT4 (180.2 against 184.0 at 256: half the workgroups
+// poll each exchange).
 void setup_persist(SnHipModel* m) {
     if (const char* e = getenv("SNHIP_PERSIST"))
         if (e[0] == '0') return;
@@ -884,7 +887,7 @@ void setup_persist(SnHipModel* m) {
         return;
     const int occ = persist_occupancy(persist_blk(m));
     if (occ < 1) return;
-    int cap = std::min(m->D / 4, ncu);
+    int cap = std::min(m->D / (m->wfmt == SNHIP_WEIGHTS_INT4 ? 8 : 4), ncu);
     if (const char* e = getenv("SNHIP_PERSIST_WG")) cap = atoi(e);
     cap = std::min(std::min(cap, ncu * occ), kPersistMaxGrid);
     int nwg = 0;
