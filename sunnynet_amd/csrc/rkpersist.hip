@@ -333,6 +333,69 @@ __device__ void small_rows(const RkPMat& W, int r0, int n, const float* X, float
     }
 }
 
+// The LoRA up-projections of head rows [c0, c0 + HS): W_2, A_2, G_2 and, when
+// nm = 4, V_2 (matrix m multiplies X0 + m kRkPRank into out(m)), in
+// small_rows' lanes and order, but in batches whose weight loads are all
+// issued before the first product: item i of the T = sum over m of K_m / 16
+// row passes goes to wave i mod NW, kUpI items per wave and batch (four
+// separate calls paid four memory latencies one after another).
+constexpr int kUpI = 4;
+struct UpPlan {
+    int lg[4];   // log2 of the units per row of matrix m
+    int nm, T;
+};
+template <bool Q>
+struct UpBatch {
+    Unit U[kUpI];
+    int mm[kUpI], ps[kUpI];
+};
+
+template <class Mat>
+__device__ __forceinline__ UpPlan up_plan(Mat&& mat, int nm) {
+    UpPlan pl;
+    pl.nm = nm;
+    pl.T = 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        pl.lg[m] = m < nm ? 31 - __builtin_clz(mat(m).K >> 4) : 0;
+        pl.T += m < nm ? 1 << pl.lg[m] : 0;
+    }
+    return pl;
+}
+
+// Loads the batch of items i0, i0 + NW, ... (wave-uniform i0).
+template <bool Q, class Mat>
+__device__ __forceinline__ void up_load(UpBatch<Q>& B, Mat&& mat, const UpPlan& pl, int i0, int c0, int lane) {
+#pragma unroll
+    for (int j = 0; j < kUpI; ++j) {
+        int m = 0, pass = min(i0 + NW * j, pl.T - 1);
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+            if (m == q && q + 1 < pl.nm && pass >= 1 << pl.lg[q]) {
+                pass -= 1 << pl.lg[q];
+                m = q + 1;
+            }
+        const int sub = lane >> pl.lg[m], u = lane - (sub << pl.lg[m]);
+        unit_load<Q>(B.U[j], mat(m), c0 + min((pass << (6 - pl.lg[m])) + sub, HS - 1), u);
+        B.mm[j] = m;
+        B.ps[j] = pass;
+    }
+}
+
+template <bool Q, class Mat, class Out>
+__device__ __forceinline__ void up_dot(const UpBatch<Q>& B, Mat&& mat, Out&& out, const UpPlan& pl, int i0,
+                                       const float* X0, int lane) {
+#pragma unroll
+    for (int j = 0; j < kUpI; ++j) {
+        if (i0 + NW * j >= pl.T) break;
+        const int m = B.mm[j], sub = lane >> pl.lg[m], u = lane - (sub << pl.lg[m]);
+        const int i = (B.ps[j] << (6 - pl.lg[m])) + sub;
+        float acc = unit_dot<Q>(B.U[j], mat(m), u, X0 + m * kRkPRank, 0.0f);
+        acc = grp_sum(i < HS ? acc : 0.0f, 1 << pl.lg[m]);
+        if (i < HS && u == 0) out(m)[i] = acc;
+    }
+}
+
 // ---- exchange words: the epoch of the launch that wrote the value in the
 // high half, the value's bits in the low half, stored and loaded as one
 // single-copy-atomic word at agent scope. A reader polls a word until it
@@ -604,99 +667,127 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             float* r_ = hv[9];
             float* kx = hv[11];                 // k of the channel (before k2)
             float* vx = hv[3];                  // v (dv goes to hv[10] below)
-            {
-                const int i = min(tid, kRkPRank - 1), c = c0 + (tid & 63);
-                const bool lora = tid < kRkPRank, chan = tid < HS;
-                const u64* at[7] = {s_lw + i, s_la + i, s_lg + i, s_lv + i, s_r + c, s_k + c, s_v + c};
-                const bool use[7] = {lora && i < Rw, lora && i < Ra, lora && i < Rg, lora && l > 0 && i < Rv,
-                                     chan, chan, chan};
-                u64 w[7];
+            // up-projections: dw, da, g and (from layer 1 on) dv
+            const int nm = l > 0 ? 4 : 3;
+            auto upm = [&](int m) -> const RkPMat& { return m == 0 ? P.w2 : m == 1 ? P.a2 : m == 2 ? P.g2 : P.v2; };
+            auto upo = [&](int m) -> float* { return hv[m == 3 ? 10 : m]; };
+            const UpPlan pl = up_plan(upm, nm);
+            const bool q4 = P.w2.block != 0;
+            const bool uni = (P.a2.block != 0) == q4 && (P.g2.block != 0) == q4 && (nm < 4 || (P.v2.block != 0) == q4);
+            auto owner = [&](auto q, bool batched) -> bool {
+                constexpr bool Q = decltype(q)::value;
+                // The head's state rows, its channel parameters and the first
+                // batch of up-projection weights are issued ahead of the wait
+                // for the phase's inputs, which (every workgroup's P1 rows and
+                // a round trip) outlasts their memory latency.
+                const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
+                                               (tid & 7) * 8);
+                const f4 pS0 = Sp[0], pS1 = Sp[1];
+                const int cc = c0 + (tid & 63);
+                const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
+                const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
+                UpBatch<Q> ub;
+                if (batched) up_load<Q>(ub, upm, pl, wv, c0, lane);
+                issued();
+                {
+                    const int i = min(tid, kRkPRank - 1), c = c0 + (tid & 63);
+                    const bool lora = tid < kRkPRank, chan = tid < HS;
+                    const u64* at[7] = {s_lw + i, s_la + i, s_lg + i, s_lv + i, s_r + c, s_k + c, s_v + c};
+                    const bool use[7] = {lora && i < Rw, lora && i < Ra, lora && i < Rg, lora && l > 0 && i < Rv,
+                                         chan, chan, chan};
+                    u64 w[7];
 #pragma unroll
-                for (int k = 0; k < 7; ++k) w[k] = use[k] ? ex_get(at[k]) : ((u64)pc.want << 32);
-                const bool ok = ex_spin(w, at, pc);
-                __syncthreads();   // every wave is done with X6 in buf
-                if (use[0]) in_w[i] = tanhf(ex_f(w[0]));
-                if (use[1]) in_a[i] = ex_f(w[1]);
-                if (use[2]) in_g[i] = sgm(ex_f(w[2]));
-                if (use[3]) in_v[i] = ex_f(w[3]);
-                if (chan) {
-                    r_[tid] = ex_f(w[4]);
-                    kx[tid] = ex_f(w[5]);
-                    vx[tid] = ex_f(w[6]);
+                    for (int k = 0; k < 7; ++k) w[k] = use[k] ? ex_get(at[k]) : ((u64)pc.want << 32);
+                    const bool ok = ex_spin(w, at, pc);
+                    __syncthreads();   // every wave is done with X6 in buf
+                    if (use[0]) in_w[i] = tanhf(ex_f(w[0]));
+                    if (use[1]) in_a[i] = ex_f(w[1]);
+                    if (use[2]) in_g[i] = sgm(ex_f(w[2]));
+                    if (use[3]) in_v[i] = ex_f(w[3]);
+                    if (chan) {
+                        r_[tid] = ex_f(w[4]);
+                        kx[tid] = ex_f(w[5]);
+                        vx[tid] = ex_f(w[6]);
+                    }
+                    if (!agree(ok)) return false;
                 }
-                if (!agree(ok)) return;
-            }
-            RKP_MARK(l * 6 + 1, 0);
-            // State rows and channel parameters, issued once the inputs are
-            // in (loads ahead of the wait would hold its first check back);
-            // the up-projections overlap them.
-            const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
-                                           (tid & 7) * 8);
-            const f4 pS0 = Sp[0], pS1 = Sp[1];
-            const int cc = c0 + (tid & 63);
-            const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
-            const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
-            small_rows(P.w2, c0, HS, in_w, hv[0], wv, lane);     // dw
-            small_rows(P.a2, c0, HS, in_a, hv[1], wv, lane);     // da
-            small_rows(P.g2, c0, HS, in_g, hv[2], wv, lane);     // g
-            if (l > 0) small_rows(P.v2, c0, HS, in_v, hv[10], wv, lane);   // dv
-            __syncthreads();
-            float* w_ = hv[4]; float* k_ = hv[5]; float* v_ = hv[6]; float* a_ = hv[7];
-            float* kn_ = hv[8]; float* y_ = hv[10];
-            if (tid < HS) {
-                const int c = c0 + tid;
-                const float ww = expf(-sgm(hv[0][tid] + pw0) * kR2);            // :236-237
-                float vv = vx[tid];
-                if (l == 0) {
-                    vfo = vv;
-                    A.vfirst[c] = vv;                                            // :240
+                RKP_MARK(l * 6 + 1, 0);
+                if (batched) {
+                    up_dot<Q>(ub, upm, upo, pl, wv, buf, lane);
+                    for (int i0 = wv + NW * kUpI; i0 < pl.T; i0 += NW * kUpI) {
+                        up_load<Q>(ub, upm, pl, i0, c0, lane);
+                        up_dot<Q>(ub, upm, upo, pl, i0, buf, lane);
+                    }
                 } else {
-                    const float mix = sgm(hv[10][tid] + pv0);                    // :244-246
-                    vv = vv + (vfo - vv) * mix;
+                    small_rows(P.w2, c0, HS, in_w, hv[0], wv, lane);
+                    small_rows(P.a2, c0, HS, in_a, hv[1], wv, lane);
+                    small_rows(P.g2, c0, HS, in_g, hv[2], wv, lane);
+                    if (l > 0) small_rows(P.v2, c0, HS, in_v, hv[10], wv, lane);
                 }
-                const float av = sgm(hv[1][tid] + pa0);                         // :251-252
-                const float kv = kx[tid];
-                const float kkv = kv * pkk;                                      // :259
-                const float k2 = kv + kv * (av - 1.0f) * pka;                   // :260
-                float nrm = sqrtf(wsum(kkv * kkv));                              // :158-162
-                if (!(nrm > 1e-12f)) nrm = 1e-12f;
-                w_[tid] = ww; k_[tid] = k2; v_[tid] = vv; a_[tid] = av; kn_[tid] = kkv * (1.0f / nrm);
-            }
-            __syncthreads();   // (y_ reuses dv's row: dv was read above)
-            // S = S diag(w) - (S kk^)(kk^ a)^T + v k^T; y = S r. Thread t owns
-            // row i = t / 8, columns 8 (t % 8) .. 8 (t % 8) + 7.
-            const int i = tid >> 3, j0 = (tid & 7) * 8;
-            float* Sr = A.S + ((size_t)l * NH + h) * HS * HS + (size_t)i * HS + j0;
-            float s[8] = {pS0.x, pS0.y, pS0.z, pS0.w, pS1.x, pS1.y, pS1.z, pS1.w};
-            float pv = 0.0f;
+                __syncthreads();
+                float* w_ = hv[4]; float* k_ = hv[5]; float* v_ = hv[6]; float* a_ = hv[7];
+                float* kn_ = hv[8]; float* y_ = hv[10];
+                if (tid < HS) {
+                    const int c = c0 + tid;
+                    const float ww = expf(-sgm(hv[0][tid] + pw0) * kR2);            // :236-237
+                    float vv = vx[tid];
+                    if (l == 0) {
+                        vfo = vv;
+                        A.vfirst[c] = vv;                                            // :240
+                    } else {
+                        const float mix = sgm(hv[10][tid] + pv0);                    // :244-246
+                        vv = vv + (vfo - vv) * mix;
+                    }
+                    const float av = sgm(hv[1][tid] + pa0);                         // :251-252
+                    const float kv = kx[tid];
+                    const float kkv = kv * pkk;                                      // :259
+                    const float k2 = kv + kv * (av - 1.0f) * pka;                   // :260
+                    float nrm = sqrtf(wsum(kkv * kkv));                              // :158-162
+                    if (!(nrm > 1e-12f)) nrm = 1e-12f;
+                    w_[tid] = ww; k_[tid] = k2; v_[tid] = vv; a_[tid] = av; kn_[tid] = kkv * (1.0f / nrm);
+                }
+                __syncthreads();   // (y_ reuses dv's row: dv was read above)
+                // S = S diag(w) - (S kk^)(kk^ a)^T + v k^T; y = S r. Thread t owns
+                // row i = t / 8, columns 8 (t % 8) .. 8 (t % 8) + 7.
+                const int i = tid >> 3, j0 = (tid & 7) * 8;
+                float* Sr = A.S + ((size_t)l * NH + h) * HS * HS + (size_t)i * HS + j0;
+                float s[8] = {pS0.x, pS0.y, pS0.z, pS0.w, pS1.x, pS1.y, pS1.z, pS1.w};
+                float pv = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
-            pv = grp_sum(pv, 8);
-            const float vi = v_[i];
-            float yacc = 0.0f;
+                for (int q = 0; q < 8; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
+                pv = grp_sum(pv, 8);
+                const float vi = v_[i];
+                float yacc = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int j = j0 + q;
-                const float ns = fmaf(s[q], w_[j], vi * k_[j] - pv * (kn_[j] * a_[j]));   // :180-181
-                s[q] = ns;
-                yacc = fmaf(ns, r_[j], yacc);
-            }
-            *reinterpret_cast<float4*>(Sr) = make_float4(s[0], s[1], s[2], s[3]);
-            *reinterpret_cast<float4*>(Sr + 4) = make_float4(s[4], s[5], s[6], s[7]);
-            yacc = grp_sum(yacc, 8);
-            if ((tid & 7) == 0) y_[i] = yacc;
-            __syncthreads();
-            if (tid < HS) {
-                // group norm, bonus, gate (:266-288)
-                const int c = c0 + tid;
-                const float yy = y_[tid];
-                const float mean = wsum(yy) / (float)HS;
-                const float d = yy - mean;
-                const float rstd = 1.0f / sqrtf(wsum(d * d) / (float)HS + kEpsGroup);
-                const float dot = wsum(r_[tid] * k_[tid] * prk);
-                const float n = d * rstd * plw + plb;
-                ex_put(s_y + c, (n + dot * v_[tid]) * hv[2][tid], ep);
-            }
+                for (int q = 0; q < 8; ++q) {
+                    const int j = j0 + q;
+                    const float ns = fmaf(s[q], w_[j], vi * k_[j] - pv * (kn_[j] * a_[j]));   // :180-181
+                    s[q] = ns;
+                    yacc = fmaf(ns, r_[j], yacc);
+                }
+                *reinterpret_cast<float4*>(Sr) = make_float4(s[0], s[1], s[2], s[3]);
+                *reinterpret_cast<float4*>(Sr + 4) = make_float4(s[4], s[5], s[6], s[7]);
+                yacc = grp_sum(yacc, 8);
+                if ((tid & 7) == 0) y_[i] = yacc;
+                __syncthreads();
+                if (tid < HS) {
+                    // group norm, bonus, gate (:266-288)
+                    const int c = c0 + tid;
+                    const float yy = y_[tid];
+                    const float mean = wsum(yy) / (float)HS;
+                    const float d = yy - mean;
+                    const float rstd = 1.0f / sqrtf(wsum(d * d) / (float)HS + kEpsGroup);
+                    const float dot = wsum(r_[tid] * k_[tid] * prk);
+                    const float n = d * rstd * plw + plb;
+                    ex_put(s_y + c, (n + dot * v_[tid]) * hv[2][tid], ep);
+                }
+                return true;
+            };
+            bool ok;
+            if (!uni) ok = owner(std::false_type{}, false);
+            else if (q4) ok = owner(std::true_type{}, true);
+            else ok = owner(std::false_type{}, true);
+            if (!ok) return;
         }
         RKP_MARK(l * 6 + 1, 1);
 
