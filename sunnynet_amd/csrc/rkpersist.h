@@ -37,7 +37,9 @@ struct RkPArgs {
     int32_t* tok_hist;
     int32_t* counter;
     int hist_cap, greedy;
-    unsigned epoch;           // this launch's epoch (> 0; every launch of the handle a new one)
+    unsigned epoch;           // the epoch of the launch's first step (> 0; step st uses epoch + st, and
+                              // no epoch is used twice between two clearings of the words)
+    int nsteps;               // steps of the launch (greedy; 1 otherwise)
     unsigned* err;
     unsigned spin_limit;
     unsigned stall;           // added to every wait target: tests force time-outs with it

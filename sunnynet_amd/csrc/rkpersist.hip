@@ -18,19 +18,24 @@
 //   P4  LN_2 + channel-mix input (every workgroup), rows of W_ck, relu^2;
 //   P5  rows of W_cv, x_b = x_a + W_cv ck.
 //
-// then LN_out and the head rows with a per-workgroup argmax key, and workgroup
-// 0 reduces the keys to the greedy token.
+// then LN_out and the head rows with a per-workgroup argmax key, and every
+// workgroup reduces the keys to the greedy token, the next step's input: a
+// greedy launch runs many steps (and a step that returns logits, one).
 //
 // Exchange without grid barriers. Every value a phase produces has its own
 // word in a per-layer slab: the launch's epoch in the high half, the value's
 // bits in the low half, written once per launch with one agent-scope store.
 // A phase's readers poll the words they need until each carries the epoch,
 // so a phase waits for exactly its inputs, in one store-to-load round trip
-// across XCDs. The kernel boundary orders one step's writes before the next
-// step's reads. The recurrent state (S, v_first) is read and written only by
-// the workgroup that owns it; the shift vectors, read by every workgroup in
-// P1 / P4 and rewritten by workgroup 0, are rewritten only once workgroup 0
-// has seen outputs of every workgroup that follow those reads.
+// across XCDs. Step st of a launch uses the epoch A.epoch + st, and a word's
+// first write in a step follows every workgroup's argmax keys of the step
+// before, so every read of the word in that step. The recurrent state (S,
+// v_first) is read and written only by the threads that own it. The shift
+// vectors, read by every workgroup in P1 / P4 and rewritten by workgroup 0,
+// are rewritten only once workgroup 0 has seen outputs of every workgroup
+// that follow those reads; they are stored and loaded at agent scope, and a
+// rewrite completes before workgroup 0's next exchange wait, so before its
+// keys, which every reader of the next step has seen.
 #include <type_traits>
 
 #include "gemv.h"
@@ -55,6 +60,9 @@ __device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x));
 
 __device__ __forceinline__ void st_ag(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_ag(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Cross-lane sums through DPP moves (VALU, no LDS round trips): within
@@ -515,11 +523,8 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     __shared__ RkPLayer Ls2[2];                  // layer tables of layers l (l & 1) and l + 1
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wg = blockIdx.x, G = gridDim.x;
-    const int D = A.D, F = A.F, L = A.L, NH = A.NH;
-    const size_t slab = rkp_slab(D, F);
-    const unsigned ep = A.epoch;
-    const PollCtl pc{A.err, A.spin_limit, A.epoch + A.stall};
+    const int wg = blockIdx.x, G0 = gridDim.x;
+    const int D0 = A.D, F0 = A.F, L0 = A.L, NH0 = A.NH;
     if (tid == 0) sdead = 0;
     if (tid < (int)(sizeof(RkPLayer) / 4))
         reinterpret_cast<int*>(&Ls2[0])[tid] = reinterpret_cast<const int*>(A.layers)[tid];
@@ -532,462 +537,482 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
         return sdead == 0;
     };
     float vfo = 0.0f;   // head owners, thread c < 64: v_first of channel c (layer 0's v)
+    int tok = *A.tok;
+    const int cnt0 = *A.counter;
 
-    // x = LN_0(E[tok]) (rwkv7.c:351-352); NaN for an out-of-range id.
-    {
-        const int t = *A.tok;
-        const bool ok = t >= 0 && t < A.vocab;
-        const float* er = A.embed + (size_t)(ok ? t : 0) * D;
-        for (int i = tid; i < D; i += NT) buf[i] = ok ? er[i] : __builtin_nanf("");
-        __syncthreads();
-        layer_norm(buf, xs, A.en_w, A.en_b, D, A.eps, red);
-    }
+    // Greedy launches run nsteps steps, step st with epoch A.epoch + st; every
+    // workgroup reduces the argmax keys to the next step's token itself.
+    for (int st = 0; st < A.nsteps; ++st) {
+        // The shape, opaque to the compiler in every step, so that what it
+        // derives is not hoisted out of the step loop and held in registers.
+        int D = D0, F = F0, L = L0, NH = NH0, G = G0;
+        asm volatile("" : "+s"(D), "+s"(F), "+s"(L), "+s"(NH), "+s"(G));
+        const size_t slab = rkp_slab(D, F);
+        const unsigned ep = A.epoch + (unsigned)st;
+        const PollCtl pc{A.err, A.spin_limit, ep + A.stall};
+        const bool last = st + 1 == A.nsteps;
 
-    for (int l = 0; l < L; ++l) {
-        u64* sl = A.xch + (size_t)l * slab;
-        u64 *s_r = sl, *s_k = sl + D, *s_v = sl + 2 * D, *s_y = sl + 3 * D, *s_xa = sl + 4 * D,
-            *s_xb = sl + 5 * D, *s_lw = sl + 6 * D, *s_la = s_lw + kRkPRank, *s_lg = s_la + kRkPRank,
-            *s_lv = s_lg + kRkPRank, *s_ck = s_lv + kRkPRank;
-        float* sh0 = A.shift + (size_t)l * 2 * D;
-        float* sh1 = sh0 + D;
-
-        // ---- P1: xn = LN_1(x); X6 = xn + lerp (shift_0 - xn); r k v, LoRA down
+        // x = LN_0(E[tok]) (rwkv7.c:351-352); NaN for an out-of-range id. From
+        // the second step on, layer 0's table goes back into slot 0 (every wave is
+        // past the previous step's last use of it: the key reduction's barrier).
         {
-            // x_b of the layer before (every wave is past its last use of xs
-            // and of the other layer-table slot once the poll's barrier is)
-            if (l > 0) {
-                const bool ok = poll_vec<kPer>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
-                if (!agree(ok)) return;
+            const bool ok = tok >= 0 && tok < A.vocab;
+            const float* er = A.embed + (size_t)(ok ? tok : 0) * D;
+            if (st > 0 && tid < (int)(sizeof(RkPLayer) / 4))
+                reinterpret_cast<int*>(&Ls2[0])[tid] = reinterpret_cast<const int*>(A.layers)[tid];
+            for (int i = tid; i < D; i += NT) buf[i] = ok ? er[i] : __builtin_nanf("");
+            __syncthreads();
+            layer_norm(buf, xs, A.en_w, A.en_b, D, A.eps, red);
+        }
+
+        for (int l = 0; l < L; ++l) {
+            u64* sl = A.xch + (size_t)l * slab;
+            u64 *s_r = sl, *s_k = sl + D, *s_v = sl + 2 * D, *s_y = sl + 3 * D, *s_xa = sl + 4 * D,
+                *s_xb = sl + 5 * D, *s_lw = sl + 6 * D, *s_la = s_lw + kRkPRank, *s_lg = s_la + kRkPRank,
+                *s_lv = s_lg + kRkPRank, *s_ck = s_lv + kRkPRank;
+            float* sh0 = A.shift + (size_t)l * 2 * D;
+            float* sh1 = sh0 + D;
+
+            // ---- P1: xn = LN_1(x); X6 = xn + lerp (shift_0 - xn); r k v, LoRA down
+            {
+                // x_b of the layer before (every wave is past its last use of xs
+                // and of the other layer-table slot once the poll's barrier is)
+                if (l > 0) {
+                    const bool ok = poll_vec<kPer>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
+                    if (!agree(ok)) return;
+                }
+                const RkPLayer& P = Ls2[l & 1];
+                // the next layer's table into the other slot
+                if (l + 1 < L && tid < (int)(sizeof(RkPLayer) / 4))
+                    reinterpret_cast<int*>(&Ls2[(l + 1) & 1])[tid] =
+                        reinterpret_cast<const int*>(A.layers + l + 1)[tid];
+                __syncthreads();
+                RKP_MARK(l * 6 + 0, 0);
+                // The workgroup's rows (r, k, v, then the LoRA down-projections,
+                // with V_1 from layer 1 on), from the segment sizes read at once.
+                const int nseg = l > 0 ? 7 : 6;
+                int M[7];
+#pragma unroll
+                for (int sg = 0; sg < 7; ++sg) M[sg] = sg < nseg ? p1_mat(P, sg).M : 0;
+                int total = 0;
+#pragma unroll
+                for (int sg = 0; sg < 7; ++sg) total += M[sg];
+                int lo, hi;
+                share(total, wg, G, lo, hi);
+                auto locate = [&](int row, int& sg, int& r) {
+                    sg = 0;
+                    r = row;
+#pragma unroll
+                    for (int q = 0; q < 6; ++q)
+                        if (sg == q && r >= M[q]) {
+                            r -= M[q];
+                            sg = q + 1;
+                        }
+                };
+                bool uni = true;
+#pragma unroll
+                for (int sg = 1; sg < 7; ++sg)
+                    uni = uni && (sg >= nseg || (p1_mat(P, sg).block == 0) == (P.r.block == 0));
+                const float* lerp = P.lerp;
+                auto body = [&](auto q, bool pre) {
+                    constexpr bool Q = decltype(q)::value;
+                    const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
+                    u64* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
+                    float shv[kPer], lrp[6][kPer];      // loaded before the LayerNorm
+#pragma unroll
+                    for (int k = 0; k < kPer; ++k) {
+                        const int ic = min(k * NT + tid, D - 1);
+                        shv[k] = ld_ag(sh0 + ic);
+#pragma unroll
+                        for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = lerp[(size_t)s6 * D + ic];
+                    }
+                    // the wave's first two rows, issued after x arrived and
+                    // before the LayerNorm, which they overlap
+                    const int row0 = lo + wv;
+                    int sA0, rA0, sB0, rB0;
+                    locate(min(row0, total - 1), sA0, rA0);
+                    locate(min(row0 + NW, hi - 1) < 0 ? 0 : min(row0 + NW, hi - 1), sB0, rB0);
+                    Unit UA, UB;
+                    if (pre && row0 < hi) {
+                        unit_load<Q>(UA, p1_mat(P, sA0), rA0, min(lane, (p1_mat(P, sA0).K >> 4) - 1));
+                        unit_load<Q>(UB, p1_mat(P, sB0), rB0, min(lane, (p1_mat(P, sB0).K >> 4) - 1));
+                    }
+                    layer_norm(xs, xn, P.ln1w, P.ln1b, D, A.eps, red);
+#pragma unroll
+                    for (int k = 0; k < kPer; ++k) {
+                        const int i = k * NT + tid;
+                        if (i < D) {
+                            const float d = shv[k] - xn[i];
+#pragma unroll
+                            for (int s6 = 0; s6 < 6; ++s6) buf[s6 * D + i] = xn[i] + lrp[s6][k] * d;
+                        }
+                    }
+                    __syncthreads();
+                    for (int row = row0; row < hi; row += 2 * NW) {
+                        const int rowB = min(row + NW, hi - 1);
+                        int sA, rA, sB, rB;
+                        locate(row, sA, rA);
+                        locate(rowB, sB, rB);
+                        float dA, dB;
+                        if (pre && row == row0) {
+                            const RkPMat& WA = p1_mat(P, sA);
+                            const RkPMat& WB = p1_mat(P, sB);
+                            const int nA = WA.K >> 4, nB = WB.K >> 4;
+                            const float a = unit_dot<Q>(UA, WA, min(lane, nA - 1), buf + xoff[sA], 0.0f);
+                            const float b = unit_dot<Q>(UB, WB, min(lane, nB - 1), buf + xoff[sB], 0.0f);
+                            dA = wsum(lane < nA ? a : 0.0f);
+                            dB = wsum(lane < nB ? b : 0.0f);
+                        } else {
+                            row_pair(p1_mat(P, sA), rA, buf + xoff[sA], p1_mat(P, sB), rB, buf + xoff[sB], lane, dA,
+                                     dB);
+                        }
+                        if (lane == 0) {
+                            ex_put(outs[sA] + rA, dA, ep);
+                            if (row + NW < hi) ex_put(outs[sB] + rB, dB, ep);
+                        }
+                    }
+                };
+                if (!uni) body(std::false_type{}, false);
+                else if (P.r.block != 0) body(std::true_type{}, true);
+                else body(std::false_type{}, true);
             }
             const RkPLayer& P = Ls2[l & 1];
-            // the next layer's table into the other slot
-            if (l + 1 < L && tid < (int)(sizeof(RkPLayer) / 4))
-                reinterpret_cast<int*>(&Ls2[(l + 1) & 1])[tid] = reinterpret_cast<const int*>(A.layers + l + 1)[tid];
-            __syncthreads();
-            RKP_MARK(l * 6 + 0, 0);
-            // The workgroup's rows (r, k, v, then the LoRA down-projections,
-            // with V_1 from layer 1 on), from the segment sizes read at once.
-            const int nseg = l > 0 ? 7 : 6;
-            int M[7];
+            RKP_MARK(l * 6 + 0, 1);
+
+            // ---- P2: head h = wg (rwkv7.c:143-189, 229-299)
+            if (wg >= NH) RKP_MARK(l * 6 + 1, 0);
+            if (wg < NH) {
+                const int h = wg, c0 = h * HS;
+                const int Rw = P.w1.M, Ra = P.a1.M, Rg = P.g1.M, Rv = P.v1.M;
+                float* in_w = buf;                  // tanh(lw)
+                float* in_a = buf + kRkPRank;       // la
+                float* in_g = buf + 2 * kRkPRank;   // sig(lg)
+                float* in_v = buf + 3 * kRkPRank;   // lv
+                float* r_ = hv[9];
+                float* kx = hv[11];                 // k of the channel (before k2)
+                float* vx = hv[3];                  // v (dv goes to hv[10] below)
+                // up-projections: dw, da, g and (from layer 1 on) dv
+                const int nm = l > 0 ? 4 : 3;
+                auto upm = [&](int m) -> const RkPMat& { return m == 0 ? P.w2 : m == 1 ? P.a2 : m == 2 ? P.g2 : P.v2; };
+                auto upo = [&](int m) -> float* { return hv[m == 3 ? 10 : m]; };
+                const UpPlan pl = up_plan(upm, nm);
+                const bool q4 = P.w2.block != 0;
+                const bool uni = (P.a2.block != 0) == q4 && (P.g2.block != 0) == q4 &&
+                                 (nm < 4 || (P.v2.block != 0) == q4);
+                auto owner = [&](auto q, bool batched) -> bool {
+                    constexpr bool Q = decltype(q)::value;
+                    // The head's state rows, its channel parameters and the first
+                    // batch of up-projection weights are issued ahead of the wait
+                    // for the phase's inputs, which (every workgroup's P1 rows and
+                    // a round trip) outlasts their memory latency.
+                    const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS +
+                                                   (size_t)(tid >> 3) * HS + (tid & 7) * 8);
+                    const f4 pS0 = Sp[0], pS1 = Sp[1];
+                    const int cc = c0 + (tid & 63);
+                    const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
+                    const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
+                    UpBatch<Q> ub;
+                    if (batched) up_load<Q>(ub, upm, pl, wv, c0, lane);
+                    issued();
+                    {
+                        const int i = min(tid, kRkPRank - 1), c = c0 + (tid & 63);
+                        const bool lora = tid < kRkPRank, chan = tid < HS;
+                        const u64* at[7] = {s_lw + i, s_la + i, s_lg + i, s_lv + i, s_r + c, s_k + c, s_v + c};
+                        const bool use[7] = {lora && i < Rw, lora && i < Ra, lora && i < Rg, lora && l > 0 && i < Rv,
+                                             chan, chan, chan};
+                        u64 w[7];
 #pragma unroll
-            for (int sg = 0; sg < 7; ++sg) M[sg] = sg < nseg ? p1_mat(P, sg).M : 0;
-            int total = 0;
-#pragma unroll
-            for (int sg = 0; sg < 7; ++sg) total += M[sg];
-            int lo, hi;
-            share(total, wg, G, lo, hi);
-            auto locate = [&](int row, int& sg, int& r) {
-                sg = 0;
-                r = row;
-#pragma unroll
-                for (int q = 0; q < 6; ++q)
-                    if (sg == q && r >= M[q]) {
-                        r -= M[q];
-                        sg = q + 1;
+                        for (int k = 0; k < 7; ++k) w[k] = use[k] ? ex_get(at[k]) : ((u64)pc.want << 32);
+                        const bool ok = ex_spin(w, at, pc);
+                        __syncthreads();   // every wave is done with X6 in buf
+                        if (use[0]) in_w[i] = tanhf(ex_f(w[0]));
+                        if (use[1]) in_a[i] = ex_f(w[1]);
+                        if (use[2]) in_g[i] = sgm(ex_f(w[2]));
+                        if (use[3]) in_v[i] = ex_f(w[3]);
+                        if (chan) {
+                            r_[tid] = ex_f(w[4]);
+                            kx[tid] = ex_f(w[5]);
+                            vx[tid] = ex_f(w[6]);
+                        }
+                        if (!agree(ok)) return false;
                     }
-            };
-            bool uni = true;
-#pragma unroll
-            for (int sg = 1; sg < 7; ++sg) uni = uni && (sg >= nseg || (p1_mat(P, sg).block == 0) == (P.r.block == 0));
-            const float* lerp = P.lerp;
-            auto body = [&](auto q, bool pre) {
-                constexpr bool Q = decltype(q)::value;
-                const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
-                u64* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
-                float shv[kPer], lrp[6][kPer];      // loaded before the LayerNorm
-#pragma unroll
-                for (int k = 0; k < kPer; ++k) {
-                    const int ic = min(k * NT + tid, D - 1);
-                    shv[k] = sh0[ic];
-#pragma unroll
-                    for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = lerp[(size_t)s6 * D + ic];
-                }
-                // the wave's first two rows, issued after x arrived and
-                // before the LayerNorm, which they overlap
-                const int row0 = lo + wv;
-                int sA0, rA0, sB0, rB0;
-                locate(min(row0, total - 1), sA0, rA0);
-                locate(min(row0 + NW, hi - 1) < 0 ? 0 : min(row0 + NW, hi - 1), sB0, rB0);
-                Unit UA, UB;
-                if (pre && row0 < hi) {
-                    unit_load<Q>(UA, p1_mat(P, sA0), rA0, min(lane, (p1_mat(P, sA0).K >> 4) - 1));
-                    unit_load<Q>(UB, p1_mat(P, sB0), rB0, min(lane, (p1_mat(P, sB0).K >> 4) - 1));
-                }
-                layer_norm(xs, xn, P.ln1w, P.ln1b, D, A.eps, red);
-#pragma unroll
-                for (int k = 0; k < kPer; ++k) {
-                    const int i = k * NT + tid;
-                    if (i < D) {
-                        const float d = shv[k] - xn[i];
-#pragma unroll
-                        for (int s6 = 0; s6 < 6; ++s6) buf[s6 * D + i] = xn[i] + lrp[s6][k] * d;
-                    }
-                }
-                __syncthreads();
-                for (int row = row0; row < hi; row += 2 * NW) {
-                    const int rowB = min(row + NW, hi - 1);
-                    int sA, rA, sB, rB;
-                    locate(row, sA, rA);
-                    locate(rowB, sB, rB);
-                    float dA, dB;
-                    if (pre && row == row0) {
-                        const RkPMat& WA = p1_mat(P, sA);
-                        const RkPMat& WB = p1_mat(P, sB);
-                        const int nA = WA.K >> 4, nB = WB.K >> 4;
-                        const float a = unit_dot<Q>(UA, WA, min(lane, nA - 1), buf + xoff[sA], 0.0f);
-                        const float b = unit_dot<Q>(UB, WB, min(lane, nB - 1), buf + xoff[sB], 0.0f);
-                        dA = wsum(lane < nA ? a : 0.0f);
-                        dB = wsum(lane < nB ? b : 0.0f);
+                    RKP_MARK(l * 6 + 1, 0);
+                    if (batched) {
+                        up_dot<Q>(ub, upm, upo, pl, wv, buf, lane);
+                        for (int i0 = wv + NW * kUpI; i0 < pl.T; i0 += NW * kUpI) {
+                            up_load<Q>(ub, upm, pl, i0, c0, lane);
+                            up_dot<Q>(ub, upm, upo, pl, i0, buf, lane);
+                        }
                     } else {
-                        row_pair(p1_mat(P, sA), rA, buf + xoff[sA], p1_mat(P, sB), rB, buf + xoff[sB], lane, dA,
-                                 dB);
+                        small_rows(P.w2, c0, HS, in_w, hv[0], wv, lane);
+                        small_rows(P.a2, c0, HS, in_a, hv[1], wv, lane);
+                        small_rows(P.g2, c0, HS, in_g, hv[2], wv, lane);
+                        if (l > 0) small_rows(P.v2, c0, HS, in_v, hv[10], wv, lane);
                     }
-                    if (lane == 0) {
-                        ex_put(outs[sA] + rA, dA, ep);
-                        if (row + NW < hi) ex_put(outs[sB] + rB, dB, ep);
+                    __syncthreads();
+                    float* w_ = hv[4]; float* k_ = hv[5]; float* v_ = hv[6]; float* a_ = hv[7];
+                    float* kn_ = hv[8]; float* y_ = hv[10];
+                    if (tid < HS) {
+                        const int c = c0 + tid;
+                        const float ww = expf(-sgm(hv[0][tid] + pw0) * kR2);            // :236-237
+                        float vv = vx[tid];
+                        if (l == 0) {
+                            vfo = vv;
+                            A.vfirst[c] = vv;                                            // :240
+                        } else {
+                            const float mix = sgm(hv[10][tid] + pv0);                    // :244-246
+                            vv = vv + (vfo - vv) * mix;
+                        }
+                        const float av = sgm(hv[1][tid] + pa0);                         // :251-252
+                        const float kv = kx[tid];
+                        const float kkv = kv * pkk;                                      // :259
+                        const float k2 = kv + kv * (av - 1.0f) * pka;                   // :260
+                        float nrm = sqrtf(wsum(kkv * kkv));                              // :158-162
+                        if (!(nrm > 1e-12f)) nrm = 1e-12f;
+                        w_[tid] = ww; k_[tid] = k2; v_[tid] = vv; a_[tid] = av; kn_[tid] = kkv * (1.0f / nrm);
                     }
-                }
-            };
-            if (!uni) body(std::false_type{}, false);
-            else if (P.r.block != 0) body(std::true_type{}, true);
-            else body(std::false_type{}, true);
-        }
-        const RkPLayer& P = Ls2[l & 1];
-        RKP_MARK(l * 6 + 0, 1);
-
-        // ---- P2: head h = wg (rwkv7.c:143-189, 229-299)
-        if (wg >= NH) RKP_MARK(l * 6 + 1, 0);
-        if (wg < NH) {
-            const int h = wg, c0 = h * HS;
-            const int Rw = P.w1.M, Ra = P.a1.M, Rg = P.g1.M, Rv = P.v1.M;
-            float* in_w = buf;                  // tanh(lw)
-            float* in_a = buf + kRkPRank;       // la
-            float* in_g = buf + 2 * kRkPRank;   // sig(lg)
-            float* in_v = buf + 3 * kRkPRank;   // lv
-            float* r_ = hv[9];
-            float* kx = hv[11];                 // k of the channel (before k2)
-            float* vx = hv[3];                  // v (dv goes to hv[10] below)
-            // up-projections: dw, da, g and (from layer 1 on) dv
-            const int nm = l > 0 ? 4 : 3;
-            auto upm = [&](int m) -> const RkPMat& { return m == 0 ? P.w2 : m == 1 ? P.a2 : m == 2 ? P.g2 : P.v2; };
-            auto upo = [&](int m) -> float* { return hv[m == 3 ? 10 : m]; };
-            const UpPlan pl = up_plan(upm, nm);
-            const bool q4 = P.w2.block != 0;
-            const bool uni = (P.a2.block != 0) == q4 && (P.g2.block != 0) == q4 && (nm < 4 || (P.v2.block != 0) == q4);
-            auto owner = [&](auto q, bool batched) -> bool {
-                constexpr bool Q = decltype(q)::value;
-                // The head's state rows, its channel parameters and the first
-                // batch of up-projection weights are issued ahead of the wait
-                // for the phase's inputs, which (every workgroup's P1 rows and
-                // a round trip) outlasts their memory latency.
-                const gptr<f4> Sp = (gptr<f4>)(glb(A.S) + ((size_t)l * NH + wg) * HS * HS + (size_t)(tid >> 3) * HS +
-                                               (tid & 7) * 8);
-                const f4 pS0 = Sp[0], pS1 = Sp[1];
-                const int cc = c0 + (tid & 63);
-                const float pw0 = glb(P.w0)[cc], pv0 = glb(P.v0)[cc], pa0 = glb(P.a0)[cc], pkk = glb(P.kk)[cc];
-                const float pka = glb(P.ka)[cc], prk = glb(P.rk)[cc], plw = glb(P.lnxw)[cc], plb = glb(P.lnxb)[cc];
-                UpBatch<Q> ub;
-                if (batched) up_load<Q>(ub, upm, pl, wv, c0, lane);
-                issued();
-                {
-                    const int i = min(tid, kRkPRank - 1), c = c0 + (tid & 63);
-                    const bool lora = tid < kRkPRank, chan = tid < HS;
-                    const u64* at[7] = {s_lw + i, s_la + i, s_lg + i, s_lv + i, s_r + c, s_k + c, s_v + c};
-                    const bool use[7] = {lora && i < Rw, lora && i < Ra, lora && i < Rg, lora && l > 0 && i < Rv,
-                                         chan, chan, chan};
-                    u64 w[7];
+                    __syncthreads();   // (y_ reuses dv's row: dv was read above)
+                    // S = S diag(w) - (S kk^)(kk^ a)^T + v k^T; y = S r. Thread t owns
+                    // row i = t / 8, columns 8 (t % 8) .. 8 (t % 8) + 7.
+                    const int i = tid >> 3, j0 = (tid & 7) * 8;
+                    float* Sr = A.S + ((size_t)l * NH + h) * HS * HS + (size_t)i * HS + j0;
+                    float s[8] = {pS0.x, pS0.y, pS0.z, pS0.w, pS1.x, pS1.y, pS1.z, pS1.w};
+                    float pv = 0.0f;
 #pragma unroll
-                    for (int k = 0; k < 7; ++k) w[k] = use[k] ? ex_get(at[k]) : ((u64)pc.want << 32);
-                    const bool ok = ex_spin(w, at, pc);
-                    __syncthreads();   // every wave is done with X6 in buf
-                    if (use[0]) in_w[i] = tanhf(ex_f(w[0]));
-                    if (use[1]) in_a[i] = ex_f(w[1]);
-                    if (use[2]) in_g[i] = sgm(ex_f(w[2]));
-                    if (use[3]) in_v[i] = ex_f(w[3]);
-                    if (chan) {
-                        r_[tid] = ex_f(w[4]);
-                        kx[tid] = ex_f(w[5]);
-                        vx[tid] = ex_f(w[6]);
-                    }
-                    if (!agree(ok)) return false;
-                }
-                RKP_MARK(l * 6 + 1, 0);
-                if (batched) {
-                    up_dot<Q>(ub, upm, upo, pl, wv, buf, lane);
-                    for (int i0 = wv + NW * kUpI; i0 < pl.T; i0 += NW * kUpI) {
-                        up_load<Q>(ub, upm, pl, i0, c0, lane);
-                        up_dot<Q>(ub, upm, upo, pl, i0, buf, lane);
-                    }
-                } else {
-                    small_rows(P.w2, c0, HS, in_w, hv[0], wv, lane);
-                    small_rows(P.a2, c0, HS, in_a, hv[1], wv, lane);
-                    small_rows(P.g2, c0, HS, in_g, hv[2], wv, lane);
-                    if (l > 0) small_rows(P.v2, c0, HS, in_v, hv[10], wv, lane);
-                }
-                __syncthreads();
-                float* w_ = hv[4]; float* k_ = hv[5]; float* v_ = hv[6]; float* a_ = hv[7];
-                float* kn_ = hv[8]; float* y_ = hv[10];
-                if (tid < HS) {
-                    const int c = c0 + tid;
-                    const float ww = expf(-sgm(hv[0][tid] + pw0) * kR2);            // :236-237
-                    float vv = vx[tid];
-                    if (l == 0) {
-                        vfo = vv;
-                        A.vfirst[c] = vv;                                            // :240
-                    } else {
-                        const float mix = sgm(hv[10][tid] + pv0);                    // :244-246
-                        vv = vv + (vfo - vv) * mix;
-                    }
-                    const float av = sgm(hv[1][tid] + pa0);                         // :251-252
-                    const float kv = kx[tid];
-                    const float kkv = kv * pkk;                                      // :259
-                    const float k2 = kv + kv * (av - 1.0f) * pka;                   // :260
-                    float nrm = sqrtf(wsum(kkv * kkv));                              // :158-162
-                    if (!(nrm > 1e-12f)) nrm = 1e-12f;
-                    w_[tid] = ww; k_[tid] = k2; v_[tid] = vv; a_[tid] = av; kn_[tid] = kkv * (1.0f / nrm);
-                }
-                __syncthreads();   // (y_ reuses dv's row: dv was read above)
-                // S = S diag(w) - (S kk^)(kk^ a)^T + v k^T; y = S r. Thread t owns
-                // row i = t / 8, columns 8 (t % 8) .. 8 (t % 8) + 7.
-                const int i = tid >> 3, j0 = (tid & 7) * 8;
-                float* Sr = A.S + ((size_t)l * NH + h) * HS * HS + (size_t)i * HS + j0;
-                float s[8] = {pS0.x, pS0.y, pS0.z, pS0.w, pS1.x, pS1.y, pS1.z, pS1.w};
-                float pv = 0.0f;
+                    for (int q = 0; q < 8; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
+                    pv = grp_sum(pv, 8);
+                    const float vi = v_[i];
+                    float yacc = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 8; ++q) pv = fmaf(s[q], kn_[j0 + q], pv);
-                pv = grp_sum(pv, 8);
-                const float vi = v_[i];
-                float yacc = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int j = j0 + q;
-                    const float ns = fmaf(s[q], w_[j], vi * k_[j] - pv * (kn_[j] * a_[j]));   // :180-181
-                    s[q] = ns;
-                    yacc = fmaf(ns, r_[j], yacc);
-                }
-                *reinterpret_cast<float4*>(Sr) = make_float4(s[0], s[1], s[2], s[3]);
-                *reinterpret_cast<float4*>(Sr + 4) = make_float4(s[4], s[5], s[6], s[7]);
-                yacc = grp_sum(yacc, 8);
-                if ((tid & 7) == 0) y_[i] = yacc;
-                __syncthreads();
-                if (tid < HS) {
-                    // group norm, bonus, gate (:266-288)
-                    const int c = c0 + tid;
-                    const float yy = y_[tid];
-                    const float mean = wsum(yy) / (float)HS;
-                    const float d = yy - mean;
-                    const float rstd = 1.0f / sqrtf(wsum(d * d) / (float)HS + kEpsGroup);
-                    const float dot = wsum(r_[tid] * k_[tid] * prk);
-                    const float n = d * rstd * plw + plb;
-                    ex_put(s_y + c, (n + dot * v_[tid]) * hv[2][tid], ep);
-                }
-                return true;
-            };
-            bool ok;
-            if (!uni) ok = owner(std::false_type{}, false);
-            else if (q4) ok = owner(std::true_type{}, true);
-            else ok = owner(std::false_type{}, true);
-            if (!ok) return;
-        }
-        RKP_MARK(l * 6 + 1, 1);
-
-        // ---- P3: x_a = x + W_o y (:290-292)
-        {
-            int lo, hi;
-            share(D, wg, G, lo, hi);
-            const bool ok = with_format<true>(P.o, [&](auto q, auto nu) -> bool {
-                constexpr bool Q = decltype(q)::value;
-                constexpr int NU = decltype(nu)::value;
-                PreRows<Q, NU, 1> pr;
-                pre_load(pr, P.o, lo + wv, NW, lane);
-                issued();
-                if (!agree(poll_vec<kPer>(s_y, D, buf, pc))) return false;
-                RKP_MARK(l * 6 + 2, 0);
-                // shift_0 <- xn (:229). Every workgroup has read shift_0 by
-                // now: the owners have all of r, k, v and the LoRA middles,
-                // and every workgroup has rows among them (at most as many
-                // workgroups as those rows).
-                if (wg == 0)
-                    for (int i = tid; i < D; i += NT) sh0[i] = xn[i];
-                for (int row = lo + wv; row < hi; row += NW) {
-                    float d[1];
-                    if (row == lo + wv) pre_dot(pr, P.o, buf, lane, d);
-                    else d[0] = row_dot(P.o, row, buf, lane);
-                    if (lane == 0) ex_put(s_xa + row, xs[row] + d[0], ep);
-                }
-                return true;
-            });
-            if (!ok) return;
-        }
-        RKP_MARK(l * 6 + 2, 1);
-
-        // ---- P4: xn2 = LN_2(x_a); xk2 = xn2 + cmk_lerp (shift_1 - xn2); ck = relu(W_ck xk2)^2
-        {
-            int lo, hi;
-            share(F, wg, G, lo, hi);
-            const bool ok = with_format<true>(P.cmk, [&](auto q, auto nu) -> bool {
-                constexpr bool Q = decltype(q)::value;
-                constexpr int NU = decltype(nu)::value;
-                // x_a first; then the mix inputs and the wave's first two
-                // rows, which the LayerNorm overlaps (loads issued before the
-                // wait would hold the wait's first check back)
-                if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
-                RKP_MARK(l * 6 + 3, 0);
-                float shv[kPer], lrp[kPer];
-#pragma unroll
-                for (int k = 0; k < kPer; ++k) {
-                    const int ic = min(k * NT + tid, D - 1);
-                    shv[k] = sh1[ic];
-                    lrp[k] = P.cmk_lerp[ic];
-                }
-                PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
-                pre_load(pr, P.cmk, lo + wv, NW, lane);
-                issued();
-                layer_norm(xs, xn2, P.ln2w, P.ln2b, D, A.eps, red);
-#pragma unroll
-                for (int k = 0; k < kPer; ++k) {
-                    const int i = k * NT + tid;
-                    if (i < D) buf[i] = xn2[i] + lrp[k] * (shv[k] - xn2[i]);
-                }
-                __syncthreads();
-                for (int row = lo + wv; row < hi; row += 2 * NW) {
-                    const int rowB = min(row + NW, hi - 1);
-                    float d[2];
-                    if (row == lo + wv) pre_dot(pr, P.cmk, buf, lane, d);
-                    else row_pair(P.cmk, row, buf, P.cmk, rowB, buf, lane, d[0], d[1]);
-                    const float tA = d[0] > 0.0f ? d[0] : 0.0f, tB = d[1] > 0.0f ? d[1] : 0.0f;
-                    if (lane == 0) {
-                        ex_put(s_ck + row, tA * tA, ep);
-                        if (row + NW < hi) ex_put(s_ck + rowB, tB * tB, ep);
+                    for (int q = 0; q < 8; ++q) {
+                        const int j = j0 + q;
+                        const float ns = fmaf(s[q], w_[j], vi * k_[j] - pv * (kn_[j] * a_[j]));   // :180-181
+                        s[q] = ns;
+                        yacc = fmaf(ns, r_[j], yacc);
                     }
-                }
-                return true;
-            });
-            if (!ok) return;
-        }
-        RKP_MARK(l * 6 + 3, 1);
-
-        // ---- P5: x_b = x_a + W_cv ck; shift_1 <- xn2 (:305-315)
-        {
-            int lo, hi;
-            share(D, wg, G, lo, hi);
-            const bool ok = with_format(P.cmv, [&](auto q, auto nu) -> bool {
-                constexpr bool Q = decltype(q)::value;
-                constexpr int NU = decltype(nu)::value;
-                PreRows<Q, NU, 1> pr;
-                pre_load(pr, P.cmv, lo + wv, NW, lane);
-                issued();
-                if (!agree(poll_vec<kPerF>(s_ck, F, buf, pc))) return false;
-                RKP_MARK(l * 6 + 4, 0);
-                // Every workgroup has read shift_1 by now: each has rows of
-                // ck (at most F workgroups).
-                if (wg == 0)
-                    for (int i = tid; i < D; i += NT) sh1[i] = xn2[i];
-                for (int row = lo + wv; row < hi; row += NW) {
-                    float d[1];
-                    if (row == lo + wv) pre_dot(pr, P.cmv, buf, lane, d);
-                    else d[0] = row_dot(P.cmv, row, buf, lane);
-                    if (lane == 0) ex_put(s_xb + row, xs[row] + d[0], ep);
-                }
-                return true;
-            });
-            if (!ok) return;
-        }
-        RKP_MARK(l * 6 + 4, 1);
-    }
-    RKP_MARK(64 * 6, 0);
-
-    // ---- head: logits = W_head LN_out(x) (:358-359), argmax keys. Passes of
-    // N rows per wave alternate between two register sets: the next pass is
-    // issued before the current one is multiplied, and the first before x
-    // arrives.
-    {
-        int lo, hi;
-        share(A.vocab, wg, G, lo, hi);
-        u64 best = 0ull;
-        auto head_rows = [&](auto q, auto nrows) -> bool {
-            constexpr bool Q = decltype(q)::value;
-            constexpr int N = decltype(nrows)::value;
-            constexpr int STEP = N * NW;
-            PreRows<Q, 1, N> ra, rb;
-            pre_load(ra, A.head, lo + wv, NW, lane);
-            issued();
-            if (!agree(poll_vec<kPer>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
-            layer_norm(xs, buf, A.on_w, A.on_b, D, A.eps, red);
-            auto finish = [&](const float (&d)[N], int row) {
-#pragma unroll
-                for (int k = 0; k < N; ++k) {
-                    const int rk = row + k * NW;
-                    if (rk < hi) {
-                        if (lane == 0) A.logits[rk] = d[k];
-                        best = max(best, argmax_key(d[k], rk));
+                    *reinterpret_cast<float4*>(Sr) = make_float4(s[0], s[1], s[2], s[3]);
+                    *reinterpret_cast<float4*>(Sr + 4) = make_float4(s[4], s[5], s[6], s[7]);
+                    yacc = grp_sum(yacc, 8);
+                    if ((tid & 7) == 0) y_[i] = yacc;
+                    __syncthreads();
+                    if (tid < HS) {
+                        // group norm, bonus, gate (:266-288)
+                        const int c = c0 + tid;
+                        const float yy = y_[tid];
+                        const float mean = wsum(yy) / (float)HS;
+                        const float d = yy - mean;
+                        const float rstd = 1.0f / sqrtf(wsum(d * d) / (float)HS + kEpsGroup);
+                        const float dot = wsum(r_[tid] * k_[tid] * prk);
+                        const float n = d * rstd * plw + plb;
+                        ex_put(s_y + c, (n + dot * v_[tid]) * hv[2][tid], ep);
                     }
-                }
-            };
-            for (int row = lo + wv; row < hi; row += 2 * STEP) {
-                pre_load(rb, A.head, row + STEP, NW, lane);
-                {
-                    float d[N];
-                    pre_dot(ra, A.head, buf, lane, d);
-                    finish(d, row);
-                }
-                pre_load(ra, A.head, row + 2 * STEP, NW, lane);
-                if (row + STEP < hi) {
-                    float d[N];
-                    pre_dot(rb, A.head, buf, lane, d);
-                    finish(d, row + STEP);
-                }
+                    return true;
+                };
+                bool ok;
+                if (!uni) ok = owner(std::false_type{}, false);
+                else if (q4) ok = owner(std::true_type{}, true);
+                else ok = owner(std::false_type{}, true);
+                if (!ok) return;
             }
-            return true;
-        };
-        const bool ok = A.head.block == 0 ? head_rows(std::false_type{}, std::integral_constant<int, 2>{})
-                                          : head_rows(std::true_type{}, std::integral_constant<int, 16>{});
-        if (!ok) return;
-        if (lane == 0) kred[wv] = best;
-        __syncthreads();
-        if (tid < 2) {
-            u64 b = kred[0];
-            for (int w = 1; w < NW; ++w) b = max(b, kred[w]);
-            ex_put_bits(A.keys + 2 * wg + tid, tid == 0 ? (uint32_t)(b >> 32) : (uint32_t)b, ep);
-        }
-    }
-    RKP_MARK(64 * 6, 1);
-    if (!A.greedy || wg != 0) return;
-    // ---- workgroup 0 reduces the keys to the greedy token
-    RKP_MARK(64 * 6 + 1, 0);
-    {
-        constexpr int KW = 2 * kRkPMaxGrid / NT;
-        u64 w[KW];
-        const u64* at[KW];
+            RKP_MARK(l * 6 + 1, 1);
+
+            // ---- P3: x_a = x + W_o y (:290-292)
+            {
+                int lo, hi;
+                share(D, wg, G, lo, hi);
+                const bool ok = with_format<true>(P.o, [&](auto q, auto nu) -> bool {
+                    constexpr bool Q = decltype(q)::value;
+                    constexpr int NU = decltype(nu)::value;
+                    PreRows<Q, NU, 1> pr;
+                    pre_load(pr, P.o, lo + wv, NW, lane);
+                    issued();
+                    if (!agree(poll_vec<kPer>(s_y, D, buf, pc))) return false;
+                    RKP_MARK(l * 6 + 2, 0);
+                    // shift_0 <- xn (:229). Every workgroup has read shift_0 by
+                    // now: the owners have all of r, k, v and the LoRA middles,
+                    // and every workgroup has rows among them (at most as many
+                    // workgroups as those rows).
+                    if (wg == 0)
+                        for (int i = tid; i < D; i += NT) st_ag(sh0 + i, xn[i]);
+                    for (int row = lo + wv; row < hi; row += NW) {
+                        float d[1];
+                        if (row == lo + wv) pre_dot(pr, P.o, buf, lane, d);
+                        else d[0] = row_dot(P.o, row, buf, lane);
+                        if (lane == 0) ex_put(s_xa + row, xs[row] + d[0], ep);
+                    }
+                    return true;
+                });
+                if (!ok) return;
+            }
+            RKP_MARK(l * 6 + 2, 1);
+
+            // ---- P4: xn2 = LN_2(x_a); xk2 = xn2 + cmk_lerp (shift_1 - xn2); ck = relu(W_ck xk2)^2
+            {
+                int lo, hi;
+                share(F, wg, G, lo, hi);
+                const bool ok = with_format<true>(P.cmk, [&](auto q, auto nu) -> bool {
+                    constexpr bool Q = decltype(q)::value;
+                    constexpr int NU = decltype(nu)::value;
+                    // x_a first; then the mix inputs and the wave's first two
+                    // rows, which the LayerNorm overlaps (loads issued before the
+                    // wait would hold the wait's first check back)
+                    if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
+                    RKP_MARK(l * 6 + 3, 0);
+                    float shv[kPer], lrp[kPer];
 #pragma unroll
-        for (int k = 0; k < KW; ++k) {
-            const int i = k * NT + tid;
-            at[k] = A.keys + min(i, 2 * G - 1);
-            w[k] = i < 2 * G ? ex_get(at[k]) : ((u64)pc.want << 32);
-        }
-        if (!agree(ex_spin(w, at, pc))) return;
-        // word 2 j + 1 of a pair sits in the next lane (NT is even)
-        u64 b = 0ull;
+                    for (int k = 0; k < kPer; ++k) {
+                        const int ic = min(k * NT + tid, D - 1);
+                        shv[k] = ld_ag(sh1 + ic);
+                        lrp[k] = P.cmk_lerp[ic];
+                    }
+                    PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
+                    pre_load(pr, P.cmk, lo + wv, NW, lane);
+                    issued();
+                    layer_norm(xs, xn2, P.ln2w, P.ln2b, D, A.eps, red);
 #pragma unroll
-        for (int k = 0; k < KW; ++k) {
-            const uint32_t hi = (uint32_t)w[k], lo = (uint32_t)__shfl_down((int)(uint32_t)w[k], 1, 64);
-            if (k * NT + tid < 2 * G && (tid & 1) == 0) b = max(b, ((u64)hi << 32) | lo);
+                    for (int k = 0; k < kPer; ++k) {
+                        const int i = k * NT + tid;
+                        if (i < D) buf[i] = xn2[i] + lrp[k] * (shv[k] - xn2[i]);
+                    }
+                    __syncthreads();
+                    for (int row = lo + wv; row < hi; row += 2 * NW) {
+                        const int rowB = min(row + NW, hi - 1);
+                        float d[2];
+                        if (row == lo + wv) pre_dot(pr, P.cmk, buf, lane, d);
+                        else row_pair(P.cmk, row, buf, P.cmk, rowB, buf, lane, d[0], d[1]);
+                        const float tA = d[0] > 0.0f ? d[0] : 0.0f, tB = d[1] > 0.0f ? d[1] : 0.0f;
+                        if (lane == 0) {
+                            ex_put(s_ck + row, tA * tA, ep);
+                            if (row + NW < hi) ex_put(s_ck + rowB, tB * tB, ep);
+                        }
+                    }
+                    return true;
+                });
+                if (!ok) return;
+            }
+            RKP_MARK(l * 6 + 3, 1);
+
+            // ---- P5: x_b = x_a + W_cv ck; shift_1 <- xn2 (:305-315)
+            {
+                int lo, hi;
+                share(D, wg, G, lo, hi);
+                const bool ok = with_format(P.cmv, [&](auto q, auto nu) -> bool {
+                    constexpr bool Q = decltype(q)::value;
+                    constexpr int NU = decltype(nu)::value;
+                    PreRows<Q, NU, 1> pr;
+                    pre_load(pr, P.cmv, lo + wv, NW, lane);
+                    issued();
+                    if (!agree(poll_vec<kPerF>(s_ck, F, buf, pc))) return false;
+                    RKP_MARK(l * 6 + 4, 0);
+                    // Every workgroup has read shift_1 by now: each has rows of
+                    // ck (at most F workgroups).
+                    if (wg == 0)
+                        for (int i = tid; i < D; i += NT) st_ag(sh1 + i, xn2[i]);
+                    for (int row = lo + wv; row < hi; row += NW) {
+                        float d[1];
+                        if (row == lo + wv) pre_dot(pr, P.cmv, buf, lane, d);
+                        else d[0] = row_dot(P.cmv, row, buf, lane);
+                        if (lane == 0) ex_put(s_xb + row, xs[row] + d[0], ep);
+                    }
+                    return true;
+                });
+                if (!ok) return;
+            }
+            RKP_MARK(l * 6 + 4, 1);
         }
-        for (int o = 32; o > 0; o >>= 1) {
-            const u64 v = __shfl_xor(b, o, 64);
-            b = max(b, v);
+        RKP_MARK(64 * 6, 0);
+
+        // ---- head: logits = W_head LN_out(x) (:358-359), argmax keys. Passes of
+        // N rows per wave alternate between two register sets: the next pass is
+        // issued before the current one is multiplied, and the first before x
+        // arrives.
+        {
+            int lo, hi;
+            share(A.vocab, wg, G, lo, hi);
+            u64 best = 0ull;
+            auto head_rows = [&](auto q, auto nrows) -> bool {
+                constexpr bool Q = decltype(q)::value;
+                constexpr int N = decltype(nrows)::value;
+                constexpr int STEP = N * NW;
+                PreRows<Q, 1, N> ra, rb;
+                pre_load(ra, A.head, lo + wv, NW, lane);
+                issued();
+                if (!agree(poll_vec<kPer>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
+                layer_norm(xs, buf, A.on_w, A.on_b, D, A.eps, red);
+                auto finish = [&](const float (&d)[N], int row) {
+#pragma unroll
+                    for (int k = 0; k < N; ++k) {
+                        const int rk = row + k * NW;
+                        if (rk < hi) {
+                            if (lane == 0 && last) A.logits[rk] = d[k];
+                            best = max(best, argmax_key(d[k], rk));
+                        }
+                    }
+                };
+                for (int row = lo + wv; row < hi; row += 2 * STEP) {
+                    pre_load(rb, A.head, row + STEP, NW, lane);
+                    {
+                        float d[N];
+                        pre_dot(ra, A.head, buf, lane, d);
+                        finish(d, row);
+                    }
+                    pre_load(ra, A.head, row + 2 * STEP, NW, lane);
+                    if (row + STEP < hi) {
+                        float d[N];
+                        pre_dot(rb, A.head, buf, lane, d);
+                        finish(d, row + STEP);
+                    }
+                }
+                return true;
+            };
+            const bool ok = A.head.block == 0 ? head_rows(std::false_type{}, std::integral_constant<int, 2>{})
+                                              : head_rows(std::true_type{}, std::integral_constant<int, 16>{});
+            if (!ok) return;
+            if (lane == 0) kred[wv] = best;
+            __syncthreads();
+            if (tid < 2) {
+                u64 b = kred[0];
+                for (int w = 1; w < NW; ++w) b = max(b, kred[w]);
+                ex_put_bits(A.keys + 2 * wg + tid, tid == 0 ? (uint32_t)(b >> 32) : (uint32_t)b, ep);
+            }
         }
-        if (lane == 0) kred[wv] = b;
-        __syncthreads();
-        if (tid == 0) {
+        RKP_MARK(64 * 6, 1);
+        if (!A.greedy) return;   // (one step)
+        // ---- every workgroup reduces the keys to the greedy token
+        RKP_MARK(64 * 6 + 1, 0);
+        {
+            constexpr int KW = 2 * kRkPMaxGrid / NT;
+            u64 w[KW];
+            const u64* at[KW];
+#pragma unroll
+            for (int k = 0; k < KW; ++k) {
+                const int i = k * NT + tid;
+                at[k] = A.keys + min(i, 2 * G - 1);
+                w[k] = i < 2 * G ? ex_get(at[k]) : ((u64)pc.want << 32);
+            }
+            if (!agree(ex_spin(w, at, pc))) return;
+            // word 2 j + 1 of a pair sits in the next lane (NT is even)
+            u64 b = 0ull;
+#pragma unroll
+            for (int k = 0; k < KW; ++k) {
+                const uint32_t hi = (uint32_t)w[k], lo = (uint32_t)__shfl_down((int)(uint32_t)w[k], 1, 64);
+                if (k * NT + tid < 2 * G && (tid & 1) == 0) b = max(b, ((u64)hi << 32) | lo);
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                const u64 v = __shfl_xor(b, o, 64);
+                b = max(b, v);
+            }
+            if (lane == 0) kred[wv] = b;
+            __syncthreads();
             u64 m = kred[0];
             for (int w2 = 1; w2 < NW; ++w2) m = max(m, kred[w2]);
-            const int32_t tk = (int32_t)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull));
-            const int step = *A.counter;
-            *A.tok = tk;
-            if (step < A.hist_cap) A.tok_hist[step] = tk;
-            *A.counter = step + 1;
+            tok = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull));
+            if (wg == 0 && tid == 0 && cnt0 + st < A.hist_cap) A.tok_hist[cnt0 + st] = tok;
         }
+    }   // steps
+    if (wg == 0 && tid == 0) {
+        *A.tok = tok;
+        *A.counter = cnt0 + A.nsteps;
     }
 }
 

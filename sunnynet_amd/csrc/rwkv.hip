@@ -157,7 +157,7 @@ struct SnHipRwkv7 {
     // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
     int p_grid = 0;
     snhip::RkPArgs p_args{};
-    unsigned p_epoch = 0;                 // epoch of the last persistent launch
+    unsigned p_epoch = 0;                 // the last epoch a persistent launch used
     unsigned long long* p_words = nullptr;   // exchange slabs and key words (zeroed: epoch 0)
     size_t p_nwords = 0;
     unsigned* p_err = nullptr;
@@ -323,10 +323,13 @@ void setup_rk_persist(SnHipRwkv7* m) {
     m->p_grid = G;
 }
 
-// reps persistent steps of sequence 0, each launch with a new epoch; the call
-// waits for them and reports a time-out of an exchange wait as an error. The kernel updates S and shift in place layer
+// reps persistent steps of sequence 0: greedy, one launch of up to
+// kRkPStepsPerLaunch steps at a time, otherwise one launch per step; every
+// step has its own epoch. The call waits for them and reports a time-out of
+// an exchange wait as an error. The kernel updates S and shift in place layer
 // by layer, so a time-out leaves them part-stepped: the handle is then refused
 // for stepping until its state is reset or set.
+constexpr int kRkPStepsPerLaunch = 1024;
 snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps) {
     RkPArgs a = m->p_args;
     a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
@@ -335,15 +338,19 @@ snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps
     a.tok_hist = m->tok_hist;
     a.hist_cap = m->hist_cap;
     SNHIP_CHECK(hipMemsetAsync(m->p_err, 0, sizeof(unsigned), m->work));
-    for (int i = 0; i < reps; ++i) {
-        if (m->p_epoch == 0xFFFFFFFFu) {
+    for (int i = 0; i < reps;) {
+        const int n = greedy ? std::min(reps - i, kRkPStepsPerLaunch) : 1;
+        if (m->p_epoch > 0xFFFFFFFFu - (unsigned)n) {
             // epochs start over from clean words
             SNHIP_CHECK(hipMemsetAsync(m->p_words, 0, m->p_nwords * sizeof(unsigned long long), m->work));
             m->p_epoch = 0;
         }
-        a.epoch = ++m->p_epoch;
+        a.epoch = m->p_epoch + 1;
+        a.nsteps = n;
+        m->p_epoch += (unsigned)n;
         const snhip_status rc = launch_rk_persist(a, m->p_grid, m->work);
         if (rc != SNHIP_OK) return rc;
+        i += n;
     }
     unsigned err = 0;
     SNHIP_CHECK(hipMemcpyAsync(&err, m->p_err, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));

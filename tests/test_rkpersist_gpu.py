@@ -7,7 +7,8 @@ argmax on every step, states within the tolerances of tests/test_rwkv7_gpu.py.
 The per-kernel path (SNHIP_RK_PERSIST=0) is a second witness. Covers fp32,
 the INT4 blob as stored (group 64, the 32-input V_2 kept fp32) and INT4 group
 32 quantized at load, the 12-layer 65536-vocab configuration, and greedy
-decoding.
+decoding, where one launch runs every step of the call (each workgroup
+reducing the argmax keys to the next token itself).
 """
 from __future__ import annotations
 
@@ -32,6 +33,17 @@ def tiny(tmp_path_factory):
     p4 = d / "tiny_q4.bin"
     p4.write_bytes(pack_rwkv7_blob(w, int4=True))
     return w, p32, p4
+
+
+@pytest.fixture(scope="module")
+def cfg4(tmp_path_factory):
+    """12 layers, D=768, 12 heads, F=3072, vocab 65536 (seed 2): the fp32
+    blob, and the oracle's blob of its INT4 g32 dequantized weights."""
+    print("rwkv7 cfg4 persistent: generating weights", flush=True)
+    w = init_rwkv7(RWKV_CFG4, 2)
+    p = tmp_path_factory.mktemp("rkp4") / "cfg4.bin"
+    p.write_bytes(pack_rwkv7_blob(w))
+    return p, pack_rwkv7_blob(dequant_weights(w, 32))
 
 
 def _pair(path, monkeypatch, **kw):
@@ -92,14 +104,11 @@ def test_persist_greedy_matches_oracle_chain(gpu, tiny):
         cur = nxt
 
 
-def test_persist_cfg4_int4(gpu, tmp_path_factory, monkeypatch):
+def test_persist_cfg4_int4(gpu, cfg4, monkeypatch):
     """12 layers, D=768, 12 heads, F=3072, vocab 65536, INT4 g32 at load."""
     cfg = RWKV_CFG4
-    print("rwkv7 cfg4 persistent: generating weights", flush=True)
-    w = init_rwkv7(cfg, 2)
-    p = tmp_path_factory.mktemp("rkp4") / "cfg4.bin"
-    p.write_bytes(pack_rwkv7_blob(w))
-    orc = oracle.RkOracle(pack_rwkv7_blob(dequant_weights(w, 32)))
+    p, ob = cfg4
+    orc = oracle.RkOracle(ob)
     hp, hg = _pair(p, monkeypatch, weights="int4", block=32)
     print("rwkv7 cfg4 persistent: stepping", flush=True)
     for t in np.random.default_rng(5).integers(0, cfg.vocab, 4):
@@ -110,6 +119,33 @@ def test_persist_cfg4_int4(gpu, tmp_path_factory, monkeypatch):
               flush=True)
         assert np.abs(a - b).max() < TOL and np.abs(a - g).max() < TOL
         assert a.argmax() == b.argmax() == g.argmax()
+
+
+def test_persist_cfg4_greedy_chain(gpu, cfg4):
+    """The benchmarked workload's form: greedy steps of the 12-layer INT4 g32
+    model at one sequence, all in one launch, then a second call continuing
+    from the state the first left; every token equal to the oracle chain's."""
+    p, ob = cfg4
+    hm = HipRwkv7(p, weights="int4", block=32)
+    assert hm.persist_grid > 0
+    orc = oracle.RkOracle(ob)
+    n = 12
+    print(f"rwkv7 cfg4 persistent greedy n={n}", flush=True)
+    lg = torch.empty(1, RWKV_CFG4.vocab, device="cuda")
+    cur = np.array([1234], np.int32)
+    out = hm.decode_greedy(torch.from_numpy(cur).cuda(), n, logits=lg).cpu().numpy()
+    for i in range(n):
+        ref = orc.step(cur)
+        nxt = ref.argmax(1).astype(np.int32)
+        assert np.array_equal(out[i], nxt), i
+        cur = nxt
+    print("worst |dlogit| last step", float(np.abs(lg.cpu().numpy() - ref).max()), flush=True)
+    assert np.abs(lg.cpu().numpy() - ref).max() < TOL
+    out2 = hm.decode_greedy(torch.from_numpy(cur).cuda(), 3).cpu().numpy()
+    for i in range(3):
+        nxt = orc.step(cur).argmax(1).astype(np.int32)
+        assert np.array_equal(out2[i], nxt), i
+        cur = nxt
 
 
 def test_persist_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
@@ -146,4 +182,17 @@ def test_persist_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
     orc.reset()
     a = np.asarray(hm.step(4), np.float32)
     assert np.abs(a - orc.step([4])[0]).max() < TOL
+    # a greedy call (many steps in one launch) gives up the same way
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm.decode_greedy(tok, 5)
+    monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    hm.reset()
+    orc.reset()
+    out = hm.decode_greedy(tok, 3).cpu().numpy()
+    cur = np.array([3], np.int32)
+    for i in range(3):
+        nxt = orc.step(cur).argmax(1).astype(np.int32)
+        assert np.array_equal(out[i], nxt), i
+        cur = nxt
     monkeypatch.delenv("SNHIP_PERSIST_SPIN")
