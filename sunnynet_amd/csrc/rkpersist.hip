@@ -100,17 +100,28 @@ __device__ __forceinline__ float bsum(float v, float* red) {
     return s;
 }
 
+// This thread's gains and biases of a LayerNorm over n <= kRkPMaxD values
+// (element k NT + tid in slot k).
+__device__ __forceinline__ void ln_params(const float* g, const float* c, int n, float (&gv)[kPer],
+                                          float (&cv)[kPer]) {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int ic = min(k * NT + (int)threadIdx.x, n - 1);
+        gv[k] = g[ic];
+        cv[k] = c[ic];
+    }
+}
+
 // y[i] = LN(x)[i] * g[i] + c[i] over n <= kRkPMaxD values in LDS
-// (rwkv7.c:127-140 form, two passes).
-__device__ void layer_norm(const float* x, float* y, const float* g, const float* c, int n, float eps,
-                           float* red) {
-    float v[kPer], gv[kPer], cv[kPer];
+// (rwkv7.c:127-140 form, two passes), with the gains and biases loaded by
+// ln_params (a phase issues them ahead of its exchange wait).
+__device__ void layer_norm(const float* x, float* y, const float (&gv)[kPer], const float (&cv)[kPer], int n,
+                           float eps, float* red) {
+    float v[kPer];
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-        const int i = k * NT + threadIdx.x, ic = min(i, n - 1);
-        gv[k] = g[ic];
-        cv[k] = c[ic];
+        const int i = k * NT + threadIdx.x;
         v[k] = i < n ? x[i] : 0.0f;
         s += v[k];
     }
@@ -129,6 +140,13 @@ __device__ void layer_norm(const float* x, float* y, const float* g, const float
         if (i < n) y[i] = (v[k] - mean) * rstd * gv[k] + cv[k];
     }
     __syncthreads();
+}
+
+__device__ void layer_norm(const float* x, float* y, const float* g, const float* c, int n, float eps,
+                           float* red) {
+    float gv[kPer], cv[kPer];
+    ln_params(g, c, n, gv, cv);
+    layer_norm(x, y, gv, cv, n, eps, red);
 }
 
 // Partial dot of one 16-value unit u of row `row` with X (LDS): fp32, or INT4
@@ -428,7 +446,9 @@ struct PollCtl {
 // Re-polls the words of w still short of the epoch (word k from src[k];
 // words a thread does not take start out ready) until all carry it. False on
 // a time-out (the thread then sets the error word) or when another
-// workgroup reported one.
+// workgroup reported one. (Two rounds in flight at once, the next issued
+// before the one in hand is waited for, made the waits longer: the doubled
+// polling traffic delayed the producers more than it shortened the polls.)
 template <int W>
 __device__ __forceinline__ bool ex_spin(u64 (&w)[W], const u64* const (&src)[W], const PollCtl& pc) {
     unsigned spins = 0;
@@ -575,13 +595,26 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
 
             // ---- P1: xn = LN_1(x); X6 = xn + lerp (shift_0 - xn); r k v, LoRA down
             {
+                // The layer's table (staged a layer ahead) gives the shift,
+                // mix and LayerNorm parameters, issued ahead of the wait for
+                // x_b of the layer before: the wait outlasts their latency.
+                const RkPLayer& P = Ls2[l & 1];
+                float shv[kPer], lrp[6][kPer], lg[kPer], lc[kPer];
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) {
+                    const int ic = min(k * NT + tid, D - 1);
+                    shv[k] = ld_ag(sh0 + ic);
+#pragma unroll
+                    for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = P.lerp[(size_t)s6 * D + ic];
+                }
+                ln_params(P.ln1w, P.ln1b, D, lg, lc);
+                issued();
                 // x_b of the layer before (every wave is past its last use of xs
                 // and of the other layer-table slot once the poll's barrier is)
                 if (l > 0) {
                     const bool ok = poll_vec<kPer>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
                     if (!agree(ok)) return;
                 }
-                const RkPLayer& P = Ls2[l & 1];
                 // the next layer's table into the other slot
                 if (l + 1 < L && tid < (int)(sizeof(RkPLayer) / 4))
                     reinterpret_cast<int*>(&Ls2[(l + 1) & 1])[tid] =
@@ -613,19 +646,10 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
 #pragma unroll
                 for (int sg = 1; sg < 7; ++sg)
                     uni = uni && (sg >= nseg || (p1_mat(P, sg).block == 0) == (P.r.block == 0));
-                const float* lerp = P.lerp;
                 auto body = [&](auto q, bool pre) {
                     constexpr bool Q = decltype(q)::value;
                     const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
                     u64* outs[7] = {s_r, s_k, s_v, s_lw, s_la, s_lg, s_lv};
-                    float shv[kPer], lrp[6][kPer];      // loaded before the LayerNorm
-#pragma unroll
-                    for (int k = 0; k < kPer; ++k) {
-                        const int ic = min(k * NT + tid, D - 1);
-                        shv[k] = ld_ag(sh0 + ic);
-#pragma unroll
-                        for (int s6 = 0; s6 < 6; ++s6) lrp[s6][k] = lerp[(size_t)s6 * D + ic];
-                    }
                     // the wave's first two rows, issued after x arrived and
                     // before the LayerNorm, which they overlap
                     const int row0 = lo + wv;
@@ -637,7 +661,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                         unit_load<Q>(UA, p1_mat(P, sA0), rA0, min(lane, (p1_mat(P, sA0).K >> 4) - 1));
                         unit_load<Q>(UB, p1_mat(P, sB0), rB0, min(lane, (p1_mat(P, sB0).K >> 4) - 1));
                     }
-                    layer_norm(xs, xn, P.ln1w, P.ln1b, D, A.eps, red);
+                    layer_norm(xs, xn, lg, lc, D, A.eps, red);
 #pragma unroll
                     for (int k = 0; k < kPer; ++k) {
                         const int i = k * NT + tid;
@@ -853,22 +877,25 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 const bool ok = with_format<true>(P.cmk, [&](auto q, auto nu) -> bool {
                     constexpr bool Q = decltype(q)::value;
                     constexpr int NU = decltype(nu)::value;
-                    // x_a first; then the mix inputs and the wave's first two
-                    // rows, which the LayerNorm overlaps (loads issued before the
-                    // wait would hold the wait's first check back)
-                    if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
-                    RKP_MARK(l * 6 + 3, 0);
-                    float shv[kPer], lrp[kPer];
+                    // The shift, mix and LayerNorm parameters ahead of the wait
+                    // for x_a (they come back within it); the wave's first two
+                    // rows after it, overlapped by the LayerNorm (weights ahead
+                    // of the wait would hold its first check back).
+                    float shv[kPer], lrp[kPer], lg[kPer], lc[kPer];
 #pragma unroll
                     for (int k = 0; k < kPer; ++k) {
                         const int ic = min(k * NT + tid, D - 1);
                         shv[k] = ld_ag(sh1 + ic);
                         lrp[k] = P.cmk_lerp[ic];
                     }
+                    ln_params(P.ln2w, P.ln2b, D, lg, lc);
+                    issued();
+                    if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
+                    RKP_MARK(l * 6 + 3, 0);
                     PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
                     pre_load(pr, P.cmk, lo + wv, NW, lane);
                     issued();
-                    layer_norm(xs, xn2, P.ln2w, P.ln2b, D, A.eps, red);
+                    layer_norm(xs, xn2, lg, lc, D, A.eps, red);
 #pragma unroll
                     for (int k = 0; k < kPer; ++k) {
                         const int i = k * NT + tid;
@@ -935,10 +962,12 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 constexpr int N = decltype(nrows)::value;
                 constexpr int STEP = N * NW;
                 PreRows<Q, 1, N> ra, rb;
+                float lg[kPer], lc[kPer];
+                ln_params(A.on_w, A.on_b, D, lg, lc);
                 pre_load(ra, A.head, lo + wv, NW, lane);
                 issued();
                 if (!agree(poll_vec<kPer>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
-                layer_norm(xs, buf, A.on_w, A.on_b, D, A.eps, red);
+                layer_norm(xs, buf, lg, lc, D, A.eps, red);
                 auto finish = [&](const float (&d)[N], int row) {
 #pragma unroll
                     for (int k = 0; k < N; ++k) {
