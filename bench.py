@@ -32,8 +32,10 @@ reference ``sn_rk_step`` timed on its INT4 blob. Every CPU leg states the
 host's sockets, physical cores and logical CPUs.
 
 Modes that run a fixed sequence and exit: ``--pmc-probe [scan|decode]`` (for
-``rocprofv3 --pmc`` counter runs) and ``--profile b1|batch|rwkv|small`` (for
-``rocprofv3 --kernel-trace`` summaries of the decode paths).
+``rocprofv3 --pmc`` counter runs), ``--profile b1|batch|rwkv|small`` (for
+``rocprofv3 --kernel-trace`` summaries of the decode paths) and
+``--hbm-probe`` (the bandwidth plain streaming kernels reach over the scan's
+byte pattern, beside the nominal peak; one JSON line).
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -755,6 +757,50 @@ def pmc_probe():
     return 0
 
 
+def hbm_probe(reps: int = 10) -> int:
+    """Achievable-bandwidth calibration on the scan's arrays (three fp32
+    arrays of 16 x 4096 x 2048): plain grid-stride streaming kernels
+    (snhip_abi_hbm_probe_dev) for c = a + b (the scan's two reads and one
+    write) and for the two reads alone, over a sweep of grid sizes, and
+    torch's device copy of one array; HIP events around `reps` launches after
+    3 warm-ups. Prints one JSON line of GB/s figures."""
+    from sunnynet_amd import _native
+    dev = torch.device("cuda:0")
+    n = SCAN_B * SCAN_T * SCAN_D
+    a = torch.ones(n, device=dev)
+    b = torch.ones(n, device=dev)
+    c = torch.empty(n, device=dev)
+    L = _native.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    out = {"arrays": f"3 x fp32 {SCAN_B}x{SCAN_T}x{SCAN_D} ({n * 4} B each)", "reps": reps, "cases": []}
+    for kind, name, nbytes in ((0, "c = a + b (2 reads + 1 write)", 3 * n * 4), (1, "read a and b", 2 * n * 4)):
+        for grid in (1024, 2048, 4096, 16384):
+            def launch():
+                _native.check(L.snhip_abi_hbm_probe_dev(kind, a.data_ptr(), b.data_ptr(), c.data_ptr(), n, grid,
+                                                        stream), "snhip_abi_hbm_probe_dev")
+            us = timed(launch)
+            out["cases"].append({"kernel": name, "grid": grid, "us": round(us, 2),
+                                 "GB/s": round(nbytes / us / 1e3, 1)})
+            log(f"[hbm] {name} grid {grid}: {us:.1f} us {nbytes / us / 1e3:.1f} GB/s")
+    us = timed(lambda: c.copy_(a))
+    out["cases"].append({"kernel": "torch copy (1 read + 1 write)", "us": round(us, 2),
+                         "GB/s": round(2 * n * 4 / us / 1e3, 1)})
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def _m100_blobs(tmp):
     from sunnynet_amd.blob import pack_sunny_blob
     from sunnynet_amd.weights import gaussian_matmuls, init_sunnynet
@@ -885,7 +931,11 @@ def main(argv=None):
                     help="run the fixed launch sequence used for rocprofv3 --pmc and exit")
     ap.add_argument("--profile", choices=["b1", "batch", "rwkv", "small"],
                     help="run a fixed decode launch sequence for rocprofv3 --kernel-trace and exit")
+    ap.add_argument("--hbm-probe", action="store_true",
+                    help="time plain streaming kernels over the scan's arrays and exit")
     args = ap.parse_args(argv)
+    if args.hbm_probe:
+        return hbm_probe()
     if args.pmc_probe == "scan":
         return pmc_probe()
     if args.pmc_probe == "decode":

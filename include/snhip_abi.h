@@ -125,6 +125,15 @@ snhip_status snhip_abi_core_bwd_dev(const float* q, const float* delta, const fl
                                     float* ddelta, float* ds0, int32_t B, int32_t T,
                                     int32_t D, void* stream);
 
+/* Bandwidth calibration (no counterpart in the reference): plain streaming
+ * kernels over n fp32 values, float4 per lane, non-temporal, grid-stride, on
+ * `grid` workgroups of 256 threads. kind 0: c = a + b (two arrays read, one
+ * written: the gated scan's byte pattern); kind 1: a and b read (their sums
+ * land in c[0 .. grid), so c needs 4 * grid floats). n a multiple of 4, the
+ * arrays 16-byte aligned. Enqueued on `stream`. */
+snhip_status snhip_abi_hbm_probe_dev(int32_t kind, const float* a, const float* b, float* c,
+                                     int64_t n, int32_t grid, void* stream);
+
 /* snhip_abi_core_bwd_dev without any device allocation: same arguments,
  * kernels and results (bit for bit). No counterpart in the reference; for
  * callers that cannot allocate (code under HIP graph capture, tight serving or

@@ -67,6 +67,7 @@ _SIGS = {
     "snhip_abi_quant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
     "snhip_abi_dequant_i4_dev": (I32, [V, V, V, I32, I32, I32, V]),
     "snhip_abi_linear_dev": (I32, [V, V, V, I32, I32, I32, V]),
+    "snhip_abi_hbm_probe_dev": (I32, [I32, V, V, V, ctypes.c_int64, I32, V]),
     # include/snhip.h
     "snhip_load": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT]),
     "snhip_load_ex": (V, [CP, INT, INT, INT, INT, INT, INT, INT, INT, I32, I32, I32]),

@@ -586,4 +586,55 @@ snhip_status launch_scan_bwd(const float* p, const float* nu, const float* s0, c
     return SNHIP_OK;
 }
 
+// ---- achievable-bandwidth calibration: plain streaming kernels over the
+// scan's byte pattern (two fp32 arrays read, one written) and over its reads
+// alone, float4 per lane, non-temporal like the scan, grid-stride. They give
+// the bandwidth a straightforward stream reaches on the device, beside the
+// nominal HBM peak the scan is quoted against.
+namespace {
+typedef float v4f_ __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_hbm_add(const v4f_* __restrict__ a, const v4f_* __restrict__ b,
+                                                 v4f_* __restrict__ c, size_t n4) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + stride < n4; i += 2 * stride) {
+        const v4f_ x0 = __builtin_nontemporal_load(a + i), x1 = __builtin_nontemporal_load(a + i + stride);
+        const v4f_ y0 = __builtin_nontemporal_load(b + i), y1 = __builtin_nontemporal_load(b + i + stride);
+        __builtin_nontemporal_store(x0 + y0, c + i);
+        __builtin_nontemporal_store(x1 + y1, c + i + stride);
+    }
+    for (; i < n4; i += stride) c[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void k_hbm_read2(const v4f_* __restrict__ a, const v4f_* __restrict__ b,
+                                                   v4f_* __restrict__ c, size_t n4) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    v4f_ acc = {0.f, 0.f, 0.f, 0.f};
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+        acc += __builtin_nontemporal_load(a + i) + __builtin_nontemporal_load(b + i);
+    // one store per workgroup-sized slice of c keeps the sums live
+    if (threadIdx.x == 0) c[blockIdx.x] = acc;
+}
+}  // namespace
+
 }  // namespace snhip
+
+extern "C" snhip_status snhip_abi_hbm_probe_dev(int32_t kind, const float* a, const float* b, float* c,
+                                                 int64_t n, int32_t grid, void* stream) {
+    using namespace snhip;
+    if (!a || !b || !c || n <= 0 || n % 4 || grid <= 0 || (kind != 0 && kind != 1) ||
+        !aligned(a, 16) || !aligned(b, 16) || !aligned(c, 16) || (kind == 1 && (int64_t)grid * 4 > n))
+        return SNHIP_E_INVAL;
+    const size_t n4 = (size_t)n / 4;
+    if (kind == 0)
+        hipLaunchKernelGGL(k_hbm_add, dim3((unsigned)grid), dim3(256), 0, as_stream(stream),
+                           reinterpret_cast<const v4f_*>(a), reinterpret_cast<const v4f_*>(b),
+                           reinterpret_cast<v4f_*>(c), n4);
+    else
+        hipLaunchKernelGGL(k_hbm_read2, dim3((unsigned)grid), dim3(256), 0, as_stream(stream),
+                           reinterpret_cast<const v4f_*>(a), reinterpret_cast<const v4f_*>(b),
+                           reinterpret_cast<v4f_*>(c), n4);
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
+}
