@@ -20,6 +20,7 @@
 // * Heads: one wave per (head, sequence), lane i owning state row i.
 // * expf / tanhf: refmath.h (glibc's algorithms).
 #include <cstring>
+#include <type_traits>
 
 #include "refmath.h"
 #include "rkseq.h"
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(64) void k_rkq_ln(RkqLnArgs A) {
     const float4* l4 = reinterpret_cast<const float4*>(A.lerp);
     const bool regs = n4 <= 64 * kLnQ;
     const bool mix1 = A.mode == RKQ_LN_MIX1, mix2 = A.mode == RKQ_LN_MIX2;
-    float4 xv[kLnQ], gv[kLnQ], cv[kLnQ], sv[kLnQ], lv[6][kLnQ];
+    float4 gv[kLnQ], cv[kLnQ], sv[kLnQ], lv[6][kLnQ];
     for (int q = t; q < n4; q += 64) {
         float4 v = src[q];
         if (!ok) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
@@ -443,10 +444,9 @@ __device__ __forceinline__ void rkq_produce(const RkqJob& J, int h, int l, int o
     }
 }
 
-template <int BLK, int NC, int S>
+template <int BLK, int NC, int S, int XD>
 __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArgs A) {
     constexpr int U4 = kRkqU / 4;                      // blocks per unit
-    constexpr int NQ = BLK / 32;                       // code uint4 per half unit
     static_assert(U4 % kRkqWD == 0 && kRkqWD == U4 / 2, "the weight window is a half unit");
     __shared__ float4 wring[3][U4][64];
     RkqJob J;
@@ -478,14 +478,22 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
 #pragma unroll
     for (int s = 0; s < S; ++s)
         xr[s] = J.X + (size_t)min(seqb + 4 * s + r4, A.B - 1) * (size_t)J.ldx;
-    float4 xw[S][U4];   // block i of the unit in multiplication; refilled with the next unit's
-    float4 ww[kRkqWD];  // weight blocks, slot = block % kRkqWD
+    // X operands run XD units ahead of the MFMAs (XD = 2: launches of at
+    // most one workgroup per CU, whose chains then wait on X less; the
+    // second set's registers would keep larger grids from residing at
+    // three workgroups per CU).
+    static_assert(XD == 1 || XD == 2, "X depth");
+    float4 xw[XD][S][U4];   // unit u's block i in xw[u % XD]; refilled with unit u + XD's
+    float4 ww[kRkqWD];      // weight blocks, slot = block % kRkqWD
     v4f acc[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < U4; ++i) xw[s][i] = *reinterpret_cast<const float4*>(xr[s] + min(4 * i, Kd - 4));
+        for (int d = 0; d < XD; ++d)
+#pragma unroll
+            for (int i = 0; i < U4; ++i)
+                xw[d][s][i] = *reinterpret_cast<const float4*>(xr[s] + min(d * kRkqU + 4 * i, Kd - 4));
     }
     // Steps 0 and 1: the producers write units 0 and 1; the window takes
     // unit 0's first half once it is complete.
@@ -493,49 +501,67 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
 #pragma unroll
     for (int j = 0; j < kRkqWD; ++j) ww[j] = wring[0][j][l];
     __syncthreads();
-    // One full unit: block i's MFMAs, then its refills (weight block
-    // i + kRkqWD, from the next unit's slot for the last half; X block i of
-    // the next unit). Straight-line, so the window stays in place.
-    auto full_unit = [&](int slot, int nslot, int knext) {
+    // One full unit from X set P: block i's MFMAs, then its refills (weight
+    // block i + kRkqWD, from the next unit's slot for the last half; X block i
+    // of unit u + XD). Straight-line, so the window stays in place.
+    auto full_unit = [&](auto par, int slot, int nslot, int knext) {
+        constexpr int P = decltype(par)::value;
 #pragma unroll
         for (int i = 0; i < U4; ++i) {
             const float4 wc = ww[i % kRkqWD];
 #pragma unroll
-            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].x, wc.x, acc[s], 0, 0, 0);
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].x, wc.x, acc[s], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].y, wc.y, acc[s], 0, 0, 0);
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].y, wc.y, acc[s], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].z, wc.z, acc[s], 0, 0, 0);
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].z, wc.z, acc[s], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].w, wc.w, acc[s], 0, 0, 0);
+            for (int s = 0; s < S; ++s) acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].w, wc.w, acc[s], 0, 0, 0);
             ww[i % kRkqWD] = i + kRkqWD < U4 ? wring[slot][i + kRkqWD][l] : wring[nslot][i + kRkqWD - U4][l];
             const int kx = min(knext + 4 * i, Kd - 4);
 #pragma unroll
-            for (int s = 0; s < S; ++s) xw[s][i] = *reinterpret_cast<const float4*>(xr[s] + kx);
+            for (int s = 0; s < S; ++s) xw[P][s][i] = *reinterpret_cast<const float4*>(xr[s] + kx);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // Steps 2 .. nu: units 0 .. nu - 2, each followed by another.
-    for (int u = 0; u < nu - 1; ++u) {
-        full_unit(u % 3, (u + 1) % 3, (u + 1) * kRkqU);
-        __syncthreads();
-    }
-    // Step nu + 1: the last unit (its refills read in-bounds leftovers).
-    const int ul = nu - 1;
-    if (!half_last) {
-        full_unit(ul % 3, (ul + 1) % 3, Kd);
-    } else {
+    auto half_unit = [&](auto par) {
+        constexpr int P = decltype(par)::value;
 #pragma unroll
         for (int i = 0; i < U4 / 2; ++i) {
             const float4 wc = ww[i % kRkqWD];
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].x, wc.x, acc[s], 0, 0, 0);
-                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].y, wc.y, acc[s], 0, 0, 0);
-                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].z, wc.z, acc[s], 0, 0, 0);
-                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[s][i].w, wc.w, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].x, wc.x, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].y, wc.y, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].z, wc.z, acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_4x4x1f32(xw[P][s][i].w, wc.w, acc[s], 0, 0, 0);
             }
         }
+    };
+    constexpr std::integral_constant<int, 0> x0{};
+    constexpr std::integral_constant<int, XD - 1> x1{};
+    // Steps 2 .. nu: units 0 .. nu - 2, each followed by another; two at a
+    // time, so that the X set of each is fixed at compile time.
+    int u = 0;
+    for (; u + 2 <= nu - 1; u += 2) {
+        full_unit(x0, u % 3, (u + 1) % 3, (u + XD) * kRkqU);
+        __syncthreads();
+        full_unit(x1, (u + 1) % 3, (u + 2) % 3, (u + 1 + XD) * kRkqU);
+        __syncthreads();
+    }
+    if (u < nu - 1) {   // one more (u even: set 0)
+        full_unit(x0, u % 3, (u + 1) % 3, (u + XD) * kRkqU);
+        __syncthreads();
+        ++u;
+    }
+    // Step nu + 1: the last unit, u = nu - 1 (its refills read in-bounds
+    // leftovers).
+    if ((u & 1) == 0 || XD == 1) {
+        if (!half_last) full_unit(x0, u % 3, (u + 1) % 3, Kd);
+        else half_unit(x0);
+    } else {
+        if (!half_last) full_unit(x1, u % 3, (u + 1) % 3, Kd);
+        else half_unit(x1);
     }
     __syncthreads();
     for (int t = nu + 2; t < nsteps; ++t) __syncthreads();
@@ -761,6 +787,20 @@ snhip_status launch_rkq_heads(const RkqHeadArgs& a, int B, hipStream_t st) {
     return SNHIP_OK;
 }
 
+// Compute units of the current device (queried once per device).
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                          ? n
+                          : 256;
+    }
+    return cached[dev];
+}
+
 // nc, s: INT4 consumer waves per workgroup and chains per consumer (0: chosen
 // here); fp32: s groups of 4 sequences per wave.
 snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int nc, int s,
@@ -825,9 +865,15 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
     }
     a.start[n] = total;
     for (int i = n + 1; i <= kRkqMaxJobs; ++i) a.start[i] = total;
+    // Measured on the RWKV-7 step at B = 64: X two units ahead takes W_o and
+    // the channel-mix value (192 workgroups) 1.5 us faster each, and makes
+    // the 656- and 768-workgroup launches 1.9 us slower.
+    const bool deep = total <= cu_count();
 #define SNHIP_RKQ_F32(S_) hipLaunchKernelGGL((k_rkq_mm_f32<S_>), dim3(total), dim3(64), 0, st, a)
 #define SNHIP_RKQ_Q4(B_, N_, S_) \
-    hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_, S_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
+    hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_, S_, 1>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
+#define SNHIP_RKQ_Q4D(B_) \
+    hipLaunchKernelGGL((k_rkq_mm_q4<B_, 1, 1, 2>), dim3(total), dim3(64 * (1 + kRkqNP)), 0, st, a)
 #define SNHIP_RKQ_Q4W(B_, N_) \
     hipLaunchKernelGGL((k_rkq_mm_q4w<B_, N_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
 #define SNHIP_RKQ_Q4B(B_)                                 \
@@ -836,7 +882,8 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
             if (NC == 1) SNHIP_RKQ_Q4W(B_, 1);            \
             else if (NC == 2) SNHIP_RKQ_Q4W(B_, 2);       \
             else SNHIP_RKQ_Q4W(B_, 4);                    \
-        } else if (NC == 1 && S == 1) SNHIP_RKQ_Q4(B_, 1, 1); \
+        } else if (NC == 1 && S == 1 && deep) SNHIP_RKQ_Q4D(B_); \
+        else if (NC == 1 && S == 1) SNHIP_RKQ_Q4(B_, 1, 1); \
         else if (NC == 2 && S == 1) SNHIP_RKQ_Q4(B_, 2, 1); \
         else if (NC == 4) SNHIP_RKQ_Q4(B_, 4, 1);        \
         else if (NC == 1) SNHIP_RKQ_Q4(B_, 1, 2);        \
@@ -853,6 +900,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
     }
 #undef SNHIP_RKQ_F32
 #undef SNHIP_RKQ_Q4
+#undef SNHIP_RKQ_Q4D
 #undef SNHIP_RKQ_Q4B
 #undef SNHIP_RKQ_Q4W
     SNHIP_CHECK(hipGetLastError());
