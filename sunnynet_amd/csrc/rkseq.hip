@@ -444,11 +444,19 @@ __device__ __forceinline__ void rkq_produce(const RkqJob& J, int h, int l, int o
     }
 }
 
+// X rows staged in LDS (XD = 0) take at most 64 KiB: rows of up to
+// kRkqXLF / (sequences per workgroup) inputs.
+constexpr int kRkqXLF = 16384;
+
 template <int BLK, int NC, int S, int XD>
 __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArgs A) {
     constexpr int U4 = kRkqU / 4;                      // blocks per unit
     static_assert(U4 % kRkqWD == 0 && kRkqWD == U4 / 2, "the weight window is a half unit");
+    constexpr int XR = XD > 0 ? XD : 1;                // X register sets
+    constexpr int NSQ = 4 * S * NC;                    // sequences of the workgroup
     __shared__ float4 wring[3][U4][64];
+    constexpr int XLK = kRkqXLF / NSQ;                 // inputs per staged row
+    __shared__ float4 xlds[XD == 0 ? NSQ * (XLK / 4) : 1];
     RkqJob J;
     int u0;
     rkq_job(A, J, u0);
@@ -464,6 +472,17 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
     // at steps 0 .. nu - 1 and multiplied at steps 2 .. nu + 1; the count is
     // rounded up to the producer's prefetch depth (idle steps at the end).
     const int nsteps = (nu + 2 + kRkqPF - 1) / kRkqPF * kRkqPF;
+    if constexpr (XD == 0) {
+        // The X rows of the workgroup's sequences into LDS, by every wave
+        // (Kd <= XLK; rows past the batch repeat the last sequence's).
+        const int kq = Kd / 4;
+        for (int idx = threadIdx.x; idx < NSQ * kq; idx += 64 * (NC + kRkqNP)) {
+            const int sq = idx / kq, q = idx - sq * kq;
+            xlds[sq * (XLK / 4) + q] =
+                *reinterpret_cast<const float4*>(J.X + (size_t)min(st * NSQ + sq, A.B - 1) * (size_t)J.ldx + 4 * q);
+        }
+        __syncthreads();
+    }
     if (wv < kRkqNP) {
         rkq_produce<BLK>(J, wv, l, orow, nu, nsteps, wring);
         return;
@@ -478,22 +497,26 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
 #pragma unroll
     for (int s = 0; s < S; ++s)
         xr[s] = J.X + (size_t)min(seqb + 4 * s + r4, A.B - 1) * (size_t)J.ldx;
-    // X operands run XD units ahead of the MFMAs (XD = 2: launches of at
-    // most one workgroup per CU, whose chains then wait on X less; the
-    // second set's registers would keep larger grids from residing at
-    // three workgroups per CU).
-    static_assert(XD == 1 || XD == 2, "X depth");
-    float4 xw[XD][S][U4];   // unit u's block i in xw[u % XD]; refilled with unit u + XD's
+    // X operands run XR units ahead of the MFMAs, from global memory (XD = 1;
+    // XD = 2 in launches of at most one workgroup per CU, whose chains then
+    // wait on X less: the second set's registers would keep larger grids
+    // from residing at three workgroups per CU) or from the rows staged in
+    // LDS (XD = 0).
+    static_assert(XD >= 0 && XD <= 2, "X depth");
+    auto ldx = [&](int s, int k) -> float4 {
+        if constexpr (XD == 0) return xlds[(c * 4 * S + 4 * s + r4) * (XLK / 4) + (k >> 2)];
+        else return *reinterpret_cast<const float4*>(xr[s] + k);
+    };
+    float4 xw[XR][S][U4];   // unit u's block i in xw[u % XR]; refilled with unit u + XR's
     float4 ww[kRkqWD];      // weight blocks, slot = block % kRkqWD
     v4f acc[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int d = 0; d < XD; ++d)
+        for (int d = 0; d < XR; ++d)
 #pragma unroll
-            for (int i = 0; i < U4; ++i)
-                xw[d][s][i] = *reinterpret_cast<const float4*>(xr[s] + min(d * kRkqU + 4 * i, Kd - 4));
+            for (int i = 0; i < U4; ++i) xw[d][s][i] = ldx(s, min(d * kRkqU + 4 * i, Kd - 4));
     }
     // Steps 0 and 1: the producers write units 0 and 1; the window takes
     // unit 0's first half once it is complete.
@@ -520,7 +543,7 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
             ww[i % kRkqWD] = i + kRkqWD < U4 ? wring[slot][i + kRkqWD][l] : wring[nslot][i + kRkqWD - U4][l];
             const int kx = min(knext + 4 * i, Kd - 4);
 #pragma unroll
-            for (int s = 0; s < S; ++s) xw[P][s][i] = *reinterpret_cast<const float4*>(xr[s] + kx);
+            for (int s = 0; s < S; ++s) xw[P][s][i] = ldx(s, kx);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -539,24 +562,24 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
         }
     };
     constexpr std::integral_constant<int, 0> x0{};
-    constexpr std::integral_constant<int, XD - 1> x1{};
+    constexpr std::integral_constant<int, XR - 1> x1{};
     // Steps 2 .. nu: units 0 .. nu - 2, each followed by another; two at a
     // time, so that the X set of each is fixed at compile time.
     int u = 0;
     for (; u + 2 <= nu - 1; u += 2) {
-        full_unit(x0, u % 3, (u + 1) % 3, (u + XD) * kRkqU);
+        full_unit(x0, u % 3, (u + 1) % 3, (u + XR) * kRkqU);
         __syncthreads();
-        full_unit(x1, (u + 1) % 3, (u + 2) % 3, (u + 1 + XD) * kRkqU);
+        full_unit(x1, (u + 1) % 3, (u + 2) % 3, (u + 1 + XR) * kRkqU);
         __syncthreads();
     }
     if (u < nu - 1) {   // one more (u even: set 0)
-        full_unit(x0, u % 3, (u + 1) % 3, (u + XD) * kRkqU);
+        full_unit(x0, u % 3, (u + 1) % 3, (u + XR) * kRkqU);
         __syncthreads();
         ++u;
     }
     // Step nu + 1: the last unit, u = nu - 1 (its refills read in-bounds
     // leftovers).
-    if ((u & 1) == 0 || XD == 1) {
+    if ((u & 1) == 0 || XR == 1) {
         if (!half_last) full_unit(x0, u % 3, (u + 1) % 3, Kd);
         else half_unit(x0);
     } else {
@@ -821,6 +844,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
     }
     int per;   // sequences per workgroup
     int S = 1, NC = 1;
+    bool xl = false;   // INT4: four one-chain consumers per workgroup, X staged in LDS
     if (block == 0) {
         const long waves1 = (long)tiles1 * ((B + 3) / 4);
         S = s ? s : (B > 8 && waves1 / 4 >= 1024) ? 4 : (B > 4 && waves1 / 2 >= 1024) ? 2 : 1;
@@ -853,6 +877,24 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
         S = s ? s : s0;
         if (!((NC == 1 || NC == 2 || NC == 4) && (S == 1 || S == 2 || S == 16)) || (NC == 4 && S == 2))
             return SNHIP_E_INVAL;
+        // One-chain launches of more than one workgroup per CU instead run
+        // one workgroup of four consumers per 16 sequences with their X rows
+        // staged in LDS once (each consumer lane otherwise loads its X from
+        // global memory one unit ahead, and at three workgroups per CU those
+        // loads' latency held the chains back). Measured on the RWKV-7 step
+        // at B = 64 (r, k, v and the LoRA downs, 656 -> 164 workgroups):
+        // 31.3 -> 21.9 us; the LoRA ups 7.3 -> 6.5. Staging the rows of
+        // smaller grids (one workgroup of one consumer per CU) was slower
+        // (B = 8 step 1384 -> 1504 us).
+        if (!nc && !s && NC == 1 && S == 1 && B >= 16 && wg11 > (long)cu_count() &&
+            env_unsigned("SNHIP_RKQ_XL", 1, 0)) {
+            bool fits = true;
+            for (int i = 0; i < n; ++i) fits = fits && jobs[i].Kd <= kRkqXLF / 16;
+            if (fits) {
+                NC = 4;
+                xl = true;
+            }
+        }
         per = (S == 16 ? 16 : 4 * S) * NC;
     }
     a.n = n;
@@ -874,6 +916,8 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
     hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_, S_, 1>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
 #define SNHIP_RKQ_Q4D(B_) \
     hipLaunchKernelGGL((k_rkq_mm_q4<B_, 1, 1, 2>), dim3(total), dim3(64 * (1 + kRkqNP)), 0, st, a)
+#define SNHIP_RKQ_Q4L(B_, N_) \
+    hipLaunchKernelGGL((k_rkq_mm_q4<B_, N_, 1, 0>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
 #define SNHIP_RKQ_Q4W(B_, N_) \
     hipLaunchKernelGGL((k_rkq_mm_q4w<B_, N_>), dim3(total), dim3(64 * (N_ + kRkqNP)), 0, st, a)
 #define SNHIP_RKQ_Q4B(B_)                                 \
@@ -882,7 +926,8 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
             if (NC == 1) SNHIP_RKQ_Q4W(B_, 1);            \
             else if (NC == 2) SNHIP_RKQ_Q4W(B_, 2);       \
             else SNHIP_RKQ_Q4W(B_, 4);                    \
-        } else if (NC == 1 && S == 1 && deep) SNHIP_RKQ_Q4D(B_); \
+        } else if (xl) SNHIP_RKQ_Q4L(B_, 4);             \
+        else if (NC == 1 && S == 1 && deep) SNHIP_RKQ_Q4D(B_); \
         else if (NC == 1 && S == 1) SNHIP_RKQ_Q4(B_, 1, 1); \
         else if (NC == 2 && S == 1) SNHIP_RKQ_Q4(B_, 2, 1); \
         else if (NC == 4) SNHIP_RKQ_Q4(B_, 4, 1);        \
@@ -901,6 +946,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
 #undef SNHIP_RKQ_F32
 #undef SNHIP_RKQ_Q4
 #undef SNHIP_RKQ_Q4D
+#undef SNHIP_RKQ_Q4L
 #undef SNHIP_RKQ_Q4B
 #undef SNHIP_RKQ_Q4W
     SNHIP_CHECK(hipGetLastError());
