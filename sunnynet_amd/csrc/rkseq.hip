@@ -456,7 +456,8 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
     constexpr int NSQ = 4 * S * NC;                    // sequences of the workgroup
     __shared__ float4 wring[3][U4][64];
     constexpr int XLK = kRkqXLF / NSQ;                 // inputs per staged row
-    __shared__ float4 xlds[XD == 0 ? NSQ * (XLK / 4) : 1];
+    constexpr int XLS = XLK / 4 + 1;                   // row stride in float4 (padded: rows on distinct banks)
+    __shared__ float4 xlds[XD == 0 ? NSQ * XLS : 1];
     RkqJob J;
     int u0;
     rkq_job(A, J, u0);
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
         const int kq = Kd / 4;
         for (int idx = threadIdx.x; idx < NSQ * kq; idx += 64 * (NC + kRkqNP)) {
             const int sq = idx / kq, q = idx - sq * kq;
-            xlds[sq * (XLK / 4) + q] =
+            xlds[sq * XLS + q] =
                 *reinterpret_cast<const float4*>(J.X + (size_t)min(st * NSQ + sq, A.B - 1) * (size_t)J.ldx + 4 * q);
         }
         __syncthreads();
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4(const RkqMMArg
     // LDS (XD = 0).
     static_assert(XD >= 0 && XD <= 2, "X depth");
     auto ldx = [&](int s, int k) -> float4 {
-        if constexpr (XD == 0) return xlds[(c * 4 * S + 4 * s + r4) * (XLK / 4) + (k >> 2)];
+        if constexpr (XD == 0) return xlds[(c * 4 * S + 4 * s + r4) * XLS + (k >> 2)];
         else return *reinterpret_cast<const float4*>(xr[s] + k);
     };
     float4 xw[XR][S][U4];   // unit u's block i in xw[u % XR]; refilled with unit u + XR's
@@ -624,6 +625,9 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4w(const RkqMMAr
     const int c = wv - kRkqNP;
     const int seqb = st * (16 * NC) + 16 * c;
     const float* xr = J.X + (size_t)min(seqb + (l & 15), A.B - 1) * (size_t)J.ldx;
+    // (X rows staged in LDS, as the one-chain kernel does for large grids,
+    // made the channel-mix key at B = 64 slower: its chains wait on the
+    // 16x16x1 issue rate, not on X.)
     float4 xw[U4];
     float4 ww[kRkqWD];
     v16f acc = {};
