@@ -874,7 +874,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
             wide_ok = wide_ok && jobs[i].Kd >= 256 && jobs[i].epi != RKQ_TANH && jobs[i].epi != RKQ_SIGMOID;
         if (wide_ok && B >= 8 && wg11 > (long)env_unsigned("SNHIP_RKQ_WIDE_GRID", 256, 0)) {
             s0 = 16;
-            nc0 = std::min(4, (B + 15) / 16);
+            nc0 = B > 32 ? 4 : B > 16 ? 2 : 1;   // chains of 16 per workgroup: 1, 2 or 4 (instantiated)
             while (nc0 > 1 && (long)tiles1 * ((B + 16 * nc0 - 1) / (16 * nc0)) < 512) nc0 /= 2;
         }
         NC = nc ? nc : nc0;

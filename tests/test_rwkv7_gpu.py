@@ -274,6 +274,30 @@ def test_cfg4_int4_b64_exact(gpu, cfg4):
         assert np.array_equal(a[pick], b)
 
 
+def test_cfg4_int4_ragged_batch_exact(gpu, cfg4):
+    """B=37: the r/k/v and LoRA-up launches then take the staged-X form
+    (four consumers per workgroup, 16 sequences of X rows in LDS), with a last
+    sequence tile of 5 rows, and the wide vocabulary head four 16-sequence
+    chains per workgroup (three would cover 37, but only 1, 2 and 4 are
+    built: B = 33..48 once asked for three and the launch was refused);
+    sequences from the first and the partial tile replayed on the oracle,
+    three steps, logits identical."""
+    p, dq = cfg4
+    cfg = RWKV_CFG4
+    B = 37
+    print(f"rwkv7 cfg4 int4 g32 B={B}, exact", flush=True)
+    hm = HipRwkv7(p, weights="int4", block=32, max_batch=B)
+    pick = [0, 15, 32, 36]
+    orc = oracle.RkOracle(dq, batch=len(pick))
+    rng = np.random.default_rng(37)
+    for _ in range(3):
+        toks = rng.integers(0, cfg.vocab, B).astype(np.int32)
+        a = hm.step_batch(torch.from_numpy(toks).cuda()).cpu().numpy()
+        b = orc.step(toks[pick])
+        print(f"B={B} worst |dlogit|", float(np.abs(a[pick] - b).max()), flush=True)
+        assert np.array_equal(a[pick], b)
+
+
 def test_loader_rejects_truncated_and_malformed_blobs(gpu, tiny, tmp_path):
     """The v3 loader checks every size before it reads (the reference's
     sn_rk_load reads past the end of such files): a file cut anywhere, a wrong
