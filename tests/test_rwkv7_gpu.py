@@ -298,6 +298,30 @@ def test_cfg4_int4_ragged_batch_exact(gpu, cfg4):
         assert np.array_equal(a[pick], b)
 
 
+def test_cfg4_int4_every_batch_size(gpu, cfg4):
+    """Every batch size 1..64 of the 12-layer INT4 model (the launch shapes
+    change with B: one or four consumers per workgroup, staged or global X,
+    narrow or wide chains and their counts): one step from the reset state,
+    the first and the last sequence identical to the oracle's (B = 1, the
+    persistent step, within the 2e-5 bar)."""
+    p, dq = cfg4
+    cfg = RWKV_CFG4
+    print("rwkv7 cfg4 int4 g32 B=1..64, one step each", flush=True)
+    hm = HipRwkv7(p, weights="int4", block=32, max_batch=64)
+    rng = np.random.default_rng(99)
+    orc = oracle.RkOracle(dq, batch=2)
+    for B in range(1, 65):
+        toks = rng.integers(0, cfg.vocab, B).astype(np.int32)
+        hm.reset()
+        a = hm.step_batch(torch.from_numpy(toks).cuda()).cpu().numpy()
+        orc.reset()
+        b = orc.step(toks[[0, B - 1]])
+        if B == 1:   # the persistent one-sequence step: within the bar
+            assert np.abs(a[[0, 0]] - b).max() < TOL and a[0].argmax() == b[0].argmax()
+        else:
+            assert np.array_equal(a[[0, B - 1]], b), B
+
+
 def test_loader_rejects_truncated_and_malformed_blobs(gpu, tiny, tmp_path):
     """The v3 loader checks every size before it reads (the reference's
     sn_rk_load reads past the end of such files): a file cut anywhere, a wrong
