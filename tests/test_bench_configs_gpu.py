@@ -8,7 +8,9 @@ instantiations and chain lengths:
 * INT4 g32 B=1: T=2048 prefill, then 256 greedy steps;
 * INT4 g32 B=8 and B=32: the persistent batched step (k_decode_batch at
   the 100M product depths with INT4 g32 weights), sampled sequences;
-* fp32 B=64: T=1024 prefill then greedy steps, sampled sequences.
+* fp32 B=64: T=1024 prefill then greedy steps, sampled sequences;
+* every batch size 1..64, INT4 and fp32, one step each (every decode path
+  and row-block count the batch size selects).
 
 INT4 references run the reference's fp32 runtime on a blob holding the
 bit-identically dequantized weights (W4A32). Bar: logits within 2e-5, argmax
@@ -129,3 +131,32 @@ def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
         print(f"{weights} B={B} sequence {b}: {n} tokens equal, last |dlogit| {d:.3g}", flush=True)
         assert d < TOL
     hm.close()
+
+
+@pytest.mark.parametrize("weights", ["int4", "fp32"])
+def test_every_batch_size_one_step(gpu, blobs, weights):
+    """Every batch size 1..64 at the 100M shape (B=1 the persistent step,
+    2..7 the GEMV graph, 8..64 the persistent batched step with one to four
+    16-row blocks and partial ones): one step from the reset state, the first
+    and the last sequence against the reference runtime, within 2e-5 and with
+    the same argmax."""
+    p32, p4, pdq = blobs
+    path, ref_path = (p4, pdq) if weights == "int4" else (p32, p32)
+    print(f"{weights} B=1..64, one step each", flush=True)
+    hm = _model(path, weights=weights, block=32, max_batch=64)
+    ref = _ref(ref_path)
+    rng = np.random.default_rng(7)
+    worst = 0.0
+    for B in range(1, 65):
+        toks = rng.integers(0, CFG.vocab_size, B).astype(np.int32)
+        hm.reset()
+        lg = hm.step_batch(torch.from_numpy(toks).to(gpu)).cpu().numpy()
+        for b in sorted({0, B - 1}):
+            ref.reset()
+            r = ref.step(int(toks[b]))
+            d = float(np.abs(lg[b] - r).max())
+            worst = max(worst, d)
+            assert d < TOL and lg[b].argmax() == r.argmax(), (B, b, d)
+    print(f"{weights} B=1..64: worst |dlogit| {worst:.3g}", flush=True)
+    hm.close()
+    ref.close()
