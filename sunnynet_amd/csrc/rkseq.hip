@@ -71,13 +71,18 @@ __device__ __forceinline__ float seq_sum(const float4* v, int n4) {
     return s;
 }
 
-// Row LayerNorm of rows up to kLnMax (= 64 lanes x kLnQ float4): lane t owns
-// float4 q = t + 64 j of the row (elements 4q .. 4q+3); its row, gain, bias,
-// shift and mix values are loaded as float4 before the sums, so the only
-// exposed latencies are one round trip and the two sequential sums.
-constexpr int kLnQ = 3;                    // float4 per lane with everything in registers (rows <= 768)
+// Row LayerNorm of rows up to kLnMax, one workgroup of LT threads per row:
+// thread t owns float4 q = t + LT j of the row (elements 4q .. 4q+3); its
+// row, gain, bias, shift and mix values are loaded as float4 before the sums,
+// so the only exposed latencies are one round trip and the two sequential
+// sums (one lane). 256 threads rather than one wave spread the row's loads
+// and the mixes' stores: 9.6 -> 8.4 us per call at D = 768, B = 64.
+constexpr int kLnR = 192;                  // float4 of a row held in registers (rows <= 768)
+constexpr int kLnT = 256;                  // threads per row
 
-__global__ __launch_bounds__(64) void k_rkq_ln(RkqLnArgs A) {
+template <int LT>
+__global__ __launch_bounds__(LT) void k_rkq_ln(RkqLnArgs A) {
+    constexpr int kLnQ = (kLnR + LT - 1) / LT;   // float4 per thread
     __shared__ float4 xs4[kLnMax / 4];
     __shared__ float4 sq4[kLnMax / 4];
     __shared__ float stat[2];
@@ -95,10 +100,10 @@ __global__ __launch_bounds__(64) void k_rkq_ln(RkqLnArgs A) {
     const float4* g4 = reinterpret_cast<const float4*>(A.g);
     const float4* c4 = reinterpret_cast<const float4*>(A.c);
     const float4* l4 = reinterpret_cast<const float4*>(A.lerp);
-    const bool regs = n4 <= 64 * kLnQ;
+    const bool regs = n4 <= LT * kLnQ;
     const bool mix1 = A.mode == RKQ_LN_MIX1, mix2 = A.mode == RKQ_LN_MIX2;
     float4 gv[kLnQ], cv[kLnQ], sv[kLnQ], lv[6][kLnQ];
-    for (int q = t; q < n4; q += 64) {
+    for (int q = t; q < n4; q += LT) {
         float4 v = src[q];
         if (!ok) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
         xs4[q] = v;
@@ -106,7 +111,7 @@ __global__ __launch_bounds__(64) void k_rkq_ln(RkqLnArgs A) {
     if (regs) {
 #pragma unroll
         for (int j = 0; j < kLnQ; ++j) {
-            const int q = min(t + 64 * j, n4 - 1);
+            const int q = min(t + LT * j, n4 - 1);
             gv[j] = g4[q];
             cv[j] = c4[q];
             if (mix1 || mix2) sv[j] = sh4[q];
@@ -122,7 +127,7 @@ __global__ __launch_bounds__(64) void k_rkq_ln(RkqLnArgs A) {
     if (t == 0) stat[0] = seq_sum(xs4, n4) / (float)D;   // sum = sum + x[i], in order
     __syncthreads();
     const float mean = stat[0];
-    for (int q = t; q < n4; q += 64) {
+    for (int q = t; q < n4; q += LT) {
         const float4 v = xs4[q];
         float4 d;
         d.x = v.x - mean; d.y = v.y - mean; d.z = v.z - mean; d.w = v.w - mean;
@@ -165,14 +170,14 @@ __global__ __launch_bounds__(64) void k_rkq_ln(RkqLnArgs A) {
     if (regs) {
 #pragma unroll
         for (int j = 0; j < kLnQ; ++j) {
-            const int q = t + 64 * j;
+            const int q = t + LT * j;
             if (q < n4) {
                 const float4 lp[6] = {lv[0][j], lv[1][j], lv[2][j], lv[3][j], lv[4][j], lv[5][j]};
                 emit(q, gv[j], cv[j], sv[j], lp);
             }
         }
     } else {
-        for (int q = t; q < n4; q += 64) {   // longer rows: parameters loaded as used
+        for (int q = t; q < n4; q += LT) {   // longer rows: parameters loaded as used
             float4 lp[6], sh = make_float4(0.f, 0.f, 0.f, 0.f);
             if (mix1 || mix2) sh = sh4[q];
             if (mix1) {
@@ -802,7 +807,7 @@ __global__ void k_refmath(const float* __restrict__ x, float* __restrict__ e, fl
 
 snhip_status launch_rkq_ln(const RkqLnArgs& a, int B, hipStream_t st) {
     if (a.D <= 0 || a.D > kLnMax || a.D % 4 || B <= 0) return SNHIP_E_INVAL;
-    hipLaunchKernelGGL(k_rkq_ln, dim3(B), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(k_rkq_ln<kLnT>, dim3(B), dim3(kLnT), 0, st, a);
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;
 }
