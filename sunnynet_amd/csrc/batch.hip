@@ -387,18 +387,16 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
         BPROF(5 * l, 0);
         for (int b = wg; b < B; b += G) {
             fresh();
-            if (l > 0 && wait(fl(l - 1, 4) + (size_t)(b >> 4) * N4, N4)) return;
-            bool xok;
-            const float* xr = in_row(l, b, xok);
+            // The row's history and the layer's gains and taps do not depend
+            // on the wait: issued ahead of it.
             const gptr<float> ng = glb(uni(P->ni_g));
             const gptr<float> nc = glb(uni(P->ni_c));
             const gptr<float> dw = glb(uni(P->dw));
             float* hb = a.hist + (size_t)b * hbs + (size_t)l * a.kh * D;
-            float xv[PERM], gv[PERM], cv[PERM], h[kTaps - 1][PERM], dv[kTaps][PERM];
+            float xv[PERM], gv[PERM], cv[PERM], h[kTaps - 1][PERM], dv[kTaps][PERM], rv[PERM];
 #pragma unroll
             for (int k = 0; k < PERM; ++k) {
                 const int i = min(k * NT + tid, D - 1);
-                xv[k] = xok ? xr[i] : __builtin_nanf("");
                 gv[k] = ng[i];
                 cv[k] = nc[i];
 #pragma unroll
@@ -406,23 +404,36 @@ __global__ __launch_bounds__(NT) void k_decode_batch(BatchArgs a) {
 #pragma unroll
                 for (int t = 0; t < kTaps; ++t) dv[t][k] = dw[(size_t)t * D + i];
             }
+            issued();
+            if (l > 0 && wait(fl(l - 1, 4) + (size_t)(b >> 4) * N4, N4)) return;
+            bool xok;
+            const float* xr = in_row(l, b, xok);
+#pragma unroll
+            for (int k = 0; k < PERM; ++k) xv[k] = xok ? xr[min(k * NT + tid, D - 1)] : __builtin_nanf("");
             float mean, rstd;
             row_stats(xv, D, a.eps, rred, tid, wv, lane, mean, rstd);
 #pragma unroll
             for (int k = 0; k < PERM; ++k) {
                 const int i = k * NT + tid;
-                if (i >= D) continue;
                 const float raw = (xv[k] - mean) * rstd * gv[k] + cv[k];
                 // acc = raw w[K-1] + hist[0] w[K-2] + hist[1] w[K-3] + hist[2] w[K-4]
                 float acc = raw * dv[kTaps - 1][k];
 #pragma unroll
                 for (int t = 0; t < kTaps - 1; ++t) acc = acc + h[t][k] * dv[kTaps - 2 - t][k];
-                st_ag(atl + (size_t)b * D + i, raw + acc);
-#pragma unroll
-                for (int t = kTaps - 2; t >= 1; --t) hb[(size_t)t * D + i] = h[t - 1][k];
-                hb[i] = raw;
+                if (i < D) st_ag(atl + (size_t)b * D + i, raw + acc);
+                rv[k] = raw;
             }
             publish(fl(l, 0) + b, ep);
+            // The history shift after the flag: P1 reads only `at`, and the
+            // history is this workgroup's own until the next step.
+#pragma unroll
+            for (int k = 0; k < PERM; ++k) {
+                const int i = k * NT + tid;
+                if (i >= D) continue;
+#pragma unroll
+                for (int t = kTaps - 2; t >= 1; --t) hb[(size_t)t * D + i] = h[t - 1][k];
+                hb[i] = rv[k];
+            }
         }
         BPROF(5 * l, 2);
         BPROF(5 * l, 3);
