@@ -978,14 +978,18 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                         }
                     }
                 };
-                for (int row = lo + wv; row < hi; row += 2 * STEP) {
-                    pre_load(rb, A.head, row + STEP, NW, lane);
+                // A pass is prefetched only when the wave has it (uniform
+                // branches): a prefetch past hi would read the next
+                // workgroup's rows for nothing and hold the key poll that
+                // follows behind its loads.
+                for (int row = __builtin_amdgcn_readfirstlane(lo + wv); row < hi; row += 2 * STEP) {
+                    if (row + STEP < hi) pre_load(rb, A.head, row + STEP, NW, lane);
                     {
                         float d[N];
                         pre_dot(ra, A.head, buf, lane, d);
                         finish(d, row);
                     }
-                    pre_load(ra, A.head, row + 2 * STEP, NW, lane);
+                    if (row + 2 * STEP < hi) pre_load(ra, A.head, row + 2 * STEP, NW, lane);
                     if (row + STEP < hi) {
                         float d[N];
                         pre_dot(rb, A.head, buf, lane, d);
