@@ -76,11 +76,12 @@ extern "C" int snhip_persist_clk(unsigned long long* out) {
 
 namespace {
 // fp32 and fp16 rows stream more bytes per phase: 8 waves per workgroup
-// measured faster for fp32, 16 for INT4.
-int threads_for(int blk) { return blk == 0 || blk == 16 ? 512 : 1024; }
-const void* kernel_for(int blk) {
-    return blk == 0 || blk == 16 ? nt512::kernel_for(blk) : nt1024::kernel_for(blk);
-}
+// measured faster for fp32, 16 for INT4 g32. INT4 g64 needs more than the
+// 128 VGPRs a 16-wave workgroup leaves each wave (it spilled 102 to scratch:
+// 307 us/step at SunnyNet-100M B=1) and runs on 8 waves (197 us/step).
+bool wide(int blk) { return blk == 0 || blk == 16 || blk == 64; }
+int threads_for(int blk) { return wide(blk) ? 512 : 1024; }
+const void* kernel_for(int blk) { return wide(blk) ? nt512::kernel_for(blk) : nt1024::kernel_for(blk); }
 }  // namespace
 
 int persist_occupancy(int blk) {
