@@ -237,16 +237,19 @@ constexpr int kRkqU = 64;                  // INT4: inputs per pipeline unit (tw
 constexpr int kRkqNP = 2;                  // producer waves of an INT4 workgroup
 
 // This workgroup's job (uniform selects: no dynamic index into the arguments).
+// The first workgroup of the job is selected in the same pass as the job
+// index: selecting it by index afterwards was folded back into an indexed
+// read of a local copy of start[], which the compiler kept in scratch memory
+// (a store and a dependent load at every launch).
 __device__ __forceinline__ void rkq_job(const RkqMMArgs& A, RkqJob& J, int& u0) {
-    int ji = 0;
+    int ji = 0, j0 = A.start[0];
 #pragma unroll
     for (int i = 1; i < kRkqMaxJobs; ++i)
-        if (i < A.n && (int)blockIdx.x >= A.start[i]) ji = i;
+        if (i < A.n && (int)blockIdx.x >= A.start[i]) { ji = i; j0 = A.start[i]; }
     J = A.j[0];
-    int j0 = A.start[0];
 #pragma unroll
     for (int i = 1; i < kRkqMaxJobs; ++i)
-        if (i == ji) { J = A.j[i]; j0 = A.start[i]; }
+        if (i == ji) J = A.j[i];
     u0 = (int)blockIdx.x - j0;
 }
 
