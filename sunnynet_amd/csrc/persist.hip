@@ -76,7 +76,8 @@ extern "C" int snhip_persist_clk(unsigned long long* out) {
 
 namespace {
 // fp32 and fp16 rows stream more bytes per phase: 8 waves per workgroup
-// measured faster for fp32, 16 for INT4 g32. INT4 g64 needs more than the
+// measured faster for fp32 and fp16 (fp16 at SunnyNet-100M B=1: 209 us/step
+// on 8 waves, 222 on 16), 16 for INT4 g32. INT4 g64 needs more than the
 // 128 VGPRs a 16-wave workgroup leaves each wave (it spilled 102 to scratch:
 // 307 us/step at SunnyNet-100M B=1) and runs on 8 waves (197 us/step).
 bool wide(int blk) { return blk == 0 || blk == 16 || blk == 64; }
