@@ -659,7 +659,8 @@ TtPlan tt_plan(const GemmArgs& g) {
     TtPlan p{};
     // Wide products (the LM head) take this path only for up to 16 rows of X
     // (one row block, no padding to 64 rows); measured at vocab 32000:
-    // INT4 B=8 head step 424 -> 405 us, but fp32 B=64 603 -> 661 us.
+    // INT4 B=8 head step 424 -> 405 us, but fp32 B=64 603 -> 661 us and
+    // INT4 B=32 (two row blocks) 428 -> 433 us.
     if (g.M > 64 || g.shift_T != 0 || g.K % TT_CH || (g.N > 8192 && g.M > 16)) return p;
     const int nch = g.K / TT_CH;
     for (int nc : {1, 2, 3, 4, 6}) {
