@@ -89,10 +89,12 @@ snhip_status snhip_prefill_host(SnHipModel* m, const int32_t* tokens, int32_t n,
 
 /* Time-outs. Every wait of the persistent kernels is bounded; a call whose
  * launch timed out returns SNHIP_E_DEVICE once its work has finished (calls
- * that run a persistent kernel wait for it). A single-sequence call leaves the
- * state as it was. A batched step may have written some layers' state: the
- * handle then refuses every stepping call (SNHIP_E_DEVICE) until snhip_reset or
- * snhip_set_state_dev gives it a valid state. */
+ * that run a persistent kernel wait for it). The workgroups of a launch stop
+ * independently, so a timed-out call may have written part of the state of the
+ * sequences it stepped (some channels of sequence 0 in a single-sequence call,
+ * some layers in a batched step): the handle then refuses every stepping call
+ * (SNHIP_E_DEVICE) until snhip_reset, or snhip_set_state_dev over at least
+ * those sequences, gives them a valid state. */
 
 /* Stream for all later work of this handle (NULL = the null stream). */
 snhip_status snhip_set_stream(SnHipModel* m, void* stream);
@@ -113,6 +115,15 @@ snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, f
  * NULL, receives the last token's logits (the sn_prefill contract). */
 snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                      int32_t T, float* logits_dev);
+
+/* The same chunked prefill with the logits of every position: logits_all_dev
+ * (B, T, vocab) fp32 on the device, row (b, t) at offset (b T + t) vocab,
+ * computed by the tied head over the final norm of each position (MFMA GEMM).
+ * Replaces SunnyNet.forward(idx, state, return_state=True)
+ * (sunnynet/model.py:89-111), which returns (B, T, V) logits and the state:
+ * the state is left in the handle (snhip_get_state_dev; history newest first). */
+snhip_status snhip_prefill_all_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                   int32_t T, float* logits_all_dev);
 
 /* Greedy decoding on the device: feeds tokens_dev (B), then repeatedly takes
  * the first maximal logit as the next token, for n_steps steps. out_tokens_dev

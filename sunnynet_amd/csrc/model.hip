@@ -603,8 +603,10 @@ struct SnHipModel {
     unsigned* h_err = nullptr;            // pinned copies of the time-out flags: [0] perr, [1] berr
     unsigned persist_spin = 1u << 22;     // poll limit (SNHIP_PERSIST_SPIN)
     unsigned persist_stall = 0;           // SNHIP_PERSIST_STALL: forces time-outs (tests), read per call
-    // A batched persistent step timed out after some layers had written their
-    // state: every stepping call fails until snhip_reset or snhip_set_state_dev.
+    // A persistent step timed out after some workgroups had written their part
+    // of the state: sequences [0, poisoned) may be part-stepped, and every
+    // stepping call fails until snhip_reset, or snhip_set_state_dev over at
+    // least that many sequences, gives them a valid state.
     int poisoned = 0;
     // Persistent batched step (batch.hip) for batches of gemm_min_batch ..
     // batch_max sequences: grid size, 0 when the shape or device does not allow it.
@@ -1318,29 +1320,27 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
     return enqueue_head(m, B, m->x, logits_out, greedy, st);
 }
 
-// After a synchronization: did a persistent launch time out at a barrier? A
-// batched step that timed out may have written some layers' state: the handle
-// is then refused for stepping until its state is reset or set.
-snhip_status persist_status(SnHipModel* m) {
-    if (m->h_err && m->h_err[0]) {
-        m->h_err[0] = 0;
-        set_last_error("persistent decode: exchange wait timed out");
-        return SNHIP_E_DEVICE;
-    }
-    if (m->h_err && m->h_err[1]) {
-        m->h_err[1] = 0;
-        m->poisoned = 1;
-        set_last_error("batched persistent decode: a dataflow wait timed out");
-        return SNHIP_E_DEVICE;
-    }
-    return SNHIP_OK;
+// After a synchronization: did a persistent launch over sequences [0, rows)
+// time out at a wait? Its workgroups stop independently: one that passed its
+// last wait before another timed out has already written its channels' state
+// (single sequence) or its layers' state (batched). Those rows are then
+// refused for stepping until their state is reset or set.
+snhip_status persist_status(SnHipModel* m, int rows) {
+    const bool single = m->h_err && m->h_err[0];
+    const bool batched = m->h_err && m->h_err[1];
+    if (!single && !batched) return SNHIP_OK;
+    m->h_err[0] = m->h_err[1] = 0;
+    m->poisoned = std::max(m->poisoned, rows);
+    set_last_error(single ? "persistent decode: exchange wait timed out"
+                          : "batched persistent decode: a dataflow wait timed out");
+    return SNHIP_E_DEVICE;
 }
 
 // Stepping calls refuse a handle whose state a timed-out step left part-written.
 snhip_status check_usable(const SnHipModel* m) {
     if (m->poisoned) {
-        set_last_error("the sequence state was left part-stepped by a timed-out batched step; "
-                       "call snhip_reset or snhip_set_state_dev first");
+        set_last_error("the sequence state was left part-stepped by a timed-out step; "
+                       "call snhip_reset, or snhip_set_state_dev over every sequence it stepped, first");
         return SNHIP_E_DEVICE;
     }
     return SNHIP_OK;
@@ -1370,7 +1370,7 @@ snhip_status run_steps(SnHipModel* m, int B, float* logits_out, bool greedy, int
             // barrier time-out is reported by this call, not a later one.
             SNHIP_CHECK(hipMemcpyAsync(m->h_err + 1, m->berr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
             SNHIP_CHECK(hipStreamSynchronize(m->work));
-            const snhip_status st = persist_status(m);
+            const snhip_status st = persist_status(m, B);
             if (st != SNHIP_OK) return st;
         }
     } else {
@@ -1452,9 +1452,12 @@ snhip_status ensure_prefill_ws(SnHipModel* m, int chunk) {
 
 // One chunk of Tc tokens for sequences [0, B), all layers, carrying s and
 // hist. Tokens already in m->pf_tok (B x Tc). If logits_out, also the last
-// token's logits.
+// token's logits. If all_logits, the logits of every token of the chunk go to
+// all_logits (B, T, vocab) at positions [c0, c0 + Tc) of each sequence (the
+// reference's forward, model.py:89-111, returns them for every position).
 snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_out,
-                                   hipStream_t st) {
+                                   hipStream_t st, float* all_logits = nullptr, int T = 0,
+                                   int c0 = 0) {
     const int D = m->D, I = m->I, R = m->R, L = m->L;
     const long rows = (long)B * Tc;
     const size_t sbs = (size_t)L * D;
@@ -1509,6 +1512,24 @@ snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_o
         hipLaunchKernelGGL(k_copy_rows, dim3(B), dim3(256), 0, st, m->pf_send, (long)D, s_l,
                            (long)sbs, D);
     }
+    if (all_logits) {
+        // Final norm of every row into pf_raw (free once the layers are done),
+        // then the tied head over those rows. Chunk rows are (b, t) with t
+        // fastest, so one product covers every sequence when the chunk is the
+        // whole prompt; otherwise each sequence's Tc rows are one product.
+        launch_ln((int)rows, m->pf_x, D, m->no_g, m->no_c, m->pf_raw, D, D, m->eps, st);
+        const size_t V = (size_t)m->vocab;
+        if (Tc == T) {
+            if ((rc = run_gemm(m, gemm_for(m, m->head, m->pf_raw, D, (int)rows, all_logits, (long)V), st)) != SNHIP_OK)
+                return rc;
+        } else {
+            for (int b = 0; b < B; ++b) {
+                GemmArgs gh = gemm_for(m, m->head, m->pf_raw + (size_t)b * Tc * D, D, Tc,
+                                       all_logits + ((size_t)b * T + c0) * V, (long)V);
+                if ((rc = run_gemm(m, gh, st)) != SNHIP_OK) return rc;
+            }
+        }
+    }
     if (logits_out) {
         hipLaunchKernelGGL(k_last_rows, dim3(B), dim3(256), 0, st, m->pf_x, m->x, Tc, D);
         if ((rc = enqueue_head(m, B, m->x, logits_out, false, st)) != SNHIP_OK) return rc;
@@ -1517,9 +1538,11 @@ snhip_status enqueue_prefill_chunk(SnHipModel* m, int B, int Tc, float* logits_o
     return SNHIP_OK;
 }
 
-// Chunked prefill of tokens (B, T) (row-major, device) from the current state.
+// Chunked prefill of tokens (B, T) (row-major, device) from the current state;
+// logits_out (B, vocab) gets the last token's logits, all_logits (B, T, vocab)
+// every token's (either may be NULL).
 snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
-                         float* logits_out) {
+                         float* logits_out, float* all_logits = nullptr) {
     if (!m->gemm_ok || m->D % 64) {
         set_last_error("chunked prefill needs dim % 64 == 0 and dim, inner, rank % 32 == 0");
         return SNHIP_E_UNSUPPORTED;
@@ -1538,7 +1561,8 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
         SNHIP_CHECK(hipMemcpy2DAsync(m->pf_tok, (size_t)Tc * sizeof(int32_t), tokens_dev + c0,
                                      (size_t)T * sizeof(int32_t), (size_t)Tc * sizeof(int32_t), B,
                                      hipMemcpyDeviceToDevice, m->work));
-        rc = enqueue_prefill_chunk(m, B, Tc, c0 + Tc >= T ? logits_out : nullptr, m->work);
+        rc = enqueue_prefill_chunk(m, B, Tc, c0 + Tc >= T ? logits_out : nullptr, m->work,
+                                   all_logits, T, c0);
         if (rc != SNHIP_OK) return rc;
     }
     SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
@@ -1552,8 +1576,9 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
 // otherwise n_steps must be 1. logits (device), if not NULL, gets the last
 // step's logits.
 // The call returns once the launches have finished and reports an exchange
-// time-out as SNHIP_E_DEVICE (the handle's state is then unchanged: the kernel
-// writes it back only after its last step). *launch_failed is set when the
+// time-out as SNHIP_E_DEVICE. Each workgroup writes its channels' state back
+// after its own last wait, so a time-out can leave sequence 0 part-stepped:
+// the handle then refuses steps until reset or set. *launch_failed is set when the
 // first cooperative launch could not be queued at all (nothing ran).
 snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_tok,
                          float* logits, bool* launch_failed) {
@@ -1593,7 +1618,7 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
     SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
     SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
     SNHIP_CHECK(hipStreamSynchronize(m->work));
-    return persist_status(m);
+    return persist_status(m, 1);
 }
 
 // One step of sequence 0 (tokens already in m->tok): the persistent kernel
@@ -1742,6 +1767,14 @@ snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, i
     return run_prefill(m, tokens_dev, B, T, logits_dev);
 }
 
+snhip_status snhip_prefill_all_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
+                                   int32_t T, float* logits_all_dev) {
+    if (!m || !tokens_dev || !logits_all_dev || B <= 0 || B > m->max_batch || T <= 0)
+        return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
+    return run_prefill(m, tokens_dev, B, T, nullptr, logits_all_dev);
+}
+
 snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                      int32_t n_steps, int32_t* out_tokens_dev,
                                      float* logits_dev) {
@@ -1806,7 +1839,7 @@ snhip_status snhip_set_state_dev(SnHipModel* m, const float* s_dev, const float*
     if (m->kh)
         SNHIP_CHECK(hipMemcpyAsync(m->hist, hist_dev, (size_t)B * m->L * m->kh * m->D * sizeof(float),
                                    hipMemcpyDeviceToDevice, m->stream));
-    m->poisoned = 0;
+    if (B >= m->poisoned) m->poisoned = 0;
     return SNHIP_OK;
 }
 

@@ -14,6 +14,36 @@
 //
 // The table entries are derived, not copied: T[i] = bits(2^(i/32)) - (i << 47),
 // with 2^(i/32) the correctly rounded double.
+//
+// Notices of the works whose published constants and steps are restated here:
+//
+// expf: ARM optimized-routines (math/expf.c, math/exp2f_data.c), as carried
+// by glibc (sysdeps/ieee754/flt-32/e_expf.c).
+//   Copyright (c) 2017-2018, Arm Limited.
+//   SPDX-License-Identifier: MIT
+//   Permission is hereby granted, free of charge, to any person obtaining a
+//   copy of this software and associated documentation files (the
+//   "Software"), to deal in the Software without restriction, including
+//   without limitation the rights to use, copy, modify, merge, publish,
+//   distribute, sublicense, and/or sell copies of the Software, and to permit
+//   persons to whom the Software is furnished to do so, subject to the
+//   following conditions: The above copyright notice and this permission
+//   notice shall be included in all copies or substantial portions of the
+//   Software. THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND,
+//   EXPRESS OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF
+//   MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN
+//   NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM,
+//   DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR
+//   OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE
+//   USE OR OTHER DEALINGS IN THE SOFTWARE.
+//
+// expm1f / tanhf: fdlibm (s_expm1.c, s_tanh.c; float forms s_expm1f.c,
+// s_tanhf.c, conversion to float by Ian Lance Taylor, Cygnus Support).
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//   Developed at SunPro, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice
+//   is preserved.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -12,10 +12,11 @@ group ``block`` (INT4 quantized at load in the reference's quant.c format),
 round trips, and ``get_state`` / ``set_state`` in the torch ``SunnyState``
 layout (s (B,L,D), hist (B,L,K-1,D), newest entry first).
 
-``HipSunnyNet`` puts the torch backend's step contract on a handle:
-``init_state(B)`` and ``forward_step(idx_t, state) -> (logits, SunnyState)``
-(sunnynet/model.py:82-87, 113-124), so a sequence can move between the torch
-path and this one mid-stream.
+``HipSunnyNet`` puts the torch backend's contract on a handle:
+``init_state(B)``, ``forward(idx, state, return_state)`` with every
+position's logits and ``forward_step(idx_t, state) -> (logits, SunnyState)``
+(sunnynet/model.py:82-124), so a sequence can move between the torch path and
+this one mid-stream.
 """
 from __future__ import annotations
 
@@ -144,6 +145,19 @@ class HipModel:
                       "snhip_prefill_batch_dev")
         return out
 
+    def prefill_all(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Chunked prefill of tokens (B, T) from the current state, returning
+        the logits of every position, (B, T, vocab) on the device (the
+        reference's ``SunnyNet.forward``, sunnynet/model.py:89-111); the state
+        after the last token stays in the handle."""
+        B, T = (int(x) for x in tokens.shape)
+        tokens = tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        out = torch.empty(B, T, self.vocab, device=self.device)
+        self._bind_stream()
+        _native.check(self._lib.snhip_prefill_all_dev(self._h, tokens.data_ptr(), B, T,
+                                                      out.data_ptr()), "snhip_prefill_all_dev")
+        return out
+
     def decode_greedy(self, tokens: torch.Tensor, n_steps: int, logits: torch.Tensor | None = None):
         """Greedy decoding on the device; returns (n_steps, B) int32 tokens."""
         B = int(tokens.shape[0])
@@ -241,6 +255,33 @@ class HipSunnyNet:
         dev = device if device is not None else h.device
         return SunnyState(torch.zeros(batch, h.layers, h.dim, device=dev, dtype=dtype),
                           torch.zeros(batch, h.layers, h.kh, h.dim, device=dev, dtype=dtype))
+
+    @torch.no_grad()
+    def forward(self, idx: torch.Tensor, state: SunnyState | None = None,
+                return_state: bool = False):
+        """model.py:89-111: idx (B, T) -> logits (B, T, V) for every position,
+        and with ``return_state`` the state after the last token. As in the
+        reference's ``forward``, the history of ``state`` and of the returned
+        state is oldest entry first (layers.py:266; ``forward_step`` uses
+        newest first). The history carried in follows stepping: for T below
+        taps - 1 the older entries of ``state.hist`` stay in the window
+        (the reference's ``forward`` restarts it from zeros there,
+        layers.py:264-266); both agree from a zero state and for longer
+        prompts."""
+        h = self.handle
+        B = int(idx.shape[0])
+        if B > h.max_batch:
+            raise ValueError(f"batch {B} exceeds the handle's max_batch {h.max_batch}")
+        if state is None:
+            state = self.init_state(B)
+        elif state.s.shape[0] != B or state.hist.shape[0] != B:
+            raise ValueError("state batch does not match idx")
+        h.set_state(state.s, torch.flip(state.hist, dims=[-2]))
+        logits = h.prefill_all(idx)
+        if not return_state:
+            return logits
+        s, hist = h.get_state(B)
+        return logits, SunnyState(s, torch.flip(hist, dims=[-2]).contiguous())
 
     @torch.no_grad()
     def forward_step(self, idx_t: torch.Tensor, state: SunnyState):

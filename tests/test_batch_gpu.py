@@ -149,7 +149,10 @@ def test_batched_barrier_timeout_reports_error(gpu, small, monkeypatch):
     monkeypatch.delenv("SNHIP_PERSIST_STALL")
     s, h = (torch.zeros(B, SMALL.layers, SMALL.dim, device=gpu),
             torch.zeros(B, SMALL.layers, SMALL.taps - 1, SMALL.dim, device=gpu))
-    hm.set_state(s, h)     # a valid state also clears the refusal
+    hm.set_state(s[:1], h[:1])   # sequences 1..B-1 may still be part-stepped
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm.step_batch_host(toks)
+    hm.set_state(s, h)     # a valid state over every stepped sequence clears the refusal
     a = hm.step_batch_host(toks)
     assert np.abs(a - oracle.SnOracle(buf, batch=B).step(toks)).max() < TOL
     monkeypatch.delenv("SNHIP_PERSIST_SPIN")

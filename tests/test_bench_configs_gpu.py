@@ -6,9 +6,10 @@ instantiations and chain lengths:
 * fp32 B=1: chunked prefill of T=1024 tokens, then 256 greedy steps in one
   persistent launch (the whole chain's tokens and the last logits);
 * INT4 g32 B=1: T=2048 prefill, then 256 greedy steps;
-* INT4 g32 B=8 and B=32: the persistent batched step (k_decode_batch at
-  the 100M product depths with INT4 g32 weights), sampled sequences;
-* fp32 B=64: T=1024 prefill then greedy steps, sampled sequences;
+* INT4 g32 B=8 and B=32: T=2048 prefill, then 256 greedy steps of the
+  persistent batched step (k_decode_batch at the 100M product depths with
+  INT4 g32 weights), three sampled sequences replayed on the reference;
+* fp32 B=64: T=1024 prefill then 256 greedy steps, three sampled sequences;
 * every batch size 1..64, INT4 and fp32, one step each (every decode path
   and row-block count the batch size selects).
 
@@ -105,11 +106,13 @@ def test_int4_b1_prefill_2048_then_256_greedy(gpu, blobs):
     _check_b1_chain(gpu, p4, pdq, 2048, "int4", 2048)
 
 
-@pytest.mark.parametrize("weights,B,T,n", [("int4", 8, 64, 32), ("int4", 32, 64, 32),
-                                            ("fp32", 64, 1024, 16)])
+@pytest.mark.parametrize("weights,B,T,n", [("int4", 8, 2048, 256), ("int4", 32, 2048, 256),
+                                            ("fp32", 64, 1024, 256)])
 def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
-    """All B sequences prefill and decode greedily on the device; three of
-    them are replayed on reference handles, token for token."""
+    """The benchmark's batched chains at full length: all B sequences prefill
+    T tokens and decode n greedy steps on the device in one call; three of
+    them are replayed on reference handles (sn_prefill, then sn_step), token
+    for token, with the last logits within 2e-5."""
     p32, p4, pdq = blobs
     path, ref_path = (p4, pdq) if weights == "int4" else (p32, p32)
     prompts = np.random.default_rng(B * 7 + T).integers(0, CFG.vocab_size, (B, T)).astype(np.int32)

@@ -164,27 +164,32 @@ def test_100m_fp32_and_int4(gpu, tmp_path_factory):
 def test_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
     """A barrier target the host raised out of reach: every workgroup gives up
     after its poll limit and leaves the kernel, and the call reports the error
-    (device-tensor step, greedy decoding and host step alike). The kernel
-    writes the state back only after its last step, so the same handle
-    continues from an untouched state once the target is normal again."""
+    (device-tensor step, greedy decoding and host step alike). Workgroups stop
+    independently and write their channels' state back after their own last
+    wait, so a timed-out call may leave sequence 0 part-stepped: the handle
+    then refuses every stepping call until a state is set (or reset), after
+    which it continues from that state as the oracle does."""
     w, buf, path = tiny
     monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
     hm = _model(path, TINY)
     assert hm.persistent_grid > 0
-    t = torch.tensor([3], dtype=torch.int32, device=gpu)
-    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
-    print("persistent time-out: device step, greedy, host step", flush=True)
-    with pytest.raises(RuntimeError, match="timed out"):
-        hm.step_batch(t)
-    with pytest.raises(RuntimeError, match="timed out"):
-        hm.decode_greedy(t, 4)
-    with pytest.raises(RuntimeError, match="timed out"):
-        hm.step_batch_host([3])
-    with pytest.raises(RuntimeError, match="timed out"):
-        hm.step(3)
-    monkeypatch.delenv("SNHIP_PERSIST_STALL")
-    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
     orc = oracle.SnOracle(buf)
+    t = torch.tensor([3], dtype=torch.int32, device=gpu)
+    a = hm.step_batch(t).cpu().numpy()[0]          # a non-zero state to restore later
+    assert np.abs(a - orc.step([3])[0]).max() < TOL
+    saved = [x.clone() for x in hm.get_state(1)]
+    print("persistent time-out: device step, greedy, host step", flush=True)
+    calls = [lambda: hm.step_batch(t), lambda: hm.decode_greedy(t, 4),
+             lambda: hm.step_batch_host([3]), lambda: hm.step(3)]
+    for call in calls:
+        monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+        with pytest.raises(RuntimeError, match="timed out"):
+            call()
+        monkeypatch.delenv("SNHIP_PERSIST_STALL")
+        with pytest.raises(RuntimeError, match="part-stepped"):
+            call()
+        hm.set_state(*saved)
+    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
     a = hm.step_batch(t).cpu().numpy()[0]
     assert np.abs(a - orc.step([3])[0]).max() < TOL
     b = np.asarray(hm.step(5), np.float32)

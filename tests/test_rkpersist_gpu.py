@@ -148,6 +148,47 @@ def test_persist_cfg4_greedy_chain(gpu, cfg4):
         cur = nxt
 
 
+def test_persist_cfg4_bench_chain(gpu, cfg4, tmp_path, ref_built):
+    """The benchmark's B=1 chain at full length: a 512-token random prompt
+    stepped one token per call, then 128 greedy steps in one launch, on one
+    INT4 g32 handle. The reference's own sn_rk_step (oracle/_ref, built from
+    rwkv7.c) runs the same chain on the blob of the dequantized weights: every
+    greedy token equal, the prompt's last logits and the chain's last logits
+    within 2e-5 (rwkv7.c:349-360)."""
+    p, ob = cfg4
+    rp = tmp_path / "cfg4_dq32.bin"
+    rp.write_bytes(ob)
+    ref = oracle.RefRk(rp, RWKV_CFG4.vocab)
+    hm = HipRwkv7(p, weights="int4", block=32)
+    assert hm.persist_grid > 0
+    prompt = np.random.default_rng(512).integers(0, RWKV_CFG4.vocab, 512).astype(np.int32)
+    lg = torch.empty(1, RWKV_CFG4.vocab, device="cuda")
+    print("rwkv7 cfg4 B=1: 512-token prompt on the device", flush=True)
+    for t in prompt:
+        hm.step_batch(torch.tensor([int(t)], dtype=torch.int32, device="cuda"), out=lg)
+    lg0 = lg.cpu().numpy()[0]
+    print("rwkv7 cfg4 B=1: 512-token prompt on the reference", flush=True)
+    for t in prompt:
+        r0 = ref.step(int(t))
+    d0 = float(np.abs(lg0 - r0).max())
+    print(f"rwkv7 cfg4 B=1 prompt: last |dlogit| {d0:.3g}", flush=True)
+    assert d0 < TOL and lg0.argmax() == r0.argmax()
+    n = 128
+    last = torch.empty(1, RWKV_CFG4.vocab, device="cuda")
+    toks = hm.decode_greedy(torch.tensor([int(lg0.argmax())], dtype=torch.int32, device="cuda"),
+                            n, logits=last).cpu().numpy()[:, 0]
+    tok, rl = int(r0.argmax()), None
+    for i in range(n):
+        rl = ref.step(tok)
+        tok = int(rl.argmax())
+        assert toks[i] == tok, f"greedy chain diverges at step {i}"
+    d1 = float(np.abs(last.cpu().numpy()[0] - rl).max())
+    print(f"rwkv7 cfg4 B=1 {n} greedy steps: tokens equal, last |dlogit| {d1:.3g}", flush=True)
+    assert d1 < TOL
+    hm.close()
+    ref.close()
+
+
 def test_persist_barrier_timeout_reports_error(gpu, tiny, monkeypatch):
     """Every exchange wait is given a target the host raised out of reach: each
     workgroup gives up after its poll limit and leaves the kernel and the call
