@@ -62,6 +62,15 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE, each scaled by the counter's reading for a plain copy of known
 # size (FETCH x2.0, WRITE x1.0): profiles/scan_gated_B16_D2048_T4096.md.
 SCAN_TRAFFIC_BYTES = 1_611_150_336
+# HBM bytes per decode step, by (weights, B), from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE over the dispatches of one greedy call of `bench.py --pmc-probe
+# decode`, calibrated like the scan's and divided by the call's steps. Filled
+# from the tables of profiles/decode_pmc_traffic.md.
+DECODE_TRAFFIC: dict = {
+    ("int4", 1): 96_539_322, ("int4", 8): 95_639_327, ("int4", 32): 174_584_418,
+    ("fp32", 1): 517_471_757, ("fp32", 64): 627_485_222, ("fp16", 1): 285_549_635,
+    ("small", 1): 1_385_494, ("rwkv7", 1): 153_234_910, ("rwkv7", 64): 843_917_140,
+}
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
 
 
@@ -117,15 +126,21 @@ def bench_scan(steps: int, warmup: int, cpu: bool):
         runtime.scan(da, db, d0, gated=True)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    # The timed region: K scans back to back, nothing else on the stream.
+    # The timed region: K scans back to back, nothing else on the stream,
+    # bracketed by HIP events on the kernel's stream (the launches' average
+    # duration behind the roofline figure) inside the host wall clock.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     for _ in range(steps):
         runtime.scan(da, db, d0, gated=True)
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # Then K more, each between two HIP events on the kernel's stream, for
-    # the per-launch duration behind the roofline figure.
+    avg_ms = ev0.elapsed_time(ev1) / steps
+    # Then K more, each alone between two HIP events (each launch then also
+    # pays the event records around it): the spread of single launches.
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
     for e0, e1 in evs:
@@ -136,10 +151,9 @@ def bench_scan(steps: int, warmup: int, cpu: bool):
     kern_ms = [e0.elapsed_time(e1) for e0, e1 in evs]
     nbytes = scan_bytes(B, T, D)
     value = nbytes * steps / wall / 1e9
-    avg_ms = float(np.mean(kern_ms))
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
-    log(f"[bench] scan: wall {wall*1e3/steps:.3f} ms/step, kernel avg {avg_ms*1e3:.1f} us "
-        f"(min {min(kern_ms)*1e3:.1f}), {achieved:.1f} GB/s")
+    log(f"[bench] scan: wall {wall*1e3/steps:.3f} ms/step, timed-region events {avg_ms*1e3:.1f} us/launch, "
+        f"{achieved:.1f} GB/s; single launches avg {np.mean(kern_ms)*1e3:.1f} (min {min(kern_ms)*1e3:.1f}) us")
     res = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -151,7 +165,8 @@ def bench_scan(steps: int, warmup: int, cpu: bool):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": SCAN_TRAFFIC_BYTES, "kernel": "k_recur_scan_buf",
-                     "kernel_avg_us": round(avg_ms * 1e3, 2)},
+                     "kernel_avg_us": round(avg_ms * 1e3, 2),
+                     "single_launch_avg_us": round(float(np.mean(kern_ms)) * 1e3, 2)},
     }
     if cpu:
         res["cpu_baseline"] = cpu_scan_baseline(a, b, s0)
@@ -336,22 +351,48 @@ def decode_step_bytes(cfg, fmt: str, B: int) -> int:
 FP32_MFMA_TFLOPS = 157.3
 
 
-def decode_roofline(cfg, fmt: str, B: int, us_per_step: float, kernel: str) -> dict:
-    """Roofline of a decode step from its measured time: HBM for the
-    weight-streaming cases, fp32 MFMA (2 flops per weight per sequence) for
-    fp32 B >= 64 and INT4 B >= 32, where the products are dense contractions."""
-    nbytes = decode_step_bytes(cfg, fmt, B)
-    flops = 2 * matmul_params(cfg) * B
+def step_roofline(nbytes: int, flops: int, us_per_step: float, kernel: str, traffic) -> dict:
+    """Roofline of a decode step from its measured time, against whichever
+    floor is higher: its algorithmic HBM bytes at 8 TB/s or its fp32 matrix
+    flops at the fp32 MFMA peak (the products run as fp32 MFMA or FMA on
+    dequantized weights). The other floor's fraction is kept beside it.
+    ``traffic``: HBM bytes per step measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated), or None."""
     sec = us_per_step * 1e-6
-    if (fmt == "fp32" and B >= 64) or (fmt == "int4" and B >= 32):
-        ach = flops / sec / 1e12
-        return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP32_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / FP32_MFMA_TFLOPS, 4), "traffic": None,
-                "kernel": kernel, "flops_per_step": flops, "bytes_per_step": nbytes}
-    ach = nbytes / sec / 1e9
-    return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
-            "bytes_per_step": nbytes, "flops_per_step": flops}
+    hbm_floor_us = nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
+    mfma_floor_us = flops / (FP32_MFMA_TFLOPS * 1e12) * 1e6
+    gbs = nbytes / sec / 1e9
+    tfs = flops / sec / 1e12
+    if mfma_floor_us > hbm_floor_us:
+        return {"bound": "mfma", "achieved": round(tfs, 2), "peak": FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tfs / FP32_MFMA_TFLOPS, 4), "traffic": traffic,
+                "kernel": kernel, "flops_per_step": flops, "bytes_per_step": nbytes,
+                "floor_us": round(mfma_floor_us, 2), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
+            "bytes_per_step": nbytes, "flops_per_step": flops, "floor_us": round(hbm_floor_us, 2),
+            "mfma_frac": round(tfs / FP32_MFMA_TFLOPS, 4)}
+
+
+def decode_roofline(cfg, fmt: str, B: int, us_per_step: float, kernel: str, traffic=None) -> dict:
+    """SunnyNet decode step: 2 flops per matrix weight per sequence."""
+    return step_roofline(decode_step_bytes(cfg, fmt, B), 2 * matmul_params(cfg) * B, us_per_step,
+                         kernel, traffic)
+
+
+def rwkv7_step_bytes(cfg, B: int) -> int:
+    """Algorithmic HBM bytes of one RWKV-7 INT4 g32 decode step: the weights
+    (0.5 B per weight and an fp32 scale per 32), and per sequence the 64 x 64
+    head states read and written."""
+    n = cfg.matmul_params()
+    return n // 2 + (n // 32) * 4 + B * 2 * cfg.layers * cfg.n_head * cfg.head_size ** 2 * 4
+
+
+def rwkv7_step_flops(cfg, B: int) -> int:
+    """Matrix flops of one RWKV-7 decode step: 2 per matrix weight per
+    sequence, plus the head-state update and read-out (about 6 flops per state
+    entry: decay, rank-1 removal, k v write, S r) per sequence."""
+    return 2 * cfg.matmul_params() * B + 6 * B * cfg.layers * cfg.n_head * cfg.head_size ** 2
 
 
 def _time_ms(fn):
@@ -408,7 +449,7 @@ def bench_decode_small(cpu: bool):
     case = {"workload": "SunnyNet small B=1 fp32: prefill 256 then 64 greedy steps",
             "prefill_ms": round(pms, 3), "us_per_step": round(us, 2), "tok_s": round(1e3 / ms, 1),
             "roofline": decode_roofline(cfg, "fp32", 1, us, "k_decode_persist<0>" if grid else
-                                        "per-kernel step")}
+                                        "per-kernel step", DECODE_TRAFFIC.get(("small", 1)))}
     case["roofline"]["bound"] = "latency"
     case["roofline"]["note"] = ("launch- and latency-bound: the step's 9.96 MB of weights stay in "
                                 "L2/MALL; frac is against the HBM peak")
@@ -494,7 +535,8 @@ def bench_decode(cpu: bool):
             case = {"weights": fmt, "B": B, "prefill_T": T, "prefill_ms": round(pms, 2),
                     "prefill_tok_s": round(B * T / pms * 1e3, 1), "us_per_step": round(us, 2),
                     "tok_s": round(B / ms * 1e3, 1),
-                    "roofline": decode_roofline(cfg, fmt, B, us, kernel)}
+                    "roofline": decode_roofline(cfg, fmt, B, us, kernel,
+                                                DECODE_TRAFFIC.get((fmt, B)))}
             log(f"[bench] decode {fmt} B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s, "
                 f"prefill T={T} {pms:.1f} ms, {case['roofline']['frac']:.4f} of {case['roofline']['bound']}")
             out["cases"].append(case)
@@ -607,9 +649,6 @@ def bench_rwkv7(cpu: bool):
     p32 = os.path.join(tmp, "rk_fp32.bin")
     with open(p32, "wb") as f:
         f.write(pack_rwkv7_blob(w))
-    n = cfg.matmul_params()
-    wbytes = n // 2 + (n // 32) * 4
-    sbytes = 2 * cfg.layers * cfg.n_head * cfg.head_size ** 2 * 4     # state read + write
     out = {"model": "RWKV-7 L=12 D=768 H=12x64 F=3072 V=65536 ranks (64,64,32,128), INT4 g32",
            "steps": 128, "prompt": 512, "cases": []}
     g = torch.Generator(device="cpu").manual_seed(321)
@@ -627,15 +666,11 @@ def bench_rwkv7(cpu: bool):
         kernel = ("k_rk_persist (the whole step)" if hm.persist_grid and B == 1 else
                   "per-kernel step: k_rkq_ln, k_rkq_mm_q4, k_rkq_heads")
         hm.close()
-        nb = wbytes + B * sbytes
-        ach = nb / (ms * 1e-3) / 1e9
+        rl = step_roofline(rwkv7_step_bytes(cfg, B), rwkv7_step_flops(cfg, B), ms * 1e3, kernel,
+                           DECODE_TRAFFIC.get(("rwkv7", B)))
+        rl["note"] = "bytes: weights plus the 64x64 head states read and written per sequence"
         case = {"weights": "int4-g32", "B": B, "us_per_step": round(ms * 1e3, 2),
-                "tok_s": round(B / ms * 1e3, 1),
-                "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                             "kernel": kernel, "bytes_per_step": nb,
-                             "note": "weights, plus the 64x64 head states read and written per "
-                                     "sequence"}}
+                "tok_s": round(B / ms * 1e3, 1), "roofline": rl}
         log(f"[bench] rwkv7 B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s")
         out["cases"].append(case)
     if cpu:
@@ -874,17 +909,26 @@ def profile_sequence(which: str) -> int:
 
 
 def pmc_probe_decode() -> int:
-    """A short fixed sequence for `rocprofv3 --pmc` runs on the decode
-    kernels: 3 plain device copies of a 512 MiB array (calibrating
-    FETCH_SIZE / WRITE_SIZE against a known byte count), then SunnyNet-100M
-    INT4 g32 B=1 (one k_decode_persist launch of 16 greedy steps, twice),
-    fp32 B=64 (4 greedy steps, one k_decode_batch launch each) and RWKV-7
-    INT4 B=1 (one k_rk_persist launch of 16 steps, twice)."""
+    """A fixed sequence for `rocprofv3 --pmc` runs on every decode case. It
+    starts with 3 plain device copies of a 512 MiB array (calibrating
+    FETCH_SIZE / WRITE_SIZE against a known byte count). Then, per case, a
+    handle is built and warmed up, and one measured call runs n greedy steps.
+    Every measured call is bracketed by marker launches of `k_hbm_read2`
+    (snhip_abi_hbm_probe_dev over 4 KiB), so a case's dispatches are the ones
+    between its two markers. The cases, in order, with steps per call:
+    SunnyNet-100M INT4 g32 B=1 (16), B=8 (8), B=32 (8); fp32 B=1 (16), B=64
+    (8); fp16 B=1 (16); SunnyNet small fp32 B=1 (16); RWKV-7 INT4 g32 B=1
+    (16), B=64 (4). Each case's line on stderr names its order, steps and
+    algorithmic bytes per step."""
     import tempfile
 
+    from sunnynet_amd import _native
+    from sunnynet_amd.blob import pack_sunny_blob
+    from sunnynet_amd.config import SMALL
     from sunnynet_amd.runtime.model import HipModel
     from sunnynet_amd.runtime.rwkv7 import HipRwkv7
     from sunnynet_amd.rwkv7 import RWKV_CFG4, init_rwkv7, pack_rwkv7_blob
+    from sunnynet_amd.weights import init_sunnynet
     dev = torch.device("cuda:0")
     x = torch.randn(128 << 20, device=dev)
     y = torch.empty_like(x)
@@ -893,30 +937,61 @@ def pmc_probe_decode() -> int:
     torch.cuda.synchronize()
     log(f"[pmc] copy bytes/launch read {x.numel() * 4} write {x.numel() * 4}")
     del x, y
-    cfg = SUNNY_100M
+    mk = torch.zeros(3, 1024, device=dev)
+    L = _native.lib()
+
+    nmark = 0
+
+    def marker():
+        nonlocal nmark
+        torch.cuda.synchronize()
+        _native.check(L.snhip_abi_hbm_probe_dev(1, mk[0].data_ptr(), mk[1].data_ptr(), mk[2].data_ptr(),
+                                                1024, 1, torch.cuda.current_stream().cuda_stream),
+                      "marker")
+        torch.cuda.synchronize()
+        nmark += 1
+
     tmp = tempfile.mkdtemp(prefix="snhip_pmc_")
     paths = _m100_blobs(tmp)
+    paths["fp16"] = paths["fp32"]
     g = torch.Generator(device="cpu").manual_seed(11)
-    for fmt, B, n in (("int4", 1, 16), ("fp32", 64, 4)):
+    order = 0
+
+    def measured(name, hm, vocab, B, n, nbytes):
+        nonlocal order
+        tok = torch.randint(0, vocab, (B,), generator=g, dtype=torch.int32).to(dev)
+        hm.decode_greedy(tok, n)
+        marker()
+        hm.decode_greedy(tok, n)
+        marker()
+        log(f"[pmc] case {order}: {name}: {n} greedy steps between markers {nmark - 2} and "
+            f"{nmark - 1} (counting from 0); algorithmic bytes/step {nbytes}")
+        order += 1
+
+    marker()
+    cfg = SUNNY_100M
+    for fmt, B, n in (("int4", 1, 16), ("int4", 8, 8), ("int4", 32, 8), ("fp32", 1, 16),
+                      ("fp32", 64, 8), ("fp16", 1, 16)):
         hm = HipModel(paths[fmt], cfg.vocab_size, cfg.dim, cfg.inner, cfg.rank, cfg.taps, cfg.layers,
                       max_batch=B, weights=fmt, block=32)
-        tok = torch.randint(0, cfg.vocab_size, (B,), generator=g, dtype=torch.int32).to(dev)
-        for _ in range(2):
-            hm.decode_greedy(tok, n)
-        torch.cuda.synchronize()
-        log(f"[pmc] SunnyNet-100M {fmt} B={B}: 2 x {n} greedy steps; algorithmic bytes/step "
-            f"{decode_step_bytes(cfg, fmt, B)}")
+        marker()
+        measured(f"SunnyNet-100M {fmt} B={B}", hm, cfg.vocab_size, B, n, decode_step_bytes(cfg, fmt, B))
         hm.close()
+    sc = SMALL
+    ps = _write_blob(tmp, "small.bin", pack_sunny_blob(init_sunnynet(sc, 0)))
+    hm = HipModel(ps, sc.vocab_size, sc.dim, sc.inner, sc.rank, sc.taps, sc.layers)
+    marker()
+    measured("SunnyNet small fp32 B=1", hm, sc.vocab_size, 1, 16, decode_step_bytes(sc, "fp32", 1))
+    hm.close()
     rc = RWKV_CFG4
     path = _write_blob(tmp, "rk.bin", pack_rwkv7_blob(init_rwkv7(rc, 2)))
-    hm = HipRwkv7(path, weights="int4", block=32, max_batch=1)
-    tok = torch.randint(0, rc.vocab, (1,), generator=g, dtype=torch.int32).to(dev)
-    for _ in range(2):
-        hm.decode_greedy(tok, 16)
+    nw = rc.matmul_params()
+    for B, n in ((1, 16), (64, 4)):
+        hm = HipRwkv7(path, weights="int4", block=32, max_batch=B)
+        marker()
+        measured(f"RWKV-7 int4 B={B}", hm, rc.vocab, B, n, rwkv7_step_bytes(rc, B))
+        hm.close()
     torch.cuda.synchronize()
-    n = rc.matmul_params()
-    log(f"[pmc] RWKV-7 int4 B=1: 2 x 16 greedy steps; weight bytes/step {n // 2 + (n // 32) * 4}")
-    hm.close()
     return 0
 
 
