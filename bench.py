@@ -170,8 +170,40 @@ def bench_scan(steps: int, warmup: int, cpu: bool):
     }
     if cpu:
         res["cpu_baseline"] = cpu_scan_baseline(a, b, s0)
+    res["host_pointer_abi"] = bench_scan_host_abi(a, b, s0)
     res["scan_bwd"] = bench_scan_bwd(da, db, d0, steps, warmup, cpu)
     return res
+
+
+def bench_scan_host_abi(a, b, s0, reps: int = 3):
+    """The stable ABI's host-pointer scan (snhip_abi_recur_scan, the entry a
+    caller of the reference's sn_abi_recur_scan binds, sn_abi.c:63-71) on the
+    same host arrays: device buffers, the copies in, the scan and the copies
+    out, PCIe included. A reported figure beside the device-resident
+    headline, never the headline."""
+    from sunnynet_amd import _native
+    L = _native.lib()
+    B, T, N = a.shape
+    out = np.empty_like(a)
+    send = np.empty_like(s0)
+    f = lambda x: x.ctypes.data
+
+    def call():
+        _native.check(L.snhip_abi_recur_scan(f(a), f(b), f(s0), f(out), f(send), B, T, N, 1),
+                      "snhip_abi_recur_scan")
+    call()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nbytes = scan_bytes(B, T, N)
+    log(f"[bench] host-pointer ABI scan: {med*1e3:.1f} ms/call, {nbytes/med/1e9:.1f} GB/s (PCIe included)")
+    return {"entry": "snhip_abi_recur_scan", "ms_per_call": round(med * 1e3, 2),
+            "GB/s": round(nbytes / med / 1e9, 2),
+            "note": f"host numpy arrays in and out (pageable), median of {reps} calls; includes "
+                    "device allocation and the PCIe copies; the headline is device-resident"}
 
 
 def bench_scan_bwd(dp_, dnu_, ds0_, steps, warmup, cpu):
@@ -522,6 +554,30 @@ def bench_decode(cpu: bool):
                 lg = hm.prefill_batch(prompts)
             pms = _time_ms(pre)
             tok = lg.argmax(1).int()
+            # prefill flops: the layers' products for every token (the head
+            # runs on the last token only: 2 V D per sequence)
+            layer_w = matmul_params(cfg) - cfg.vocab_size * cfg.dim
+            pf_flops = 2 * layer_w * B * T + 2 * cfg.vocab_size * cfg.dim * B
+            extra = {}
+            if fmt == "fp32" and B == 64:
+                # the reference's forward: logits at every position (B, T, V)
+                st_s, st_h = hm.get_state(B)
+                hm.reset()
+                lall = None
+
+                def pre_all():
+                    nonlocal lall
+                    lall = hm.prefill_all(prompts)
+                ams = _time_ms(pre_all)
+                all_flops = 2 * matmul_params(cfg) * B * T
+                extra = {"prefill_all_ms": round(ams, 2),
+                         "prefill_all_tflops": round(all_flops / ams / 1e9, 1),
+                         "prefill_all_note": "every position's logits (B, T, V), the head GEMM over "
+                                             "all B T rows included"}
+                del lall
+                hm.set_state(st_s, st_h)
+                log(f"[bench] prefill fp32 B=64 T={T} with every position's logits: {ams:.1f} ms, "
+                    f"{all_flops / ams / 1e9:.1f} TFLOP/s")
             hm.decode_greedy(tok, 8)                    # capture + warm the step graph
             torch.cuda.synchronize()
             n = out["steps"]
@@ -533,7 +589,9 @@ def bench_decode(cpu: bool):
             hm.close()
             us = ms * 1e3
             case = {"weights": fmt, "B": B, "prefill_T": T, "prefill_ms": round(pms, 2),
-                    "prefill_tok_s": round(B * T / pms * 1e3, 1), "us_per_step": round(us, 2),
+                    "prefill_tok_s": round(B * T / pms * 1e3, 1),
+                    "prefill_tflops": round(pf_flops / pms / 1e9, 2), **extra,
+                    "us_per_step": round(us, 2),
                     "tok_s": round(B / ms * 1e3, 1),
                     "roofline": decode_roofline(cfg, fmt, B, us, kernel,
                                                 DECODE_TRAFFIC.get((fmt, B)))}

@@ -116,6 +116,16 @@ snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, f
 snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,
                                      int32_t T, float* logits_dev);
 
+/* sn_dbg_layer (sunnynet/runtime/sunnynet.c:336-345): steps sequence 0 from
+ * the embedding of `token` through layers 0..layer (updating their state and
+ * history, as the reference does) and writes that layer's intermediates to
+ * the HOST buffer dbg of 7 dim + rank + 2 inner floats, in the reference's
+ * order (sunnynet.c:278-289): LN_in output, at (after the conv), v = V at, the
+ * gate half of U v, u (after the competitive gate), the new state, z (after
+ * the wedge), LN_I(z), W_eff s_old and the layer's output. Runs the per-kernel
+ * (GEMV) step. SNHIP_E_INVAL for a token or layer out of range. */
+snhip_status snhip_dbg_layer(SnHipModel* m, int32_t token, int32_t layer, float* dbg);
+
 /* The same chunked prefill with the logits of every position: logits_all_dev
  * (B, T, vocab) fp32 on the device, row (b, t) at offset (b T + t) vocab,
  * computed by the tied head over the final norm of each position (MFMA GEMM).

@@ -91,6 +91,7 @@ _SIGS = {
     "snhip_decode_greedy_dev": (I32, [V, V, I32, I32, V, V]),
     "snhip_prefill_batch_dev": (I32, [V, V, I32, I32, V]),
     "snhip_prefill_all_dev": (I32, [V, V, I32, I32, V]),
+    "snhip_dbg_layer": (I32, [V, I32, I32, V]),
     "snhip_get_state_dev": (I32, [V, V, V, I32]),
     "snhip_set_state_dev": (I32, [V, V, V, I32]),
     # include/snhip_rwkv7.h

@@ -1218,6 +1218,40 @@ snhip_status enqueue_head(SnHipModel* m, int B, const float* x, float* logits_ou
     return SNHIP_OK;
 }
 
+// Layer l of the GEMV step for sequences [0, B), after LN_in + conv wrote
+// m->at: v = V at and sfb = W_eff s_old (one launch), q = U v, the gates and
+// the state update (m->u, s'), z = wedge(W_z u), yn = LN_I(z), and
+// x' = W_c yn + b s' + sfb + x into m->x (sunnynet.c:239-276). Every
+// intermediate stays in its buffer until the next layer (snhip_dbg_layer
+// reads them).
+snhip_status enqueue_layer_gemv(SnHipModel* m, int B, int l, hipStream_t st) {
+    const int D = m->D, I = m->I, R = m->R, L = m->L;
+    const size_t sbs = (size_t)L * D;
+    const Layer& A = m->layers[l];
+    float* s_l = m->s + (size_t)l * D;
+    const long n = (long)B * D;
+    GemvJob jv = make_job(A.V, B, m->at, D, m->v, R);
+    GemvJob js = make_job(A.Ws, B, s_l, (int)sbs, m->sfb, D);
+    SNHIP_CHECK(launch_gemv(m, jv, js, st));
+    GemvJob ju = make_job(A.U, B, m->v, R, m->q, 2 * D);
+    GemvJob none{};
+    SNHIP_CHECK(launch_gemv(m, ju, none, st));
+    hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
+    GemvJob jz = make_job(A.Wz, B, m->u, D, m->z, I);
+    jz.epi = EPI_WEDGE;
+    jz.a_tanh = A.a_tanh;
+    SNHIP_CHECK(launch_gemv(m, jz, none, st));
+    launch_ln(B, m->z, I, A.nm_g, A.nm_c, m->yn, I, I, m->eps, st);
+    GemvJob jc = make_job(A.Wc, B, m->yn, I, m->x, D);
+    jc.epi = EPI_RESID;
+    jc.b_gain = A.b_gain;
+    jc.s = s_l; jc.lds = (int)sbs;
+    jc.sfb = m->sfb; jc.ldf = D;
+    SNHIP_CHECK(launch_gemv(m, jc, none, st));
+    return SNHIP_OK;
+}
+
 // Enqueue one decode step for sequences [0, B) on `st`; tokens in m->tok.
 // greedy: the head also reduces the first maximal logit per sequence and a
 // final kernel writes it to m->tok (the next step's input) and m->tok_hist.
@@ -1296,26 +1330,8 @@ snhip_status enqueue_step(SnHipModel* m, int B, float* logits_out, bool greedy, 
             if ((rc = run_gemm(m, gc, st)) != SNHIP_OK) return rc;
             continue;
         }
-        // v = V at and sfb = W_eff s (old state), one launch.
-        GemvJob jv = make_job(A.V, B, m->at, D, m->v, R);
-        GemvJob js = make_job(A.Ws, B, s_l, (int)sbs, m->sfb, D);
-        SNHIP_CHECK(launch_gemv(m, jv, js, st));
-        GemvJob ju = make_job(A.U, B, m->v, R, m->q, 2 * D);
-        GemvJob none{};
-        SNHIP_CHECK(launch_gemv(m, ju, none, st));
-        hipLaunchKernelGGL(k_compete_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                           m->q, A.delta, s_l, sbs, m->u, B, D, m->clamp, m->p_floor);
-        GemvJob jz = make_job(A.Wz, B, m->u, D, m->z, I);
-        jz.epi = EPI_WEDGE;
-        jz.a_tanh = A.a_tanh;
-        SNHIP_CHECK(launch_gemv(m, jz, none, st));
-        launch_ln(B, m->z, I, A.nm_g, A.nm_c, m->yn, I, I, m->eps, st);
-        GemvJob jc = make_job(A.Wc, B, m->yn, I, m->x, D);
-        jc.epi = EPI_RESID;
-        jc.b_gain = A.b_gain;
-        jc.s = s_l; jc.lds = (int)sbs;
-        jc.sfb = m->sfb; jc.ldf = D;
-        SNHIP_CHECK(launch_gemv(m, jc, none, st));
+        const snhip_status rc = enqueue_layer_gemv(m, B, l, st);
+        if (rc != SNHIP_OK) return rc;
     }
     return enqueue_head(m, B, m->x, logits_out, greedy, st);
 }
@@ -1765,6 +1781,47 @@ snhip_status snhip_prefill_batch_dev(SnHipModel* m, const int32_t* tokens_dev, i
     if (!m || !tokens_dev || B <= 0 || B > m->max_batch || T <= 0) return SNHIP_E_INVAL;
     if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     return run_prefill(m, tokens_dev, B, T, logits_dev);
+}
+
+snhip_status snhip_dbg_layer(SnHipModel* m, int32_t token, int32_t layer, float* dbg) {
+    if (!m || !dbg || layer < 0 || layer >= m->L || token < 0 || token >= m->vocab) return SNHIP_E_INVAL;
+    if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
+    const int D = m->D, I = m->I, R = m->R;
+    const size_t hbs = (size_t)m->L * (m->kh ? m->kh : 1) * D;
+    hipStream_t st = m->work;
+    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
+    SNHIP_CHECK(hipStreamWaitEvent(st, m->ev_in, 0));
+    SNHIP_CHECK(hipMemcpyAsync(m->tok, &token, sizeof(int32_t), hipMemcpyHostToDevice, st));
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, m->tok, m->embed, m->x, D, m->vocab);
+    for (int l = 0; l <= layer; ++l) {
+        const Layer& A = m->layers[l];
+        float* h_l = m->hist + (size_t)l * (m->kh ? m->kh : 1) * D;
+        // the layer's input x is needed for the dump's residual: the GEMV
+        // step adds it in W_c's epilogue, in place
+        launch_ln_conv(1, m->x, A.ni_g, A.ni_c, A.dw, h_l, hbs, m->at, D, m->K, m->eps, st);
+        const snhip_status rc = enqueue_layer_gemv(m, 1, l, st);
+        if (rc != SNHIP_OK) return rc;
+    }
+    // sunnynet.c:278-289: raw, at, v, gate, u, s', z (after the wedge), yn, sfb, out.
+    // q = U v holds its rows in the qrow_u / qrow_g order: the gates are
+    // gathered back to channel order on the host.
+    struct Part { const float* src; int n; };
+    const float* raw = m->K > 1 ? m->hist + (size_t)layer * m->kh * D : m->at;
+    std::vector<float> q(2 * (size_t)D);
+    const Part parts[] = {{raw, D}, {m->at, D}, {m->v, R}, {nullptr, D}, {m->u, D},
+                          {m->s + (size_t)layer * D, D}, {m->z, I}, {m->yn, I}, {m->sfb, D},
+                          {m->x, D}};
+    SNHIP_CHECK(hipMemcpyAsync(q.data(), m->q, q.size() * sizeof(float), hipMemcpyDeviceToHost, st));
+    float* out = dbg;
+    float* gate = nullptr;
+    for (const Part& pt : parts) {
+        if (pt.src) SNHIP_CHECK(hipMemcpyAsync(out, pt.src, (size_t)pt.n * sizeof(float), hipMemcpyDeviceToHost, st));
+        else gate = out;
+        out += pt.n;
+    }
+    SNHIP_CHECK(hipStreamSynchronize(st));
+    for (int i = 0; i < D; ++i) gate[i] = q[qrow_g(i)];
+    return SNHIP_OK;
 }
 
 snhip_status snhip_prefill_all_dev(SnHipModel* m, const int32_t* tokens_dev, int32_t B,

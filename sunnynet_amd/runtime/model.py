@@ -74,6 +74,7 @@ class HipModel:
         self._lib = _native.lib()
         self.device = torch.device(device or "cuda:0")
         self.vocab, self.dim, self.layers, self.taps = vocab, dim, layers, taps
+        self.inner, self.rank = inner, rank
         self.kh = max(0, taps - 1)
         self.max_batch = int(max_batch)
         with torch.cuda.device(self.device):
@@ -156,6 +157,24 @@ class HipModel:
         self._bind_stream()
         _native.check(self._lib.snhip_prefill_all_dev(self._h, tokens.data_ptr(), B, T,
                                                       out.data_ptr()), "snhip_prefill_all_dev")
+        return out
+
+    def dbg_layer(self, token: int, layer: int) -> dict:
+        """sn_dbg_layer (sunnynet/runtime/sunnynet.c:336-345): steps sequence 0
+        from ``token``'s embedding through layers 0..layer (their state
+        advances, as in the reference) and returns that layer's
+        intermediates by name (host float32 arrays)."""
+        D, I, R = self.dim, self.inner, self.rank
+        buf = np.empty(7 * D + R + 2 * I, np.float32)
+        self._bind_stream()
+        _native.check(self._lib.snhip_dbg_layer(self._h, int(token), int(layer), buf.ctypes.data),
+                      "snhip_dbg_layer")
+        names = (("raw", D), ("at", D), ("v", R), ("gate", D), ("u", D), ("s", D), ("zn", I),
+                 ("yn", I), ("sfb", D), ("out", D))
+        out, o = {}, 0
+        for n, k in names:
+            out[n] = buf[o:o + k].copy()
+            o += k
         return out
 
     def decode_greedy(self, tokens: torch.Tensor, n_steps: int, logits: torch.Tensor | None = None):
