@@ -150,10 +150,10 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
  * cooperative launch, or SNHIP_PERSIST=0 in the environment at load). */
 int32_t snhip_persistent_grid(const SnHipModel* m);
 
-/* Grid size of the persistent batched step (steps of 8 to 64 sequences run
+/* Grid size of the persistent batched step (steps of 3 to 64 sequences run
  * every layer in one cooperative launch, then the head), or 0 when this handle
  * uses the per-kernel step for them (shapes other than the compiled product
- * depths, max_batch below 8, no cooperative launch, or SNHIP_BATCH_PERSIST=0
+ * depths, max_batch below 3, no cooperative launch, or SNHIP_BATCH_PERSIST=0
  * in the environment at load). No counterpart in the reference: its C runtime
  * steps one sequence at a time (sunnynet.c:212). */
 int32_t snhip_batch_grid(const SnHipModel* m);

@@ -1,6 +1,6 @@
 // Persistent decode step for a batch of sequences: every layer of one step in
 // one cooperative launch (the batched path of snhip_step_batch_dev /
-// snhip_decode_greedy_dev from 8 sequences up).
+// snhip_decode_greedy_dev from 3 sequences up).
 //
 // The math is the decode step of sunnynet/runtime/sunnynet.c:212-334 for each
 // sequence. Per layer the grid walks through five phases:

@@ -580,7 +580,7 @@ struct SnHipModel {
     bool use_graphs = true;
     // Decode batches of at least this many sequences run their matmuls on the
     // MFMA GEMM; smaller batches use the GEMV kernels.
-    int gemm_min_batch = 8;
+    int gemm_min_batch = 3;
     bool gemm_ok = true;
     float* gemm_work = nullptr;           // split-K partials
     size_t gemm_work_floats = 0;
@@ -595,6 +595,14 @@ struct SnHipModel {
     // Persistent single-sequence decode (persist.hip): grid size, 0 when the
     // model's shape or the device does not allow it.
     int persist_wg = 0;
+    // Multi-sequence persistent decode (INT4 g32, 2..ms_max sequences): grid
+    // size (0: off), exchange words, new-state words and history rings sized
+    // for ms_max sequences.
+    int ms_wg = 0;
+    int ms_max = 0;
+    unsigned long long* ms_ex = nullptr;
+    unsigned long long* ms_sx = nullptr;
+    float* ms_ring = nullptr;
     snhip::PLayer* dlayers = nullptr;     // device copy of the layer table
     unsigned long long* pex = nullptr;    // exchange words (2 x kPersistExWords)
     unsigned long long* psx = nullptr;    // new-state words (L x 2 x D)
@@ -868,6 +876,32 @@ bool host_err(SnHipModel* m) {
     return true;
 }
 
+// Enables the multi-sequence persistent decode for INT4 g32 handles of two or
+// more sequences, used for steps of two (SNHIP_PERSIST_MS=0 turns it off;
+// SNHIP_PERSIST_MS_WG caps the grid). One workgroup per eight channels, as the
+// single-sequence INT4 kernel. SunnyNet-100M INT4 B=2: 278.0 us/step, against
+// 849.7 on the GEMV step; three and more sequences take the batched kernel.
+void setup_persist_ms(SnHipModel* m, int ncu) {
+    if (env_unsigned("SNHIP_PERSIST_MS", 1, 0) == 0) return;
+    if (m->wfmt != SNHIP_WEIGHTS_INT4 || m->block != 32 || m->max_batch < 2) return;
+    const int nmax = std::min(m->max_batch, kPersistMsMax);
+    if (persist_ms_occupancy(nmax) < 1) return;
+    int cap = std::min(m->D / 8, ncu);
+    if (const char* e = getenv("SNHIP_PERSIST_MS_WG")) cap = atoi(e);
+    cap = std::min(cap, ncu);
+    int nwg = 0;
+    for (int g = cap; g >= 1 && !nwg; --g)
+        if (persist_ms_grid_ok(g, m->D, m->I, m->R, m->vocab)) nwg = g;
+    if (nwg < 1) return;
+    const int NS = kPersistMsMax;                       // the kernel's word stride
+    m->ms_ex = dalloc<unsigned long long>(m, 2 * (size_t)kPersistMsExWords);
+    m->ms_sx = dalloc<unsigned long long>(m, (size_t)m->L * 2 * m->D * NS);
+    m->ms_ring = dalloc<float>(m, (size_t)nwg * m->L * m->kh * m->D * NS);
+    if (!m->ms_ex || !m->ms_sx || !m->ms_ring) return;
+    m->ms_max = nmax;
+    m->ms_wg = nwg;
+}
+
 // Enables the persistent single-sequence decode when the shape fits it and the
 // device supports cooperative launches (SNHIP_PERSIST=0 turns it off;
 // SNHIP_PERSIST_WG caps the grid size). The grid is the largest size the
@@ -902,6 +936,7 @@ void setup_persist(SnHipModel* m) {
     m->perr = dalloc<unsigned>(m, 1);
     if (!m->pex || !m->psx || !m->pring || !m->perr || !layer_table(m) || !host_err(m)) return;
     m->persist_wg = nwg;
+    setup_persist_ms(m, ncu);
 }
 
 // Enables the persistent batched step (batch.hip) when the shape fits it and
@@ -1637,6 +1672,69 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
     return persist_status(m, 1);
 }
 
+// n_steps decode steps of sequences [0, B) (2 <= B <= ms_max) in
+// multi-sequence persistent launches on the internal stream, as run_persist:
+// the first tokens in m->tok; greedy: out_tok (n_steps, B) receives each
+// step's tokens; logits (B, vocab, device), if not NULL, the last step's.
+snhip_status run_persist_ms(SnHipModel* m, int B, int n_steps, bool greedy, int32_t* out_tok,
+                            float* logits, bool* launch_failed) {
+    constexpr int kMaxStepsPerLaunch = 1 << 20;
+    const int NS = kPersistMsMax;
+    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
+    SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
+    SNHIP_CHECK(hipMemsetAsync(m->perr, 0, sizeof(unsigned), m->work));
+    PersistArgs a{};
+    a.layers = m->dlayers;
+    a.L = m->L; a.D = m->D; a.I = m->I; a.R = m->R; a.K = m->K; a.kh = m->kh;
+    a.vocab = m->vocab; a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
+    a.embed = m->embed; a.no_g = m->no_g; a.no_c = m->no_c;
+    a.head = pmat(m->head);
+    a.s = m->s; a.hist = m->hist;
+    a.ring = m->ms_ring; a.ex = m->ms_ex; a.sx = m->ms_sx; a.err = m->perr;
+    a.greedy = greedy ? 1 : 0;
+    a.spin_limit = m->persist_spin;
+    a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
+    a.ns = B;
+    (void)NS;
+    for (int done = 0; done < n_steps;) {
+        const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
+        SNHIP_CHECK(hipMemsetAsync(m->ms_ex, 0, 2 * (size_t)kPersistMsExWords * sizeof(unsigned long long), m->work));
+        SNHIP_CHECK(hipMemsetAsync(m->ms_sx, 0, (size_t)m->L * 2 * m->D * NS * sizeof(unsigned long long), m->work));
+        a.tok_in = done == 0 ? m->tok : out_tok + (size_t)(done - 1) * B;
+        a.out_tok = greedy ? out_tok + (size_t)done * B : nullptr;
+        a.logits = done + n == n_steps ? logits : nullptr;
+        a.n_steps = n;
+        const snhip_status rc = launch_decode_persist_ms(a, m->ms_wg, m->work);
+        if (rc != SNHIP_OK) {
+            if (done == 0 && launch_failed) *launch_failed = true;
+            return rc;
+        }
+        done += n;
+    }
+    SNHIP_CHECK(hipMemcpyAsync(m->h_err, m->perr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
+    SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
+    SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
+    SNHIP_CHECK(hipStreamSynchronize(m->work));
+    return persist_status(m, B);
+}
+
+// Does a step of B sequences run as the multi-sequence persistent kernel?
+bool uses_ms(const SnHipModel* m, int B) { return m->ms_wg > 0 && B >= 2 && B <= m->ms_max; }
+
+// One step of sequences [0, B), B >= 2 (tokens in m->tok): the multi-sequence
+// persistent kernel when it takes B, else the per-kernel or batched step. A
+// failed cooperative launch turns the multi-sequence path off and falls back.
+snhip_status step_many(SnHipModel* m, int B, float* logits_out) {
+    if (uses_ms(m, B)) {
+        bool launch_failed = false;
+        const snhip_status rc = run_persist_ms(m, B, 1, false, nullptr, logits_out, &launch_failed);
+        if (!launch_failed) return rc;
+        m->ms_wg = 0;
+        (void)hipGetLastError();
+    }
+    return run_steps(m, B, logits_out, false, 1);
+}
+
 // One step of sequence 0 (tokens already in m->tok): the persistent kernel
 // when enabled, else the captured per-kernel step. A failed cooperative launch
 // turns the persistent path off for this handle and falls back.
@@ -1721,7 +1819,7 @@ snhip_status snhip_step_batch_dev(SnHipModel* m, const int32_t* tokens_dev, int3
     if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     const snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
     if (rc != SNHIP_OK) return rc;
-    return B == 1 ? step_one(m, logits_dev) : run_steps(m, B, logits_dev, false, 1);
+    return B == 1 ? step_one(m, logits_dev) : step_many(m, B, logits_dev);
 }
 
 snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, float* logits) {
@@ -1729,7 +1827,7 @@ snhip_status snhip_step_batch(SnHipModel* m, const int32_t* tokens, int32_t B, f
     if (!tokens_ok(m, tokens, B)) return SNHIP_E_INVAL;
     if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     snhip_status rc = put_tokens(m, tokens, B, hipMemcpyHostToDevice);
-    if (rc == SNHIP_OK) rc = B == 1 ? step_one(m, m->logits) : run_steps(m, B, m->logits, false, 1);
+    if (rc == SNHIP_OK) rc = B == 1 ? step_one(m, m->logits) : step_many(m, B, m->logits);
     if (rc != SNHIP_OK) return rc;
     SNHIP_CHECK(hipMemcpyAsync(logits, m->logits, (size_t)B * m->vocab * sizeof(float),
                                hipMemcpyDeviceToHost, m->stream));
@@ -1845,6 +1943,15 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
         rc = run_persist(m, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
         if (!launch_failed) return rc;
         m->persist_wg = 0;
+        (void)hipGetLastError();
+    }
+    if (uses_ms(m, B)) {
+        snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
+        if (rc != SNHIP_OK) return rc;
+        bool launch_failed = false;
+        rc = run_persist_ms(m, B, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
+        if (!launch_failed) return rc;
+        m->ms_wg = 0;
         (void)hipGetLastError();
     }
     if ((long)n_steps * B > (long)m->hist_cap || !m->tok_hist) {

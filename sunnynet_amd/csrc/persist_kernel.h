@@ -844,6 +844,19 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
     }
 }
 
+#if SNHIP_PERSIST_NT == 512
+#include "persist_ms.h"
+
+// The multi-sequence kernel for up to ns sequences (INT4 g32 rows). Built for
+// two: at three and more the batched kernel measured faster (SunnyNet-100M
+// INT4: B=3 404.6 against 348.0 us/step, B=4 455.4 against 349.8; the
+// eight-sequence form needs more than 256 registers and spills).
+const void* kernel_for_ms(int ns) {
+    (void)ns;
+    return (const void*)k_decode_persist_ms<32, 2>;
+}
+#endif
+
 const void* kernel_for(int blk) {
     return blk == 0 ? (const void*)k_decode_persist<0>
          : blk == 16 ? (const void*)k_decode_persist<16>

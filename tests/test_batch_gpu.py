@@ -1,4 +1,4 @@
-"""The persistent batched step (every layer of a step of 8..64 sequences in one
+"""The persistent batched step (every layer of a step of 3..64 sequences in one
 cooperative launch, each tile waiting on the flags of the tiles it reads)
 against the oracle and the per-kernel step path.
 

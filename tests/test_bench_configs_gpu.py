@@ -139,7 +139,8 @@ def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
 @pytest.mark.parametrize("weights", ["int4", "fp32"])
 def test_every_batch_size_one_step(gpu, blobs, weights):
     """Every batch size 1..64 at the 100M shape (B=1 the persistent step,
-    2..7 the GEMV graph, 8..64 the persistent batched step with one to four
+    2 the two-sequence persistent kernel (INT4) or the GEMV graph (fp32),
+    3..64 the persistent batched step with one to four
     16-row blocks and partial ones): one step from the reset state, the first
     and the last sequence against the reference runtime, within 2e-5 and with
     the same argmax."""

@@ -175,11 +175,12 @@ def test_greedy_decode_on_device(gpu, small):
         cur = nxt
 
 
-@pytest.mark.parametrize("block,B", [(32, 4), (64, 4), (32, 16), (64, 16)])
+@pytest.mark.parametrize("block,B", [(32, 2), (64, 2), (32, 4), (64, 4), (32, 16), (64, 16)])
 def test_int4_matches_dequantized_oracle(gpu, tmp_path_factory, block, B):
     """INT4 group-quantized weights (N(0, 0.02) matmuls): HIP dequantizes in
-    registers (GEMV below 8 sequences, MFMA GEMM from 8); the oracle runs fp32
-    on the bit-identical dequantized blob."""
+    registers (two sequences: the two-sequence persistent kernel for group 32,
+    the GEMV step for group 64; from three the batched kernel); the oracle
+    runs fp32 on the bit-identical dequantized blob."""
     print(f"small int4 block={block} B={B}", flush=True)
     w = gaussian_matmuls(init_sunnynet(SMALL, 0), seed=3)
     path = _write(tmp_path_factory, f"small_g{block}.bin", pack_sunny_blob(w))

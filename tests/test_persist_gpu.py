@@ -48,6 +48,14 @@ def small(tmp_path_factory):
     return w, buf, _blob(tmp_path_factory, "small.bin", buf)
 
 
+@pytest.fixture(scope="module")
+def small_int4_path(tmp_path_factory):
+    """SunnyNet small with N(0, 0.02) matmuls: the fp32 blob (quantized to
+    INT4 g32 at load) and the blob of its dequantized weights (the oracle's)."""
+    w = gaussian_matmuls(init_sunnynet(SMALL, 0), seed=3)
+    return _blob(tmp_path_factory, "small_g.bin", pack_sunny_blob(w)), dequant_blob(w, 32)
+
+
 def _greedy_vs_oracle(gpu, hm, orc, start, n):
     """decode_greedy on the device vs the oracle's greedy chain; also the
     last step's logits."""
@@ -216,3 +224,59 @@ def test_ordinary_launch_equals_cooperative(gpu, small, monkeypatch, B):
         hm.close()
     assert torch.equal(res[0][0], res[1][0])
     assert torch.equal(res[0][1], res[1][1])
+
+
+def test_two_sequence_kernel(gpu, small_int4_path, monkeypatch):
+    """Two sequences share each step's INT4 weight loads in one persistent
+    launch (persist_ms.h): stepping, a greedy chain across calls and a
+    time-out that refuses both part-stepped sequences until their state is
+    set, against the oracle on the dequantized weights within 2e-5, and the
+    same tokens as the GEMV step (SNHIP_PERSIST_MS=0)."""
+    path, dq = small_int4_path
+    hm = _model(path, SMALL, weights="int4", block=32, max_batch=2)
+    orc = oracle.SnOracle(dq, batch=2)
+    rng = np.random.default_rng(22)
+    print("two-sequence kernel: stepping", flush=True)
+    for _ in range(6):
+        t = rng.integers(0, SMALL.vocab_size, 2).astype(np.int32)
+        a = hm.step_batch(torch.from_numpy(t).to(gpu)).cpu().numpy()
+        b = orc.step(t)
+        assert np.abs(a - b).max() < TOL and np.array_equal(a.argmax(1), b.argmax(1))
+    print("two-sequence kernel: greedy chains", flush=True)
+    cur = np.array([7, 9], np.int32)
+    lg = torch.empty(2, SMALL.vocab_size, device=gpu)
+    for n in (5, 3):
+        out = hm.decode_greedy(torch.from_numpy(cur).to(gpu), n, logits=lg).cpu().numpy()
+        for i in range(n):
+            ref = orc.step(cur)
+            nxt = ref.argmax(1).astype(np.int32)
+            assert np.array_equal(out[i], nxt), (n, i)
+            cur = nxt
+        assert np.abs(lg.cpu().numpy() - ref).max() < TOL
+    saved = [x.clone() for x in hm.get_state(2)]
+    monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
+    hm2 = _model(path, SMALL, weights="int4", block=32, max_batch=2)
+    hm2.set_state(*saved)
+    monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
+    print("two-sequence kernel: time-out", flush=True)
+    with pytest.raises(RuntimeError, match="timed out"):
+        hm2.decode_greedy(torch.from_numpy(cur).to(gpu), 2)
+    monkeypatch.delenv("SNHIP_PERSIST_STALL")
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm2.step_batch(torch.from_numpy(cur).to(gpu))
+    hm2.set_state(saved[0][:1], saved[1][:1])      # sequence 1 may still be part-stepped
+    with pytest.raises(RuntimeError, match="part-stepped"):
+        hm2.step_batch(torch.from_numpy(cur).to(gpu))
+    hm2.set_state(*saved)
+    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
+    a = hm2.step_batch(torch.from_numpy(cur).to(gpu)).cpu().numpy()
+    assert np.abs(a - orc.step(cur)).max() < TOL
+    monkeypatch.setenv("SNHIP_PERSIST_MS", "0")
+    hg = _model(path, SMALL, weights="int4", block=32, max_batch=2)
+    monkeypatch.delenv("SNHIP_PERSIST_MS")
+    hg.set_state(*saved)
+    hm.set_state(*saved)
+    t = torch.from_numpy(cur).to(gpu)
+    assert torch.equal(hm.decode_greedy(t, 6), hg.decode_greedy(t, 6))
+    for h in (hm, hm2, hg):
+        h.close()
