@@ -587,21 +587,27 @@ __global__ __launch_bounds__(NT) void k_decode_persist_ms(PersistArgs a) {
     }
 
     // Owners write back each sequence's state and history (newest first) of
-    // their channels, for every layer.
+    // their channels, for every layer. A ring entry is read by the thread that
+    // wrote it in phase A (element k NT + tid).
     const int T = a.n_steps;
     for (int l = 0; l < L; ++l) {
         const float* ring_l = ring_wg + (size_t)l * KH * D * NS;
         const u64* sl = a.sx + ((size_t)l * 2 + ((T - 1) & 1)) * D * NS;
-        for (int e = tid; e < cpw * NS; e += NT) {
-            const int c = e / NS, q = e - c * NS, i = c0 + c;
-            if (q >= ns) continue;
-            a.s[q * sst + (size_t)l * D + i] = ll_f(ll_get(sl + (size_t)i * NS + q));
 #pragma unroll
-            for (int j = KH - 1; j >= 0; --j) {
-                const int age = T - 1 - j;
-                float* hj = a.hist + q * hst + ((size_t)l * KH + j) * D + i;
-                *hj = age >= 0 ? ring_l[((size_t)(age % KH) * D + i) * NS + q]
-                               : a.hist[q * hst + ((size_t)l * KH + (j - T)) * D + i];
+        for (int k = 0; k < PD; ++k) {
+            const int i = k * NT + tid;
+            if (i >= D || i < c0 || i >= c0 + cpw) continue;
+#pragma unroll
+            for (int q = 0; q < NS; ++q) {
+                if (q >= ns) break;
+                a.s[q * sst + (size_t)l * D + i] = ll_f(ll_get(sl + (size_t)i * NS + q));
+#pragma unroll
+                for (int j = KH - 1; j >= 0; --j) {
+                    const int age = T - 1 - j;
+                    float* hj = a.hist + q * hst + ((size_t)l * KH + j) * D + i;
+                    *hj = age >= 0 ? ring_l[((size_t)(age % KH) * D + i) * NS + q]
+                                   : a.hist[q * hst + ((size_t)l * KH + (j - T)) * D + i];
+                }
             }
         }
     }

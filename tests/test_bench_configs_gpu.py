@@ -6,6 +6,8 @@ instantiations and chain lengths:
 * fp32 B=1: chunked prefill of T=1024 tokens, then 256 greedy steps in one
   persistent launch (the whole chain's tokens and the last logits);
 * INT4 g32 B=1: T=2048 prefill, then 256 greedy steps;
+* INT4 g32 B=2: T=2048 prefill, then 256 greedy steps of the two-sequence
+  persistent kernel, both sequences replayed on the reference;
 * INT4 g32 B=8 and B=32: T=2048 prefill, then 256 greedy steps of the
   persistent batched step (k_decode_batch at the 100M product depths with
   INT4 g32 weights), three sampled sequences replayed on the reference;
@@ -106,8 +108,8 @@ def test_int4_b1_prefill_2048_then_256_greedy(gpu, blobs):
     _check_b1_chain(gpu, p4, pdq, 2048, "int4", 2048)
 
 
-@pytest.mark.parametrize("weights,B,T,n", [("int4", 8, 2048, 256), ("int4", 32, 2048, 256),
-                                            ("fp32", 64, 1024, 256)])
+@pytest.mark.parametrize("weights,B,T,n", [("int4", 2, 2048, 256), ("int4", 8, 2048, 256),
+                                            ("int4", 32, 2048, 256), ("fp32", 64, 1024, 256)])
 def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
     """The benchmark's batched chains at full length: all B sequences prefill
     T tokens and decode n greedy steps on the device in one call; three of
@@ -117,13 +119,13 @@ def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
     path, ref_path = (p4, pdq) if weights == "int4" else (p32, p32)
     prompts = np.random.default_rng(B * 7 + T).integers(0, CFG.vocab_size, (B, T)).astype(np.int32)
     hm = _model(path, weights=weights, block=32, max_batch=B)
-    assert hm.batch_grid > 0
+    assert hm.batch_grid > 0 or B == 2
     lg0 = hm.prefill_batch(torch.from_numpy(prompts).to(gpu)).cpu().numpy()
     start = torch.from_numpy(lg0.argmax(1).astype(np.int32)).to(gpu)
     last = torch.empty(B, CFG.vocab_size, device=gpu)
     toks = hm.decode_greedy(start, n, logits=last).cpu().numpy()
     last = last.cpu().numpy()
-    for b in (0, B // 2 + 1, B - 1):
+    for b in sorted({0, min(B // 2 + 1, B - 1), B - 1}):
         print(f"{weights} B={B}: reference chain of sequence {b}", flush=True)
         ref = _ref(ref_path)
         rl0, rtoks, rlast = _ref_greedy(ref, prompts[b], n)
