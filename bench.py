@@ -67,9 +67,9 @@ SCAN_TRAFFIC_BYTES = 1_611_150_336
 # decode`, calibrated like the scan's and divided by the call's steps. Filled
 # from the tables of profiles/decode_pmc_traffic.md.
 DECODE_TRAFFIC: dict = {
-    ("int4", 1): 96_539_322, ("int4", 8): 95_639_327, ("int4", 32): 174_584_418,
-    ("fp32", 1): 517_471_757, ("fp32", 64): 627_485_222, ("fp16", 1): 285_549_635,
-    ("small", 1): 1_385_494, ("rwkv7", 1): 153_234_910, ("rwkv7", 64): 843_917_140,
+    ("int4", 1): 96_622_294, ("int4", 8): 156_227_720, ("int4", 32): 174_581_634,
+    ("fp32", 1): 517_615_839, ("fp32", 64): 627_481_094, ("fp16", 1): 285_593_769,
+    ("small", 1): 1_378_358, ("rwkv7", 1): 153_236_742, ("rwkv7", 64): 843_919_572,
 }
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
 
@@ -582,8 +582,11 @@ def bench_decode(cpu: bool):
             torch.cuda.synchronize()
             n = out["steps"]
             ms = _time_ms(lambda: hm.decode_greedy(tok, n)) / n
-            kernel = (f"k_decode_persist<{ {'int4': 32, 'fp16': 16}.get(fmt, 0)}> (the whole step)"
-                      if B == 1 and hm.persistent_grid else
+            blk = {'int4': 32, 'fp16': 16}.get(fmt, 0)
+            slices = hm.persistent_grid_for(B) if B > 1 else 0
+            kernel = (f"k_decode_persist<{blk}> (the whole step)" if B == 1 and hm.persistent_grid else
+                      f"k_decode_persist<{blk}> on {B} grid slices of {slices // B} workgroups "
+                      f"(the whole step)" if slices else
                       "k_decode_batch (layers) + head GEMM + greedy argmax" if hm.batch_grid else
                       "per-kernel step")
             hm.close()

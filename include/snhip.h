@@ -150,8 +150,19 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
  * cooperative launch, or SNHIP_PERSIST=0 in the environment at load). */
 int32_t snhip_persistent_grid(const SnHipModel* m);
 
-/* Grid size of the persistent batched step (steps of 3 to 64 sequences run
- * every layer in one cooperative launch, then the head), or 0 when this handle
+/* Workgroups of the persistent decode when steps of B sequences run as B
+ * copies of the single-sequence kernel in one cooperative launch, each
+ * sequence on its own equal slice of the grid (B * slice; the slice for B = 1
+ * is snhip_persistent_grid), or 0 when steps of B sequences take another path.
+ * Defaults: B <= 16 for INT4 rows, B <= 4 for fp32 / fp16 rows;
+ * SNHIP_PERSIST_MI in the environment at load sets the limit (1: off). No
+ * counterpart in the reference: its C runtime steps one sequence at a time
+ * (sunnynet.c:212). */
+int32_t snhip_persistent_grid_batch(const SnHipModel* m, int32_t B);
+
+/* Grid size of the persistent batched step (steps of 3 to 64 sequences that
+ * the single-sequence kernel does not take run every layer in one cooperative
+ * launch, then the head), or 0 when this handle
  * uses the per-kernel step for them (shapes other than the compiled product
  * depths, max_batch below 3, no cooperative launch, or SNHIP_BATCH_PERSIST=0
  * in the environment at load). No counterpart in the reference: its C runtime

@@ -85,6 +85,7 @@ _SIGS = {
     "snhip_set_stream": (I32, [V, V]),
     "snhip_max_batch": (I32, [V]),
     "snhip_persistent_grid": (I32, [V]),
+    "snhip_persistent_grid_batch": (I32, [V, I32]),
     "snhip_batch_grid": (I32, [V]),
     "snhip_step_batch_dev": (I32, [V, V, I32, V]),
     "snhip_step_batch": (I32, [V, V, I32, V]),

@@ -53,18 +53,23 @@ struct PersistArgs {
     int n_steps, greedy;
     unsigned spin_limit;    // polls before a wait gives up
     unsigned stall;         // added to every awaited epoch: > 0 only to test the time-out path
-    int ns;                 // sequences (the multi-sequence kernel; 1 otherwise)
+    // k_decode_persist: independent sequences, one per equal slice of the
+    // grid (0 or 1: one). Sequence q runs on workgroups [q G, (q+1) G),
+    // G = grid / ni, with its own exchange words (ex + 2 q kPersistExWords,
+    // sx + q L 2 D), state and history rows (s + q L D, hist + q L kh D),
+    // first token tok_in[q], tokens out_tok[step ni + q] and logits
+    // logits + q vocab; ring is (grid, L, kh, D) over the whole grid.
+    int ni;
 };
 
 // Exchange words per epoch slot (>= inner, rank, dim and two per workgroup).
 constexpr int kPersistExWords = 2048;
-// The multi-sequence kernel's: NS x (inner, rank, dim) and 2 NS per workgroup.
-constexpr int kPersistMsExWords = 16384;
-constexpr int kPersistMsMax = 2;              // sequences, at most
 
 // Conv taps the kernel is built for, and its largest grid.
 constexpr int kPersistTaps = 4;
 constexpr int kPersistMaxGrid = 1024;
+// Sequences one launch of the single-sequence kernel steps at most (a.ni).
+constexpr int kPersistMiMax = 64;
 
 // Workgroups per CU the kernel can keep resident (0 if it cannot run).
 int persist_occupancy(int blk);
@@ -73,13 +78,6 @@ int persist_occupancy(int blk);
 // every workgroup gets rows of V, W_z and the head.
 bool persist_grid_ok(int G, int D, int I, int R, int vocab);
 snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipStream_t st);
-
-// The multi-sequence persistent decode (INT4 g32 rows, a.ns = 2..8 sequences,
-// persist_ms.h): whether a grid of G workgroups fits its per-workgroup bounds,
-// its workgroups per CU for up to ns sequences, and its launch.
-bool persist_ms_grid_ok(int G, int D, int I, int R, int vocab);
-int persist_ms_occupancy(int ns);
-snhip_status launch_decode_persist_ms(const PersistArgs& a, int nwg, hipStream_t st);
 
 // Persistent step of a batch of sequences (batch.hip): every layer of one
 // decode step in one cooperative launch, phases separated by grid barriers.

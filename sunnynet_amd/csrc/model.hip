@@ -595,14 +595,11 @@ struct SnHipModel {
     // Persistent single-sequence decode (persist.hip): grid size, 0 when the
     // model's shape or the device does not allow it.
     int persist_wg = 0;
-    // Multi-sequence persistent decode (INT4 g32, 2..ms_max sequences): grid
-    // size (0: off), exchange words, new-state words and history rings sized
-    // for ms_max sequences.
-    int ms_wg = 0;
-    int ms_max = 0;
-    unsigned long long* ms_ex = nullptr;
-    unsigned long long* ms_sx = nullptr;
-    float* ms_ring = nullptr;
+    // The same kernel stepping 2..mi_max sequences at once, each on its own
+    // slice of mi_grid[B] workgroups (0: off); pex / psx hold mi_max
+    // sequences' words and pring one ring per workgroup of the largest grid.
+    int mi_max = 0;
+    int mi_grid[snhip::kPersistMiMax + 1] = {};
     snhip::PLayer* dlayers = nullptr;     // device copy of the layer table
     unsigned long long* pex = nullptr;    // exchange words (2 x kPersistExWords)
     unsigned long long* psx = nullptr;    // new-state words (L x 2 x D)
@@ -876,30 +873,34 @@ bool host_err(SnHipModel* m) {
     return true;
 }
 
-// Enables the multi-sequence persistent decode for INT4 g32 handles of two or
-// more sequences, used for steps of two (SNHIP_PERSIST_MS=0 turns it off;
-// SNHIP_PERSIST_MS_WG caps the grid). One workgroup per eight channels, as the
-// single-sequence INT4 kernel. SunnyNet-100M INT4 B=2: 278.0 us/step, against
-// 849.7 on the GEMV step; three and more sequences take the batched kernel.
-void setup_persist_ms(SnHipModel* m, int ncu) {
-    if (env_unsigned("SNHIP_PERSIST_MS", 1, 0) == 0) return;
-    if (m->wfmt != SNHIP_WEIGHTS_INT4 || m->block != 32 || m->max_batch < 2) return;
-    const int nmax = std::min(m->max_batch, kPersistMsMax);
-    if (persist_ms_occupancy(nmax) < 1) return;
-    int cap = std::min(m->D / 8, ncu);
-    if (const char* e = getenv("SNHIP_PERSIST_MS_WG")) cap = atoi(e);
-    cap = std::min(cap, ncu);
-    int nwg = 0;
-    for (int g = cap; g >= 1 && !nwg; --g)
-        if (persist_ms_grid_ok(g, m->D, m->I, m->R, m->vocab)) nwg = g;
-    if (nwg < 1) return;
-    const int NS = kPersistMsMax;                       // the kernel's word stride
-    m->ms_ex = dalloc<unsigned long long>(m, 2 * (size_t)kPersistMsExWords);
-    m->ms_sx = dalloc<unsigned long long>(m, (size_t)m->L * 2 * m->D * NS);
-    m->ms_ring = dalloc<float>(m, (size_t)nwg * m->L * m->kh * m->D * NS);
-    if (!m->ms_ex || !m->ms_sx || !m->ms_ring) return;
-    m->ms_max = nmax;
-    m->ms_wg = nwg;
+// Grids of the single-sequence kernel stepping B = 2..mi_max sequences in one
+// launch: each sequence gets the largest grid the kernel accepts (at most cap,
+// the one-sequence grid, and ncu / B, so the whole launch is one workgroup per
+// CU). Workgroup w of every sequence sits on the same XCD (slices are
+// multiples of 8 workgroups) and reads the same weight rows in the same phase,
+// so most rows reach the other sequences from that XCD's L2: eight sequences
+// of SunnyNet-100M INT4 fetch 131 MB per step from HBM (rocprofv3 FETCH_SIZE),
+// against 87 MB for one sequence alone. mi_max defaults to the
+// sizes measured faster than the batched kernel (SunnyNet-100M, one MI355X,
+// us/step): INT4 g32 up to 16 (B=2 183.7 against 281.5, B=4 206.4 / 349.6,
+// B=8 252.5 / 369.7, B=16 359.2 / 400.3; B=24 541.3 against 430.1), fp32 and
+// fp16 rows up to 4 (B=2 253.1 / 731.1, B=4 351.7 / 379.2; B=8 513.9 against
+// 399.8). SNHIP_PERSIST_MI sets it (1: off). Returns the sequences the
+// exchange words must hold.
+int setup_persist_mi(SnHipModel* m, int ncu, int cap) {
+    const unsigned dflt = m->wfmt == SNHIP_WEIGHTS_INT4 ? 16 : 4;
+    int lim = std::min(m->max_batch, kPersistMiMax);
+    lim = std::min(lim, (int)std::min(env_unsigned("SNHIP_PERSIST_MI", dflt, 0), (unsigned)kPersistMiMax));
+    m->mi_max = 0;
+    for (int b = 2; b <= lim; ++b) {
+        int g = 0;
+        for (int c = std::min(cap, ncu / b); c >= 1 && !g; --c)
+            if (persist_grid_ok(c, m->D, m->I, m->R, m->vocab)) g = c;
+        if (g < 1) break;
+        m->mi_grid[b] = g;
+        m->mi_max = b;
+    }
+    return std::max(1, m->mi_max);
 }
 
 // Enables the persistent single-sequence decode when the shape fits it and the
@@ -930,13 +931,18 @@ void setup_persist(SnHipModel* m) {
     for (int g = cap; g >= 1 && !nwg; --g)
         if (persist_grid_ok(g, m->D, m->I, m->R, m->vocab)) nwg = g;
     if (nwg < 1) return;
-    m->pex = dalloc<unsigned long long>(m, 2 * (size_t)kPersistExWords);
-    m->psx = dalloc<unsigned long long>(m, (size_t)m->L * 2 * m->D);
-    m->pring = dalloc<float>(m, (size_t)nwg * m->L * m->kh * m->D);
+    const int nseq = setup_persist_mi(m, ncu, cap);
+    int ring_wg = nwg;
+    for (int b = 2; b <= m->mi_max; ++b) ring_wg = std::max(ring_wg, b * m->mi_grid[b]);
+    m->pex = dalloc<unsigned long long>(m, 2 * (size_t)kPersistExWords * nseq);
+    m->psx = dalloc<unsigned long long>(m, (size_t)m->L * 2 * m->D * nseq);
+    m->pring = dalloc<float>(m, (size_t)ring_wg * m->L * m->kh * m->D);
     m->perr = dalloc<unsigned>(m, 1);
-    if (!m->pex || !m->psx || !m->pring || !m->perr || !layer_table(m) || !host_err(m)) return;
+    if (!m->pex || !m->psx || !m->pring || !m->perr || !layer_table(m) || !host_err(m)) {
+        m->mi_max = 0;
+        return;
+    }
     m->persist_wg = nwg;
-    setup_persist_ms(m, ncu);
 }
 
 // Enables the persistent batched step (batch.hip) when the shape fits it and
@@ -1621,17 +1627,18 @@ snhip_status run_prefill(SnHipModel* m, const int32_t* tokens_dev, int B, int T,
     return SNHIP_OK;
 }
 
-// n_steps decode steps of sequence 0 in persistent launches on the internal
-// stream (ordered like run_steps). The first input token is in m->tok. greedy:
-// out_tok (n_steps) receives each step's argmax token, fed to the next step;
-// otherwise n_steps must be 1. logits (device), if not NULL, gets the last
-// step's logits.
+// n_steps decode steps of sequences [0, B) in persistent launches on the
+// internal stream (ordered like run_steps): B = 1 on the persist_wg grid, else
+// (2 <= B <= mi_max) each sequence on its own mi_grid[B] workgroups of one
+// launch. The first input tokens are in m->tok. greedy: out_tok (n_steps, B)
+// receives each step's argmax tokens, fed to the next step; otherwise n_steps
+// must be 1. logits (B, vocab, device), if not NULL, gets the last step's.
 // The call returns once the launches have finished and reports an exchange
 // time-out as SNHIP_E_DEVICE. Each workgroup writes its channels' state back
-// after its own last wait, so a time-out can leave sequence 0 part-stepped:
+// after its own last wait, so a time-out can leave the sequences part-stepped:
 // the handle then refuses steps until reset or set. *launch_failed is set when the
 // first cooperative launch could not be queued at all (nothing ran).
-snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_tok,
+snhip_status run_persist(SnHipModel* m, int B, int n_steps, bool greedy, int32_t* out_tok,
                          float* logits, bool* launch_failed) {
     constexpr int kMaxStepsPerLaunch = 1 << 20;   // keeps exchange epochs far from wrapping
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
@@ -1648,63 +1655,19 @@ snhip_status run_persist(SnHipModel* m, int n_steps, bool greedy, int32_t* out_t
     a.greedy = greedy ? 1 : 0;
     a.spin_limit = m->persist_spin;
     a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
+    a.ni = B;
     const int blk = persist_blk(m);
+    const int grid = B == 1 ? m->persist_wg : B * m->mi_grid[B];
     for (int done = 0; done < n_steps;) {
         const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
         // Epochs restart at 1 in every launch: clear the words of the last one.
-        SNHIP_CHECK(hipMemsetAsync(m->pex, 0, 2 * (size_t)kPersistExWords * sizeof(unsigned long long), m->work));
-        SNHIP_CHECK(hipMemsetAsync(m->psx, 0, (size_t)m->L * 2 * m->D * sizeof(unsigned long long), m->work));
-        a.tok_in = done == 0 ? m->tok : out_tok + done - 1;
-        a.out_tok = greedy ? out_tok + done : nullptr;
-        a.logits = done + n == n_steps ? logits : nullptr;
-        a.n_steps = n;
-        const snhip_status rc = launch_decode_persist(a, m->persist_wg, blk, m->work);
-        if (rc != SNHIP_OK) {
-            if (done == 0 && launch_failed) *launch_failed = true;
-            return rc;
-        }
-        done += n;
-    }
-    SNHIP_CHECK(hipMemcpyAsync(m->h_err, m->perr, sizeof(unsigned), hipMemcpyDeviceToHost, m->work));
-    SNHIP_CHECK(hipEventRecord(m->ev_out, m->work));
-    SNHIP_CHECK(hipStreamWaitEvent(m->stream, m->ev_out, 0));
-    SNHIP_CHECK(hipStreamSynchronize(m->work));
-    return persist_status(m, 1);
-}
-
-// n_steps decode steps of sequences [0, B) (2 <= B <= ms_max) in
-// multi-sequence persistent launches on the internal stream, as run_persist:
-// the first tokens in m->tok; greedy: out_tok (n_steps, B) receives each
-// step's tokens; logits (B, vocab, device), if not NULL, the last step's.
-snhip_status run_persist_ms(SnHipModel* m, int B, int n_steps, bool greedy, int32_t* out_tok,
-                            float* logits, bool* launch_failed) {
-    constexpr int kMaxStepsPerLaunch = 1 << 20;
-    const int NS = kPersistMsMax;
-    SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
-    SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
-    SNHIP_CHECK(hipMemsetAsync(m->perr, 0, sizeof(unsigned), m->work));
-    PersistArgs a{};
-    a.layers = m->dlayers;
-    a.L = m->L; a.D = m->D; a.I = m->I; a.R = m->R; a.K = m->K; a.kh = m->kh;
-    a.vocab = m->vocab; a.clamp = m->clamp; a.eps = m->eps; a.p_floor = m->p_floor;
-    a.embed = m->embed; a.no_g = m->no_g; a.no_c = m->no_c;
-    a.head = pmat(m->head);
-    a.s = m->s; a.hist = m->hist;
-    a.ring = m->ms_ring; a.ex = m->ms_ex; a.sx = m->ms_sx; a.err = m->perr;
-    a.greedy = greedy ? 1 : 0;
-    a.spin_limit = m->persist_spin;
-    a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
-    a.ns = B;
-    (void)NS;
-    for (int done = 0; done < n_steps;) {
-        const int n = std::min(n_steps - done, kMaxStepsPerLaunch);
-        SNHIP_CHECK(hipMemsetAsync(m->ms_ex, 0, 2 * (size_t)kPersistMsExWords * sizeof(unsigned long long), m->work));
-        SNHIP_CHECK(hipMemsetAsync(m->ms_sx, 0, (size_t)m->L * 2 * m->D * NS * sizeof(unsigned long long), m->work));
+        SNHIP_CHECK(hipMemsetAsync(m->pex, 0, 2 * (size_t)kPersistExWords * B * sizeof(unsigned long long), m->work));
+        SNHIP_CHECK(hipMemsetAsync(m->psx, 0, (size_t)m->L * 2 * m->D * B * sizeof(unsigned long long), m->work));
         a.tok_in = done == 0 ? m->tok : out_tok + (size_t)(done - 1) * B;
         a.out_tok = greedy ? out_tok + (size_t)done * B : nullptr;
         a.logits = done + n == n_steps ? logits : nullptr;
         a.n_steps = n;
-        const snhip_status rc = launch_decode_persist_ms(a, m->ms_wg, m->work);
+        const snhip_status rc = launch_decode_persist(a, grid, blk, m->work);
         if (rc != SNHIP_OK) {
             if (done == 0 && launch_failed) *launch_failed = true;
             return rc;
@@ -1718,18 +1681,20 @@ snhip_status run_persist_ms(SnHipModel* m, int B, int n_steps, bool greedy, int3
     return persist_status(m, B);
 }
 
-// Does a step of B sequences run as the multi-sequence persistent kernel?
-bool uses_ms(const SnHipModel* m, int B) { return m->ms_wg > 0 && B >= 2 && B <= m->ms_max; }
+// Does a step of B >= 2 sequences run as B instances of the single-sequence
+// persistent kernel in one launch?
+bool uses_mi(const SnHipModel* m, int B) { return m->persist_wg > 0 && B >= 2 && B <= m->mi_max; }
 
-// One step of sequences [0, B), B >= 2 (tokens in m->tok): the multi-sequence
-// persistent kernel when it takes B, else the per-kernel or batched step. A
-// failed cooperative launch turns the multi-sequence path off and falls back.
+// One step of sequences [0, B), B >= 2 (tokens in m->tok): the single-sequence
+// persistent kernel on a slice of the grid per sequence when it takes B, else
+// the per-kernel or batched step. A failed cooperative launch turns the
+// persistent path for B >= 2 off and falls back.
 snhip_status step_many(SnHipModel* m, int B, float* logits_out) {
-    if (uses_ms(m, B)) {
+    if (uses_mi(m, B)) {
         bool launch_failed = false;
-        const snhip_status rc = run_persist_ms(m, B, 1, false, nullptr, logits_out, &launch_failed);
+        const snhip_status rc = run_persist(m, B, 1, false, nullptr, logits_out, &launch_failed);
         if (!launch_failed) return rc;
-        m->ms_wg = 0;
+        m->mi_max = 0;
         (void)hipGetLastError();
     }
     return run_steps(m, B, logits_out, false, 1);
@@ -1741,7 +1706,7 @@ snhip_status step_many(SnHipModel* m, int B, float* logits_out) {
 snhip_status step_one(SnHipModel* m, float* logits_out) {
     if (m->persist_wg) {
         bool launch_failed = false;
-        const snhip_status rc = run_persist(m, 1, false, nullptr, logits_out, &launch_failed);
+        const snhip_status rc = run_persist(m, 1, 1, false, nullptr, logits_out, &launch_failed);
         if (!launch_failed) return rc;
         m->persist_wg = 0;
         (void)hipGetLastError();
@@ -1804,6 +1769,12 @@ int snhip_vocab(const SnHipModel* m) { return m ? m->vocab : 0; }
 int snhip_ready(const SnHipModel* m) { return m && m->ready; }
 int32_t snhip_max_batch(const SnHipModel* m) { return m ? m->max_batch : 0; }
 int32_t snhip_persistent_grid(const SnHipModel* m) { return m ? m->persist_wg : 0; }
+
+int32_t snhip_persistent_grid_batch(const SnHipModel* m, int32_t B) {
+    if (!m || B < 1 || B > m->max_batch) return 0;
+    if (B == 1) return m->persist_wg;
+    return uses_mi(m, B) ? B * m->mi_grid[B] : 0;
+}
 
 int32_t snhip_batch_grid(const SnHipModel* m) { return m ? m->batch_wg : 0; }
 
@@ -1940,18 +1911,18 @@ snhip_status snhip_decode_greedy_dev(SnHipModel* m, const int32_t* tokens_dev, i
         snhip_status rc = put_tokens(m, tokens_dev, 1, hipMemcpyDeviceToDevice);
         if (rc != SNHIP_OK) return rc;
         bool launch_failed = false;
-        rc = run_persist(m, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
+        rc = run_persist(m, 1, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
         if (!launch_failed) return rc;
         m->persist_wg = 0;
         (void)hipGetLastError();
     }
-    if (uses_ms(m, B)) {
+    if (uses_mi(m, B)) {
         snhip_status rc = put_tokens(m, tokens_dev, B, hipMemcpyDeviceToDevice);
         if (rc != SNHIP_OK) return rc;
         bool launch_failed = false;
-        rc = run_persist_ms(m, B, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
+        rc = run_persist(m, B, n_steps, true, out_tokens_dev, logits_dev, &launch_failed);
         if (!launch_failed) return rc;
-        m->ms_wg = 0;
+        m->mi_max = 0;
         (void)hipGetLastError();
     }
     if ((long)n_steps * B > (long)m->hist_cap || !m->tok_hist) {

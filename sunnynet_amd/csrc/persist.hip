@@ -46,8 +46,6 @@
 // leaves at its next poll.
 #include "decode.h"
 
-#include <algorithm>
-
 #define SNHIP_PERSIST_NT 1024
 #define SNHIP_PERSIST_NS nt1024
 #include "persist_kernel.h"
@@ -100,36 +98,10 @@ bool persist_grid_ok(int G, int D, int I, int R, int vocab) {
     return G <= R && G <= I && G <= vocab;
 }
 
-bool persist_ms_grid_ok(int G, int D, int I, int R, int vocab) {
-    if (!persist_grid_ok(G, D, I, R, vocab) || G > nt512::kMsMaxGrid) return false;
-    const int cpw = D / G, ngrp = cpw >= 8 ? cpw / 8 : 1;
-    const int rows = std::max(std::max((R + G - 1) / G + cpw, 16 * ngrp), (I + G - 1) / G);
-    return cpw <= nt512::kMsOwn && rows <= nt512::kMsRows;
-}
-
-int persist_ms_occupancy(int ns) {
-    int nb = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, nt512::kernel_for_ms(ns), 512, 0);
-    return e == hipSuccess ? nb : 0;
-}
-
-snhip_status launch_decode_persist_ms(const PersistArgs& a, int nwg, hipStream_t st) {
-    if (a.D > kPersistMaxD || a.I > kPersistMaxK || a.R > kPersistMaxK || a.K != kPersistTaps || a.D % 8 ||
-        a.L > kPersistMaxL || a.ns < 1 || a.ns > kPersistMsMax || !a.head.q ||
-        !persist_ms_grid_ok(nwg, a.D, a.I, a.R, a.vocab) || a.n_steps < 1 ||
-        (a.greedy && !a.out_tok) || (!a.greedy && a.n_steps != 1)) {
-        set_last_error("multi-sequence persistent decode: unsupported shape or arguments");
-        return SNHIP_E_INVAL;
-    }
-    PersistArgs args = a;
-    void* kargs[] = {&args};
-    SNHIP_CHECK(launch_persistent(nt512::kernel_for_ms(a.ns), dim3(nwg), dim3(512), kargs, st));
-    return SNHIP_OK;
-}
-
 snhip_status launch_decode_persist(const PersistArgs& a, int nwg, int blk, hipStream_t st) {
+    const int ni = a.ni > 1 ? a.ni : 1;
     if (a.D > kPersistMaxD || a.I > kPersistMaxK || a.R > kPersistMaxK || a.K != kPersistTaps || a.D % 8 || a.L > kPersistMaxL ||
-        !persist_grid_ok(nwg, a.D, a.I, a.R, a.vocab) || a.n_steps < 1 ||
+        ni > kPersistMiMax || nwg % ni || !persist_grid_ok(nwg / ni, a.D, a.I, a.R, a.vocab) || a.n_steps < 1 ||
         (a.greedy && !a.out_tok) || (!a.greedy && a.n_steps != 1)) {
         set_last_error("persistent decode: unsupported shape or arguments");
         return SNHIP_E_INVAL;

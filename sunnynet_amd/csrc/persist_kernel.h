@@ -559,8 +559,20 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
         tid = opq(tid);
         lane = tid & 63;
     };
-    const int G = gridDim.x, wg = blockIdx.x;
     const int D = a.D, I = a.I, R = a.R, L = a.L;
+    // Independent sequences run on equal slices of the grid: this workgroup
+    // is workgroup wg of sequence sq's G (one sequence: sq = 0, G = the grid).
+    const int NI = a.ni > 1 ? a.ni : 1;
+    const int G = gridDim.x / NI, sq = blockIdx.x / G, wg = blockIdx.x - sq * G;
+    if (NI > 1) {
+        a.s += (size_t)sq * L * D;
+        a.hist += (size_t)sq * L * KH * D;
+        a.ex += (size_t)sq * 2 * kPersistExWords;
+        a.sx += (size_t)sq * L * 2 * D;
+        a.tok_in += sq;
+        if (a.out_tok) a.out_tok += sq;
+        if (a.logits) a.logits += (size_t)sq * a.vocab;
+    }
     const int cpw = D / G, c0 = wg * cpw;                     // owned channels
     const int grp0 = c0 >> 3, ngrp = cpw >= 8 ? cpw >> 3 : 1; // owned channel groups
     const PollCtl pc{a.err, a.spin_limit};
@@ -618,7 +630,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
     unsigned ep = 0;                  // epoch of the last exchange produced
     const unsigned stall = a.stall;   // > 0 only to test the time-out path
     int tok = a.tok_in[0];
-    float* ring_wg = a.ring + (size_t)wg * L * KH * D;
+    float* ring_wg = a.ring + (size_t)blockIdx.x * L * KH * D;
     constexpr int WMAX = 2 * PD;      // exchange words per thread (A: x and s)
     static_assert(WMAX >= PK, "gather words");
 
@@ -816,7 +828,7 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
 #pragma unroll
             for (int i = 1; i < NWV; ++i) kk = max(kk, kred[i]);
             tok = (int)(0xFFFFFFFFu - (uint32_t)(kk & 0xFFFFFFFFull));
-            if (wg == 0 && tid == 0) a.out_tok[step] = tok;
+            if (wg == 0 && tid == 0) a.out_tok[(size_t)step * NI] = tok;
             barrier_lds();
         }
     }
@@ -843,19 +855,6 @@ __global__ __launch_bounds__(NT) void k_decode_persist(PersistArgs a) {
         }
     }
 }
-
-#if SNHIP_PERSIST_NT == 512
-#include "persist_ms.h"
-
-// The multi-sequence kernel for up to ns sequences (INT4 g32 rows). Built for
-// two: at three and more the batched kernel measured faster (SunnyNet-100M
-// INT4: B=3 404.6 against 348.0 us/step, B=4 455.4 against 349.8; the
-// eight-sequence form needs more than 256 registers and spills).
-const void* kernel_for_ms(int ns) {
-    (void)ns;
-    return (const void*)k_decode_persist_ms<32, 2>;
-}
-#endif
 
 const void* kernel_for(int blk) {
     return blk == 0 ? (const void*)k_decode_persist<0>

@@ -198,6 +198,11 @@ class HipModel:
         """Workgroups of the persistent B=1 decode kernel (0: per-kernel steps)."""
         return int(self._lib.snhip_persistent_grid(self._h))
 
+    def persistent_grid_for(self, B: int) -> int:
+        """Workgroups of the persistent decode for steps of B sequences, each on
+        its own slice of the grid (0: B takes the batched or per-kernel step)."""
+        return int(self._lib.snhip_persistent_grid_batch(self._h, B))
+
     def get_state(self, B: int | None = None):
         B = self.max_batch if B is None else B
         s = torch.empty(B, self.layers, self.dim, device=self.device)

@@ -6,11 +6,12 @@ instantiations and chain lengths:
 * fp32 B=1: chunked prefill of T=1024 tokens, then 256 greedy steps in one
   persistent launch (the whole chain's tokens and the last logits);
 * INT4 g32 B=1: T=2048 prefill, then 256 greedy steps;
-* INT4 g32 B=2: T=2048 prefill, then 256 greedy steps of the two-sequence
-  persistent kernel, both sequences replayed on the reference;
-* INT4 g32 B=8 and B=32: T=2048 prefill, then 256 greedy steps of the
-  persistent batched step (k_decode_batch at the 100M product depths with
-  INT4 g32 weights), three sampled sequences replayed on the reference;
+* INT4 g32 B=2 and B=8: T=2048 prefill, then 256 greedy steps of the
+  single-sequence persistent kernel on a grid slice per sequence (128 and 32
+  workgroups each), both / three sampled sequences replayed on the reference;
+* INT4 g32 B=32: T=2048 prefill, then 256 greedy steps of the persistent
+  batched step (k_decode_batch at the 100M product depths with INT4 g32
+  weights), three sampled sequences replayed on the reference;
 * fp32 B=64: T=1024 prefill then 256 greedy steps, three sampled sequences;
 * every batch size 1..64, INT4 and fp32, one step each (every decode path
   and row-block count the batch size selects).
@@ -119,7 +120,8 @@ def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
     path, ref_path = (p4, pdq) if weights == "int4" else (p32, p32)
     prompts = np.random.default_rng(B * 7 + T).integers(0, CFG.vocab_size, (B, T)).astype(np.int32)
     hm = _model(path, weights=weights, block=32, max_batch=B)
-    assert hm.batch_grid > 0 or B == 2
+    slices = weights == "int4" and B <= 16
+    assert hm.persistent_grid_for(B) > 0 if slices else hm.batch_grid > 0
     lg0 = hm.prefill_batch(torch.from_numpy(prompts).to(gpu)).cpu().numpy()
     start = torch.from_numpy(lg0.argmax(1).astype(np.int32)).to(gpu)
     last = torch.empty(B, CFG.vocab_size, device=gpu)
@@ -141,11 +143,11 @@ def test_batched_chain_sampled(gpu, blobs, weights, B, T, n):
 @pytest.mark.parametrize("weights", ["int4", "fp32"])
 def test_every_batch_size_one_step(gpu, blobs, weights):
     """Every batch size 1..64 at the 100M shape (B=1 the persistent step,
-    2 the two-sequence persistent kernel (INT4) or the GEMV graph (fp32),
-    3..64 the persistent batched step with one to four
-    16-row blocks and partial ones): one step from the reset state, the first
-    and the last sequence against the reference runtime, within 2e-5 and with
-    the same argmax."""
+    2..16 (INT4) or 2..4 (fp32) the persistent step on a grid slice per
+    sequence (eight grid sizes), the rest the persistent batched step with
+    two to four 16-row blocks and partial ones): one step from the reset
+    state, the first and the last sequence against the reference runtime,
+    within 2e-5 and with the same argmax."""
     p32, p4, pdq = blobs
     path, ref_path = (p4, pdq) if weights == "int4" else (p32, p32)
     print(f"{weights} B=1..64, one step each", flush=True)

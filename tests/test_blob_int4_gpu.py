@@ -1,7 +1,8 @@
 """Loading the INT4 blob: a handle built from it holds the same codes and
 scales as one that quantizes the fp32 blob at load, so every decode path gives
-bit-identical logits (B=1 persistent kernel, GEMV batch, batched kernel,
-chunked prefill); and the loader refuses the format where it does not apply.
+bit-identical logits (B=1 persistent kernel, the same kernel on a grid slice
+per sequence at B=3 and 16, the batched kernel at B=24, chunked prefill); and
+the loader refuses the format where it does not apply.
 """
 from __future__ import annotations
 
@@ -35,7 +36,7 @@ def blobs(tmp_path_factory):
 def test_int4_blob_loads_bit_identical(gpu, blobs, block):
     print(f"INT4 blob block={block}", flush=True)
     rng = np.random.default_rng(block)
-    for B in (1, 3, 16):
+    for B in (1, 3, 16, 24):
         ha = _model(blobs / "f32.bin", SMALL, weights="int4", block=block, max_batch=B)
         hb = _model(blobs / f"q{block}.bin", SMALL, weights="int4", block=block, max_batch=B)
         for _ in range(4):

@@ -125,11 +125,15 @@ def test_reference_surface(gpu, small):
     assert hm.vocab == SMALL.vocab_size
 
 
-@pytest.mark.parametrize("B", [3, 8, 11, 16, 33])
-def test_batched_matches_oracle(gpu, small, B):
+@pytest.mark.parametrize("B", [2, 3, 8, 11, 16, 33])
+def test_batched_matches_oracle(gpu, small, monkeypatch, B):
+    """fp32 steps of B sequences on the GEMV (B=2) or batched step (the
+    per-sequence grid slices turned off by SNHIP_PERSIST_MI=1)."""
     w, buf, path = small
     print(f"small fp32 batched B={B}", flush=True)
+    monkeypatch.setenv("SNHIP_PERSIST_MI", "1")
     hm = _model(path, SMALL, max_batch=64)
+    assert hm.persistent_grid_for(B) == 0
     orc = oracle.SnOracle(buf, batch=B)
     rng = np.random.default_rng(B)
     for _ in range(12):
@@ -175,16 +179,24 @@ def test_greedy_decode_on_device(gpu, small):
         cur = nxt
 
 
-@pytest.mark.parametrize("block,B", [(32, 2), (64, 2), (32, 4), (64, 4), (32, 16), (64, 16)])
-def test_int4_matches_dequantized_oracle(gpu, tmp_path_factory, block, B):
+@pytest.mark.parametrize("block,B,path", [(32, 2, "slices"), (64, 2, "slices"), (32, 2, "gemv"),
+                                          (64, 2, "gemv"), (32, 4, "slices"), (64, 4, "batched"),
+                                          (32, 16, "slices"), (64, 16, "batched")])
+def test_int4_matches_dequantized_oracle(gpu, tmp_path_factory, monkeypatch, block, B, path):
     """INT4 group-quantized weights (N(0, 0.02) matmuls): HIP dequantizes in
-    registers (two sequences: the two-sequence persistent kernel for group 32,
-    the GEMV step for group 64; from three the batched kernel); the oracle
-    runs fp32 on the bit-identical dequantized blob."""
-    print(f"small int4 block={block} B={B}", flush=True)
+    registers on every path a step of B sequences can take (the
+    single-sequence persistent kernel on a grid slice per sequence, the GEMV
+    step for two sequences, and the batched kernel, the last two with the
+    slices turned off by SNHIP_PERSIST_MI=1); the oracle runs fp32 on the
+    bit-identical dequantized blob."""
+    print(f"small int4 block={block} B={B} {path}", flush=True)
+    if path != "slices":
+        monkeypatch.setenv("SNHIP_PERSIST_MI", "1")
     w = gaussian_matmuls(init_sunnynet(SMALL, 0), seed=3)
-    path = _write(tmp_path_factory, f"small_g{block}.bin", pack_sunny_blob(w))
-    hm = _model(path, SMALL, weights="int4", block=block, max_batch=B)
+    blob = _write(tmp_path_factory, f"small_g{block}.bin", pack_sunny_blob(w))
+    hm = _model(blob, SMALL, weights="int4", block=block, max_batch=B)
+    assert (hm.persistent_grid_for(B) > 0) == (path == "slices")
+    assert path != "batched" or hm.batch_grid > 0
     orc = oracle.SnOracle(dequant_blob(w, block), batch=B)
     rng = np.random.default_rng(block + B)
     for _ in range(24):
@@ -273,6 +285,7 @@ def test_graph_replays_match_eager(gpu, small, monkeypatch, B):
     whose split-K tile counters are re-armed by every launch)."""
     w, buf, path = small
     print(f"small graph vs eager B={B}", flush=True)
+    monkeypatch.setenv("SNHIP_PERSIST_MI", "1")     # B=4 on the batched step, not grid slices
     rng = np.random.default_rng(11)
     seqs = [rng.integers(0, SMALL.vocab_size, B).astype(np.int32) for _ in range(10)]
     hg = _model(path, SMALL, max_batch=B)

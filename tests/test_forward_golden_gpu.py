@@ -31,8 +31,8 @@ def _model(path, cfg, **kw):
 
 @pytest.mark.parametrize("name", ["tiny", "small"])
 def test_forward_step_matches_reference_fixture(gpu, tmp_path, name):
-    """forward_step along the recorded greedy chain (tiny B=2: the GEMV step;
-    small B=1: the persistent step)."""
+    """forward_step along the recorded greedy chain (tiny B=2: the persistent
+    step on a grid slice per sequence; small B=1: the persistent step)."""
     cfg, seed, z = load_case(name)
     tokens, logits = z["tokens"], z["logits"]
     T, B = tokens.shape

@@ -226,57 +226,90 @@ def test_ordinary_launch_equals_cooperative(gpu, small, monkeypatch, B):
     assert torch.equal(res[0][1], res[1][1])
 
 
-def test_two_sequence_kernel(gpu, small_int4_path, monkeypatch):
-    """Two sequences share each step's INT4 weight loads in one persistent
-    launch (persist_ms.h): stepping, a greedy chain across calls and a
-    time-out that refuses both part-stepped sequences until their state is
-    set, against the oracle on the dequantized weights within 2e-5, and the
-    same tokens as the GEMV step (SNHIP_PERSIST_MS=0)."""
+@pytest.mark.parametrize("fmt,B", [("int4", 2), ("int4", 5), ("int4", 16), ("fp32", 3)])
+def test_sequences_on_grid_slices(gpu, small, small_int4_path, fmt, B):
+    """Steps of B sequences run as B copies of the single-sequence kernel in
+    one launch, each on its own slice of the grid: after a prefill, every
+    sequence's greedy tokens, last logits, state and history equal those of
+    its own one-sequence launch bit for bit, and so do single steps (device
+    tokens); from the zero state the greedy chains follow the oracle (on the
+    dequantized weights for INT4) within 2e-5 with the same argmax."""
+    if fmt == "int4":
+        path, dq = small_int4_path
+        kw = dict(weights="int4", block=32)
+    else:
+        _, dq, path = small
+        kw = {}
+    hm = _model(path, SMALL, max_batch=B, **kw)
+    h1 = _model(path, SMALL, **kw)
+    assert h1.persistent_grid > 0
+    g = hm.persistent_grid_for(B)
+    assert g > 0 and g % B == 0, g
+    print(f"small {fmt} B={B}: {g // B} workgroups per sequence", flush=True)
+    rng = np.random.default_rng(100 + B)
+    prompts = rng.integers(0, SMALL.vocab_size, (B, 20)).astype(np.int32)
+    hm.prefill_batch(torch.from_numpy(prompts).to(gpu))
+    s0, k0 = (x.clone() for x in hm.get_state(B))
+    start = torch.from_numpy(rng.integers(0, SMALL.vocab_size, B).astype(np.int32)).to(gpu)
+    n = 9
+    lg = torch.empty(B, SMALL.vocab_size, device=gpu)
+    out = hm.decode_greedy(start, n, logits=lg).cpu().numpy()
+    s1, k1 = (x.cpu().numpy() for x in hm.get_state(B))
+    one = hm.step_batch(torch.from_numpy(out[-1]).to(gpu)).cpu().numpy()
+    lg = lg.cpu().numpy()
+    for b in range(B):
+        h1.set_state(s0[b:b + 1], k0[b:b + 1])
+        lb = torch.empty(1, SMALL.vocab_size, device=gpu)
+        ob = h1.decode_greedy(start[b:b + 1], n, logits=lb).cpu().numpy()[:, 0]
+        assert np.array_equal(ob, out[:, b]), b
+        assert np.array_equal(lb.cpu().numpy()[0], lg[b]), b
+        sb, kb = (x.cpu().numpy()[0] for x in h1.get_state(1))
+        assert np.array_equal(sb, s1[b]) and np.array_equal(kb, k1[b]), b
+        step = h1.step_batch(torch.from_numpy(out[-1, b:b + 1]).to(gpu)).cpu().numpy()[0]
+        assert np.array_equal(step, one[b]), b
+    hm.reset()
+    orc = oracle.SnOracle(dq, batch=B)
+    cur = rng.integers(0, SMALL.vocab_size, B).astype(np.int32)
+    out = hm.decode_greedy(torch.from_numpy(cur).to(gpu), 6).cpu().numpy()
+    for i in range(6):
+        ref = orc.step(cur)
+        nxt = ref.argmax(1).astype(np.int32)
+        assert np.array_equal(out[i], nxt), i
+        cur = nxt
+    a = hm.step_batch(torch.from_numpy(cur).to(gpu)).cpu().numpy()
+    assert np.abs(a - orc.step(cur)).max() < TOL
+    hm.close()
+    h1.close()
+
+
+def test_sequences_on_grid_slices_timeout(gpu, small_int4_path, monkeypatch):
+    """A time-out in a launch of four sequences ends every slice (the error
+    word is shared): the call reports it, all four sequences are refused as
+    part-stepped, setting the state of three of them is not enough, and after
+    all four are set the handle steps them as the oracle does."""
     path, dq = small_int4_path
-    hm = _model(path, SMALL, weights="int4", block=32, max_batch=2)
-    orc = oracle.SnOracle(dq, batch=2)
-    rng = np.random.default_rng(22)
-    print("two-sequence kernel: stepping", flush=True)
-    for _ in range(6):
-        t = rng.integers(0, SMALL.vocab_size, 2).astype(np.int32)
-        a = hm.step_batch(torch.from_numpy(t).to(gpu)).cpu().numpy()
-        b = orc.step(t)
-        assert np.abs(a - b).max() < TOL and np.array_equal(a.argmax(1), b.argmax(1))
-    print("two-sequence kernel: greedy chains", flush=True)
-    cur = np.array([7, 9], np.int32)
-    lg = torch.empty(2, SMALL.vocab_size, device=gpu)
-    for n in (5, 3):
-        out = hm.decode_greedy(torch.from_numpy(cur).to(gpu), n, logits=lg).cpu().numpy()
-        for i in range(n):
-            ref = orc.step(cur)
-            nxt = ref.argmax(1).astype(np.int32)
-            assert np.array_equal(out[i], nxt), (n, i)
-            cur = nxt
-        assert np.abs(lg.cpu().numpy() - ref).max() < TOL
-    saved = [x.clone() for x in hm.get_state(2)]
+    B = 4
     monkeypatch.setenv("SNHIP_PERSIST_SPIN", "2048")
-    hm2 = _model(path, SMALL, weights="int4", block=32, max_batch=2)
-    hm2.set_state(*saved)
+    hm = _model(path, SMALL, weights="int4", block=32, max_batch=B)
+    assert hm.persistent_grid_for(B) > 0
+    orc = oracle.SnOracle(dq, batch=B)
+    cur = np.array([7, 9, 11, 13], np.int32)
+    t = torch.from_numpy(cur).to(gpu)
+    a = hm.step_batch(t).cpu().numpy()
+    assert np.abs(a - orc.step(cur)).max() < TOL
+    saved = [x.clone() for x in hm.get_state(B)]
+    print("four sequences on grid slices: time-out", flush=True)
     monkeypatch.setenv("SNHIP_PERSIST_STALL", "1")
-    print("two-sequence kernel: time-out", flush=True)
     with pytest.raises(RuntimeError, match="timed out"):
-        hm2.decode_greedy(torch.from_numpy(cur).to(gpu), 2)
+        hm.decode_greedy(t, 2)
     monkeypatch.delenv("SNHIP_PERSIST_STALL")
     with pytest.raises(RuntimeError, match="part-stepped"):
-        hm2.step_batch(torch.from_numpy(cur).to(gpu))
-    hm2.set_state(saved[0][:1], saved[1][:1])      # sequence 1 may still be part-stepped
+        hm.step_batch(t)
+    hm.set_state(saved[0][:3], saved[1][:3])
     with pytest.raises(RuntimeError, match="part-stepped"):
-        hm2.step_batch(torch.from_numpy(cur).to(gpu))
-    hm2.set_state(*saved)
-    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
-    a = hm2.step_batch(torch.from_numpy(cur).to(gpu)).cpu().numpy()
-    assert np.abs(a - orc.step(cur)).max() < TOL
-    monkeypatch.setenv("SNHIP_PERSIST_MS", "0")
-    hg = _model(path, SMALL, weights="int4", block=32, max_batch=2)
-    monkeypatch.delenv("SNHIP_PERSIST_MS")
-    hg.set_state(*saved)
+        hm.step_batch(t)
     hm.set_state(*saved)
-    t = torch.from_numpy(cur).to(gpu)
-    assert torch.equal(hm.decode_greedy(t, 6), hg.decode_greedy(t, 6))
-    for h in (hm, hm2, hg):
-        h.close()
+    monkeypatch.delenv("SNHIP_PERSIST_SPIN")
+    a = hm.step_batch(t).cpu().numpy()
+    assert np.abs(a - orc.step(cur)).max() < TOL
+    hm.close()

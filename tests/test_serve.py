@@ -5,7 +5,8 @@ Requests must be independent: under continuous batching every request's
 greedy tokens equal those of the same request run alone through the oracle
 (prompt stepped token by token as sn_prefill does, then greedy), whatever the
 admission order, slot moves and batch size of each step (1..max_batch, so the
-B=1 persistent kernel, the GEMV batch and the batched kernel all take part).
+B=1 persistent kernel, the same kernel on a grid slice per sequence (2..4
+sequences) and the batched kernel (5..8) all take part).
 """
 from __future__ import annotations
 
