@@ -67,9 +67,10 @@ SCAN_TRAFFIC_BYTES = 1_611_150_336
 # decode`, calibrated like the scan's and divided by the call's steps. Filled
 # from the tables of profiles/decode_pmc_traffic.md.
 DECODE_TRAFFIC: dict = {
-    ("int4", 1): 96_622_294, ("int4", 8): 156_227_720, ("int4", 32): 174_581_634,
-    ("fp32", 1): 517_615_839, ("fp32", 64): 627_481_094, ("fp16", 1): 285_593_769,
-    ("small", 1): 1_378_358, ("rwkv7", 1): 153_236_742, ("rwkv7", 64): 843_919_572,
+    ("int4", 1): 96_466_653, ("int4", 8): 155_521_575, ("int4", 32): 174_586_226,
+    ("fp32", 1): 517_571_761, ("fp32", 64): 627_475_191, ("fp16", 1): 285_594_889,
+    ("small", 1): 1_388_874, ("rwkv7", 1): 116_087_372, ("rwkv7", 64): 843_921_460,
+    ("rwkv7-persist", 1): 153_085_884,
 }
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
 
@@ -697,7 +698,8 @@ def cpu_gemv_i4_baseline(w4):
 def bench_rwkv7(cpu: bool):
     """RWKV-7 12 layers, D=768, 12 heads of 64, F=3072, vocab 65536 (seed-2
     synthetic weights), INT4 g32 quantized at load: a 512-token random prompt
-    by stepping, then 128 greedy steps on the device at B=1 and B=64."""
+    by stepping, then 128 greedy steps on the device at B=1 and B=64 (the
+    default, bit-exact step), and at B=1 on the opt-in persistent step."""
     import tempfile
 
     from sunnynet_amd.runtime.rwkv7 import HipRwkv7
@@ -713,8 +715,17 @@ def bench_rwkv7(cpu: bool):
     out = {"model": "RWKV-7 L=12 D=768 H=12x64 F=3072 V=65536 ranks (64,64,32,128), INT4 g32",
            "steps": 128, "prompt": 512, "cases": []}
     g = torch.Generator(device="cpu").manual_seed(321)
-    for B in (1, 64):
+    # The default (bit-exact per-kernel) step at B=1 and B=64, then the opt-in
+    # persistent step at B=1 (SNHIP_RK_PERSIST=1: not bit-exact, measured up
+    # to 1.3e-4 from sn_rk_step), reported beside it.
+    for B, persist in ((1, False), (64, False), (1, True)):
+        if persist:
+            os.environ["SNHIP_RK_PERSIST"] = "1"
         hm = HipRwkv7(p32, weights="int4", block=32, max_batch=B)
+        os.environ.pop("SNHIP_RK_PERSIST", None)
+        if persist and not hm.persist_grid:
+            hm.close()
+            continue
         prompts = torch.randint(0, cfg.vocab, (out["prompt"], B), generator=g, dtype=torch.int32).to(dev)
         lg = torch.empty(B, cfg.vocab, device=dev)
         for t in range(out["prompt"]):
@@ -728,11 +739,14 @@ def bench_rwkv7(cpu: bool):
                   "per-kernel step: k_rkq_ln, k_rkq_mm_q4, k_rkq_heads")
         hm.close()
         rl = step_roofline(rwkv7_step_bytes(cfg, B), rwkv7_step_flops(cfg, B), ms * 1e3, kernel,
-                           DECODE_TRAFFIC.get(("rwkv7", B)))
+                           DECODE_TRAFFIC.get(("rwkv7-persist" if persist else "rwkv7", B)))
         rl["note"] = "bytes: weights plus the 64x64 head states read and written per sequence"
         case = {"weights": "int4-g32", "B": B, "us_per_step": round(ms * 1e3, 2),
-                "tok_s": round(B / ms * 1e3, 1), "roofline": rl}
-        log(f"[bench] rwkv7 B={B}: {case['us_per_step']} us/step, {case['tok_s']} tok/s")
+                "tok_s": round(B / ms * 1e3, 1), "roofline": rl,
+                "parity": ("opt-in (SNHIP_RK_PERSIST=1): logits within 2e-4 of sn_rk_step, not bit-exact"
+                           if persist else "bit-exact to sn_rk_step")}
+        log(f"[bench] rwkv7 B={B}{' opt-in persistent' if persist else ''}: {case['us_per_step']} us/step, "
+            f"{case['tok_s']} tok/s")
         out["cases"].append(case)
     if cpu:
         out["cpu_baseline"] = cpu_rwkv7_baseline(w, tmp)
@@ -912,7 +926,8 @@ def profile_sequence(which: str) -> int:
         prefill of 1024 random ids, then 256 greedy steps at B=1, fp32 then INT4.
     batch: 64 greedy steps from random tokens at fp32 B=64, INT4 B=8, INT4 B=32.
     rwkv: RWKV-7 (12 layers, D=768, vocab 65536, seed-2 weights, INT4 g32 at
-        load), 8 warm-up then 64 greedy steps at B=1 and at B=64.
+        load), 8 warm-up then 64 greedy steps at B=1 and at B=64, then at B=1
+        on the opt-in persistent step.
     small: SunnyNet small (seed 0), prefill of 256 random ids, 64 greedy steps.
     """
     import tempfile
@@ -926,8 +941,11 @@ def profile_sequence(which: str) -> int:
         from sunnynet_amd.rwkv7 import RWKV_CFG4, init_rwkv7, pack_rwkv7_blob
         cfg = RWKV_CFG4
         path = _write_blob(tmp, "rk.bin", pack_rwkv7_blob(init_rwkv7(cfg, 2)))
-        for B in (1, 64):
+        for B, persist in ((1, False), (64, False), (1, True)):
+            if persist:
+                os.environ["SNHIP_RK_PERSIST"] = "1"
             hm = HipRwkv7(path, weights="int4", block=32, max_batch=B)
+            os.environ.pop("SNHIP_RK_PERSIST", None)
             tok = torch.randint(0, cfg.vocab, (B,), generator=g, dtype=torch.int32).to(dev)
             hm.decode_greedy(tok, 8)
             hm.decode_greedy(tok, 64)
@@ -979,8 +997,8 @@ def pmc_probe_decode() -> int:
     between its two markers. The cases, in order, with steps per call:
     SunnyNet-100M INT4 g32 B=1 (16), B=8 (8), B=32 (8); fp32 B=1 (16), B=64
     (8); fp16 B=1 (16); SunnyNet small fp32 B=1 (16); RWKV-7 INT4 g32 B=1
-    (16), B=64 (4). Each case's line on stderr names its order, steps and
-    algorithmic bytes per step."""
+    (16), B=64 (4), B=1 on the opt-in persistent step (16). Each case's line on
+    stderr names its order, steps and algorithmic bytes per step."""
     import tempfile
 
     from sunnynet_amd import _native
@@ -1047,10 +1065,14 @@ def pmc_probe_decode() -> int:
     rc = RWKV_CFG4
     path = _write_blob(tmp, "rk.bin", pack_rwkv7_blob(init_rwkv7(rc, 2)))
     nw = rc.matmul_params()
-    for B, n in ((1, 16), (64, 4)):
+    for B, n, persist in ((1, 16, False), (64, 4, False), (1, 16, True)):
+        if persist:
+            os.environ["SNHIP_RK_PERSIST"] = "1"
         hm = HipRwkv7(path, weights="int4", block=32, max_batch=B)
+        os.environ.pop("SNHIP_RK_PERSIST", None)
         marker()
-        measured(f"RWKV-7 int4 B={B}", hm, rc.vocab, B, n, rwkv7_step_bytes(rc, B))
+        measured(f"RWKV-7 int4 B={B}{' persistent (opt-in)' if persist else ''}", hm, rc.vocab, B, n,
+                 rwkv7_step_bytes(rc, B))
         hm.close()
     torch.cuda.synchronize()
     return 0

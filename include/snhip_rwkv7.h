@@ -63,7 +63,7 @@ int snhip_rk_vocab(const SnHipRwkv7* m);
 int snhip_rk_ready(const SnHipRwkv7* m);
 
 /* ---- extensions ---------------------------------------------------------- */
-/* Time-outs: the single-sequence persistent step updates S and shift in place
+/* Time-outs: the opt-in persistent step updates S and shift in place
  * layer by layer; a call whose launch timed out returns SNHIP_E_DEVICE and the
  * handle refuses every stepping call (SNHIP_E_DEVICE) until snhip_rk_reset or
  * snhip_rk_set_state_dev. The void mirrors drop the status: use
@@ -71,11 +71,23 @@ int snhip_rk_ready(const SnHipRwkv7* m);
 snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream);
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m);
 /* Workgroups of the one-launch-per-step kernel that runs steps of a single
- * sequence (0 when that path is off: SNHIP_RK_PERSIST=0, no cooperative
- * launch, or a shape it does not take). Calls that take it (B = 1) return
- * once their steps have finished, so that a grid-barrier time-out is
- * reported as SNHIP_E_DEVICE. No reference counterpart. */
+ * sequence, or 0 when that path is off. It is off unless SNHIP_RK_PERSIST=1
+ * is in the environment at load (and needs a cooperative launch and a shape
+ * it takes): its sums run in parallel rather than in the reference's order,
+ * and its logits were measured up to 1.3e-4 from the reference's sn_rk_step
+ * (the default per-kernel step is bit-exact), at 1.8x the speed at B = 1.
+ * Calls that take it return once their steps have finished, so that a
+ * time-out of its exchange waits is reported as SNHIP_E_DEVICE. No
+ * reference counterpart. */
 int32_t snhip_rk_persist_grid(const SnHipRwkv7* m);
+/* With that kernel on: workgroups of the launch when steps of B sequences
+ * run as B copies of it, each sequence on its own equal slice of the grid
+ * (B * slice; for B = 1 the value above), or 0 when steps of B sequences take
+ * the per-kernel path. B <= 8 by default; SNHIP_RK_PERSIST_MI=n in the
+ * environment at load sets the limit (1: off, at most 32). Each sequence's
+ * results equal its one-sequence launch's bit for bit; time-outs behave as
+ * for one sequence. No reference counterpart. */
+int32_t snhip_rk_persist_grid_batch(const SnHipRwkv7* m, int32_t B);
 /* One step of sequences [0, B): tokens_dev (B) int32, logits_dev (B, vocab). */
 snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
                                      float* logits_dev);

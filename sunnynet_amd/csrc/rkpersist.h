@@ -34,9 +34,17 @@ struct RkPArgs {
     float* logits;            // (vocab)
     unsigned long long* keys; // (2 grid) exchange words of the argmax keys
     int32_t* tok;             // the step's input token (and, greedy, the next one)
-    int32_t* tok_hist;
-    int32_t* counter;
+    int32_t* tok_hist;        // greedy: (steps, ni) tokens, from row hist0 on
+    int32_t* counter;         // set to hist0 + nsteps after a greedy launch
     int hist_cap, greedy;
+    int hist0;                // greedy steps of the call before this launch
+    // Independent sequences, one per equal slice of the grid (0 or 1: one).
+    // Sequence q runs on workgroups [q G, (q+1) G), G = grid / ni, with its
+    // own state (S + q L NH 64 64, shift + q L 2 D, vfirst + q D), exchange
+    // and key words (xch and keys + q words), token tok[q], token column q of
+    // tok_hist and logits + q vocab.
+    int ni;
+    size_t words;
     unsigned epoch;           // the epoch of the launch's first step (> 0; step st uses epoch + st, and
                               // no epoch is used twice between two clearings of the words)
     int nsteps;               // steps of the launch (greedy; 1 otherwise)
@@ -46,6 +54,7 @@ struct RkPArgs {
 };
 
 constexpr int kRkPMaxD = 1024, kRkPMaxF = 4096, kRkPRank = 256, kRkPMaxGrid = 1024;
+constexpr int kRkPMiMax = 32;   // sequences one launch steps at most (a.ni)
 
 // Exchange words of one layer's slab (one 64-bit word per value: the epoch
 // of the launch that wrote it above the value's bits): r, k, v, y, x after

@@ -543,8 +543,20 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     __shared__ RkPLayer Ls2[2];                  // layer tables of layers l (l & 1) and l + 1
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wg = blockIdx.x, G0 = gridDim.x;
     const int D0 = A.D, F0 = A.F, L0 = A.L, NH0 = A.NH;
+    // Independent sequences run on equal slices of the grid: this workgroup
+    // is workgroup wg of sequence sq's G0 (one sequence: sq = 0, G0 = the grid).
+    const int NI = A.ni > 1 ? A.ni : 1;
+    const int G0 = gridDim.x / NI, sq = blockIdx.x / G0, wg = blockIdx.x - sq * G0;
+    if (NI > 1) {
+        A.S += (size_t)sq * L0 * NH0 * HS * HS;
+        A.shift += (size_t)sq * L0 * 2 * D0;
+        A.vfirst += (size_t)sq * D0;
+        A.xch += (size_t)sq * A.words;
+        A.keys += (size_t)sq * A.words;
+        A.tok += sq;
+        A.logits += (size_t)sq * A.vocab;
+    }
     if (tid == 0) sdead = 0;
     if (tid < (int)(sizeof(RkPLayer) / 4))
         reinterpret_cast<int*>(&Ls2[0])[tid] = reinterpret_cast<const int*>(A.layers)[tid];
@@ -558,7 +570,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     };
     float vfo = 0.0f;   // head owners, thread c < 64: v_first of channel c (layer 0's v)
     int tok = *A.tok;
-    const int cnt0 = *A.counter;
+    const int cnt0 = A.hist0;
 
     // Greedy launches run nsteps steps, step st with epoch A.epoch + st; every
     // workgroup reduces the argmax keys to the next step's token itself.
@@ -1040,12 +1052,13 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
             u64 m = kred[0];
             for (int w2 = 1; w2 < NW; ++w2) m = max(m, kred[w2]);
             tok = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull));
-            if (wg == 0 && tid == 0 && cnt0 + st < A.hist_cap) A.tok_hist[cnt0 + st] = tok;
+            const long hrow = (long)(cnt0 + st) * NI + sq;
+            if (wg == 0 && tid == 0 && hrow < A.hist_cap) A.tok_hist[hrow] = tok;
         }
     }   // steps
     if (wg == 0 && tid == 0) {
         *A.tok = tok;
-        *A.counter = cnt0 + A.nsteps;
+        if (sq == 0) *A.counter = cnt0 + A.nsteps;
     }
 }
 
@@ -1082,7 +1095,9 @@ int rkp_grid(int NH) {
 }
 
 snhip_status launch_rk_persist(const RkPArgs& a, int G, hipStream_t st) {
-    if (G < 8 || G % 8 || G < a.NH || G > kRkPMaxGrid) {
+    const int ni = a.ni > 1 ? a.ni : 1;
+    if (G % ni || G / ni < 8 || (G / ni) % 8 || G / ni < a.NH || G > kRkPMaxGrid ||
+        (ni > 1 && a.words < (size_t)a.L * rkp_slab(a.D, a.F) + 2 * (size_t)(G / ni))) {
         set_last_error("RWKV-7 persistent step: bad grid");
         return SNHIP_E_INVAL;
     }

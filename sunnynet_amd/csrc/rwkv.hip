@@ -156,6 +156,12 @@ struct SnHipRwkv7 {
     // One-sequence steps as one cooperative launch each (rkpersist.hip);
     // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
     int p_grid = 0;
+    // Steps of B = 2..p_mi_max sequences: the same kernel on a slice of
+    // p_mi_grid[B] workgroups per sequence, one launch for all; the words
+    // hold p_mi_max sequences' slabs, p_seq_words apart.
+    int p_mi_max = 0;
+    int p_mi_grid[snhip::kRkPMiMax + 1] = {};
+    size_t p_seq_words = 0;
     snhip::RkPArgs p_args{};
     unsigned p_epoch = 0;                 // the last epoch a persistent launch used
     unsigned long long* p_words = nullptr;   // exchange slabs and key words (zeroed: epoch 0)
@@ -271,15 +277,22 @@ bool take_mat(SnHipRwkv7* m, Cur& c, RMat& M, int in, int out, float* tmp0, floa
 
 RkPMat pmat(const RMat& M) { return RkPMat{M.w, M.q, M.sc, M.M, M.Kd, M.q ? M.block : 0}; }
 
-// The one-sequence persistent step (rkpersist.hip), when the device and the
-// shape allow it: its layer table, exchange slabs and key words. The grid is
-// at most one workgroup per CU, and at most the rows of the first product
-// (r, k, v and the LoRA middles) and of the channel-mix key, so that every
-// workgroup produces rows of both: the kernel relies on that to know when
-// every workgroup has read the shift vectors it then overwrites.
+// The one-sequence persistent step (rkpersist.hip), opt-in (SNHIP_RK_PERSIST=1
+// at load), when the device and the shape allow it: its layer table,
+// exchange slabs and key words. It is not the default because its products
+// and LayerNorms sum in parallel, not in the reference's sequential order,
+// and RWKV-7 amplifies that rounding: on the 12-layer model (INT4 g32) its
+// logits were up to 1.26e-4 from sn_rk_step over 256 first steps from the
+// zero state (32 of them past 2e-5) and up to 2.7e-5 over a 512-token
+// prompt and 128 greedy steps, while the per-kernel step is bit-exact. It
+// runs a step in 369 us against 658 for the per-kernel step at B = 1.
+// The grid is at most one workgroup per CU (SNHIP_RK_PERSIST_WG caps it; it
+// is rounded down to a multiple of 8), and at most the rows of the first
+// product (r, k, v and the LoRA middles) and of the channel-mix key, so that
+// every workgroup produces rows of both: the kernel relies on that to know
+// when every workgroup has read the shift vectors it then overwrites.
 void setup_rk_persist(SnHipRwkv7* m) {
-    if (const char* e = getenv("SNHIP_RK_PERSIST"))
-        if (e[0] == '0') return;
+    if (env_unsigned("SNHIP_RK_PERSIST", 0, 0) == 0) return;
     m->p_spin = env_unsigned("SNHIP_PERSIST_SPIN", m->p_spin, 1);
     std::vector<int> rk(4 * (size_t)m->L);
     for (int l = 0; l < m->L; ++l) {
@@ -288,6 +301,7 @@ void setup_rk_persist(SnHipRwkv7* m) {
     }
     if (!rkp_shape_ok(m->D, m->F, m->HS, m->NH, reinterpret_cast<const int(*)[4]>(rk.data()), m->L)) return;
     int G = rkp_grid(m->NH);
+    if (const char* e = getenv("SNHIP_RK_PERSIST_WG")) G = std::min(G, atoi(e));
     int p1rows = 1 << 30;
     for (int l = 0; l < m->L; ++l) p1rows = std::min(p1rows, 3 * m->D + rk[4 * l] + rk[4 * l + 1] + rk[4 * l + 3]);
     G = std::min(G, std::min(p1rows, m->F)) / 8 * 8;
@@ -303,8 +317,26 @@ void setup_rk_persist(SnHipRwkv7* m) {
         P.a0 = A.a0; P.v0 = A.v0; P.kk = A.kk; P.ka = A.ka; P.rk = A.rk; P.lnxw = A.lnxw; P.lnxb = A.lnxb;
         P.cmk_lerp = A.cmk_lerp;
     }
+    // Slices for B = 2..p_mi_max (SNHIP_RK_PERSIST_MI=n, default 8): the
+    // largest multiple of 8 workgroups, at least the head count, that B
+    // slices fit in the one-sequence grid. Each sequence's results equal its
+    // one-sequence launch's bit for bit (the kernel's arithmetic does not
+    // depend on the grid size). Measured at B=1 on one MI355X (RWKV-7
+    // 12 x 768, INT4 g32): 372.6 us/step on 256 workgroups, 442.1 on 128,
+    // 597.5 on 64, 901.2 on 32, 1558.0 on 16, against 1,225.7 (B=2) and
+    // 1,348.1 (B=8) us/step for the per-kernel step.
+    m->p_mi_max = 0;
+    const int lim = std::min(std::min(m->max_batch, kRkPMiMax),
+                             (int)std::min(env_unsigned("SNHIP_RK_PERSIST_MI", 8, 0), (unsigned)kRkPMiMax));
+    for (int b = 2; b <= lim; ++b) {
+        const int g = G / b / 8 * 8;
+        if (g < 8 || g < m->NH) break;
+        m->p_mi_grid[b] = g;
+        m->p_mi_max = b;
+    }
     RkPLayer* dtab = ralloc<RkPLayer>(m, tab.size());
-    m->p_nwords = (size_t)m->L * rkp_slab(m->D, m->F) + 2 * (size_t)G;
+    m->p_seq_words = (size_t)m->L * rkp_slab(m->D, m->F) + 2 * (size_t)G;
+    m->p_nwords = m->p_seq_words * std::max(1, m->p_mi_max);
     m->p_words = ralloc<unsigned long long>(m, m->p_nwords);
     m->p_err = ralloc<unsigned>(m, 1);
     if (!dtab || !m->p_words || !m->p_err ||
@@ -320,23 +352,30 @@ void setup_rk_persist(SnHipRwkv7* m) {
     a.S = m->S; a.shift = m->shift; a.vfirst = m->vfirst; a.xch = xch; a.keys = keys;
     a.tok = m->tok; a.counter = m->counter;
     a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = 0;
+    a.words = m->p_seq_words;
     m->p_grid = G;
 }
 
-// reps persistent steps of sequence 0: greedy, one launch of up to
-// kRkPStepsPerLaunch steps at a time, otherwise one launch per step; every
-// step has its own epoch. The call waits for them and reports a time-out of
-// an exchange wait as an error. The kernel updates S and shift in place layer
-// by layer, so a time-out leaves them part-stepped: the handle is then refused
-// for stepping until its state is reset or set.
+// Do steps of B sequences run as B slices of the persistent kernel?
+bool uses_mi(const SnHipRwkv7* m, int B) { return m->p_grid > 0 && B >= 2 && B <= m->p_mi_max; }
+
+// reps persistent steps of sequences [0, B) (B = 1, or 2..p_mi_max on a grid
+// slice each): greedy, one launch of up to kRkPStepsPerLaunch steps at a
+// time, otherwise one launch per step; every step has its own epoch. The
+// call waits for them and reports a time-out of an exchange wait as an error.
+// The kernel updates S and shift in place layer by layer, so a time-out
+// leaves them part-stepped: the handle is then refused for stepping until its
+// state is reset or set.
 constexpr int kRkPStepsPerLaunch = 1024;
-snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps) {
+snhip_status run_persist(SnHipRwkv7* m, int B, float* logits_out, bool greedy, int reps) {
     RkPArgs a = m->p_args;
     a.stall = env_unsigned("SNHIP_PERSIST_STALL", 0, 0);
     a.logits = logits_out;
     a.greedy = greedy ? 1 : 0;
     a.tok_hist = m->tok_hist;
     a.hist_cap = m->hist_cap;
+    a.ni = B;
+    const int grid = B == 1 ? m->p_grid : B * m->p_mi_grid[B];
     SNHIP_CHECK(hipMemsetAsync(m->p_err, 0, sizeof(unsigned), m->work));
     for (int i = 0; i < reps;) {
         const int n = greedy ? std::min(reps - i, kRkPStepsPerLaunch) : 1;
@@ -347,8 +386,9 @@ snhip_status run_persist(SnHipRwkv7* m, float* logits_out, bool greedy, int reps
         }
         a.epoch = m->p_epoch + 1;
         a.nsteps = n;
+        a.hist0 = i;
         m->p_epoch += (unsigned)n;
-        const snhip_status rc = launch_rk_persist(a, m->p_grid, m->work);
+        const snhip_status rc = launch_rk_persist(a, grid, m->work);
         if (rc != SNHIP_OK) return rc;
         i += n;
     }
@@ -657,8 +697,8 @@ snhip_status run_steps(SnHipRwkv7* m, int B, float* logits_out, bool greedy, int
     if (check_usable(m) != SNHIP_OK) return SNHIP_E_DEVICE;
     SNHIP_CHECK(hipEventRecord(m->ev_in, m->stream));
     SNHIP_CHECK(hipStreamWaitEvent(m->work, m->ev_in, 0));
-    if (B == 1 && m->p_grid > 0) {
-        const snhip_status rc = run_persist(m, logits_out, greedy, reps);
+    if ((B == 1 && m->p_grid > 0) || uses_mi(m, B)) {
+        const snhip_status rc = run_persist(m, B, logits_out, greedy, reps);
         if (rc != SNHIP_OK) return rc;
     } else if (!m->use_graphs) {
         for (int i = 0; i < reps; ++i) {
@@ -800,6 +840,12 @@ snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream) {
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m) { return m ? m->max_batch : 0; }
 
 int32_t snhip_rk_persist_grid(const SnHipRwkv7* m) { return m ? m->p_grid : 0; }
+
+int32_t snhip_rk_persist_grid_batch(const SnHipRwkv7* m, int32_t B) {
+    if (!m || B < 1 || B > m->max_batch) return 0;
+    if (B == 1) return m->p_grid;
+    return uses_mi(m, B) ? B * m->p_mi_grid[B] : 0;
+}
 
 snhip_status snhip_rk_step_batch_dev(SnHipRwkv7* m, const int32_t* tokens_dev, int32_t B,
                                      float* logits_dev) {

@@ -55,6 +55,11 @@ class HipRwkv7:
         (0 when off)."""
         return int(self._lib.snhip_rk_persist_grid(self._h))
 
+    def persist_grid_for(self, B: int) -> int:
+        """Workgroups of the persistent launch for steps of B sequences, each
+        on its own slice of the grid (0: B takes the per-kernel path)."""
+        return int(self._lib.snhip_rk_persist_grid_batch(self._h, B))
+
     def _bind_stream(self):
         _native.check(self._lib.snhip_rk_set_stream(self._h, _native.stream_handle(self.device)),
                       "snhip_rk_set_stream")
