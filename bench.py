@@ -699,7 +699,9 @@ def bench_rwkv7(cpu: bool):
     """RWKV-7 12 layers, D=768, 12 heads of 64, F=3072, vocab 65536 (seed-2
     synthetic weights), INT4 g32 quantized at load: a 512-token random prompt
     by stepping, then 128 greedy steps on the device at B=1 and B=64 (the
-    default, bit-exact step), and at B=1 on the opt-in persistent step."""
+    default steps, both bit-exact: the exact one-launch kernel at B=1, the
+    per-kernel step at B=64), and at B=1 on the opt-in fast one-launch
+    kernel."""
     import tempfile
 
     from sunnynet_amd.runtime.rwkv7 import HipRwkv7
@@ -715,8 +717,8 @@ def bench_rwkv7(cpu: bool):
     out = {"model": "RWKV-7 L=12 D=768 H=12x64 F=3072 V=65536 ranks (64,64,32,128), INT4 g32",
            "steps": 128, "prompt": 512, "cases": []}
     g = torch.Generator(device="cpu").manual_seed(321)
-    # The default (bit-exact per-kernel) step at B=1 and B=64, then the opt-in
-    # persistent step at B=1 (SNHIP_RK_PERSIST=1: not bit-exact, measured up
+    # The default (bit-exact) steps at B=1 and B=64, then the opt-in fast
+    # one-launch step at B=1 (SNHIP_RK_PERSIST=1: not bit-exact, measured up
     # to 1.3e-4 from sn_rk_step), reported beside it.
     for B, persist in ((1, False), (64, False), (1, True)):
         if persist:
@@ -735,17 +737,24 @@ def bench_rwkv7(cpu: bool):
         torch.cuda.synchronize()
         steps = out["steps"]
         ms = _time_ms(lambda: hm.decode_greedy(tok, steps)) / steps
-        kernel = ("k_rk_persist (the whole step)" if hm.persist_grid and B == 1 else
+        exact = bool(hm.persist_grid) and hm.persist_exact and B == 1
+        kernel = ("k_rk_exact (the whole step)" if exact else
+                  "k_rk_persist (the whole step)" if hm.persist_grid and B == 1 else
                   "per-kernel step: k_rkq_ln, k_rkq_mm_q4, k_rkq_heads")
         hm.close()
+        key = ("rwkv7-persist" if persist else "rwkv7-exact" if exact else "rwkv7", B)
         rl = step_roofline(rwkv7_step_bytes(cfg, B), rwkv7_step_flops(cfg, B), ms * 1e3, kernel,
-                           DECODE_TRAFFIC.get(("rwkv7-persist" if persist else "rwkv7", B)))
+                           DECODE_TRAFFIC.get(key))
         rl["note"] = "bytes: weights plus the 64x64 head states read and written per sequence"
+        if exact:
+            rl["note"] += ("; this kernel reads fp32 copies of the layer matrices (each output one "
+                           "sequential FMA chain in the reference's order), and its floor is those "
+                           "chains' latency, not HBM")
         case = {"weights": "int4-g32", "B": B, "us_per_step": round(ms * 1e3, 2),
                 "tok_s": round(B / ms * 1e3, 1), "roofline": rl,
                 "parity": ("opt-in (SNHIP_RK_PERSIST=1): logits within 2e-4 of sn_rk_step, not bit-exact"
                            if persist else "bit-exact to sn_rk_step")}
-        log(f"[bench] rwkv7 B={B}{' opt-in persistent' if persist else ''}: {case['us_per_step']} us/step, "
+        log(f"[bench] rwkv7 B={B}{' opt-in fast one-launch' if persist else ''}: {case['us_per_step']} us/step, "
             f"{case['tok_s']} tok/s")
         out["cases"].append(case)
     if cpu:
@@ -926,8 +935,8 @@ def profile_sequence(which: str) -> int:
         prefill of 1024 random ids, then 256 greedy steps at B=1, fp32 then INT4.
     batch: 64 greedy steps from random tokens at fp32 B=64, INT4 B=8, INT4 B=32.
     rwkv: RWKV-7 (12 layers, D=768, vocab 65536, seed-2 weights, INT4 g32 at
-        load), 8 warm-up then 64 greedy steps at B=1 and at B=64, then at B=1
-        on the opt-in persistent step.
+        load), 8 warm-up then 64 greedy steps at B=1 (the exact one-launch
+        kernel) and at B=64, then at B=1 on the opt-in fast one-launch kernel.
     small: SunnyNet small (seed 0), prefill of 256 random ids, 64 greedy steps.
     """
     import tempfile
@@ -950,7 +959,8 @@ def profile_sequence(which: str) -> int:
             hm.decode_greedy(tok, 8)
             hm.decode_greedy(tok, 64)
             torch.cuda.synchronize()
-            log(f"[profile] rwkv7 int4 B={B}: 64 greedy steps (persistent grid {hm.persist_grid})")
+            log(f"[profile] rwkv7 int4 B={B}: 64 greedy steps (one-launch grid {hm.persist_grid}, "
+                f"exact {hm.persist_exact})")
             hm.close()
         return 0
     if which == "small":
@@ -1071,7 +1081,9 @@ def pmc_probe_decode() -> int:
         hm = HipRwkv7(path, weights="int4", block=32, max_batch=B)
         os.environ.pop("SNHIP_RK_PERSIST", None)
         marker()
-        measured(f"RWKV-7 int4 B={B}{' persistent (opt-in)' if persist else ''}", hm, rc.vocab, B, n,
+        label = (" fast one-launch (opt-in)" if persist else
+                 " exact one-launch" if hm.persist_grid and hm.persist_exact and B == 1 else "")
+        measured(f"RWKV-7 int4 B={B}{label}", hm, rc.vocab, B, n,
                  rwkv7_step_bytes(rc, B))
         hm.close()
     torch.cuda.synchronize()

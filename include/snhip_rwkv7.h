@@ -63,27 +63,30 @@ int snhip_rk_vocab(const SnHipRwkv7* m);
 int snhip_rk_ready(const SnHipRwkv7* m);
 
 /* ---- extensions ---------------------------------------------------------- */
-/* Time-outs: the opt-in persistent step updates S and shift in place
+/* Time-outs: the one-launch steps update S and shift in place
  * layer by layer; a call whose launch timed out returns SNHIP_E_DEVICE and the
  * handle refuses every stepping call (SNHIP_E_DEVICE) until snhip_rk_reset or
  * snhip_rk_set_state_dev. The void mirrors drop the status: use
  * snhip_abi_rwkv7_step / snhip_abi_rwkv7_prefill to see it. */
 snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream);
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m);
-/* Workgroups of the one-launch-per-step kernel that runs steps of a single
- * sequence, or 0 when that path is off. It is off unless SNHIP_RK_PERSIST=1
- * is in the environment at load (and needs a cooperative launch and a shape
- * it takes): its sums run in parallel rather than in the reference's order,
- * and its logits were measured up to 1.3e-4 from the reference's sn_rk_step
- * (the default per-kernel step is bit-exact), at 1.8x the speed at B = 1.
- * Calls that take it return once their steps have finished, so that a
- * time-out of its exchange waits is reported as SNHIP_E_DEVICE. No
- * reference counterpart. */
+/* Workgroups of the one-launch step that runs steps of a single sequence
+ * (one cooperative launch per call of greedy steps, one per step otherwise),
+ * or 0 when steps of one sequence take the per-kernel step (no cooperative
+ * launch, a shape it does not take, or SNHIP_RK_EXACT=0 in the environment
+ * at load). By default it is the exact-order kernel, whose logits equal the
+ * reference's sn_rk_step bit for bit. With SNHIP_RK_PERSIST=1 at load it is
+ * instead a kernel that sums in parallel, not bit-exact (measured up to
+ * 1.3e-4 from sn_rk_step). Calls that take either return once their steps
+ * have finished, so that a time-out of an exchange wait is reported as
+ * SNHIP_E_DEVICE. No reference counterpart. */
 int32_t snhip_rk_persist_grid(const SnHipRwkv7* m);
-/* With that kernel on: workgroups of the launch when steps of B sequences
- * run as B copies of it, each sequence on its own equal slice of the grid
- * (B * slice; for B = 1 the value above), or 0 when steps of B sequences take
- * the per-kernel path. B <= 8 by default; SNHIP_RK_PERSIST_MI=n in the
+/* 1 when that one-launch step is the exact-order kernel, else 0. */
+int32_t snhip_rk_persist_exact(const SnHipRwkv7* m);
+/* Workgroups of the launch when steps of B sequences run as B copies of that
+ * one-launch step, each sequence on its own equal slice of the grid (B *
+ * slice; for B = 1 the value above), or 0 when steps of B sequences take the
+ * per-kernel path. B <= 8 by default; SNHIP_RK_PERSIST_MI=n in the
  * environment at load sets the limit (1: off, at most 32). Each sequence's
  * results equal its one-sequence launch's bit for bit; time-outs behave as
  * for one sequence. No reference counterpart. */

@@ -109,6 +109,7 @@ _SIGS = {
     "snhip_rk_max_batch": (I32, [V]),
     "snhip_rk_persist_grid": (I32, [V]),
     "snhip_rk_persist_grid_batch": (I32, [V, I32]),
+    "snhip_rk_persist_exact": (I32, [V]),
     "snhip_rk_step_batch_dev": (I32, [V, V, I32, V]),
     "snhip_rk_decode_greedy_dev": (I32, [V, V, I32, I32, V, V]),
     "snhip_rk_get_state_dev": (I32, [V, V, V, I32]),

@@ -70,8 +70,10 @@ inline constexpr uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-// glibc expf (round to nearest).
-__host__ __device__ inline float expf(float x) {
+// glibc expf (round to nearest), with the table read from tab (kExp2Tab's
+// entries; a kernel may pass a copy in LDS: indexed per lane, the constant
+// array is a global-memory load on the critical path).
+__host__ __device__ inline float expf_tab(float x, const uint64_t* tab) {
     constexpr double kN = 32.0;
     constexpr double C0 = 0x1.c6af84b912394p-5 / kN / kN / kN;
     constexpr double C1 = 0x1.ebfce50fac4f3p-3 / kN / kN;
@@ -92,7 +94,7 @@ __host__ __device__ inline float expf(float x) {
     const uint64_t ki = d2u(kd);
     kd -= Shift;
     const double r = fma(InvLn2N, xd, -kd);
-    const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
     const double s = u2d(t);
     const double p = fma(C0, r, C1);
     const double r2 = r * r;
@@ -101,6 +103,8 @@ __host__ __device__ inline float expf(float x) {
     y = y * s;
     return (float)y;
 }
+
+__host__ __device__ inline float expf(float x) { return expf_tab(x, kExp2Tab); }
 
 // fdlibm expm1f.
 __host__ __device__ inline float expm1f(float x) {
@@ -195,6 +199,9 @@ __host__ __device__ inline float tanhf(float x) {
 
 // The reference's logistic, 1 / (1 + expf(-x)) (rwkv7.c).
 __host__ __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+__host__ __device__ __forceinline__ float sigmoid_tab(float x, const uint64_t* tab) {
+    return 1.0f / (1.0f + expf_tab(-x, tab));
+}
 
 }  // namespace refmath
 }  // namespace snhip

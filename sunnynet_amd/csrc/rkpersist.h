@@ -63,6 +63,13 @@ constexpr int kRkPMiMax = 32;   // sequences one launch steps at most (a.ni)
 __host__ __device__ inline size_t rkp_slab(int D, int F) { return (size_t)6 * D + 4 * kRkPRank + F; }
 
 bool rkp_shape_ok(int D, int F, int HS, int NH, const int (*ranks)[4], int L);
+// The exact-order kernel (rkexact.hip): its shapes, grid and launch. Its
+// layer table's matrices are fp32 (output, input) rows (block 0); the head
+// may be INT4 (group 32 or 64) or fp32.
+bool rke_shape_ok(int D, int F, int HS, int NH, const int (*ranks)[4], int L);
+bool rke_grid_ok(int G, int D, int F, int p1rows);
+int rke_grid(int NH);
+snhip_status launch_rk_exact(const RkPArgs& a, int G, hipStream_t st);
 // Workgroups of the launch (a multiple of 8, one per CU), or 0 when the
 // device cannot run it.
 int rkp_grid(int NH);

@@ -40,9 +40,11 @@
 
 #include "gemv.h"
 #include "rkpersist.h"
+#include "rkxch.h"
 
 namespace snhip {
 namespace {
+using namespace rkx;
 
 constexpr int NT = 512, NW = NT / 64, HS = 64;
 constexpr float kR2 = 0.6065306597126334f;   // 1/sqrt(e), rwkv7.c:38
@@ -58,12 +60,6 @@ __device__ __forceinline__ gptr<T> glb(const T* p) { return (gptr<T>)p; }
 
 __device__ __forceinline__ float sgm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-__device__ __forceinline__ void st_ag(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_ag(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Cross-lane sums through DPP moves (VALU, no LDS round trips): within
 // aligned groups of 2, 4, 8 and 16 lanes (quad permutations, then the half
@@ -422,83 +418,6 @@ __device__ __forceinline__ void up_dot(const UpBatch<Q>& B, Mat&& mat, Out&& out
     }
 }
 
-// ---- exchange words: the epoch of the launch that wrote the value in the
-// high half, the value's bits in the low half, stored and loaded as one
-// single-copy-atomic word at agent scope. A reader polls a word until it
-// carries its launch's epoch, so data and readiness travel in one round trip
-// and no grid barrier is needed.
-__device__ __forceinline__ void ex_put_bits(u64* p, uint32_t bits, unsigned ep) {
-    __hip_atomic_store(p, ((u64)ep << 32) | (u64)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void ex_put(u64* p, float v, unsigned ep) { ex_put_bits(p, __float_as_uint(v), ep); }
-__device__ __forceinline__ u64 ex_get(const u64* p) {
-    return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool ex_ok(u64 w, unsigned ep) { return (uint32_t)(w >> 32) == ep; }
-__device__ __forceinline__ float ex_f(u64 w) { return __uint_as_float((uint32_t)w); }
-
-struct PollCtl {
-    unsigned* err;
-    unsigned limit;
-    unsigned want;   // the launch's epoch (plus the test stall)
-};
-
-// Re-polls the words of w still short of the epoch (word k from src[k];
-// words a thread does not take start out ready) until all carry it. False on
-// a time-out (the thread then sets the error word) or when another
-// workgroup reported one. (Two rounds in flight at once, the next issued
-// before the one in hand is waited for, made the waits longer: the doubled
-// polling traffic delayed the producers more than it shortened the polls.)
-template <int W>
-__device__ __forceinline__ bool ex_spin(u64 (&w)[W], const u64* const (&src)[W], const PollCtl& pc) {
-    unsigned spins = 0;
-    while (true) {
-        bool all = true;
-#pragma unroll
-        for (int k = 0; k < W; ++k) all = all && ex_ok(w[k], pc.want);
-        if (all) return true;
-        if ((++spins & 255) == 0) {
-            if (__hip_atomic_load(pc.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
-            if (spins > pc.limit) {
-                __hip_atomic_store(pc.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                return false;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < W; ++k)
-            if (!ex_ok(w[k], pc.want)) w[k] = ex_get(src[k]);
-    }
-}
-
-// Words [0, n) of src into dst (LDS), word i by thread i mod NT; W words per
-// thread at most (n <= W NT). The workgroup's barrier between the polls and
-// the writes: every wave is done with what dst held before (the caller's
-// agree() then orders the writes before any read).
-template <int W>
-__device__ __forceinline__ bool poll_vec(const u64* src, int n, float* dst, const PollCtl& pc) {
-    const int tid = threadIdx.x;
-    u64 w[W];
-    const u64* at[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-        const int i = k * NT + tid;
-        at[k] = src + min(i, n - 1);
-        w[k] = i < n ? ex_get(at[k]) : ((u64)pc.want << 32);
-    }
-    const bool ok = ex_spin(w, at, pc);
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-        const int i = k * NT + tid;
-        if (i < n) dst[i] = ex_f(w[k]);
-    }
-    return ok;
-}
-
-// Keeps loads issued so far where they are (the optimizer would sink them to
-// their use, past the barrier wait).
-__device__ __forceinline__ void issued() { asm volatile("" ::: "memory"); }
-
 // The P1 products in order: W_r, W_k, W_v, W_1, A_1, G_1, V_1.
 __device__ __forceinline__ const RkPMat& p1_mat(const RkPLayer& P, int s) {
     switch (s) {
@@ -524,12 +443,6 @@ __device__ unsigned long long g_rkp_prof[2][64 * 6 + 2][2];
 #else
 #define RKP_MARK(ph, k) do { } while (0)
 #endif
-
-// This workgroup's share [lo, hi) of n rows.
-__device__ __forceinline__ void share(int n, int wg, int G, int& lo, int& hi) {
-    lo = (int)((long)n * wg / G);
-    hi = (int)((long)n * (wg + 1) / G);
-}
 
 __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
     __shared__ float xs[kRkPMaxD];            // x entering the phase
@@ -624,7 +537,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 // x_b of the layer before (every wave is past its last use of xs
                 // and of the other layer-table slot once the poll's barrier is)
                 if (l > 0) {
-                    const bool ok = poll_vec<kPer>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
+                    const bool ok = poll_vec<kPer, NT>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
                     if (!agree(ok)) return;
                 }
                 // the next layer's table into the other slot
@@ -862,7 +775,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     PreRows<Q, NU, 1> pr;
                     pre_load(pr, P.o, lo + wv, NW, lane);
                     issued();
-                    if (!agree(poll_vec<kPer>(s_y, D, buf, pc))) return false;
+                    if (!agree(poll_vec<kPer, NT>(s_y, D, buf, pc))) return false;
                     RKP_MARK(l * 6 + 2, 0);
                     // shift_0 <- xn (:229). Every workgroup has read shift_0 by
                     // now: the owners have all of r, k, v and the LoRA middles,
@@ -902,7 +815,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     }
                     ln_params(P.ln2w, P.ln2b, D, lg, lc);
                     issued();
-                    if (!agree(poll_vec<kPer>(s_xa, D, xs, pc))) return false;
+                    if (!agree(poll_vec<kPer, NT>(s_xa, D, xs, pc))) return false;
                     RKP_MARK(l * 6 + 3, 0);
                     PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
                     pre_load(pr, P.cmk, lo + wv, NW, lane);
@@ -941,7 +854,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     PreRows<Q, NU, 1> pr;
                     pre_load(pr, P.cmv, lo + wv, NW, lane);
                     issued();
-                    if (!agree(poll_vec<kPerF>(s_ck, F, buf, pc))) return false;
+                    if (!agree(poll_vec<kPerF, NT>(s_ck, F, buf, pc))) return false;
                     RKP_MARK(l * 6 + 4, 0);
                     // Every workgroup has read shift_1 by now: each has rows of
                     // ck (at most F workgroups).
@@ -978,7 +891,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 ln_params(A.on_w, A.on_b, D, lg, lc);
                 pre_load(ra, A.head, lo + wv, NW, lane);
                 issued();
-                if (!agree(poll_vec<kPer>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
+                if (!agree(poll_vec<kPer, NT>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
                 layer_norm(xs, buf, lg, lc, D, A.eps, red);
                 auto finish = [&](const float (&d)[N], int row) {
 #pragma unroll

@@ -156,6 +156,7 @@ struct SnHipRwkv7 {
     // One-sequence steps as one cooperative launch each (rkpersist.hip);
     // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
     int p_grid = 0;
+    bool p_exact = false;                 // the kernel is k_rk_exact (else k_rk_persist)
     // Steps of B = 2..p_mi_max sequences: the same kernel on a slice of
     // p_mi_grid[B] workgroups per sequence, one launch for all; the words
     // hold p_mi_max sequences' slabs, p_seq_words apart.
@@ -277,60 +278,83 @@ bool take_mat(SnHipRwkv7* m, Cur& c, RMat& M, int in, int out, float* tmp0, floa
 
 RkPMat pmat(const RMat& M) { return RkPMat{M.w, M.q, M.sc, M.M, M.Kd, M.q ? M.block : 0}; }
 
-// The one-sequence persistent step (rkpersist.hip), opt-in (SNHIP_RK_PERSIST=1
-// at load), when the device and the shape allow it: its layer table,
-// exchange slabs and key words. It is not the default because its products
-// and LayerNorms sum in parallel, not in the reference's sequential order,
-// and RWKV-7 amplifies that rounding: on the 12-layer model (INT4 g32) its
-// logits were up to 1.26e-4 from sn_rk_step over 256 first steps from the
-// zero state (32 of them past 2e-5) and up to 2.7e-5 over a 512-token
-// prompt and 128 greedy steps, while the per-kernel step is bit-exact. It
-// runs a step in 369 us against 658 for the per-kernel step at B = 1.
+// The one-launch step for one sequence (or one per grid slice), when the
+// device and the shape allow it: its layer table, exchange slabs and key
+// words. Two kernels share them:
+// * k_rk_exact (rkexact.hip), the default (SNHIP_RK_EXACT=0 turns it off):
+//   every rounding in the reference's order, so its logits equal
+//   sn_rk_step's bit for bit; its layer table points at fp32 (output, input)
+//   copies of the layer matrices (INT4 rows dequantized to the values the
+//   reference multiplies: 361 MB at 12 x 768, F = 3072), since a sequential
+//   chain per output runs fastest on four-value fp32 reads;
+// * k_rk_persist (rkpersist.hip), opt-in (SNHIP_RK_PERSIST=1): products and
+//   LayerNorms summed in parallel, which RWKV-7 amplifies: on the 12-layer
+//   INT4 model its logits were up to 1.26e-4 from sn_rk_step over 256 first
+//   steps from the zero state (32 of them past 2e-5) and up to 2.7e-5 over a
+//   512-token prompt and 128 greedy steps.
 // The grid is at most one workgroup per CU (SNHIP_RK_PERSIST_WG caps it; it
 // is rounded down to a multiple of 8), and at most the rows of the first
 // product (r, k, v and the LoRA middles) and of the channel-mix key, so that
-// every workgroup produces rows of both: the kernel relies on that to know
-// when every workgroup has read the shift vectors it then overwrites.
+// every workgroup that takes rows of them has some: the kernels rely on that
+// to know when every workgroup has read the shift vectors they then
+// overwrite (k_rk_exact also checks its own row split: rke_grid_ok).
 void setup_rk_persist(SnHipRwkv7* m) {
-    if (env_unsigned("SNHIP_RK_PERSIST", 0, 0) == 0) return;
+    const bool fast = env_unsigned("SNHIP_RK_PERSIST", 0, 0) != 0;
+    const bool exact = !fast && env_unsigned("SNHIP_RK_EXACT", 1, 0) != 0;
+    if (!fast && !exact) return;
     m->p_spin = env_unsigned("SNHIP_PERSIST_SPIN", m->p_spin, 1);
     std::vector<int> rk(4 * (size_t)m->L);
     for (int l = 0; l < m->L; ++l) {
         const RkLayer& A = m->layers[l];
         rk[4 * l] = A.Rw; rk[4 * l + 1] = A.Ra; rk[4 * l + 2] = A.Rv; rk[4 * l + 3] = A.Rg;
     }
-    if (!rkp_shape_ok(m->D, m->F, m->HS, m->NH, reinterpret_cast<const int(*)[4]>(rk.data()), m->L)) return;
-    int G = rkp_grid(m->NH);
+    const auto* rk4 = reinterpret_cast<const int(*)[4]>(rk.data());
+    if (!(exact ? rke_shape_ok(m->D, m->F, m->HS, m->NH, rk4, m->L)
+                : rkp_shape_ok(m->D, m->F, m->HS, m->NH, rk4, m->L)))
+        return;
+    int G = exact ? rke_grid(m->NH) : rkp_grid(m->NH);
     if (const char* e = getenv("SNHIP_RK_PERSIST_WG")) G = std::min(G, atoi(e));
-    int p1rows = 1 << 30;
-    for (int l = 0; l < m->L; ++l) p1rows = std::min(p1rows, 3 * m->D + rk[4 * l] + rk[4 * l + 1] + rk[4 * l + 3]);
+    int p1rows = 1 << 30, p1max = 0;   // the first product's rows: fewest and most over the layers
+    for (int l = 0; l < m->L; ++l) {
+        const int n = 3 * m->D + rk[4 * l] + rk[4 * l + 1] + rk[4 * l + 3];
+        p1rows = std::min(p1rows, n);
+        p1max = std::max(p1max, n + (l > 0 ? rk[4 * l + 2] : 0));
+    }
     G = std::min(G, std::min(p1rows, m->F)) / 8 * 8;
-    if (G < 8 || G < m->NH) return;
+    if (G < 8 || G < m->NH || (exact && !rke_grid_ok(G, m->D, m->F, p1max))) return;
+    // exact: each layer matrix as fp32 (output, input) rows
+    auto rows_f32 = [&](const RMat& M, bool& ok) -> RkPMat {
+        if (!M.q) return RkPMat{M.w, nullptr, nullptr, M.M, M.Kd, 0};
+        float* w = ralloc<float>(m, (size_t)M.M * M.Kd);
+        if (!w || launch_dequant_i4(M.q, M.sc, w, M.M, M.Kd, M.block, nullptr) != SNHIP_OK) ok = false;
+        return RkPMat{w, nullptr, nullptr, M.M, M.Kd, 0};
+    };
+    bool ok = true;
+    auto mat = [&](const RMat& M) -> RkPMat { return exact ? rows_f32(M, ok) : pmat(M); };
     std::vector<RkPLayer> tab(m->L);
     for (int l = 0; l < m->L; ++l) {
         const RkLayer& A = m->layers[l];
         RkPLayer& P = tab[l];
-        P.r = pmat(A.r); P.k = pmat(A.k); P.v = pmat(A.v); P.w1 = pmat(A.w1); P.a1 = pmat(A.a1);
-        P.g1 = pmat(A.g1); P.v1 = pmat(A.v1); P.w2 = pmat(A.w2); P.a2 = pmat(A.a2); P.g2 = pmat(A.g2);
-        P.v2 = pmat(A.v2); P.o = pmat(A.o); P.cmk = pmat(A.cmk); P.cmv = pmat(A.cmv);
+        P.r = mat(A.r); P.k = mat(A.k); P.v = mat(A.v); P.w1 = mat(A.w1); P.a1 = mat(A.a1);
+        P.g1 = mat(A.g1); P.v1 = l > 0 ? mat(A.v1) : pmat(A.v1); P.w2 = mat(A.w2); P.a2 = mat(A.a2);
+        P.g2 = mat(A.g2); P.v2 = l > 0 ? mat(A.v2) : pmat(A.v2); P.o = mat(A.o); P.cmk = mat(A.cmk);
+        P.cmv = mat(A.cmv);
         P.ln1w = A.ln1w; P.ln1b = A.ln1b; P.ln2w = A.ln2w; P.ln2b = A.ln2b; P.lerp = A.lerp; P.w0 = A.w0;
         P.a0 = A.a0; P.v0 = A.v0; P.kk = A.kk; P.ka = A.ka; P.rk = A.rk; P.lnxw = A.lnxw; P.lnxb = A.lnxb;
         P.cmk_lerp = A.cmk_lerp;
     }
+    if (!ok) return;
     // Slices for B = 2..p_mi_max (SNHIP_RK_PERSIST_MI=n, default 8): the
     // largest multiple of 8 workgroups, at least the head count, that B
     // slices fit in the one-sequence grid. Each sequence's results equal its
-    // one-sequence launch's bit for bit (the kernel's arithmetic does not
-    // depend on the grid size). Measured at B=1 on one MI355X (RWKV-7
-    // 12 x 768, INT4 g32): 372.6 us/step on 256 workgroups, 442.1 on 128,
-    // 597.5 on 64, 901.2 on 32, 1558.0 on 16, against 1,225.7 (B=2) and
-    // 1,348.1 (B=8) us/step for the per-kernel step.
+    // one-sequence launch's bit for bit (neither kernel's arithmetic depends
+    // on the grid size).
     m->p_mi_max = 0;
     const int lim = std::min(std::min(m->max_batch, kRkPMiMax),
                              (int)std::min(env_unsigned("SNHIP_RK_PERSIST_MI", 8, 0), (unsigned)kRkPMiMax));
     for (int b = 2; b <= lim; ++b) {
         const int g = G / b / 8 * 8;
-        if (g < 8 || g < m->NH) break;
+        if (g < 8 || g < m->NH || (exact && !rke_grid_ok(g, m->D, m->F, p1max))) break;
         m->p_mi_grid[b] = g;
         m->p_mi_max = b;
     }
@@ -354,6 +378,7 @@ void setup_rk_persist(SnHipRwkv7* m) {
     a.err = m->p_err; a.spin_limit = m->p_spin; a.stall = 0;
     a.words = m->p_seq_words;
     m->p_grid = G;
+    m->p_exact = exact;
 }
 
 // Do steps of B sequences run as B slices of the persistent kernel?
@@ -388,7 +413,7 @@ snhip_status run_persist(SnHipRwkv7* m, int B, float* logits_out, bool greedy, i
         a.nsteps = n;
         a.hist0 = i;
         m->p_epoch += (unsigned)n;
-        const snhip_status rc = launch_rk_persist(a, grid, m->work);
+        const snhip_status rc = m->p_exact ? launch_rk_exact(a, grid, m->work) : launch_rk_persist(a, grid, m->work);
         if (rc != SNHIP_OK) return rc;
         i += n;
     }
@@ -840,6 +865,8 @@ snhip_status snhip_rk_set_stream(SnHipRwkv7* m, void* stream) {
 int32_t snhip_rk_max_batch(const SnHipRwkv7* m) { return m ? m->max_batch : 0; }
 
 int32_t snhip_rk_persist_grid(const SnHipRwkv7* m) { return m ? m->p_grid : 0; }
+
+int32_t snhip_rk_persist_exact(const SnHipRwkv7* m) { return m && m->p_grid > 0 && m->p_exact ? 1 : 0; }
 
 int32_t snhip_rk_persist_grid_batch(const SnHipRwkv7* m, int32_t B) {
     if (!m || B < 1 || B > m->max_batch) return 0;

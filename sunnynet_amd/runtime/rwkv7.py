@@ -55,6 +55,12 @@ class HipRwkv7:
         (0 when off)."""
         return int(self._lib.snhip_rk_persist_grid(self._h))
 
+    @property
+    def persist_exact(self) -> bool:
+        """Whether the one-launch step is the exact-order kernel (bit-identical
+        to the reference's sn_rk_step)."""
+        return bool(self._lib.snhip_rk_persist_exact(self._h))
+
     def persist_grid_for(self, B: int) -> int:
         """Workgroups of the persistent launch for steps of B sequences, each
         on its own slice of the grid (0: B takes the per-kernel path)."""

@@ -220,8 +220,9 @@ def test_converter_cli_writes_the_blob(tmp_path):
 @pytest.mark.gpu
 def test_rwkv7_gguf_ragged_ranks_on_the_gpu_handle(gpu, tmp_path):
     """A GGUF file converted with ragged per-layer LoRA ranks, loaded by the
-    HIP handle (snhip_rk_load): every step's logits equal the oracle's (the
-    per-kernel step at B=2 follows the reference's rounding order)."""
+    HIP handle (snhip_rk_load): every step's logits equal the oracle's (B=2
+    runs the exact one-launch kernel on two grid slices, which follows the
+    reference's rounding order)."""
     import torch
 
     from sunnynet_amd.runtime.rwkv7 import HipRwkv7

@@ -1,6 +1,6 @@
-"""The one-launch-per-step RWKV-7 path for a single sequence (rkpersist.hip),
-opt-in with SNHIP_RK_PERSIST=1 (every test here sets it), against the oracle
-and against the per-kernel (graph) path, the default.
+"""The fast one-launch-per-step RWKV-7 kernel (rkpersist.hip), opt-in with
+SNHIP_RK_PERSIST=1 (every test here sets it), against the oracle and against
+the per-kernel step.
 
 Bar: logits within PTOL = 2e-4 absolute of the C oracle (bit-identical to the
 reference's sn_rk_step on fp32 blobs) with the same argmax on every step,
@@ -9,8 +9,9 @@ products and LayerNorms in parallel rather than in the reference's sequential
 order, and RWKV-7 amplifies that rounding, most from the zero state: on the
 12-layer INT4 model its logits were up to 1.26e-4 from sn_rk_step over 256
 first steps (32 of them past 2e-5) and up to 2.7e-5 over the benchmark's
-640-step chain. That is why it is not the default: the per-kernel step is
-bit-exact (tests/test_rwkv7_gpu.py). For comparison, the reference's own
+640-step chain. That is why it is not the default: the default one-launch
+kernel (rkexact.hip, tests/test_rkexact_gpu.py) and the per-kernel step are
+bit-exact. For comparison, the reference's own
 tests hold its C runtime to 1e-3 against its numpy restatement
 (tests/test_rwkv7_c.py:29-50). Covers fp32, the INT4 blob as stored (group
 64, the 32-input V_2 kept fp32) and INT4 group 32 quantized at load, the
@@ -62,16 +63,19 @@ def cfg4(tmp_path_factory):
 
 
 def _pair(path, monkeypatch, **kw):
+    """The fast kernel's handle and a per-kernel one."""
     hp = HipRwkv7(path, **kw)
     monkeypatch.setenv("SNHIP_RK_PERSIST", "0")
+    monkeypatch.setenv("SNHIP_RK_EXACT", "0")
     hg = HipRwkv7(path, **kw)
     monkeypatch.setenv("SNHIP_RK_PERSIST", "1")
-    assert hp.persist_grid > 0 and hg.persist_grid == 0
+    monkeypatch.delenv("SNHIP_RK_EXACT")
+    assert hp.persist_grid > 0 and not hp.persist_exact and hg.persist_grid == 0
     return hp, hg
 
 
 @pytest.mark.parametrize("fmt", ["fp32", "int4_blob", "int4_g32"])
-def test_persist_matches_oracle_and_graph_path(gpu, tiny, monkeypatch, fmt):
+def test_persist_matches_oracle_and_per_kernel_step(gpu, tiny, monkeypatch, fmt):
     w, p32, p4 = tiny
     print(f"rwkv7 persistent B=1 tiny {fmt}", flush=True)
     if fmt == "fp32":
@@ -130,7 +134,7 @@ def test_persist_cfg4_int4(gpu, cfg4, monkeypatch):
         a = np.asarray(hp.step(int(t)), np.float32)
         g = np.asarray(hg.step(int(t)), np.float32)
         b = orc.step([t])[0]
-        print("worst |dlogit| persist", float(np.abs(a - b).max()), "graph", float(np.abs(g - b).max()),
+        print("worst |dlogit| persist", float(np.abs(a - b).max()), "per-kernel", float(np.abs(g - b).max()),
               flush=True)
         assert np.abs(a - b).max() < PTOL and np.abs(a - g).max() < PTOL
         assert a.argmax() == b.argmax() == g.argmax()

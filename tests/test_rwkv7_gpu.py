@@ -4,12 +4,13 @@ The oracle is bit-identical to the reference's sn_rk_step on fp32 blobs
 (tests/test_rwkv7_oracle.py). INT4: the oracle runs the fp32 path on the
 bit-identically dequantized weights (W4A32).
 
-Bars. The per-kernel step (every batch of two or more sequences, and single
-sequences when the persistent kernel is off) follows the reference's
-rounding order everywhere, so its logits and states must EQUAL the oracle's,
-bit for bit, step after step. The single-sequence persistent kernel
-(rkpersist.hip) splits its dot products across lanes: logits within 2e-5
-absolute, the same argmax on every token.
+Bars. Both default paths follow the reference's rounding order everywhere,
+so their logits and states must EQUAL the oracle's, bit for bit, step after
+step: the one-launch exact kernel (rkexact.hip: one sequence, and 2..8 on
+grid slices; tests/test_rkexact_gpu.py covers it in depth) and the
+per-kernel step (larger batches, ragged LoRA ranks, or every step with
+SNHIP_RK_EXACT=0). The opt-in fast one-launch kernel (rkpersist.hip, summing
+in parallel) has its own bar in tests/test_rkpersist_gpu.py.
 """
 from __future__ import annotations
 
@@ -80,21 +81,21 @@ def _check_steps(hm, orc, toks, B=1, tol=TOL):
     return worst
 
 
-def _graph(path, monkeypatch, **kw):
-    """A handle whose single-sequence steps take the per-kernel step."""
-    monkeypatch.setenv("SNHIP_RK_PERSIST", "0")
+def _per_kernel(path, monkeypatch, **kw):
+    """A handle whose steps all take the per-kernel step (SNHIP_RK_EXACT=0)."""
+    monkeypatch.setenv("SNHIP_RK_EXACT", "0")
     h = HipRwkv7(path, **kw)
-    monkeypatch.delenv("SNHIP_RK_PERSIST")
+    monkeypatch.delenv("SNHIP_RK_EXACT")
     assert h.persist_grid == 0
     return h
 
 
 def test_tiny_fp32_b1(gpu, tiny):
-    """A handle as loaded (B=1 on the default per-kernel step): exact."""
+    """A handle as loaded (B=1 on the default exact one-launch kernel): exact."""
     w, p32, _ = tiny
     print("rwkv7 tiny fp32 B=1", flush=True)
     hm = HipRwkv7(p32)
-    assert hm.persist_grid == 0
+    assert hm.persist_grid > 0 and hm.persist_exact
     orc = oracle.RkOracle(p32.read_bytes())
     _check_steps(hm, orc, np.random.default_rng(1).integers(0, RWKV_TINY.vocab, 32), tol=EXACT)
     S, sh = hm.get_state(1)
@@ -126,10 +127,10 @@ def test_reference_class_surface(gpu, tiny):
         HipRwkv7(p32, RWKV_TINY.vocab + 1)
 
 
-def test_tiny_graph_b1_exact(gpu, tiny, monkeypatch):
+def test_tiny_per_kernel_b1_exact(gpu, tiny, monkeypatch):
     w, p32, _ = tiny
     print("rwkv7 tiny fp32 B=1 per-kernel step, exact", flush=True)
-    hm = _graph(p32, monkeypatch)
+    hm = _per_kernel(p32, monkeypatch)
     orc = oracle.RkOracle(p32.read_bytes())
     _check_steps(hm, orc, np.random.default_rng(1).integers(0, RWKV_TINY.vocab, 32), tol=EXACT)
     S, sh = hm.get_state(1)
@@ -142,7 +143,7 @@ def test_tiny_batched_exact(gpu, tiny, B):
     w, p32, _ = tiny
     print(f"rwkv7 tiny fp32 B={B}, exact", flush=True)
     hm = HipRwkv7(p32, max_batch=16)
-    assert hm.persist_grid_for(B) == 0
+    assert (hm.persist_grid_for(B) > 0) == (B <= 8)   # grid slices up to 8 sequences
     orc = oracle.RkOracle(p32.read_bytes(), batch=B)
     rng = np.random.default_rng(B)
     _check_steps(hm, orc, [rng.integers(0, RWKV_TINY.vocab, B) for _ in range(10)], B=B, tol=EXACT)
@@ -153,14 +154,15 @@ def test_tiny_batched_exact(gpu, tiny, B):
 
 def test_int4_blob_stored(gpu, tiny, monkeypatch):
     """INT4 (group 64) matrices of the v3 blob run as stored; the 32-input
-    V_2 stays fp32. B=1 and B=3 exact."""
+    V_2 stays fp32. B=1 (per-kernel and one-launch) and B=3 exact."""
     w, _, p4 = tiny
     print("rwkv7 tiny int4 blob", flush=True)
     toks = np.random.default_rng(2).integers(0, RWKV_TINY.vocab, 24)
-    hg = _graph(p4, monkeypatch)
+    hg = _per_kernel(p4, monkeypatch)
     _check_steps(hg, oracle.RkOracle(p4.read_bytes()), toks, tol=EXACT)   # dequantizes at load
+    _check_steps(HipRwkv7(p4), oracle.RkOracle(p4.read_bytes()), toks, tol=EXACT)
     h3 = HipRwkv7(p4, max_batch=3)
-    assert h3.persist_grid_for(3) == 0
+    assert h3.persist_grid_for(3) > 0
     rng = np.random.default_rng(22)
     _check_steps(h3, oracle.RkOracle(p4.read_bytes(), batch=3),
                  [rng.integers(0, RWKV_TINY.vocab, 3) for _ in range(8)], B=3, tol=EXACT)
@@ -171,7 +173,7 @@ def test_int4_g32_at_load(gpu, tiny, tmp_path):
     w, p32, _ = tiny
     print("rwkv7 tiny fp32 blob quantized to int4 g32 at load, exact", flush=True)
     hm = HipRwkv7(p32, weights="int4", block=32, max_batch=4)
-    assert hm.persist_grid_for(4) == 0
+    assert hm.persist_grid_for(4) > 0
     orc = oracle.RkOracle(pack_rwkv7_blob(dequant_weights(w, 32)), batch=4)
     rng = np.random.default_rng(3)
     _check_steps(hm, orc, [rng.integers(0, RWKV_TINY.vocab, 4) for _ in range(12)], B=4, tol=EXACT)
@@ -191,8 +193,9 @@ def test_ragged_ranks_and_tail_columns_exact(gpu, tmp_path, monkeypatch):
     p.write_bytes(pack_rwkv7_blob(w, ranks=ranks))
     print("rwkv7 ragged ranks B=1 and B=5, exact", flush=True)
     toks = np.random.default_rng(5).integers(0, RWKV_TINY.vocab, 12)
-    _check_steps(_graph(p, monkeypatch), oracle.RkOracle(p.read_bytes()), toks, tol=EXACT)
+    _check_steps(_per_kernel(p, monkeypatch), oracle.RkOracle(p.read_bytes()), toks, tol=EXACT)
     h5 = HipRwkv7(p, max_batch=5)
+    assert h5.persist_grid == 0       # the one-launch kernels take power-of-two ranks only
     rng = np.random.default_rng(55)
     _check_steps(h5, oracle.RkOracle(p.read_bytes(), batch=5),
                  [rng.integers(0, RWKV_TINY.vocab, 5) for _ in range(6)], B=5, tol=EXACT)
@@ -248,13 +251,12 @@ def cfg4(tmp_path_factory):
 
 def test_cfg4_int4_b1(gpu, cfg4):
     """12 layers, D=768, 12 heads, vocab 65536, INT4 g32 at load (seed 2),
-    B=1 on the handle as loaded: exact (the opt-in persistent step is tested
-    in tests/test_rkpersist_gpu.py)."""
+    B=1 on the handle as loaded (the exact one-launch kernel): exact."""
     p, dq = cfg4
     toks = np.random.default_rng(4).integers(0, RWKV_CFG4.vocab, 4)
     print("rwkv7 cfg4 int4 g32 B=1, exact", flush=True)
     hm = HipRwkv7(p, weights="int4", block=32)
-    assert hm.persist_grid == 0
+    assert hm.persist_grid > 0 and hm.persist_exact
     _check_steps(hm, oracle.RkOracle(dq), toks, tol=EXACT)
 
 
@@ -301,10 +303,12 @@ def test_cfg4_int4_ragged_batch_exact(gpu, cfg4):
 
 
 def test_cfg4_int4_every_batch_size(gpu, cfg4):
-    """Every batch size 1..64 of the 12-layer INT4 model (the launch shapes
-    change with B: one or four consumers per workgroup, staged or global X,
-    narrow or wide chains and their counts): one step from the reset state,
-    the first and the last sequence identical to the oracle's."""
+    """Every batch size 1..64 of the 12-layer INT4 model (1..8 on the exact
+    one-launch kernel, one grid slice per sequence; from 9 on the per-kernel
+    step, whose launch shapes change with B: one or four consumers per
+    workgroup, staged or global X, narrow or wide chains and their counts):
+    one step from the reset state, the first and the last sequence identical
+    to the oracle's."""
     p, dq = cfg4
     cfg = RWKV_CFG4
     print("rwkv7 cfg4 int4 g32 B=1..64, one step each", flush=True)
@@ -363,7 +367,6 @@ def test_dbg_equals_reference_sn_rk_dbg(gpu, tiny, monkeypatch, ref_built, layer
     keep stepping identically afterwards (the dump advanced the same
     layers' state)."""
     w, p32 = tiny[0], tiny[1]
-    monkeypatch.setenv("SNHIP_RK_PERSIST", "0")      # the exact per-kernel step before the dump
     hm = HipRwkv7(p32, RWKV_TINY.vocab)
     ref = oracle.RefRk(p32, RWKV_TINY.vocab)
     for t in (5, 77, 300):
