@@ -1114,7 +1114,8 @@ def main(argv=None):
         return profile_sequence(args.profile)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one GPU only: this build has no multi-GPU path "
-            "(each channel / sequence shards with no communication; see DESIGN.md).")
+            "(the scan shards by channel and decode by sequence, with no communication, "
+            "so N GPUs would run N independent copies).")
         return 2
     res = None
     if args.workload in ("all", "scan"):

@@ -74,6 +74,10 @@ __device__ __forceinline__ const float* uni(const float* p) {
     const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
     return (const float*)(((unsigned long long)hi << 32) | lo);
 }
+// A weight read that is used once per step: non-temporal, so that the
+// step's stream of weights does not push the kernel's code, its exchange
+// words and the state out of the L2.
+__device__ __forceinline__ f4 stream_ld(gptr<f4> p) { return __builtin_nontemporal_load(p); }
 // LDS reads through an LDS-typed pointer: ds_read (counted by lgkmcnt only),
 // so waiting for x does not also wait for the weight reads in flight.
 typedef __attribute__((address_space(3))) const f4 l_f4;
@@ -177,27 +181,82 @@ __device__ __forceinline__ void ln_load(LnP& p, const float* g, const float* c, 
     }
 }
 
+// sum = sum + v[i] over the 256 KL4 values a wave holds, value 4 KL4 j + e
+// in lane j, element e (v[e / 4][e % 4]), in order: each lane adds its values
+// to the running sum of the lanes before, which passes from lane j to lane
+// j + 1 as a wave-uniform value. Every lane returns the total.
+template <int KL4>
+__device__ __forceinline__ float lane_seq_sum(const f4 (&v)[KL4]) {
+    float acc = 0.0f;
+    for (int j = 0; j < 64; ++j) {
+        float a = acc;
+#pragma unroll
+        for (int q = 0; q < KL4; ++q) {
+            a = a + v[q].x;
+            a = a + v[q].y;
+            a = a + v[q].z;
+            a = a + v[q].w;
+        }
+        acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), j));
+    }
+    return acc;
+}
+
+// LN statistics of n = 256 KL4 values in LDS by wave 0, lane-sliced: the
+// mean as a sequential sum, then the squared deviations' sum, with the
+// values in registers throughout (no LDS pass between the two sums).
+template <int KL4>
+__device__ __forceinline__ void ln_stats_lanes(const float* src, int n, float eps, float* stat) {
+    const int lane = threadIdx.x & 63;
+    f4 v[KL4];
+#pragma unroll
+    for (int q = 0; q < KL4; ++q) v[q] = lds4(src)[lane * KL4 + q];
+    const float mean = lane_seq_sum(v) / (float)n;
+#pragma unroll
+    for (int q = 0; q < KL4; ++q) {
+        f4 d;
+        d.x = v[q].x - mean; d.y = v[q].y - mean; d.z = v[q].z - mean; d.w = v[q].w - mean;
+        v[q].x = d.x * d.x; v[q].y = d.y * d.y; v[q].z = d.z * d.z; v[q].w = d.w * d.w;
+    }
+    const float var = lane_seq_sum(v);
+    if (lane == 0) {
+        stat[0] = mean;
+        stat[1] = 1.0f / sqrtf(var / (float)n + eps);
+    }
+}
+
 // dst = LN(src) g + c over n <= kRkPMaxD values in LDS (rwkv7.c:127-140):
-// the mean and the variance as sequential sums by thread 0. sq: n floats of
-// LDS scratch.
+// the mean and the variance as sequential sums (by wave 0 lane-sliced when
+// n is 256, 512, 768 or 1024, else by thread 0). sq: n floats of LDS scratch.
 __device__ __forceinline__ void ln_exact(const float* src, float* dst, float* sq, const LnP& p, int n, float eps,
                                          float* stat) {
     const int t = threadIdx.x;
-    if (t == 0) stat[0] = seq_sum(lds4(src), n >> 2) / (float)n;
-    __syncthreads();
-    const float mean = stat[0];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int i = k * NT + t;
-        if (i < n) {
-            const float d = src[i] - mean;
-            sq[i] = d * d;
+    const int kl = n % 256 ? 0 : n / 256;
+    if (kl >= 1 && kl <= 4) {
+        if (t < 64) {
+            if (kl == 1) ln_stats_lanes<1>(src, n, eps, stat);
+            else if (kl == 2) ln_stats_lanes<2>(src, n, eps, stat);
+            else if (kl == 3) ln_stats_lanes<3>(src, n, eps, stat);
+            else ln_stats_lanes<4>(src, n, eps, stat);
         }
+        __syncthreads();
+    } else {
+        if (t == 0) stat[0] = seq_sum(lds4(src), n >> 2) / (float)n;
+        __syncthreads();
+        const float m0 = stat[0];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = k * NT + t;
+            if (i < n) {
+                const float d = src[i] - m0;
+                sq[i] = d * d;
+            }
+        }
+        __syncthreads();
+        if (t == 0) stat[1] = 1.0f / sqrtf(seq_sum(lds4(sq), n >> 2) / (float)n + eps);
+        __syncthreads();
     }
-    __syncthreads();
-    if (t == 0) stat[1] = 1.0f / sqrtf(seq_sum(lds4(sq), n >> 2) / (float)n + eps);
-    __syncthreads();
-    const float rstd = stat[1];
+    const float mean = stat[0], rstd = stat[1];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = k * NT + t;
@@ -237,13 +296,10 @@ __device__ __forceinline__ int chunk_for(int R) {
     return fits(256) ? 256 : fits(128) ? 128 : fits(64) ? 64 : 32;
 }
 
-// Whole-phase staging: R rows of K inputs fit the two register slots and,
-// padded, the two LDS buffers.
-__device__ __forceinline__ bool whole_fits(int R, int K) {
-    return R * (K >> 2) <= 2 * kPend * NT && R * (K + 4) <= 2 * kStg;
-}
+// Whole-phase staging: R rows of K inputs fit, padded, the two LDS buffers.
+__device__ __forceinline__ bool whole_fits(int R, int K) { return R * (K + 4) <= 2 * kStg; }
 
-// Row and float4 column of float4 element i (i < 2 kPend NT) of rows of C4
+// Row and float4 column of float4 element i (i < 2 kStg / 4) of rows of C4
 // float4: a float reciprocal, then one correction step (the quotient is off
 // by less than 1).
 __device__ __forceinline__ void split(int i, int C4, float inv, int& r, int& c4) {
@@ -260,9 +316,9 @@ __device__ __forceinline__ void split(int i, int C4, float inv, int& r, int& c4)
 
 // One product phase's staging plan (uniform values). A chunk is C4 float4 of
 // each row, stored in LDS at row stride RS floats. Whole phase: one chunk of
-// K4 float4 split over the two slots (slot 1 from element kPend NT on),
-// stored from stg on; chunked: slot s holds chunk ch with ch & 1 == s, stored
-// into buffer s.
+// K4 float4, loaded straight into LDS from stg on (whole_issue_lds);
+// chunked: register slot s holds chunk ch with ch & 1 == s, stored into
+// buffer s.
 struct Stager {
     int R, K4, C4, RS, nch;
     float inv;
@@ -280,20 +336,43 @@ __device__ __forceinline__ Stager stager(int R, int K) {
     return S;
 }
 
+// The whole phase straight into LDS: float4 slot q of the padded rows (row q
+// / (K4 + 1), column q % (K4 + 1); the pad column loads the row's last float4
+// again) by global_load_lds, whose 64 lanes write 64 consecutive slots from a
+// wave-uniform base. No registers hold the weights and no pass stores them;
+// the data is in LDS once the loads retire (vmcnt). The caller's barrier
+// before it: every wave is done with stg.
+template <class WR>
+__device__ __forceinline__ void whole_issue_lds(float* stg, const Stager& S, WR&& wrow) {
+    typedef const __attribute__((address_space(1))) void gvoid;
+    typedef __attribute__((address_space(3))) void lvoid;
+    const int W4 = S.K4 + 1, n = S.R * W4, tid = threadIdx.x;
+    const float inv = 1.0f / (float)W4;
+    for (int base = 0; base < n; base += NT) {
+        const int q = base + tid;
+        if (q < n) {
+            int r, c4;
+            split(q, W4, inv, r, c4);
+            const gptr<f4> src = wrow(r) + min(c4, S.K4 - 1);
+            __builtin_amdgcn_global_load_lds((gvoid*)src, (lvoid*)(stg + 4 * (base + (tid & ~63))), 16, 0, 0);
+        }
+    }
+}
+
 // Issues chunk ch into register slot SLOT (row r from wrow(r), a float4
-// pointer). One code path for every plan: the slots are compile-time indices
-// and no branch selects among layouts, so no register of a load in flight is
-// copied (a copy waits for the load).
+// pointer). The slots are compile-time indices and no branch selects among
+// layouts, so no register of a load in flight is copied (a copy waits for
+// the load).
 template <int SLOT, class WR>
 __device__ __forceinline__ void stg_issue(Pend& P, const Stager& S, int ch, WR&& wrow) {
-    const int first = S.whole ? SLOT * kPend * NT : 0, n = S.R * S.C4, col0 = S.whole ? 0 : ch * S.C4;
+    const int first = 0, n = S.R * S.C4, col0 = ch * S.C4;
 #pragma unroll
     for (int p = 0; p < kPend; ++p) {
         const int i = first + (int)threadIdx.x + p * NT;
         if (i < n) {
             int r, c4;
             split(i, S.C4, S.inv, r, c4);
-            P.v[SLOT][p] = wrow(r)[min(col0 + c4, S.K4 - 1)];
+            P.v[SLOT][p] = stream_ld(wrow(r) + min(col0 + c4, S.K4 - 1));
         }
     }
 }
@@ -301,7 +380,7 @@ __device__ __forceinline__ void stg_issue(Pend& P, const Stager& S, int ch, WR&&
 // Stores register slot SLOT into LDS from b on (rows at stride S.RS).
 template <int SLOT>
 __device__ __forceinline__ void stg_commit(const Pend& P, const Stager& S, float* b) {
-    const int first = S.whole ? SLOT * kPend * NT : 0, n = S.R * S.C4;
+    const int first = 0, n = S.R * S.C4;
 #pragma unroll
     for (int p = 0; p < kPend; ++p) {
         const int i = first + (int)threadIdx.x + p * NT;
@@ -325,11 +404,17 @@ __device__ __forceinline__ float tail_chain(const float* W, int K, int row, cons
     return acc;
 }
 
-// Issue: the whole phase, or its first two chunks (before the caller's wait).
+// Issue: the whole phase (into stg), or its first two chunks (before the
+// caller's wait).
 template <class WR>
-__device__ __forceinline__ void stager_issue(Pend& P, const Stager& S, WR&& wrow) {
+__device__ __forceinline__ void stager_issue(Pend& P, float* stg, const Stager& S, WR&& wrow) {
+    if (S.whole) {
+        __syncthreads();
+        whole_issue_lds(stg, S, wrow);
+        return;
+    }
     stg_issue<0>(P, S, 0, wrow);
-    if (S.whole || S.nch > 1) stg_issue<1>(P, S, 1, wrow);
+    if (S.nch > 1) stg_issue<1>(P, S, 1, wrow);
 }
 
 // Run, after the caller's wait: thread r < R ends with row r's sum and calls
@@ -340,8 +425,7 @@ __device__ __forceinline__ void stager_run(Pend& P, float* stg, const Stager& S,
     const bool mine = t < S.R;
     const l_f4* x = lds4(mine ? xrow(t) : xrow(0));
     if (S.whole) {
-        stg_commit<0>(P, S, stg);
-        stg_commit<1>(P, S, stg);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's loads into LDS
         __syncthreads();
         if (mine) out(t, lds_chain(lds4(stg + t * S.RS), x, S.K4, 0.0f));
         return;
@@ -390,7 +474,7 @@ __device__ __forceinline__ void lsc_issue(LscRow<KL4>& W, int R, WR&& wrow) {
     if (wv < R) {
         const gptr<f4> w = wrow(wv) + lane * KL4;
 #pragma unroll
-        for (int q = 0; q < KL4; ++q) W.w[q] = w[q];
+        for (int q = 0; q < KL4; ++q) W.w[q] = stream_ld(w + q);
     }
 }
 
@@ -423,13 +507,13 @@ struct Phase {
     LscRow<KL4> W;
     Stager S;
     template <class WR>
-    __device__ __forceinline__ void issue(Pend& P, int R, int K, WR&& wrow) {
+    __device__ __forceinline__ void issue(Pend& P, float* stg, int R, int K, WR&& wrow) {
         if constexpr (KL4 > 0) {
             S.R = R;
             lsc_issue(W, R, wrow);
         } else {
             S = stager(R, K);
-            stager_issue(P, S, wrow);
+            stager_issue(P, stg, S, wrow);
         }
     }
     template <class WR, class OUT>
@@ -569,6 +653,11 @@ __device__ __forceinline__ float row_any(const RkPMat& W, int row, const float* 
         return tail ? chain_i4<32, false>(q, sc, lds4(x), ng) : chain_i4<32, true>(q, sc, lds4(x), ng);
     return tail ? chain_i4<64, false>(q, sc, lds4(x), ng) : chain_i4<64, true>(q, sc, lds4(x), ng);
 }
+
+// Before a wait: every wave of the workgroup is past the phase before. Waves
+// that finish a phase early then sleep at the barrier instead of polling
+// while the phase's chains (one or a few waves) still run.
+__device__ __forceinline__ void quiet() { __syncthreads(); }
 
 __device__ __forceinline__ float hsum8(const float* v) {
     const float c0 = v[0] + v[4], c1 = v[1] + v[5], c2 = v[2] + v[6], c3 = v[3] + v[7];
@@ -790,7 +879,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 float shv[kPer], lrp[6][kPer];
                 f4 sv[kSPer];
                 if (!owner) {
-                    stager_issue(pend, S, wrow);   // the first weights, ahead of the wait
+                    stager_issue(pend, stg, S, wrow);   // the first weights, ahead of the wait
                     // the LayerNorm, shift and mix parameters, ahead of the wait too
                     ln_load(lp, P.ln1w, P.ln1b, D);
 #pragma unroll
@@ -810,6 +899,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 // x_b of the layer before (every wave is past its last use of
                 // xs and of the other table slot once the poll's barrier is)
                 if (l > 0) {
+                    quiet();
                     const bool ok = poll_vec<kPer, NT>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
                     if (!agree(ok)) return;
                 }
@@ -891,6 +981,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                     clnb = P.lnxb[c];
                 }
                 issued();
+                quiet();
                 {
                     const int i = min(tid, kRkPRank - 1), c = c0 + (tid & 63);
                     const bool lora = tid < kRkPRank, chan = tid < HS;
@@ -1035,9 +1126,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 auto wrow = [&](int i) -> gptr<f4> { return (gptr<f4>)(glb(wb) + (size_t)i * D); };
                 const bool ok = with_kl(lsc_kl(hi - lo, D), [&](auto kl) -> bool {
                     Phase<decltype(kl)::value> ph;
-                    ph.issue(pend, hi - lo, D, wrow);
+                    ph.issue(pend, stg, hi - lo, D, wrow);
                     issued();
                     RKE_MARK(l, 5);
+                    quiet();
                     if (!agree(poll_vec<kPer, NT>(s_y, D, buf, pc))) return false;
                     RKE_MARK(l, 6);
                     // shift_0 <- xn (rwkv7.c:229), by a workgroup past the head
@@ -1063,7 +1155,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 const float* wb = uni(P.cmk.w) + (size_t)lo * D;
                 auto wrow = [&](int i) -> gptr<f4> { return (gptr<f4>)(glb(wb) + (size_t)i * D); };
                 const Stager S = stager(hi - lo, D);
-                stager_issue(pend, S, wrow);
+                stager_issue(pend, stg, S, wrow);
                 LnP lp;
                 ln_load(lp, P.ln2w, P.ln2b, D);
                 float shv[kPer], lrp[kPer];
@@ -1075,6 +1167,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 }
                 issued();
                 RKE_MARK(l, 7);
+                quiet();
                 if (!agree(poll_vec<kPer, NT>(s_xa, D, xs, pc))) return;
                 RKE_MARK(l, 8);
                 ln_exact(xs, xn2, sq, lp, D, A.eps, stat);
@@ -1105,9 +1198,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 auto wrow = [&](int i) -> gptr<f4> { return (gptr<f4>)(glb(wb) + (size_t)i * F); };
                 const bool ok = with_kl(lsc_kl(hi - lo, F), [&](auto kl) -> bool {
                     Phase<decltype(kl)::value> ph;
-                    ph.issue(pend, hi - lo, F, wrow);
+                    ph.issue(pend, stg, hi - lo, F, wrow);
                     issued();
                     RKE_MARK(l, 9);
+                    quiet();
                     if (!agree(poll_vec<kPerF, NT>(s_ck, F, buf, pc))) return false;
                     RKE_MARK(l, 10);
                     // Every workgroup has read shift_1 by now: each has rows of ck.
@@ -1129,6 +1223,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         {
             LnP lp;
             ln_load(lp, A.on_w, A.on_b, D);
+            quiet();
             if (!agree(poll_vec<kPer, NT>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return;
             ln_exact(xs, buf, sq, lp, D, A.eps, stat);
             int lo, hi;
