@@ -537,6 +537,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 // x_b of the layer before (every wave is past its last use of xs
                 // and of the other layer-table slot once the poll's barrier is)
                 if (l > 0) {
+                    __syncthreads();   // waves done early sleep here instead of polling
                     const bool ok = poll_vec<kPer, NT>(A.xch + (size_t)(l - 1) * slab + 5 * D, D, xs, pc);
                     if (!agree(ok)) return;
                 }
@@ -775,6 +776,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     PreRows<Q, NU, 1> pr;
                     pre_load(pr, P.o, lo + wv, NW, lane);
                     issued();
+                    __syncthreads();
                     if (!agree(poll_vec<kPer, NT>(s_y, D, buf, pc))) return false;
                     RKP_MARK(l * 6 + 2, 0);
                     // shift_0 <- xn (:229). Every workgroup has read shift_0 by
@@ -815,6 +817,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     }
                     ln_params(P.ln2w, P.ln2b, D, lg, lc);
                     issued();
+                    __syncthreads();
                     if (!agree(poll_vec<kPer, NT>(s_xa, D, xs, pc))) return false;
                     RKP_MARK(l * 6 + 3, 0);
                     PreRows<Q, NU, 2> pr;                   // rows lo + wv and lo + wv + NW
@@ -854,6 +857,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                     PreRows<Q, NU, 1> pr;
                     pre_load(pr, P.cmv, lo + wv, NW, lane);
                     issued();
+                    __syncthreads();
                     if (!agree(poll_vec<kPerF, NT>(s_ck, F, buf, pc))) return false;
                     RKP_MARK(l * 6 + 4, 0);
                     // Every workgroup has read shift_1 by now: each has rows of
@@ -891,6 +895,7 @@ __global__ __launch_bounds__(NT) void k_rk_persist(RkPArgs A) {
                 ln_params(A.on_w, A.on_b, D, lg, lc);
                 pre_load(ra, A.head, lo + wv, NW, lane);
                 issued();
+                __syncthreads();
                 if (!agree(poll_vec<kPer, NT>(A.xch + (size_t)(L - 1) * slab + 5 * D, D, xs, pc))) return false;
                 layer_norm(xs, buf, lg, lc, D, A.eps, red);
                 auto finish = [&](const float (&d)[N], int row) {
