@@ -67,10 +67,10 @@ SCAN_TRAFFIC_BYTES = 1_611_150_336
 # decode`, calibrated like the scan's and divided by the call's steps. Filled
 # from the tables of profiles/decode_pmc_traffic.md.
 DECODE_TRAFFIC: dict = {
-    ("int4", 1): 96_466_653, ("int4", 8): 155_521_575, ("int4", 32): 174_586_226,
-    ("fp32", 1): 517_571_761, ("fp32", 64): 627_475_191, ("fp16", 1): 285_594_889,
-    ("small", 1): 1_388_874, ("rwkv7", 1): 116_087_372, ("rwkv7", 64): 843_921_460,
-    ("rwkv7-persist", 1): 153_085_884,
+    ("int4", 1): 96_480_189, ("int4", 8): 156_178_634, ("int4", 32): 174_586_178,
+    ("fp32", 1): 517_492_516, ("fp32", 64): 627_625_344, ("fp16", 1): 285_596_977,
+    ("small", 1): 1_372_454, ("rwkv7-exact", 1): 459_086_488, ("rwkv7", 64): 843_898_581,
+    ("rwkv7-persist", 1): 149_506_321,
 }
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
 
