@@ -305,13 +305,9 @@ __device__ __forceinline__ bool whole_fits(int R, int K) { return R * (K + 4) <=
 __device__ __forceinline__ void split(int i, int C4, float inv, int& r, int& c4) {
     r = (int)((float)i * inv);
     c4 = i - r * C4;
-    if (c4 < 0) {
-        --r;
-        c4 += C4;
-    } else if (c4 >= C4) {
-        ++r;
-        c4 -= C4;
-    }
+    const int adj = (int)(c4 >= C4) - (int)(c4 < 0);   // no branch
+    r += adj;
+    c4 -= adj * C4;
 }
 
 // One product phase's staging plan (uniform values). A chunk is C4 float4 of
@@ -348,6 +344,9 @@ __device__ __forceinline__ void whole_issue_lds(float* stg, const Stager& S, WR&
     typedef __attribute__((address_space(3))) void lvoid;
     const int W4 = S.K4 + 1, n = S.R * W4, tid = threadIdx.x;
     const float inv = 1.0f / (float)W4;
+    // unrolled: the loop's back edge made the compiler copy ~20 live
+    // registers per trip
+#pragma unroll 8
     for (int base = 0; base < n; base += NT) {
         const int q = base + tid;
         if (q < n) {
@@ -846,25 +845,38 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 } else {
                     share(total, wg, G, lo, hi);
                 }
+                // segment and row of P1 row `row` (selects, no branches)
                 auto locate = [&](int row, int& sg, int& r) {
                     sg = 0;
                     r = row;
 #pragma unroll
-                    for (int q = 0; q < 6; ++q)
-                        if (sg == q && r >= M[q]) {
-                            r -= M[q];
-                            sg = q + 1;
-                        }
+                    for (int q = 0; q < 6; ++q) {
+                        const bool adv = sg == q && r >= M[q];
+                        r = adv ? r - M[q] : r;
+                        sg = adv ? q + 1 : sg;
+                    }
                 };
                 const int xoff[7] = {0, 2 * D, 3 * D, D, 4 * D, 5 * D, 3 * D};
                 // this workgroup's rows from segment sA's row rA on: nA of them
                 // there, the rest from the start of the next segment (a share
                 // spans two segments at most when no segment is shorter than
                 // it; otherwise every row is located on its own)
+                // (uniform values: the branch below is a scalar one, so a
+                // workgroup whose share is in two segments never runs the
+                // general lookup per row)
                 int sA, rA;
                 locate(lo, sA, rA);
-                const int nA = M[sA] - rA;
-                const bool two = hi - lo <= nA || (sA + 1 < nseg && hi - lo - nA <= M[sA + 1]);
+                sA = __builtin_amdgcn_readfirstlane(sA);
+                rA = __builtin_amdgcn_readfirstlane(rA);
+                int MA = M[0], MB = M[1];   // M[sA], M[sA + 1] (no run-time index)
+#pragma unroll
+                for (int q = 1; q < 7; ++q) {
+                    MA = sA == q ? M[q] : MA;
+                    MB = sA + 1 == q ? M[q] : MB;
+                }
+                const int nA = __builtin_amdgcn_readfirstlane(MA - rA);
+                const bool two = __builtin_amdgcn_readfirstlane(
+                                     hi - lo <= nA || (sA + 1 < nseg && hi - lo - nA <= MB)) != 0;
                 const float* bA = uni(p1_mat(P, sA).w) + (size_t)rA * D;
                 const float* bB = uni(p1_mat(P, min(sA + 1, nseg - 1)).w);
                 auto wrow = [&](int i) -> gptr<f4> {
