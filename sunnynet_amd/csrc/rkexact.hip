@@ -82,6 +82,15 @@ __device__ __forceinline__ f4 stream_ld(gptr<f4> p) { return __builtin_nontempor
 // so waiting for x does not also wait for the weight reads in flight.
 typedef __attribute__((address_space(3))) const f4 l_f4;
 __device__ __forceinline__ const l_f4* lds4(const float* p) { return (const l_f4*)p; }
+// The same pointer with its whole address in a vector register, for loops of
+// reads through a pointer every lane holds alike: from a wave-uniform base the
+// compiler rebuilds every read's address (two moves, or an add when the base
+// is past 64 KB and does not fit the reads' offset field).
+__device__ __forceinline__ const l_f4* vaddr(const l_f4* p) {
+    uint32_t a = (uint32_t)(size_t)p;
+    asm volatile("" : "+v"(a));
+    return (const l_f4*)(size_t)a;
+}
 
 // One wave runs each chain below, so the wave's instruction issue bounds it:
 // a dependent VALU op every ~5.4 clocks, and every ds_read_b128 takes issue
@@ -98,6 +107,7 @@ constexpr int kPad = 32;
 // multiple of 16).
 __device__ __forceinline__ float seq_sum(const l_f4* v, int n4) {
     constexpr int W = 8;
+    v = vaddr(v);
     f4 r[2][W];
     float s = 0.0f;
 #pragma unroll
@@ -128,6 +138,7 @@ __device__ __forceinline__ float seq_sum(const l_f4* v, int n4) {
 // (twelve reads outstanding; reads reach 6 float4 past the last multiple of 8).
 __device__ __forceinline__ float lds_chain(const l_f4* w, const l_f4* x, int n4, float acc) {
     constexpr int W = 2, AH = 3, NS = AH + 1;
+    x = vaddr(x);   // x may be the same for every lane
     f4 wr[NS][W], xr[NS][W];
 #pragma unroll
     for (int a = 0; a < AH; ++a)
@@ -551,6 +562,7 @@ __device__ __forceinline__ auto with_kl(int kl, F&& f) {
 template <bool FUSED>
 __device__ __forceinline__ float chain_f32(gptr<f4> w, const l_f4* x, int K4) {
     constexpr int PF = 8;
+    x = vaddr(x);
     f4 a[PF];
 #pragma unroll
     for (int j = 0; j < PF; ++j) a[j] = w[min(j, K4 - 1)];
@@ -581,6 +593,7 @@ __device__ __forceinline__ float chain_f32(gptr<f4> w, const l_f4* x, int K4) {
 
 template <int BLK, bool FUSED>
 __device__ __forceinline__ float chain_i4(gptr<u4> q, gptr<float> sc, const l_f4* x, int ng) {
+    x = vaddr(x);
     constexpr int NQ = BLK / 32;   // 16-byte reads per group
     constexpr int NP = 4;          // groups in flight
     u4 cb[NP][NQ];
@@ -1077,11 +1090,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                     // state row t (rwkv7.c:165-187), four columns at a time
                     // from the LDS copy; column j's terms go to partial j mod 8
                     const l_f4* srow = lds4(buf + tid * kSRow);
+                    const l_f4 *kn4p = vaddr(lds4(kn_)), *a4p = vaddr(lds4(a_)), *k4p = vaddr(lds4(k_)),
+                               *w4p = vaddr(lds4(w_)), *r4p = vaddr(lds4(r_));
                     const float vv = v_[tid];
                     float proj[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int c = 0; c < HS / 4; ++c) {
-                        const f4 s4 = srow[c], kn4 = lds4(kn_)[c];
+                        const f4 s4 = srow[c], kn4 = kn4p[c];
                         const int q = 4 * (c & 1);
                         proj[q] = fmaf(s4.x, kn4.x, proj[q]);
                         proj[q + 1] = fmaf(s4.y, kn4.y, proj[q + 1]);
@@ -1093,8 +1108,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                     float* Srow = Sh + (size_t)tid * HS;
 #pragma unroll
                     for (int c = 0; c < HS / 4; ++c) {
-                        const f4 s4 = srow[c], kn4 = lds4(kn_)[c], a4 = lds4(a_)[c], k4 = lds4(k_)[c],
-                                 w4 = lds4(w_)[c], r4 = lds4(r_)[c];
+                        const f4 s4 = srow[c], kn4 = kn4p[c], a4 = a4p[c], k4 = k4p[c], w4 = w4p[c], r4 = r4p[c];
                         const int q = 4 * (c & 1);
                         f4 ns;
 #pragma unroll
