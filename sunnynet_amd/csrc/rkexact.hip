@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "gemv.h"
+#include "lanesum.h"
 #include "refmath.h"
 #include "rkpersist.h"
 #include "rkxch.h"
@@ -192,47 +193,22 @@ __device__ __forceinline__ void ln_load(LnP& p, const float* g, const float* c, 
     }
 }
 
-// sum = sum + v[i] over the 256 KL4 values a wave holds, value 4 KL4 j + e
-// in lane j, element e (v[e / 4][e % 4]), in order: each lane adds its values
-// to the running sum of the lanes before, which passes from lane j to lane
-// j + 1 as a wave-uniform value. Every lane returns the total.
-template <int KL4>
-__device__ __forceinline__ float lane_seq_sum(const f4 (&v)[KL4]) {
-    float acc = 0.0f;
-    for (int j = 0; j < 64; ++j) {
-        float a = acc;
-#pragma unroll
-        for (int q = 0; q < KL4; ++q) {
-            a = a + v[q].x;
-            a = a + v[q].y;
-            a = a + v[q].z;
-            a = a + v[q].w;
-        }
-        acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), j));
-    }
-    return acc;
-}
-
-// LN statistics of n = 256 KL4 values in LDS by wave 0, lane-sliced: the
-// mean as a sequential sum, then the squared deviations' sum, with the
-// values in registers throughout (no LDS pass between the two sums).
+// LN statistics of n = 256 KL4 values in LDS by wave 0, lane-sliced
+// (lanesum.h): the values stay in registers for both sums.
 template <int KL4>
 __device__ __forceinline__ void ln_stats_lanes(const float* src, int n, float eps, float* stat) {
     const int lane = threadIdx.x & 63;
-    f4 v[KL4];
-#pragma unroll
-    for (int q = 0; q < KL4; ++q) v[q] = lds4(src)[lane * KL4 + q];
-    const float mean = lane_seq_sum(v) / (float)n;
+    float v[4 * KL4];
 #pragma unroll
     for (int q = 0; q < KL4; ++q) {
-        f4 d;
-        d.x = v[q].x - mean; d.y = v[q].y - mean; d.z = v[q].z - mean; d.w = v[q].w - mean;
-        v[q].x = d.x * d.x; v[q].y = d.y * d.y; v[q].z = d.z * d.z; v[q].w = d.w * d.w;
+        const f4 x = lds4(src)[lane * KL4 + q];
+        v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
     }
-    const float var = lane_seq_sum(v);
+    float mean, rstd;
+    lane_ln_stats(v, n, eps, mean, rstd);
     if (lane == 0) {
         stat[0] = mean;
-        stat[1] = 1.0f / sqrtf(var / (float)n + eps);
+        stat[1] = rstd;
     }
 }
 

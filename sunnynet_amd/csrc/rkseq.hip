@@ -22,6 +22,7 @@
 #include <cstring>
 #include <type_traits>
 
+#include "lanesum.h"
 #include "refmath.h"
 #include "rkseq.h"
 #include "snhip_rwkv7.h"
@@ -124,21 +125,48 @@ __global__ __launch_bounds__(LT) void k_rkq_ln(RkqLnArgs A) {
         }
     }
     __syncthreads();
-    if (t == 0) stat[0] = seq_sum(xs4, n4) / (float)D;   // sum = sum + x[i], in order
-    __syncthreads();
-    const float mean = stat[0];
-    for (int q = t; q < n4; q += LT) {
-        const float4 v = xs4[q];
-        float4 d;
-        d.x = v.x - mean; d.y = v.y - mean; d.z = v.z - mean; d.w = v.w - mean;
-        d.x = d.x * d.x; d.y = d.y * d.y; d.z = d.z * d.z; d.w = d.w * d.w;
-        sq4[q] = d;
+    // sum = sum + x[i], then vsum = vsum + d * d, in order: lane-sliced in
+    // wave 0 (lanesum.h) for rows of 256, 512, 768 or 1024, else by thread 0
+    const int kl = D % 256 ? 0 : D / 256;
+    if (kl >= 1 && kl <= 4) {
+        if (t < 64) {
+            auto go = [&](auto k) {
+                constexpr int KL4 = decltype(k)::value;
+                float v[4 * KL4];
+#pragma unroll
+                for (int q = 0; q < KL4; ++q) {
+                    const float4 x = xs4[t * KL4 + q];
+                    v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+                }
+                float m, r;
+                lane_ln_stats(v, D, A.eps, m, r);
+                if (t == 0) {
+                    stat[0] = m;
+                    stat[1] = r;
+                }
+            };
+            if (kl == 1) go(std::integral_constant<int, 1>{});
+            else if (kl == 2) go(std::integral_constant<int, 2>{});
+            else if (kl == 3) go(std::integral_constant<int, 3>{});
+            else go(std::integral_constant<int, 4>{});
+        }
+        __syncthreads();
+    } else {
+        if (t == 0) stat[0] = seq_sum(xs4, n4) / (float)D;
+        __syncthreads();
+        const float m0 = stat[0];
+        for (int q = t; q < n4; q += LT) {
+            const float4 v = xs4[q];
+            float4 d;
+            d.x = v.x - m0; d.y = v.y - m0; d.z = v.z - m0; d.w = v.w - m0;
+            d.x = d.x * d.x; d.y = d.y * d.y; d.z = d.z * d.z; d.w = d.w * d.w;
+            sq4[q] = d;
+        }
+        __syncthreads();
+        if (t == 0) stat[1] = 1.0f / sqrtf(seq_sum(sq4, n4) / (float)D + A.eps);
+        __syncthreads();
     }
-    __syncthreads();
-    if (t == 0)                         // vsum = vsum + d * d, in order
-        stat[1] = 1.0f / sqrtf(seq_sum(sq4, n4) / (float)D + A.eps);
-    __syncthreads();
-    const float rstd = stat[1];
+    const float mean = stat[0], rstd = stat[1];
     float4* o4 = reinterpret_cast<float4*>(A.out);
     auto norm = [&](float x, float g, float c) { return (x - mean) * rstd * g + c; };
     auto emit = [&](int q, float4 g, float4 c, float4 sh, const float4* lp) {
