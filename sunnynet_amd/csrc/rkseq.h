@@ -35,8 +35,17 @@ struct RkqJob {
 };
 constexpr int kRkqMaxJobs = 8;
 
-// Jobs share the weight format: block 0 = fp32, 32 or 64 = INT4 group.
+// Jobs share the weight format: block 0 = fp32 rows, 32 or 64 = INT4 group,
+// -1 = tiled fp32 (float4 (t * Kd / 4 + kb) * 64 + l = inputs 4 kb .. 4 kb + 3
+// of row 64 t + l, then a zeroed pad; launch_rkq_block4 makes them).
 snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStream_t st);
+// floats of the tiled fp32 form of an M x Kd matrix, pad included
+size_t rkq_tiled_floats(int M, int Kd);
+// out (rkq_tiled_floats) = the tiled fp32 form of an M x Kd matrix given as
+// fp32 rows w (block 0) or INT4 codes q and scales sc (block 32 or 64), each
+// value the one the products multiply by.
+snhip_status launch_rkq_block4(const float* w, const uint8_t* q, const float* sc, int block, int M, int Kd,
+                               float* out, hipStream_t st);
 // The same with the INT4 workgroup shape given: nc consumer waves of s chains
 // of 4 sequences (nc in {1, 2, 4}, s in {1, 2}, not 4 x 2), or s = 16: one
 // 16x16x1 chain of 16 sequences per consumer; 0 = chosen by B and the grid.

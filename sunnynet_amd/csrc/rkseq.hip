@@ -19,6 +19,8 @@
 //   sequential sum while the others prepare the squared deviations.
 // * Heads: one wave per (head, sequence), lane i owning state row i.
 // * expf / tanhf: refmath.h (glibc's algorithms).
+#include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <type_traits>
 
@@ -32,6 +34,7 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
 constexpr float kR2 = 0.6065306597126334f;   // 1/sqrt(e), rwkv7.c:38
 constexpr float kEpsGroup = 6.4e-4f;          // rwkv7.c:39
@@ -224,9 +227,12 @@ struct RkqMMArgs {
     int start[kRkqMaxJobs + 1];   // first workgroup of each job
     int tiles_out[kRkqMaxJobs];   // 64-row tiles of each job
     int n, B, seq_tiles;
+    int xs_per_wave;              // tiled fp32: float4 of LDS per wave
 };
 
 __device__ __forceinline__ float dequant_at(const RkqJob& J, int row, int k, int blk) {
+    if (blk < 0)   // tiled fp32 (k_rkq_mm_w4)
+        return J.w[(((size_t)(row >> 6) * (size_t)(J.Kd >> 2) + (size_t)(k >> 2)) * 64 + (row & 63)) * 4 + (k & 3)];
     if (!blk) return J.w[(size_t)row * J.Kd + k];
     const int half = blk / 2, g = k / blk, e = k % blk;
     const uint8_t byte = J.q[(size_t)row * (J.Kd / 2) + (size_t)g * half + (e % half)];
@@ -259,6 +265,17 @@ __device__ __forceinline__ void step4(const float4 (&x4)[S], float w0, float w1,
     mfma_k<S>(xv, w3, acc);
 }
 
+template <int S>
+__device__ __forceinline__ void step4(const v4f (&x4)[S], float w0, float w1, float w2, float w3, v4f (&acc)[S]) {
+    float xv[S];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) xv[s] = x4[s][c];
+        mfma_k<S>(xv, c == 0 ? w0 : c == 1 ? w1 : c == 2 ? w2 : w3, acc);
+    }
+}
+
 // Inputs per chunk staged in LDS at once (X rows; INT4 codes in registers).
 constexpr int kRkqKC = 768;
 constexpr int kRkqU = 64;                  // INT4: inputs per pipeline unit (two producer halves of 32)
@@ -269,16 +286,19 @@ constexpr int kRkqNP = 2;                  // producer waves of an INT4 workgrou
 // index: selecting it by index afterwards was folded back into an indexed
 // read of a local copy of start[], which the compiler kept in scratch memory
 // (a store and a dependent load at every launch).
-__device__ __forceinline__ void rkq_job(const RkqMMArgs& A, RkqJob& J, int& u0) {
+__device__ __forceinline__ void rkq_job_at(const RkqMMArgs& A, int wg, RkqJob& J, int& u0) {
     int ji = 0, j0 = A.start[0];
 #pragma unroll
     for (int i = 1; i < kRkqMaxJobs; ++i)
-        if (i < A.n && (int)blockIdx.x >= A.start[i]) { ji = i; j0 = A.start[i]; }
+        if (i < A.n && wg >= A.start[i]) { ji = i; j0 = A.start[i]; }
     J = A.j[0];
 #pragma unroll
     for (int i = 1; i < kRkqMaxJobs; ++i)
         if (i == ji) J = A.j[i];
-    u0 = (int)blockIdx.x - j0;
+    u0 = wg - j0;
+}
+__device__ __forceinline__ void rkq_job(const RkqMMArgs& A, RkqJob& J, int& u0) {
+    rkq_job_at(A, (int)blockIdx.x, J, u0);
 }
 
 // Tail columns and the epilogue of one lane's 4 sequences (seq0 .. seq0+3)
@@ -386,6 +406,205 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) rkq_finish(J, A.B, 0, seq0 + 4 * s, out, acc[s]);
+}
+
+// Tiled fp32 weights (block = -1), made at load from the INT4 codes with the
+// producers' dequantization, or from fp32 rows: float4 (t * nb + kb) * 64 + l
+// holds inputs 4 kb .. 4 kb + 3 of row 64 t + l (rows past M repeat row
+// M - 1), nb = Kd / 4, followed by kRkwPad float4 that loads past the end
+// may touch. One wave per workgroup: 64 rows x S groups of 4 sequences,
+// nothing shared with other waves, so no barrier paces its chains. A chain
+// step is one dependent v_mfma_f32_4x4x1_16b_f32 (~13 cycles on gfx950),
+// and every other instruction of the wave lengthens it (measured: X read from
+// LDS once per 4 inputs, 13.3 -> 15.3 cycles per input; with 64-bit address
+// arithmetic for a weight load added, 21), so a block of 4 inputs issues
+// only its MFMAs, one buffer load of the next weights (1 KiB of consecutive
+// memory; the scalar offset advances, the lane offset and the immediate stay
+// fixed) and one LDS read of X at an immediate offset from the lane's base.
+// The wave's X rows go straight into LDS at the start (one load latency);
+// its weight blocks run rkw_pf blocks ahead in registers. Workgroups are
+// renumbered so that consecutive numbers run on one XCD (dispatch is
+// round-robin over the 8 XCDs): the sequence tiles of an output tile then
+// read its weights from one L2.
+template <int S>
+constexpr int rkw_pf() { return S == 1 ? 48 : S == 2 ? 40 : 24; }
+constexpr int kRkwXA = 4;          // X blocks read from LDS ahead of the MFMAs
+constexpr int kRkwXMax = 4096;     // float4 of X per workgroup (64 KiB): S * Kd <= this
+constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: > rkw_pf)
+constexpr int kRkwL2 = 32;         // weight blocks a wave prefetches into the L2 at most
+// s_waitcnt vmcnt(n) (expcnt, lgkmcnt at their maximum; gfx9 split vmcnt field)
+constexpr int rkw_vmcnt(int n) { return ((n >> 4) & 3) << 14 | 0x0F70 | (n & 15); }
+
+// Direct-to-LDS loads the compiler does not see (inline asm): lane l's 16
+// (4) bytes at gaddr go to LDS byte lds + 16 l (4 l), lds wave-uniform. M0,
+// which holds the LDS base, is saved and restored around the load, and one
+// wait state separates its write from the load. Seen by the compiler
+// (builtin), these writes to LDS counted as pending at every later LDS read
+// of the kernel's chain loop, which then waited for all loads at the top of
+// each trip and drained the weight prefetch; in a function of their own,
+// the call boundary waited for every load. The caller waits for them itself
+// (they are its oldest loads) before its first read of what they bring.
+__device__ __forceinline__ void dma_lds16(const void* gaddr, uint32_t lds) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(gaddr), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ void dma_lds4(const void* gaddr, uint32_t lds) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(gaddr), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// An LDS address (LDS-typed, so reads through it are ds_read, counted by
+// lgkmcnt only) held in a vector register as far as the compiler knows, so
+// that reads through it keep their whole address in the one register and
+// take the rest as an immediate offset.
+typedef __attribute__((address_space(3))) const v4f lds_f4;
+__device__ __forceinline__ const lds_f4* lds_vbase(const float4* p) {
+    uint32_t a = (uint32_t)(size_t)(const lds_f4*)p;
+    asm volatile("" : "+v"(a));
+    return (const lds_f4*)(size_t)a;
+}
+
+template <int S, int NW>
+__global__ __launch_bounds__(64 * NW) void k_rkq_mm_w4(const RkqMMArgs A) {
+    constexpr int PF = rkw_pf<S>();
+    constexpr int R = 4 * S;   // sequences of the wave
+    static_assert(PF % kRkwXA == 0, "the X ring restarts with each weight group");
+    extern __shared__ float4 xsh[];
+    // NW independent waves per workgroup (one per SIMD): sequence tiles
+    // NW u0 .. NW u0 + NW - 1 of one output tile; a wave past the last tile
+    // has no work (nothing here waits on another wave)
+    const int T = (int)gridDim.x, b = (int)blockIdx.x, q8 = T / 8, r8 = T % 8, x8 = b % 8;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    RkqJob J;
+    int u0;
+    rkq_job_at(A, x8 * q8 + min(x8, r8) + b / 8, J, u0);
+    const int wg_per_tile = (A.seq_tiles + NW - 1) / NW;
+    const int ot = u0 / wg_per_tile, st = (u0 % wg_per_tile) * NW + wv;
+    if (st >= A.seq_tiles) return;
+    float4* xs = xsh + (size_t)wv * (A.xs_per_wave);
+    const int l = threadIdx.x & 63, r4 = l & 3;
+    const int out = ot * 64 + l;
+    const int seq0 = st * R;
+    const int nb = J.Kd / 4;
+    // the whole tiled matrix with its padding; block kb of this tile at
+    // scalar offset (ot * nb + kb) * 1 KiB, lane offset 16 l
+    const uint32_t bytes = (uint32_t)(((size_t)((J.M + 63) / 64) * nb * 64 + kRkwPad) * sizeof(float4));
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(J.w), (short)0, (int)bytes,
+                                                                        0x00020000);
+    const int vo = 16 * l;
+    const int sob = ot * nb * 1024;
+    auto ldw = [&](int kb) -> float4 {
+        const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rw, vo, sob + kb * 1024, 0);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+    };
+    // The wave's X rows into LDS (float4 f = kb * R + row: lane l of pass f0
+    // brings float4 f0 + l; past the end the last one again, into the
+    // padding of the launch's LDS size).
+    const int nx = nb * R;
+    for (int f0 = 0; f0 < nx; f0 += 64) {
+        const int f = min(f0 + l, nx - 1);
+        const int kb = f / R, row = f - kb * R;
+        dma_lds16(J.X + (size_t)min(seq0 + row, A.B - 1) * (size_t)J.ldx + 4 * kb, lds_addr(xs + f0));
+    }
+    // The L2 prefetch: this sequence tile's share of the output tile's
+    // weights (at most kRkwL2 blocks; lane l touches bytes 16 l .. + 4 of each
+    // 1 KiB block, so every 128-byte line) into a 256-byte LDS slot nothing
+    // reads. The sequence tiles of an output tile each take their own part,
+    // so its weights leave HBM together at the start rather than block by
+    // block as every chain reaches them.
+    {
+        const int share = (nb + A.seq_tiles - 1) / A.seq_tiles, pf0 = min(st * share, nb);
+        const int npf = min(min(share, nb - pf0), kRkwL2);
+        const char* wb = reinterpret_cast<const char*>(J.w) + (size_t)(sob + pf0 * 1024) + 16 * l;
+        const uint32_t dump = lds_addr(xs + A.xs_per_wave - 16);
+        for (int j = 0; j < npf; ++j) dma_lds4(wb + 1024 * j, dump);
+    }
+    float4 w[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) w[i] = ldw(i);
+    // X (and the L2 prefetch) in: every load but the PF weight loads above
+    __builtin_amdgcn_s_waitcnt(rkw_vmcnt(PF));
+    __builtin_amdgcn_sched_barrier(0);
+    v4f xa[kRkwXA][S];
+    v4f acc[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
+    {
+        const lds_f4* xq = lds_vbase(xs + r4);   // block kb of group s: xq[kb * R + 4 s]
+#pragma unroll
+        for (int j = 0; j < kRkwXA; ++j)
+#pragma unroll
+            for (int s = 0; s < S; ++s) xa[j][s] = xq[j * R + 4 * s];
+    }
+    // X past block nb - 1 is read from the launch's LDS padding and weights
+    // past the tile from the next tile or the padding, never used.
+    int b0 = 0;
+    for (; b0 + PF <= nb; b0 += PF) {
+        const lds_f4* xq = lds_vbase(xs + r4 + b0 * R);
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+            step4<S>(xa[i % kRkwXA], w[i].x, w[i].y, w[i].z, w[i].w, acc);
+            w[i] = ldw(b0 + PF + i);
+#pragma unroll
+            for (int s = 0; s < S; ++s) xa[i % kRkwXA][s] = xq[(i + kRkwXA) * R + 4 * s];
+            // each block's refill stays with it (the scheduler otherwise sank
+            // the group's weight loads below its last MFMA)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const int rem = nb - b0;   // < PF blocks, already in registers
+    const lds_f4* xq = lds_vbase(xs + r4 + b0 * R);
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+        if (i < rem) {
+            step4<S>(xa[i % kRkwXA], w[i].x, w[i].y, w[i].z, w[i].w, acc);
+#pragma unroll
+            for (int s = 0; s < S; ++s) xa[i % kRkwXA][s] = xq[(i + kRkwXA) * R + 4 * s];
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) rkq_finish(J, A.B, -1, seq0 + 4 * s, out, acc[s]);
+}
+
+// The tiled form (above) of an M x Kd matrix: each value the one the
+// products use (dequant_at: fp32 rows, or INT4 codes dequantized as the
+// producers do); the padding is zeroed.
+__global__ __launch_bounds__(256) void k_rkq_block4(RkqJob J, int blk, float4* out) {
+    const int nb = J.Kd / 4;
+    const size_t n = (size_t)((J.M + 63) / 64) * nb * 64;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n + kRkwPad) return;
+    if (i >= n) {
+        out[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const int l = (int)(i % 64), kb = (int)((i / 64) % nb), t = (int)(i / 64 / nb);
+    const int o = min(64 * t + l, J.M - 1);
+    float4 v;
+    v.x = dequant_at(J, o, 4 * kb, blk);
+    v.y = dequant_at(J, o, 4 * kb + 1, blk);
+    v.z = dequant_at(J, o, 4 * kb + 2, blk);
+    v.w = dequant_at(J, o, 4 * kb + 3, blk);
+    out[i] = v;
 }
 
 // INT4 weights: a workgroup of kRkqNP producer waves and NC consumer waves
@@ -865,27 +1084,62 @@ int cu_count() {
 }
 
 // nc, s: INT4 consumer waves per workgroup and chains per consumer (0: chosen
-// here); fp32: s groups of 4 sequences per wave.
+// here); fp32 rows: s groups of 4 sequences per wave; tiled fp32: nc waves
+// per workgroup, s groups of 4 sequences per wave.
 snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int nc, int s,
                                hipStream_t st) {
-    if (n <= 0 || n > kRkqMaxJobs || B <= 0 || (block != 0 && block != 32 && block != 64))
+    if (n <= 0 || n > kRkqMaxJobs || B <= 0 || (block != -1 && block != 0 && block != 32 && block != 64))
         return SNHIP_E_INVAL;
     RkqMMArgs a{};
-    int tiles1 = 0;
+    int tiles1 = 0, kmax = 0;
     for (int i = 0; i < n; ++i) {
         const RkqJob& J = jobs[i];
-        const int kq = block ? block : 4;
+        const int kq = block > 0 ? block : 4;
         if (J.M <= 0 || J.Kd <= 0 || J.Kd % kq || J.ldx % 4 || !J.X || !J.Y ||
-            (block ? (!J.q || !J.sc || J.Kd % 32) : !J.w))
+            (block > 0 ? (!J.q || !J.sc || J.Kd % 32) : !J.w))
             return SNHIP_E_INVAL;
         a.j[i] = J;
         a.tiles_out[i] = (J.M + 63) / 64;
         tiles1 += a.tiles_out[i];
+        kmax = std::max(kmax, J.Kd);
     }
     int per;   // sequences per workgroup
     int S = 1, NC = 1;
     bool xl = false;   // INT4: four one-chain consumers per workgroup, X staged in LDS
-    if (block == 0) {
+    size_t shm = 0;
+    int NW = 1;   // tiled fp32: waves per workgroup
+    if (block < 0) {
+        // One chain per wave; the waves of one output tile's sequence tiles
+        // in workgroups of NW (one per SIMD) once there are more waves than
+        // CUs; more than four per CU: two chains per wave, and so on.
+        const long cus = cu_count();
+        auto waves = [&](int s_) { return (long)tiles1 * ((B + 4 * s_ - 1) / (4 * s_)); };
+        // SNHIP_RKQ_W4_SHAPE=S,NW (tuning): that shape wherever it fits
+        if (!s && !nc)
+            if (const char* e = getenv("SNHIP_RKQ_W4_SHAPE")) {
+                int s_ = 0, n_ = 0;
+                if (sscanf(e, "%d,%d", &s_, &n_) == 2 && (s_ == 1 || s_ == 2 || s_ == 4) &&
+                    (n_ == 1 || n_ == 2 || n_ == 4) && s_ * kmax <= kRkwXMax &&
+                    (size_t)n_ * ((s_ * kmax + 63) / 64 * 64 + kRkwXA * 4 * s_ + 16) * sizeof(float4) <= 65536) {
+                    s = s_;
+                    nc = n_;
+                }
+            }
+        S = 1;
+        if (s) S = s;
+        else
+            while (S < 4 && waves(S) > 4 * cus) S *= 2;
+        while (!s && S > 1 && S * kmax > kRkwXMax) S /= 2;
+        if ((S != 1 && S != 2 && S != 4) || S * kmax > kRkwXMax) return SNHIP_E_INVAL;
+        NW = nc ? nc : waves(S) <= cus ? 1 : waves(S) <= 2 * cus ? 2 : 4;
+        // per wave: X (S Kd float4, rounded up to the staging's 64) and the
+        // read-ahead past the last block; at most 64 KiB per workgroup
+        a.xs_per_wave = (S * kmax + 63) / 64 * 64 + kRkwXA * 4 * S + 16;   // + the prefetch's dump slot
+        while (!nc && NW > 1 && (size_t)NW * a.xs_per_wave * sizeof(float4) > 65536) NW /= 2;
+        shm = (size_t)NW * a.xs_per_wave * sizeof(float4);
+        if ((NW != 1 && NW != 2 && NW != 4) || shm > 65536) return SNHIP_E_INVAL;
+        per = 4 * S;
+    } else if (block == 0) {
         const long waves1 = (long)tiles1 * ((B + 3) / 4);
         S = s ? s : (B > 8 && waves1 / 4 >= 1024) ? 4 : (B > 4 && waves1 / 2 >= 1024) ? 2 : 1;
         if (S != 1 && S != 2 && S != 4) return SNHIP_E_INVAL;
@@ -943,7 +1197,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
     int total = 0;
     for (int i = 0; i < n; ++i) {
         a.start[i] = total;
-        total += a.tiles_out[i] * a.seq_tiles;
+        total += a.tiles_out[i] * ((a.seq_tiles + NW - 1) / NW);
     }
     a.start[n] = total;
     for (int i = n + 1; i <= kRkqMaxJobs; ++i) a.start[i] = total;
@@ -974,7 +1228,20 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
         else if (NC == 1) SNHIP_RKQ_Q4(B_, 1, 2);        \
         else SNHIP_RKQ_Q4(B_, 2, 2);                     \
     } while (0)
-    if (block == 0) {
+    if (block < 0) {
+#define SNHIP_RKW(S_, N_) hipLaunchKernelGGL((k_rkq_mm_w4<S_, N_>), dim3(total), dim3(64 * N_), shm, st, a)
+#define SNHIP_RKW_S(S_)                        \
+    do {                                       \
+        if (NW == 1) SNHIP_RKW(S_, 1);         \
+        else if (NW == 2) SNHIP_RKW(S_, 2);    \
+        else SNHIP_RKW(S_, 4);                 \
+    } while (0)
+        if (S == 1) SNHIP_RKW_S(1);
+        else if (S == 2) SNHIP_RKW_S(2);
+        else SNHIP_RKW_S(4);
+#undef SNHIP_RKW_S
+#undef SNHIP_RKW
+    } else if (block == 0) {
         if (S == 1) SNHIP_RKQ_F32(1);
         else if (S == 2) SNHIP_RKQ_F32(2);
         else SNHIP_RKQ_F32(4);
@@ -995,6 +1262,24 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
 
 snhip_status launch_rkq_mm(const RkqJob* jobs, int n, int B, int block, hipStream_t st) {
     return launch_rkq_mm_cfg(jobs, n, B, block, 0, 0, st);
+}
+
+size_t rkq_tiled_floats(int M, int Kd) {
+    return ((size_t)((M + 63) / 64) * (size_t)(Kd / 4) * 64 + kRkwPad) * 4;
+}
+
+snhip_status launch_rkq_block4(const float* w, const uint8_t* q, const float* sc, int block, int M, int Kd,
+                               float* out, hipStream_t st) {
+    if (M <= 0 || Kd <= 0 || Kd % 4 || !out || (block != 0 && block != 32 && block != 64) ||
+        (block ? (!q || !sc || Kd % block) : !w))
+        return SNHIP_E_INVAL;
+    RkqJob J{};
+    J.w = w; J.q = q; J.sc = sc; J.M = M; J.Kd = Kd;
+    const size_t n = rkq_tiled_floats(M, Kd) / 4;
+    hipLaunchKernelGGL(k_rkq_block4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, J, block,
+                       reinterpret_cast<float4*>(out));
+    SNHIP_CHECK(hipGetLastError());
+    return SNHIP_OK;
 }
 
 }  // namespace snhip

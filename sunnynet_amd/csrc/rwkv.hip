@@ -123,6 +123,7 @@ struct RMat {
     uint8_t* q = nullptr;
     float* sc = nullptr;
     int block = 0;
+    float* w4 = nullptr;   // the tiled fp32 form the per-kernel steps multiply (or null)
 };
 
 struct RkLayer {
@@ -381,6 +382,46 @@ void setup_rk_persist(SnHipRwkv7* m) {
     m->p_exact = exact;
 }
 
+// The tiled fp32 form of every layer matrix (rkseq.h: block -1), for the
+// per-kernel steps: their products then run one independent wave per 64
+// rows and 4-16 sequences, streaming 1 KiB weight blocks, with no producer
+// waves and no barrier per 64 inputs. Made when some batch size up to
+// max_batch steps per kernel (SNHIP_RKQ_W4=0: never); each is 4 bytes per
+// weight (plus 64 KiB of padding). The vocabulary head keeps its own format.
+void setup_rkq_w4(SnHipRwkv7* m) {
+    if (env_unsigned("SNHIP_RKQ_W4", 1, 0) == 0) return;
+    const int one_launch = m->p_grid > 0 ? std::max(1, m->p_mi_max) : 0;
+    if (m->max_batch <= one_launch) return;
+    bool ok = true;
+    auto make = [&](RMat& M) {
+        if (!ok || M.M <= 0 || M.Kd <= 0 || M.Kd % 4 || (!M.q && !M.w) ||
+            rkq_tiled_floats(M.M, M.Kd) * sizeof(float) >= ((size_t)1 << 31))   // the kernel's 32-bit offsets
+            return;
+        float* w4 = ralloc<float>(m, rkq_tiled_floats(M.M, M.Kd));
+        if (!w4 || launch_rkq_block4(M.w, M.q, M.sc, M.q ? M.block : 0, M.M, M.Kd, w4, nullptr) != SNHIP_OK) {
+            ok = false;
+            return;
+        }
+        M.w4 = w4;
+    };
+    for (int l = 0; l < m->L; ++l) {
+        RkLayer& A = m->layers[l];
+        for (RMat* M : {&A.r, &A.k, &A.v, &A.o, &A.w1, &A.w2, &A.a1, &A.a2, &A.v1, &A.v2, &A.g1, &A.g2,
+                        &A.cmk, &A.cmv})
+            make(*M);
+    }
+    if (hipDeviceSynchronize() != hipSuccess) ok = false;
+    if (!ok) {
+        // all or nothing: the products then keep the stored format
+        for (int l = 0; l < m->L; ++l) {
+            RkLayer& A = m->layers[l];
+            for (RMat* M : {&A.r, &A.k, &A.v, &A.o, &A.w1, &A.w2, &A.a1, &A.a2, &A.v1, &A.v2, &A.g1, &A.g2,
+                            &A.cmk, &A.cmv})
+                M->w4 = nullptr;
+        }
+    }
+}
+
 // Do steps of B sequences run as B slices of the persistent kernel?
 bool uses_mi(const SnHipRwkv7* m, int B) { return m->p_grid > 0 && B >= 2 && B <= m->p_mi_max; }
 
@@ -580,6 +621,7 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
     }
     if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
     setup_rk_persist(m);
+    setup_rkq_w4(m);
     m->ready = 1;
     return m;
 }
@@ -596,12 +638,12 @@ struct MMList {
         if (n == kRkqMaxJobs) return SNHIP_E_INVAL;
         RkqJob j{};
         j.X = X; j.ldx = ldx;
-        j.w = W.w; j.q = W.q; j.sc = W.sc;
+        j.w = W.w4 ? W.w4 : W.w; j.q = W.w4 ? nullptr : W.q; j.sc = W.w4 ? nullptr : W.sc;
         j.M = W.M; j.Kd = W.Kd;
         j.Y = Y; j.ldy = ldy;
         j.epi = epi;
         jobs[n] = j;
-        blk[n] = W.q ? W.block : 0;
+        blk[n] = W.w4 ? -1 : W.q ? W.block : 0;
         ++n;
         return SNHIP_OK;
     }

@@ -260,12 +260,21 @@ def test_cfg4_int4_b1(gpu, cfg4):
     _check_steps(hm, oracle.RkOracle(dq), toks, tol=EXACT)
 
 
-def test_cfg4_int4_b64_exact(gpu, cfg4):
+def _w4(monkeypatch, w4):
+    """SNHIP_RKQ_W4 for the next handle: "1" (default) multiplies the per-kernel
+    products on input-blocked fp32 copies made at load (one independent wave
+    per tile), "0" on the INT4 codes (producer waves dequantizing into LDS)."""
+    monkeypatch.setenv("SNHIP_RKQ_W4", w4)
+
+
+@pytest.mark.parametrize("w4", ["1", "0"])
+def test_cfg4_int4_b64_exact(gpu, cfg4, monkeypatch, w4):
     """B=64 (the benchmark's batched configuration): five sequences replayed
     on the oracle, four steps, logits identical."""
     p, dq = cfg4
     cfg = RWKV_CFG4
-    print("rwkv7 cfg4 int4 g32 B=64, exact", flush=True)
+    print(f"rwkv7 cfg4 int4 g32 B=64, exact, SNHIP_RKQ_W4={w4}", flush=True)
+    _w4(monkeypatch, w4)
     hm = HipRwkv7(p, weights="int4", block=32, max_batch=64)
     pick = [0, 17, 31, 48, 63]
     orc = oracle.RkOracle(dq, batch=len(pick))
@@ -278,7 +287,8 @@ def test_cfg4_int4_b64_exact(gpu, cfg4):
         assert np.array_equal(a[pick], b)
 
 
-def test_cfg4_int4_ragged_batch_exact(gpu, cfg4):
+@pytest.mark.parametrize("w4", ["1", "0"])
+def test_cfg4_int4_ragged_batch_exact(gpu, cfg4, monkeypatch, w4):
     """B=37: the r/k/v and LoRA-up launches then take the staged-X form
     (four consumers per workgroup, 16 sequences of X rows in LDS), with a last
     sequence tile of 5 rows, and the wide vocabulary head four 16-sequence
@@ -289,7 +299,8 @@ def test_cfg4_int4_ragged_batch_exact(gpu, cfg4):
     p, dq = cfg4
     cfg = RWKV_CFG4
     B = 37
-    print(f"rwkv7 cfg4 int4 g32 B={B}, exact", flush=True)
+    print(f"rwkv7 cfg4 int4 g32 B={B}, exact, SNHIP_RKQ_W4={w4}", flush=True)
+    _w4(monkeypatch, w4)
     hm = HipRwkv7(p, weights="int4", block=32, max_batch=B)
     pick = [0, 15, 32, 36]
     orc = oracle.RkOracle(dq, batch=len(pick))
@@ -302,7 +313,8 @@ def test_cfg4_int4_ragged_batch_exact(gpu, cfg4):
         assert np.array_equal(a[pick], b)
 
 
-def test_cfg4_int4_every_batch_size(gpu, cfg4):
+@pytest.mark.parametrize("w4", ["1", "0"])
+def test_cfg4_int4_every_batch_size(gpu, cfg4, monkeypatch, w4):
     """Every batch size 1..64 of the 12-layer INT4 model (1..8 on the exact
     one-launch kernel, one grid slice per sequence; from 9 on the per-kernel
     step, whose launch shapes change with B: one or four consumers per
@@ -311,7 +323,8 @@ def test_cfg4_int4_every_batch_size(gpu, cfg4):
     to the oracle's."""
     p, dq = cfg4
     cfg = RWKV_CFG4
-    print("rwkv7 cfg4 int4 g32 B=1..64, one step each", flush=True)
+    print(f"rwkv7 cfg4 int4 g32 B=1..64, one step each, SNHIP_RKQ_W4={w4}", flush=True)
+    _w4(monkeypatch, w4)
     hm = HipRwkv7(p, weights="int4", block=32, max_batch=64)
     rng = np.random.default_rng(99)
     orc = oracle.RkOracle(dq, batch=2)
