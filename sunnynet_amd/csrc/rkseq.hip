@@ -431,7 +431,6 @@ constexpr int rkw_pf() { return S == 1 ? 48 : S == 2 ? 40 : 24; }
 constexpr int kRkwXA = 4;          // X blocks read from LDS ahead of the MFMAs
 constexpr int kRkwXMax = 4096;     // float4 of X per workgroup (64 KiB): S * Kd <= this
 constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: > rkw_pf)
-constexpr int kRkwL2 = 32;         // weight blocks a wave prefetches into the L2 at most
 // s_waitcnt vmcnt(n) (expcnt, lgkmcnt at their maximum; gfx9 split vmcnt field)
 constexpr int rkw_vmcnt(int n) { return ((n >> 4) & 3) << 14 | 0x0F70 | (n & 15); }
 
@@ -442,8 +441,9 @@ constexpr int rkw_vmcnt(int n) { return ((n >> 4) & 3) << 14 | 0x0F70 | (n & 15)
 // (builtin), these writes to LDS counted as pending at every later LDS read
 // of the kernel's chain loop, which then waited for all loads at the top of
 // each trip and drained the weight prefetch; in a function of their own,
-// the call boundary waited for every load. The caller waits for them itself
-// (they are its oldest loads) before its first read of what they bring.
+// the call boundary waited for every load. The caller waits for them itself:
+// before its first read of what they bring, and for all of them before the
+// wave ends (its LDS may then go to another workgroup).
 __device__ __forceinline__ void dma_lds16(const void* gaddr, uint32_t lds) {
     uint32_t save;
     asm volatile(
@@ -525,24 +525,28 @@ __global__ __launch_bounds__(64 * NW) void k_rkq_mm_w4(const RkqMMArgs A) {
         const int kb = f / R, row = f - kb * R;
         dma_lds16(J.X + (size_t)min(seq0 + row, A.B - 1) * (size_t)J.ldx + 4 * kb, lds_addr(xs + f0));
     }
-    // The L2 prefetch: this sequence tile's share of the output tile's
-    // weights (at most kRkwL2 blocks; lane l touches bytes 16 l .. + 4 of each
+    float4 w[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) w[i] = ldw(i);
+    // X in: every load but the PF weight loads above
+    __builtin_amdgcn_s_waitcnt(rkw_vmcnt(PF));
+    __builtin_amdgcn_sched_barrier(0);
+    // The L2 prefetch, issued once X is in (so the chains do not wait for
+    // it): this sequence tile's share of the output tile's weights past the
+    // first PF blocks (at most 63 - PF blocks, so that the wave's loads in
+    // flight fit the wait counter; lane l touches bytes 16 l .. + 4 of each
     // 1 KiB block, so every 128-byte line) into a 256-byte LDS slot nothing
     // reads. The sequence tiles of an output tile each take their own part,
-    // so its weights leave HBM together at the start rather than block by
-    // block as every chain reaches them.
+    // so its weights leave HBM together rather than block by block as every
+    // chain reaches them.
     {
-        const int share = (nb + A.seq_tiles - 1) / A.seq_tiles, pf0 = min(st * share, nb);
-        const int npf = min(min(share, nb - pf0), kRkwL2);
+        const int rest = max(nb - PF, 0), share = (rest + A.seq_tiles - 1) / A.seq_tiles;
+        const int pf0 = PF + min(st * share, rest);
+        const int npf = min(min(share, nb - pf0), 63 - PF);
         const char* wb = reinterpret_cast<const char*>(J.w) + (size_t)(sob + pf0 * 1024) + 16 * l;
         const uint32_t dump = lds_addr(xs + A.xs_per_wave - 16);
         for (int j = 0; j < npf; ++j) dma_lds4(wb + 1024 * j, dump);
     }
-    float4 w[PF];
-#pragma unroll
-    for (int i = 0; i < PF; ++i) w[i] = ldw(i);
-    // X (and the L2 prefetch) in: every load but the PF weight loads above
-    __builtin_amdgcn_s_waitcnt(rkw_vmcnt(PF));
     __builtin_amdgcn_sched_barrier(0);
     v4f xa[kRkwXA][S];
     v4f acc[S];
@@ -581,6 +585,7 @@ __global__ __launch_bounds__(64 * NW) void k_rkq_mm_w4(const RkqMMArgs A) {
             for (int s = 0; s < S; ++s) xa[i % kRkwXA][s] = xq[(i + kRkwXA) * R + 4 * s];
         }
     }
+    __builtin_amdgcn_s_waitcnt(rkw_vmcnt(0));   // the L2 prefetch's writes to LDS, before the wave can end
 #pragma unroll
     for (int s = 0; s < S; ++s) rkq_finish(J, A.B, -1, seq0 + 4 * s, out, acc[s]);
 }
