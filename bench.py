@@ -67,10 +67,10 @@ SCAN_TRAFFIC_BYTES = 1_611_150_336
 # decode`, calibrated like the scan's and divided by the call's steps. Filled
 # from the tables of profiles/decode_pmc_traffic.md.
 DECODE_TRAFFIC: dict = {
-    ("int4", 1): 96_480_189, ("int4", 8): 156_178_634, ("int4", 32): 174_586_178,
-    ("fp32", 1): 517_492_516, ("fp32", 64): 627_625_344, ("fp16", 1): 285_596_977,
-    ("small", 1): 1_372_454, ("rwkv7-exact", 1): 459_086_488, ("rwkv7", 64): 843_898_581,
-    ("rwkv7-persist", 1): 149_506_321,
+    ("int4", 1): 96_525_699, ("int4", 8): 155_992_914, ("int4", 32): 174_590_113,
+    ("fp32", 1): 517_375_353, ("fp32", 64): 627_634_736, ("fp16", 1): 285_576_898,
+    ("small", 1): 1_386_042, ("rwkv7-exact", 1): 457_100_727, ("rwkv7", 64): 1_068_981_923,
+    ("rwkv7-persist", 1): 149_502_529,
 }
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
 
@@ -740,7 +740,7 @@ def bench_rwkv7(cpu: bool):
         exact = bool(hm.persist_grid) and hm.persist_exact and B == 1
         kernel = ("k_rk_exact (the whole step)" if exact else
                   "k_rk_persist (the whole step)" if hm.persist_grid and B == 1 else
-                  "per-kernel step: k_rkq_ln, k_rkq_mm_q4, k_rkq_heads")
+                  "per-kernel step: k_rkq_ln, k_rkq_mm_w4 (tiled fp32 copies), k_rkq_heads")
         hm.close()
         key = ("rwkv7-persist" if persist else "rwkv7-exact" if exact else "rwkv7", B)
         rl = step_roofline(rwkv7_step_bytes(cfg, B), rwkv7_step_flops(cfg, B), ms * 1e3, kernel,
