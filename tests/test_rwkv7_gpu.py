@@ -313,6 +313,31 @@ def test_cfg4_int4_ragged_batch_exact(gpu, cfg4, monkeypatch, w4):
         assert np.array_equal(a[pick], b)
 
 
+@pytest.mark.parametrize("shape", ["1,1", "1,2", "1,4", "2,1", "2,2", "2,4", "4,1", "4,2"])
+def test_cfg4_int4_tiled_product_shapes(gpu, cfg4, monkeypatch, shape):
+    """Every workgroup shape of the tiled fp32 products (S chains of 4
+    sequences per wave, NW waves per workgroup), forced with
+    SNHIP_RKQ_W4_SHAPE wherever it fits (the channel-mix value's K = 3072
+    takes one chain per wave; a shape over 64 KiB of LDS falls back to the
+    chosen one): B = 37, so the last sequence tile is partial and a
+    workgroup's last waves may have no tile; sequences of the first and the
+    partial tile replayed on the oracle, two steps, logits identical."""
+    p, dq = cfg4
+    cfg = RWKV_CFG4
+    B = 37
+    print(f"rwkv7 cfg4 int4 g32 B={B}, tiled products forced to S,NW={shape}", flush=True)
+    monkeypatch.setenv("SNHIP_RKQ_W4_SHAPE", shape)
+    hm = HipRwkv7(p, weights="int4", block=32, max_batch=B)
+    pick = [0, 3, 33, 36]
+    orc = oracle.RkOracle(dq, batch=len(pick))
+    rng = np.random.default_rng(7)
+    for _ in range(2):
+        toks = rng.integers(0, cfg.vocab, B).astype(np.int32)
+        a = hm.step_batch(torch.from_numpy(toks).cuda()).cpu().numpy()
+        b = orc.step(toks[pick])
+        assert np.array_equal(a[pick], b), float(np.abs(a[pick] - b).max())
+
+
 @pytest.mark.parametrize("w4", ["1", "0"])
 def test_cfg4_int4_every_batch_size(gpu, cfg4, monkeypatch, w4):
     """Every batch size 1..64 of the 12-layer INT4 model (1..8 on the exact
