@@ -86,6 +86,17 @@ struct RkqHeadArgs {
     float* y;            // (B, D)
     int D, NH, first;
     float* dbg;          // if set: sequence 0's k, v, a, ww at dbg + 2D, 3D, 4D, 6D (rwkv7.c:308-319)
+    // The LoRA up-projections w2, a2, g2, v2 computed here from their INT4
+    // codes (up_blk 32 or 64, ranks up_k <= 128; v2 not in layer 0) instead
+    // of read from dw, da, g, dv (up_blk 0): inputs lw, la, lg, lv of
+    // sequence b at up_x[m] + b * up_ldx; the gate also goes to g (the dump
+    // reads it there).
+    const uint8_t* up_q[4];
+    const float* up_sc[4];
+    const float* up_x[4];
+    int up_k[4];
+    int up_blk, up_ldx;
+    float* g_out;
 };
 snhip_status launch_rkq_heads(const RkqHeadArgs& a, int B, hipStream_t st);
 

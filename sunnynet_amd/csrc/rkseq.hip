@@ -937,6 +937,57 @@ __global__ __launch_bounds__(64 * (NC + kRkqNP)) void k_rkq_mm_q4w(const RkqMMAr
 }
 
 // ---------------------------------------------------------------- heads
+// One group of an INT4 row (BLK inputs; the codes in BLK / 32 chunks of 16
+// bytes, scale sc) on top of acc: acc = fmaf(x[i], w[i], acc) for i in order,
+// w[i] dequantized as fma(q, sc, -8 sc) (dequant_at's value). Input i is
+// byte i % (BLK / 2) of the group, low nibble for the first half.
+template <int BLK>
+__device__ __forceinline__ float up_group(float acc, const uint4* qv, float sc, const float* x) {
+    constexpr int HALF = BLK / 2;
+    const float m8 = -8.0f * sc;
+#pragma unroll
+    for (int i = 0; i < BLK; ++i) {
+        const int bi = i % HALF, ch = bi / 16, by = bi % 16;
+        const uint32_t word = by < 4 ? qv[ch].x : by < 8 ? qv[ch].y : by < 12 ? qv[ch].z : qv[ch].w;
+        const uint32_t bt = (word >> (8 * (by % 4))) & 0xFFu;
+        const uint32_t q = i < HALF ? (bt & 0xFu) : (bt >> 4);
+        acc = fmaf(x[i], fmaf((float)q, sc, m8), acc);
+    }
+    return acc;
+}
+
+// The four LoRA up-projections of channel c for sequence b (see RkqHeadArgs):
+// every code chunk is loaded first (up to 4 per matrix, clamped so that no
+// load depends on the rank), then each output is one sequential chain from
+// 0 over its inputs, as the products compute it.
+template <int BLK>
+__device__ __forceinline__ void up_proj(const RkqHeadArgs& A, int b, int c, float (&out)[4]) {
+    constexpr int NQ = BLK / 32, CH = 4;   // chunks per group; chunks per matrix at most
+    uint4 qv[4][CH];
+    float sc[4][CH / NQ];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // rank 0 (layer 0's v2 slot, naming another matrix): one group's
+        // loads of row c of that matrix, in bounds, never used
+        const int K = A.up_k[m] > 0 ? A.up_k[m] : BLK, nch = K / 32;
+        const uint4* q = reinterpret_cast<const uint4*>(A.up_q[m] + (size_t)c * (size_t)(K / 2));
+        const float* s = A.up_sc[m] + (size_t)c * (size_t)(K / BLK);
+#pragma unroll
+        for (int j = 0; j < CH; ++j) qv[m][j] = q[min(j, nch - 1)];
+#pragma unroll
+        for (int g = 0; g < CH / NQ; ++g) sc[m][g] = s[min(g, K / BLK - 1)];
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        float acc = 0.0f;
+        const float* x = A.up_x[m] + (size_t)b * (size_t)A.up_ldx;
+#pragma unroll
+        for (int g = 0; g < CH / NQ; ++g)
+            if (g < A.up_k[m] / BLK) acc = up_group<BLK>(acc, &qv[m][g * NQ], sc[m][g], x + g * BLK);
+        out[m] = acc;
+    }
+}
+
 __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
     __shared__ float w_[kHS], k_[kHS], v_[kHS], a_[kHS], kn_[kHS], r_[kHS], y_[kHS], dt_[kHS],
         sq_[kHS], part[8], stat[3];
@@ -952,12 +1003,22 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
         const float4 v4 = *reinterpret_cast<const float4*>(Sr + q);
         s[q] = v4.x; s[q + 1] = v4.y; s[q + 2] = v4.z; s[q + 3] = v4.w;
     }
-    const float dw = A.dw[row + c], w0 = A.w0[c], v_in = A.v[row + c];
+    float dw, da, dv, gv;
+    if (A.up_blk) {
+        float up[4];
+        if (A.up_blk == 32) up_proj<32>(A, b, c, up);
+        else up_proj<64>(A, b, c, up);
+        dw = up[0]; da = up[1]; gv = up[2]; dv = A.first ? 0.0f : up[3];
+        A.g_out[row + c] = gv;
+    } else {
+        dw = A.dw[row + c]; da = A.da[row + c]; gv = A.g[row + c];
+        dv = A.first ? 0.0f : A.dv[row + c];
+    }
+    const float w0 = A.w0[c], v_in = A.v[row + c];
     const float vf = A.first ? 0.0f : A.vfirst[row + c];
-    const float dv = A.first ? 0.0f : A.dv[row + c];
-    const float v0 = A.v0[c], da = A.da[row + c], a0 = A.a0[c], kv = A.k[row + c];
+    const float v0 = A.v0[c], a0 = A.a0[c], kv = A.k[row + c];
     const float kkw = A.kk_w[c], kaw = A.ka_w[c], rv = A.r[row + c], rkw = A.rk_w[c];
-    const float lnw = A.lnx_w[c], lnb = A.lnx_b[c], gv = A.g[row + c];
+    const float lnw = A.lnx_w[c], lnb = A.lnx_b[c];
     // Channel terms (rwkv7.c:236-260).
     const float ww = refmath::expf(-refmath::sigmoid(dw + w0) * kR2);
     float vv = v_in;
@@ -1069,6 +1130,17 @@ snhip_status launch_rkq_ln(const RkqLnArgs& a, int B, hipStream_t st) {
 
 snhip_status launch_rkq_heads(const RkqHeadArgs& a, int B, hipStream_t st) {
     if (a.D != a.NH * kHS || B <= 0) return SNHIP_E_INVAL;
+    if (a.up_blk) {
+        if ((a.up_blk != 32 && a.up_blk != 64) || !a.g_out) return SNHIP_E_INVAL;
+        // every slot names a matrix the loads may read (an unused v2 slot in
+        // layer 0: any of the others, rank 0, so its chain is empty)
+        for (int m = 0; m < 4; ++m) {
+            const int K = a.up_k[m];
+            if (!a.up_q[m] || !a.up_sc[m] || !a.up_x[m] || K < 0 || K > 128 || K % a.up_blk ||
+                (K == 0 && !(m == 3 && a.first)))
+                return SNHIP_E_INVAL;
+        }
+    }
     hipLaunchKernelGGL(k_rkq_heads, dim3(a.NH, B), dim3(64), 0, st, a);
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;

@@ -154,6 +154,7 @@ struct SnHipRwkv7 {
     hipEvent_t ev_in = nullptr, ev_out = nullptr;
     std::map<std::tuple<int, const void*, int>, hipGraphExec_t> graphs;
     bool use_graphs = true;
+    bool fuse_ups = true;   // LoRA up-projections inside the heads kernel (SNHIP_RKQ_FUSE_UPS=0: apart)
     // One-sequence steps as one cooperative launch each (rkpersist.hip);
     // p_grid = 0 when off (SNHIP_RK_PERSIST=0, or a shape it does not take).
     int p_grid = 0;
@@ -620,6 +621,7 @@ SnHipRwkv7* load_rk(const char* path, int max_batch, int wfmt, int block) {
         return nullptr;
     }
     if (const char* e = getenv("SNHIP_NO_GRAPH")) m->use_graphs = !(e[0] == '1');
+    m->fuse_ups = env_unsigned("SNHIP_RKQ_FUSE_UPS", 1, 0) != 0;
     setup_rk_persist(m);
     setup_rkq_w4(m);
     m->ready = 1;
@@ -705,12 +707,39 @@ snhip_status enqueue_step(SnHipRwkv7* m, int B, float* logits_out, bool greedy, 
         if ((rc = mm.add(A.g1, xg, ld6, lg, ldl, RKQ_SIGMOID)) != SNHIP_OK) return rc;
         if (l > 0 && (rc = mm.add(A.v1, xv, ld6, lv, ldl, RKQ_STORE)) != SNHIP_OK) return rc;
         if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, RKQ_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.a2, la, ldl, m->da, D, RKQ_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.add(A.g2, lg, ldl, m->g, D, RKQ_STORE)) != SNHIP_OK) return rc;
-        if (l > 0 && (rc = mm.add(A.v2, lv, ldl, m->dv, D, RKQ_STORE)) != SNHIP_OK) return rc;
-        if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        // The LoRA up-projections run inside the heads kernel when they are
+        // INT4 of one group size with ranks up to 128 (SNHIP_RKQ_FUSE_UPS=0:
+        // never): it computes each channel's four short chains from the
+        // codes, and the step saves a launch per layer.
+        const bool fuse = m->fuse_ups && A.w2.q && A.a2.q && A.g2.q && (l == 0 || A.v2.q) &&
+                          (A.w2.block == 32 || A.w2.block == 64) && A.a2.block == A.w2.block &&
+                          A.g2.block == A.w2.block && (l == 0 || A.v2.block == A.w2.block) &&
+                          A.w2.Kd <= 128 && A.a2.Kd <= 128 && A.g2.Kd <= 128 && (l == 0 || A.v2.Kd <= 128) &&
+                          A.w2.Kd % A.w2.block == 0 && A.a2.Kd % A.w2.block == 0 &&
+                          A.g2.Kd % A.w2.block == 0 && (l == 0 || A.v2.Kd % A.w2.block == 0) &&
+                          A.w2.M == D && A.a2.M == D && A.g2.M == D && (l == 0 || A.v2.M == D);
+        if (!fuse) {
+            if ((rc = mm.add(A.w2, lw, ldl, m->dw, D, RKQ_STORE)) != SNHIP_OK) return rc;
+            if ((rc = mm.add(A.a2, la, ldl, m->da, D, RKQ_STORE)) != SNHIP_OK) return rc;
+            if ((rc = mm.add(A.g2, lg, ldl, m->g, D, RKQ_STORE)) != SNHIP_OK) return rc;
+            if (l > 0 && (rc = mm.add(A.v2, lv, ldl, m->dv, D, RKQ_STORE)) != SNHIP_OK) return rc;
+            if ((rc = mm.flush(st)) != SNHIP_OK) return rc;
+        }
         RkqHeadArgs H{};
+        if (fuse) {
+            const RMat* up[4] = {&A.w2, &A.a2, &A.g2, l > 0 ? &A.v2 : &A.w2};
+            const float* ux[4] = {lw, la, lg, l > 0 ? lv : lw};
+            const int uk[4] = {A.w2.Kd, A.a2.Kd, A.g2.Kd, l > 0 ? A.v2.Kd : 0};
+            for (int i = 0; i < 4; ++i) {
+                H.up_q[i] = up[i]->q;
+                H.up_sc[i] = up[i]->sc;
+                H.up_x[i] = ux[i];
+                H.up_k[i] = uk[i];
+            }
+            H.up_blk = A.w2.block;
+            H.up_ldx = ldl;
+            H.g_out = m->g;
+        }
         H.r = m->r; H.k = m->k; H.v = m->v; H.dw = m->dw; H.da = m->da; H.dv = m->dv; H.g = m->g;
         H.vfirst = m->vfirst;
         H.w0 = A.w0; H.a0 = A.a0; H.v0 = A.v0; H.kk_w = A.kk; H.ka_w = A.ka; H.rk_w = A.rk;
