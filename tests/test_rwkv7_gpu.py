@@ -267,14 +267,17 @@ def _w4(monkeypatch, w4):
     monkeypatch.setenv("SNHIP_RKQ_W4", w4)
 
 
-@pytest.mark.parametrize("w4", ["1", "0"])
-def test_cfg4_int4_b64_exact(gpu, cfg4, monkeypatch, w4):
+@pytest.mark.parametrize("w4,fuse", [("1", "1"), ("0", "1"), ("1", "0")])
+def test_cfg4_int4_b64_exact(gpu, cfg4, monkeypatch, w4, fuse):
     """B=64 (the benchmark's batched configuration): five sequences replayed
-    on the oracle, four steps, logits identical."""
+    on the oracle, four steps, logits identical; with the LoRA up-projections
+    inside the heads kernel (default) and in their own launch
+    (SNHIP_RKQ_FUSE_UPS=0)."""
     p, dq = cfg4
     cfg = RWKV_CFG4
-    print(f"rwkv7 cfg4 int4 g32 B=64, exact, SNHIP_RKQ_W4={w4}", flush=True)
+    print(f"rwkv7 cfg4 int4 g32 B=64, exact, SNHIP_RKQ_W4={w4} SNHIP_RKQ_FUSE_UPS={fuse}", flush=True)
     _w4(monkeypatch, w4)
+    monkeypatch.setenv("SNHIP_RKQ_FUSE_UPS", fuse)
     hm = HipRwkv7(p, weights="int4", block=32, max_batch=64)
     pick = [0, 17, 31, 48, 63]
     orc = oracle.RkOracle(dq, batch=len(pick))
