@@ -956,44 +956,70 @@ __device__ __forceinline__ float up_group(float acc, const uint4* qv, float sc, 
     return acc;
 }
 
-// The four LoRA up-projections of channel c for sequence b (see RkqHeadArgs):
-// every code chunk is loaded first (up to 4 per matrix, clamped so that no
-// load depends on the rank), then each output is one sequential chain from
-// 0 over its inputs, as the products compute it.
+// LoRA up-projection m of channel c for sequence b (see RkqHeadArgs): every
+// code chunk is loaded first (up to 4, clamped so that no load depends on the
+// rank), then the output is one sequential chain from 0 over its inputs, as
+// the products compute it.
 template <int BLK>
-__device__ __forceinline__ void up_proj(const RkqHeadArgs& A, int b, int c, float (&out)[4]) {
+__device__ __forceinline__ float up_one(const RkqHeadArgs& A, int b, int c, int m) {
     constexpr int NQ = BLK / 32, CH = 4;   // chunks per group; chunks per matrix at most
-    uint4 qv[4][CH];
-    float sc[4][CH / NQ];
+    // rank 0 (layer 0's v2 slot, naming another matrix): one group's loads of
+    // row c of that matrix, in bounds, never used
+    const int Kr = A.up_k[m], K = Kr > 0 ? Kr : BLK, nch = K / 32;
+    const uint4* q = reinterpret_cast<const uint4*>(A.up_q[m] + (size_t)c * (size_t)(K / 2));
+    const float* sp = A.up_sc[m] + (size_t)c * (size_t)(K / BLK);
+    uint4 qv[CH];
+    float sc[CH / NQ];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        // rank 0 (layer 0's v2 slot, naming another matrix): one group's
-        // loads of row c of that matrix, in bounds, never used
-        const int K = A.up_k[m] > 0 ? A.up_k[m] : BLK, nch = K / 32;
-        const uint4* q = reinterpret_cast<const uint4*>(A.up_q[m] + (size_t)c * (size_t)(K / 2));
-        const float* s = A.up_sc[m] + (size_t)c * (size_t)(K / BLK);
+    for (int j = 0; j < CH; ++j) qv[j] = q[min(j, nch - 1)];
 #pragma unroll
-        for (int j = 0; j < CH; ++j) qv[m][j] = q[min(j, nch - 1)];
+    for (int g = 0; g < CH / NQ; ++g) sc[g] = sp[min(g, K / BLK - 1)];
+    float acc = 0.0f;
+    const float* x = A.up_x[m] + (size_t)b * (size_t)A.up_ldx;
 #pragma unroll
-        for (int g = 0; g < CH / NQ; ++g) sc[m][g] = s[min(g, K / BLK - 1)];
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        float acc = 0.0f;
-        const float* x = A.up_x[m] + (size_t)b * (size_t)A.up_ldx;
-#pragma unroll
-        for (int g = 0; g < CH / NQ; ++g)
-            if (g < A.up_k[m] / BLK) acc = up_group<BLK>(acc, &qv[m][g * NQ], sc[m][g], x + g * BLK);
-        out[m] = acc;
-    }
+    for (int g = 0; g < CH / NQ; ++g)
+        if (g < Kr / BLK) acc = up_group<BLK>(acc, &qv[g * NQ], sc[g], x + g * BLK);
+    return acc;
 }
 
-__global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
+// NWV = 4 (the up-projections fused in): waves 1..3 compute them into LDS
+// (wave 1: w2; wave 2: a2, then v2; wave 3: g2) while wave 0 loads its state
+// row; after one workgroup barrier they end and wave 0 runs the rest alone.
+// NWV = 1: one wave, the up-projections read from dw, da, g, dv.
+template <int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_rkq_heads(RkqHeadArgs A) {
     __shared__ float w_[kHS], k_[kHS], v_[kHS], a_[kHS], kn_[kHS], r_[kHS], y_[kHS], dt_[kHS],
         sq_[kHS], part[8], stat[3];
-    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    __shared__ float upv[NWV > 1 ? 4 : 1][kHS];
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x & 63;
+    // The workgroup's syncs after the up-projections: with NWV > 1 wave 0 is
+    // the only wave left, and its LDS operations complete in program order,
+    // so a fence that keeps the compiler from moving them across is enough
+    // (no barrier waits on the waves that have ended).
+    auto sync = [] {
+        if constexpr (NWV > 1) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else {
+            __syncthreads();
+        }
+    };
     const size_t row = (size_t)b * A.D;
     const int c = h * kHS + t;
+    if constexpr (NWV > 1) {
+        const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if (wv != 0) {
+            auto one = [&](int m) {
+                upv[m][t] = A.up_blk == 32 ? up_one<32>(A, b, c, m) : up_one<64>(A, b, c, m);
+            };
+            if (wv == 1) one(0);
+            else if (wv == 2) { one(1); one(3); }
+            else one(2);
+            __syncthreads();
+            return;
+        }
+    }
     // Every input of the wave is loaded before any is used: the state row,
     // the channel's products and parameters, and the epilogue's.
     float* Sr = A.S + (size_t)b * A.s_bstride + (size_t)h * kHS * kHS + (size_t)t * kHS;
@@ -1004,11 +1030,9 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
         s[q] = v4.x; s[q + 1] = v4.y; s[q + 2] = v4.z; s[q + 3] = v4.w;
     }
     float dw, da, dv, gv;
-    if (A.up_blk) {
-        float up[4];
-        if (A.up_blk == 32) up_proj<32>(A, b, c, up);
-        else up_proj<64>(A, b, c, up);
-        dw = up[0]; da = up[1]; gv = up[2]; dv = A.first ? 0.0f : up[3];
+    if constexpr (NWV > 1) {
+        __syncthreads();   // the up-projections in
+        dw = upv[0][t]; da = upv[1][t]; gv = upv[2][t]; dv = A.first ? 0.0f : upv[3][t];
         A.g_out[row + c] = gv;
     } else {
         dw = A.dw[row + c]; da = A.da[row + c]; gv = A.g[row + c];
@@ -1039,7 +1063,7 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
     }
     w_[t] = ww; k_[t] = k2; v_[t] = vv; a_[t] = av; kn_[t] = kkv; r_[t] = rv;
     dt_[t] = rv * k2 * rkw;
-    __syncthreads();
+    sync();
     // |kk|: eight stride-8 partial sums of squares (rwkv7.c:156-162).
     if (t < 8) {
         float ss = 0.0f;
@@ -1050,17 +1074,17 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
         }
         part[t] = ss;
     }
-    __syncthreads();
+    sync();
     if (t == 0) {
         float nrm = sqrtf(hsum8(part));
         if (!(nrm > 1e-12f)) nrm = 1e-12f;
         stat[0] = 1.0f / nrm;
     }
-    __syncthreads();
+    sync();
     const float kn = kkv * stat[0];
-    __syncthreads();
+    sync();
     kn_[t] = kn;
-    __syncthreads();
+    sync();
     // State row t (rwkv7.c:165-187).
     float proj[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1083,7 +1107,7 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
     for (int q = 0; q < kHS; q += 4)
         *reinterpret_cast<float4*>(Sr + q) = make_float4(s[q], s[q + 1], s[q + 2], s[q + 3]);
     y_[t] = hsum8(yacc);
-    __syncthreads();
+    sync();
     // Group norm, bonus, gate (rwkv7.c:266-288): the mean and the bonus dot
     // as sequential sums (lanes 0 and 1 side by side), then the variance.
     if (t < 2) {
@@ -1093,19 +1117,19 @@ __global__ __launch_bounds__(64) void k_rkq_heads(RkqHeadArgs A) {
         for (int i = 0; i < kHS; ++i) acc = acc + src[i];
         stat[1 + t] = acc;
     }
-    __syncthreads();
+    sync();
     const float mean = stat[1] / (float)kHS, dot = stat[2];
     const float yy = y_[t];
     const float dd = yy - mean;
     sq_[t] = dd * dd;
-    __syncthreads();
+    sync();
     if (t == 0) {
         float var = 0.0f;
 #pragma unroll 8
         for (int i = 0; i < kHS; ++i) var = var + sq_[i];
         stat[0] = 1.0f / sqrtf(var / (float)kHS + kEpsGroup);
     }
-    __syncthreads();
+    sync();
     const float n = (yy - mean) * stat[0] * lnw + lnb;
     A.y[row + c] = (n + dot * vv) * gv;
 }
@@ -1141,7 +1165,8 @@ snhip_status launch_rkq_heads(const RkqHeadArgs& a, int B, hipStream_t st) {
                 return SNHIP_E_INVAL;
         }
     }
-    hipLaunchKernelGGL(k_rkq_heads, dim3(a.NH, B), dim3(64), 0, st, a);
+    if (a.up_blk) hipLaunchKernelGGL(k_rkq_heads<4>, dim3(a.NH, B), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(k_rkq_heads<1>, dim3(a.NH, B), dim3(64), 0, st, a);
     SNHIP_CHECK(hipGetLastError());
     return SNHIP_OK;
 }
