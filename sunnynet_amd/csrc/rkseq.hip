@@ -426,8 +426,12 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 // renumbered so that consecutive numbers run on one XCD (dispatch is
 // round-robin over the 8 XCDs): the sequence tiles of an output tile then
 // read its weights from one L2.
-template <int S>
-constexpr int rkw_pf() { return S == 1 ? 48 : S == 2 ? 40 : 24; }
+// Weight blocks in flight per wave. Measured on the RWKV-7 step (cfg4 INT4,
+// one chain per wave): with one wave per CU (B = 16) 48 beat 24 by 2 %; with
+// four (r/k/v, the LoRA ups and the channel-mix key at B = 64) 24 beat 48 by
+// 2 %, the CU's loads in flight at once then being four waves' worth.
+template <int S, int NW>
+constexpr int rkw_pf() { return S == 1 ? (NW == 1 ? 48 : NW == 2 ? 40 : 24) : S == 2 ? 40 : 24; }
 constexpr int kRkwXA = 4;          // X blocks read from LDS ahead of the MFMAs
 constexpr int kRkwXMax = 4096;     // float4 of X per workgroup (64 KiB): S * Kd <= this
 constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: > rkw_pf)
@@ -485,7 +489,7 @@ __device__ __forceinline__ const lds_f4* lds_vbase(const float4* p) {
 
 template <int S, int NW>
 __global__ __launch_bounds__(64 * NW) void k_rkq_mm_w4(const RkqMMArgs A) {
-    constexpr int PF = rkw_pf<S>();
+    constexpr int PF = rkw_pf<S, NW>();
     constexpr int R = 4 * S;   // sequences of the wave
     static_assert(PF % kRkwXA == 0, "the X ring restarts with each weight group");
     extern __shared__ float4 xsh[];
