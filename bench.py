@@ -69,7 +69,7 @@ SCAN_TRAFFIC_BYTES = 1_611_150_336
 DECODE_TRAFFIC: dict = {
     ("int4", 1): 96_525_699, ("int4", 8): 155_992_914, ("int4", 32): 174_590_113,
     ("fp32", 1): 517_375_353, ("fp32", 64): 627_634_736, ("fp16", 1): 285_576_898,
-    ("small", 1): 1_386_042, ("rwkv7-exact", 1): 457_100_727, ("rwkv7", 64): 1_068_981_923,
+    ("small", 1): 1_386_042, ("rwkv7-exact", 1): 457_100_727, ("rwkv7", 64): 1_047_303_436,
     ("rwkv7-persist", 1): 149_502_529,
 }
 METRIC = "decode tok/s @B=1,B=64 (SunnyNet-100M); gated-scan HBM GB/s % of peak"
