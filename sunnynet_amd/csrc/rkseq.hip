@@ -426,12 +426,11 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 // renumbered so that consecutive numbers run on one XCD (dispatch is
 // round-robin over the 8 XCDs): the sequence tiles of an output tile then
 // read its weights from one L2.
-// Weight blocks in flight per wave. Measured on the RWKV-7 step (cfg4 INT4,
-// one chain per wave): with one wave per CU (B = 16) 48 beat 24 by 2 %; with
-// four (r/k/v, the LoRA ups and the channel-mix key at B = 64) 24 beat 48 by
-// 2 %, the CU's loads in flight at once then being four waves' worth.
-template <int S, int NW>
-constexpr int rkw_pf() { return S == 1 ? (NW == 1 ? 48 : NW == 2 ? 40 : 24) : S == 2 ? 40 : 24; }
+// Weight blocks in flight per wave (PF): chosen by the launcher, 48 while
+// the launch's waves fit one per CU and 24 beyond, when each CU's loads in
+// flight are several waves' worth (measured on the RWKV-7 step, cfg4 INT4:
+// at B = 16 48 beat 24 by 2 %, at B = 64 24 beat 48 by 2 % on the launches of
+// 656 - 768 waves).
 constexpr int kRkwXA = 4;          // X blocks read from LDS ahead of the MFMAs
 constexpr int kRkwXMax = 4096;     // float4 of X per workgroup (64 KiB): S * Kd <= this
 constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: > rkw_pf)
@@ -487,9 +486,8 @@ __device__ __forceinline__ const lds_f4* lds_vbase(const float4* p) {
     return (const lds_f4*)(size_t)a;
 }
 
-template <int S, int NW>
+template <int S, int NW, int PF>
 __global__ __launch_bounds__(64 * NW) void k_rkq_mm_w4(const RkqMMArgs A) {
-    constexpr int PF = rkw_pf<S, NW>();
     constexpr int R = 4 * S;   // sequences of the wave
     static_assert(PF % kRkwXA == 0, "the X ring restarts with each weight group");
     extern __shared__ float4 xsh[];
@@ -1214,6 +1212,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
     bool xl = false;   // INT4: four one-chain consumers per workgroup, X staged in LDS
     size_t shm = 0;
     int NW = 1;   // tiled fp32: waves per workgroup
+    bool wdeep = true;   // tiled fp32: the deeper weight stream (at most one wave per CU)
     if (block < 0) {
         // One chain per wave; the waves of one output tile's sequence tiles
         // in workgroups of NW (one per SIMD) once there are more waves than
@@ -1237,7 +1236,11 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
             while (S < 4 && waves(S) > 4 * cus) S *= 2;
         while (!s && S > 1 && S * kmax > kRkwXMax) S /= 2;
         if ((S != 1 && S != 2 && S != 4) || S * kmax > kRkwXMax) return SNHIP_E_INVAL;
-        NW = nc ? nc : waves(S) <= cus ? 1 : waves(S) <= 2 * cus ? 2 : 4;
+        // One wave per workgroup (grouping an output tile's waves 2 or 4 per
+        // workgroup measured 2 % slower at B = 64 once the stream depth
+        // follows the waves per CU); NW only when forced.
+        NW = nc ? nc : 1;
+        wdeep = waves(S) <= cus;
         // per wave: X (S Kd float4, rounded up to the staging's 64) and the
         // read-ahead past the last block; at most 64 KiB per workgroup
         a.xs_per_wave = (S * kmax + 63) / 64 * 64 + kRkwXA * 4 * S + 16;   // + the prefetch's dump slot
@@ -1335,17 +1338,26 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
         else SNHIP_RKQ_Q4(B_, 2, 2);                     \
     } while (0)
     if (block < 0) {
-#define SNHIP_RKW(S_, N_) hipLaunchKernelGGL((k_rkq_mm_w4<S_, N_>), dim3(total), dim3(64 * N_), shm, st, a)
-#define SNHIP_RKW_S(S_)                        \
-    do {                                       \
-        if (NW == 1) SNHIP_RKW(S_, 1);         \
-        else if (NW == 2) SNHIP_RKW(S_, 2);    \
-        else SNHIP_RKW(S_, 4);                 \
-    } while (0)
-        if (S == 1) SNHIP_RKW_S(1);
-        else if (S == 2) SNHIP_RKW_S(2);
-        else SNHIP_RKW_S(4);
-#undef SNHIP_RKW_S
+#define SNHIP_RKW(S_, N_, P_) \
+    hipLaunchKernelGGL((k_rkq_mm_w4<S_, N_, P_>), dim3(total), dim3(64 * N_), shm, st, a)
+        if (S == 1) {
+            if (NW == 1) {
+                if (wdeep) SNHIP_RKW(1, 1, 48);
+                else SNHIP_RKW(1, 1, 24);
+            } else if (NW == 2) {
+                SNHIP_RKW(1, 2, 40);
+            } else {
+                SNHIP_RKW(1, 4, 24);
+            }
+        } else if (S == 2) {
+            if (NW == 1) SNHIP_RKW(2, 1, 40);
+            else if (NW == 2) SNHIP_RKW(2, 2, 40);
+            else SNHIP_RKW(2, 4, 40);
+        } else {
+            if (NW == 1) SNHIP_RKW(4, 1, 24);
+            else if (NW == 2) SNHIP_RKW(4, 2, 24);
+            else SNHIP_RKW(4, 4, 24);
+        }
 #undef SNHIP_RKW
     } else if (block == 0) {
         if (S == 1) SNHIP_RKQ_F32(1);
