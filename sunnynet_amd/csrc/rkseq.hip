@@ -427,10 +427,10 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 // round-robin over the 8 XCDs): the sequence tiles of an output tile then
 // read its weights from one L2.
 // Weight blocks in flight per wave (PF): chosen by the launcher, 48 while
-// the launch's waves fit one per CU and 24 beyond, when each CU's loads in
+// the launch's waves fit one per CU and 16 beyond, when each CU's loads in
 // flight are several waves' worth (measured on the RWKV-7 step, cfg4 INT4:
-// at B = 16 48 beat 24 by 2 %, at B = 64 24 beat 48 by 2 % on the launches of
-// 656 - 768 waves).
+// at B = 16 48 beat 24 by 2 % and 56 by 1 %; at B = 64, on the launches of
+// 656 - 768 waves, 24 beat 48 by 2 % and 16 beat 24 by 0.4 %).
 constexpr int kRkwXA = 4;          // X blocks read from LDS ahead of the MFMAs
 constexpr int kRkwXMax = 4096;     // float4 of X per workgroup (64 KiB): S * Kd <= this
 constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: > rkw_pf)
@@ -1343,7 +1343,7 @@ snhip_status launch_rkq_mm_cfg(const RkqJob* jobs, int n, int B, int block, int 
         if (S == 1) {
             if (NW == 1) {
                 if (wdeep) SNHIP_RKW(1, 1, 48);
-                else SNHIP_RKW(1, 1, 24);
+                else SNHIP_RKW(1, 1, 16);
             } else if (NW == 2) {
                 SNHIP_RKW(1, 2, 40);
             } else {
