@@ -544,7 +544,10 @@ __global__ __launch_bounds__(64 * NW) void k_rkq_mm_w4(const RkqMMArgs A) {
     {
         const int rest = max(nb - PF, 0), share = (rest + A.seq_tiles - 1) / A.seq_tiles;
         const int pf0 = PF + min(st * share, rest);
-        const int npf = min(min(share, nb - pf0), 63 - PF);
+        // only in the shallow form (several waves per CU): with one wave per
+        // CU the deep stream alone was faster (B = 16 1,145 -> 1,125 us/step
+        // without it; B = 64 1,304 -> 1,297 with it on the shallow launches only)
+        const int npf = PF < 48 ? min(min(share, nb - pf0), 63 - PF) : 0;
         const char* wb = reinterpret_cast<const char*>(J.w) + (size_t)(sob + pf0 * 1024) + 16 * l;
         const uint32_t dump = lds_addr(xs + A.xs_per_wave - 16);
         for (int j = 0; j < npf; ++j) dma_lds4(wb + 1024 * j, dump);
