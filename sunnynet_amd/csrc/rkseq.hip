@@ -412,8 +412,9 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 // producers' dequantization, or from fp32 rows: float4 (t * nb + kb) * 64 + l
 // holds inputs 4 kb .. 4 kb + 3 of row 64 t + l (rows past M repeat row
 // M - 1), nb = Kd / 4, followed by kRkwPad float4 that loads past the end
-// may touch. One wave per workgroup: 64 rows x S groups of 4 sequences,
-// nothing shared with other waves, so no barrier paces its chains. A chain
+// may touch. One wave per 64 rows x S groups of 4 sequences (one wave per
+// workgroup unless a tuning shape groups NW of an output tile's waves),
+// nothing shared between waves, so no barrier paces its chains. A chain
 // step is one dependent v_mfma_f32_4x4x1_16b_f32 (~13 cycles on gfx950),
 // and every other instruction of the wave lengthens it (measured: X read from
 // LDS once per 4 inputs, 13.3 -> 15.3 cycles per input; with 64-bit address
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 // memory; the scalar offset advances, the lane offset and the immediate stay
 // fixed) and one LDS read of X at an immediate offset from the lane's base.
 // The wave's X rows go straight into LDS at the start (one load latency);
-// its weight blocks run rkw_pf blocks ahead in registers. Workgroups are
+// its weight blocks run PF blocks ahead in registers. Workgroups are
 // renumbered so that consecutive numbers run on one XCD (dispatch is
 // round-robin over the 8 XCDs): the sequence tiles of an output tile then
 // read its weights from one L2.
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(64) void k_rkq_mm_f32(const RkqMMArgs A) {
 // 656 - 768 waves, 24 beat 48 by 2 % and 16 beat 24 by 0.4 %).
 constexpr int kRkwXA = 4;          // X blocks read from LDS ahead of the MFMAs
 constexpr int kRkwXMax = 4096;     // float4 of X per workgroup (64 KiB): S * Kd <= this
-constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: > rkw_pf)
+constexpr int kRkwPad = 64 * 64;   // float4 after a tiled matrix (64 blocks: the stream reads up to PF - 1 past a tile)
 // s_waitcnt vmcnt(n) (expcnt, lgkmcnt at their maximum; gfx9 split vmcnt field)
 constexpr int rkw_vmcnt(int n) { return ((n >> 4) & 3) << 14 | 0x0F70 | (n & 15); }
 
